@@ -1,0 +1,184 @@
+/*
+ * shadowkv_amd — C ABI of the MI355X (gfx950) ShadowKV sparse-decode kernels.
+ *
+ * Every entry point takes raw device pointers (or a device-accessible pinned-host
+ * pointer where stated), element strides as int64_t, plain int shapes and a HIP
+ * stream passed as `void*` (a hipStream_t; NULL is the legacy default stream).
+ * Every entry point is asynchronous on that stream, allocates nothing, and returns
+ * SKV_OK (0) or a nonzero status; skv_last_error() then describes the failure.
+ *
+ * bf16 tensors are passed as uint16_t bit patterns. Citations name the reference
+ * interface (WilliamBy/ShadowKV, path:line) each entry point replaces.
+ */
+#ifndef SHADOWKV_AMD_H
+#define SHADOWKV_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SKV_OK 0
+#define SKV_EINVAL 1       /* bad pointer, shape, stride or alignment */
+#define SKV_EUNSUPPORTED 2 /* shape outside what the kernels implement */
+#define SKV_ELAUNCH 3      /* HIP launch or runtime error */
+
+/* Library version string and the message of the last failing call on this host thread. */
+const char* skv_version(void);
+const char* skv_last_error(void);
+
+/* Translate a pinned host pointer (hipHostMalloc / torch pin_memory) to the device
+ * address kernels must use for it. No reference counterpart: the reference relies on
+ * CUDA UVA implicitly (kernels/copy.cuh:492 reads the host pointer directly). */
+int skv_host_device_pointer(const void* host_ptr, void** device_ptr);
+
+/* ---- a3: cache-hit reorder ------------------------------------------------------
+ * Replaces reorder_keys_and_compute_offsets (kernels/functions.h:37-42,
+ * kernels/gather_copy.cu:189-235, device kernels/map.cuh:475-516).
+ * Per row r < batch_size*heads, with old = cached_pos_ids[r, :map_size] (slot order)
+ * and new = cur_pos_ids[r, :map_size] (unique chunk ids, any order):
+ *   cached_pos_ids[r] <- [hit ids ordered by ascending old slot] ++ [miss ids ascending]
+ *   offsets[r]        <- [old slots of the hits, ascending]     ++ [miss ids ascending]
+ *   cnts[r]           <- number of hits
+ * map_size may be any value in [1, 2048] (the reference launches only 128/256/512/1024).
+ * Old ids must be unique apart from -1 (empty slot, never a hit); new ids unique and >= 0. */
+int skv_reorder_keys_and_compute_offsets(int64_t* cached_pos_ids, const int64_t* cur_pos_ids,
+                                         int32_t* offsets, int32_t* cnts, int batch_size, int heads,
+                                         int map_size, void* stream);
+
+/* ---- a4: value fetch into the GPU chunk cache ---------------------------------------
+ * Replaces gather_copy_with_offsets (kernels/functions.h:44-51, kernels/gather_copy.cu:239-324,
+ * device kernels/copy.cuh:438-498). For row r, chunk unit = chunk_elems bf16 values:
+ *   slot(i) = v_cache_buffer + r*gpu_v_stride + gpu_v_offset + i*chunk_elems
+ *   i <  cnts[r]: slot(i) <- slot(offsets[r,i])              (in-place forward compaction)
+ *   i >= cnts[r]: slot(i) <- values + r*cpu_v_length + offsets[r,i]*chunk_elems (host store)
+ * `values` is the device address of the pinned host store (see skv_host_device_pointer).
+ * The reference's `temp` staging buffer and `signals` flags have no equivalent here.
+ * gpu_v_length must equal map_size*chunk_elems (the reference's per-row temp length). */
+int skv_gather_copy_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
+                                 const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length,
+                                 int64_t gpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
+                                 int map_size, int chunk_elems, void* stream);
+
+/* ---- a5: key-hit compaction ------------------------------------------------------------
+ * Replaces gather_copy_d2d_with_offsets (kernels/functions.h:27-35, kernels/gather_copy.cu:112-185,
+ * device kernels/copy.cuh:353-390): the i < cnts[r] part of skv_gather_copy_with_offsets on `keys`. */
+int skv_gather_copy_d2d_with_offsets(void* keys, const int32_t* offsets, const int32_t* cnts,
+                                     int batch_size, int heads, int64_t gpu_k_length,
+                                     int64_t gpu_k_offset, int64_t gpu_k_stride, int map_size,
+                                     int chunk_elems, void* stream);
+
+/* Plain chunk gather without cache hits. Replaces gather_copy (kernels/functions.h:23-25,
+ * kernels/gather_copy.cu:47-109): dst + r*gpu_v_length + i*chunk_elems <-
+ * values + r*cpu_v_length + position_ids[r*map_size+i]*chunk_elems. */
+int skv_gather_copy(const void* values, void* v_cache_buffer, const int64_t* position_ids,
+                    int batch_size, int heads, int64_t cpu_v_length, int64_t gpu_v_length,
+                    int map_size, int chunk_elems, void* stream);
+
+/* ---- a7: RoPE ---------------------------------------------------------------------------
+ * Replaces apply_rotary_pos_emb_new (kernels/functions.h:61-67, kernels/rope_new.cu:26-84):
+ * output[b,h,s] = rope(x[b,h,s], cos_sin[position_ids[b,h,s]]) with the half-split layout,
+ * cos_sin row = [cos(half_dim) | sin(half_dim)], per-op bf16 rounding. */
+int skv_apply_rotary_pos_emb_new(const uint16_t* x, const uint16_t* cos_sin, const int64_t* position_ids,
+                                 uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
+                                 int64_t stride_xb, int64_t stride_xh, int64_t stride_xs, int64_t stride_xe,
+                                 int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h,
+                                 int64_t stride_pid_s, int half_dim, void* stream);
+
+/* Replaces apply_rotary_pos_emb_push_cache_opt (kernels/functions.h:88-97, kernels/rope_new.cu:224-302):
+ * for rows s with s/chunk_size >= cnts[b*heads+h] and start+s < end, writes
+ * rope(x[b,h,s], cos_sin[position_ids[b,h,s/chunk]*chunk + s%chunk]) to output[b,h,start+s]. */
+int skv_apply_rotary_pos_emb_push_cache_opt(
+    const uint16_t* x, const uint16_t* cos_sin, const int32_t* position_ids, uint16_t* output,
+    const int32_t* cnts, int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb,
+    int64_t stride_xh, int64_t stride_xs, int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b,
+    int64_t stride_pid_h, int64_t stride_pid_s, int64_t stride_output_b, int64_t stride_output_h,
+    int64_t stride_output_s, int offset_output_s_start, int offset_output_s_end, int half_dim,
+    int chunk_size, void* stream);
+
+/* Replaces apply_rotary_pos_emb_push_cache_opt_glm (kernels/functions.h:99-108,
+ * kernels/rope_new.cu:305-404): GLM interleaved pairs (2i, 2i+1), i < 32, with
+ * cos_sin row = [cos(32) | sin(32)]; dims 64..127 copied unchanged. */
+int skv_apply_rotary_pos_emb_push_cache_opt_glm(
+    const uint16_t* x, const uint16_t* cos_sin, const int32_t* position_ids, uint16_t* output,
+    const int32_t* cnts, int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb,
+    int64_t stride_xh, int64_t stride_xs, int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b,
+    int64_t stride_pid_h, int64_t stride_pid_s, int64_t stride_output_b, int64_t stride_output_h,
+    int64_t stride_output_s, int offset_output_s_start, int offset_output_s_end, int half_dim,
+    int chunk_size, void* stream);
+
+/* ---- a6: low-rank key rebuild ------------------------------------------------------------
+ * Replaces batch_gather_gemm (kernels/functions.h:110-116, kernels/batch_gather_gemm.cu:136-213):
+ * for bh < batch_size*heads and rows r in [offset_array[bh]*chunk_size, sparse_budget):
+ *   output[bh, r, :] = bf16( a[bh/heads, pos(r), :rank] . b[bh, :, :rank]^T ),
+ *   pos(r) = position_ids[bh*(sparse_budget/chunk_size) + r/chunk_size]*chunk_size + r%chunk_size.
+ * a: [batch, seq_len, rank]; b: [batch*heads, embed_dim, rank]; output [batch*heads, sparse_budget, embed_dim].
+ * Hit rows (r < offset_array[bh]*chunk_size) are left untouched. embed_dim must be 128. */
+int skv_batch_gather_gemm(const uint16_t* a, const uint16_t* b, const int32_t* position_ids,
+                          uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
+                          int rank, int sparse_budget, int max_seq_len, int chunk_size,
+                          const int32_t* offset_array, void* stream);
+
+/* a6+a7 fused: the rebuild above followed by the RoPE push, in one pass, writing rotated keys
+ * of miss rows straight into the key cache. Replaces batch_gather_gemm_rotary_pos_emb_cuda
+ * (models/tensor_op.py:206-243 = batch_gather_gemm + apply_rotary_pos_emb_push_cache_opt[_glm]).
+ *   u row of (b,h,p):  u + b*u_stride_b + h*u_stride_h + p*u_stride_row      (u_stride_h = 0: head-shared U)
+ *   sv of (b,h):       sv + b*sv_stride_b + h*sv_stride_h, [head_dim rows][rank], row stride sv_stride_n
+ *   chunk ids:         position_ids[b*pid_stride_b + h*pid_stride_h + c]       (int64)
+ *   out row of (b,h,r): cache + b*stride_cache_b + h*stride_cache_h + (sparse_start+r)*stride_cache_s
+ * rope_mode 0: half-split with cos_sin row [cos(64)|sin(64)]; 1: GLM interleaved (see above).
+ * Rows whose position falls outside [0, u_rows) or [0, cos_sin_rows) are not written.
+ * head_dim must be 128, rank a multiple of 8 in [8, 192]. */
+int skv_rebuild_k_rope(const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
+                       int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b, int64_t sv_stride_h,
+                       int64_t sv_stride_n, const int64_t* position_ids, int64_t pid_stride_b, int64_t pid_stride_h,
+                       const int32_t* cnts, const uint16_t* cos_sin, int64_t stride_cos_sin, int64_t cos_sin_rows,
+                       int rope_mode,
+                       uint16_t* cache, int64_t stride_cache_b, int64_t stride_cache_h,
+                       int64_t stride_cache_s, int sparse_start, int batch_size, int heads,
+                       int num_chunks, int chunk_size, int rank, int head_dim, void* stream);
+
+/* ---- a1: landmark scoring ------------------------------------------------------------------
+ * Replaces batch_gemm_softmax (kernels/functions.h:118-121, kernels/batch_gemm_softmax.cu:143-196):
+ *   D[z, i, j]       = bf16(alpha * sum_k A[z, i, k] * B[z, j, k])          (A [batch][m][k], B [batch][n][k])
+ *   softmax[z, i, :] = bf16(softmax_fp32(D[z, i, :]))
+ * norm/sum [batch][m][ceil(n/256)] receive per-256-column partial max and sum of exp(D - max).
+ * k must be 128, m in [1, 16], beta must be 0 (the reference passes no C operand). */
+int skv_batch_gemm_softmax(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
+                           uint16_t* softmax, int batch_count, int m, int n, int k, float alpha,
+                           float beta, void* stream);
+
+/* a1+a2 fused front: the scoring above, then the GQA max over the m rows of each batch entry,
+ * written as out[z, j] = max_i softmax[z, i, j] (bf16). Replaces batch_gemm_softmax + torch.max
+ * (models/kvcache/shadow.py:553-568). D/norm/sum are caller-provided scratch as above. */
+int skv_score_gqa_max(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
+                      uint16_t* out, int batch_count, int m, int n, int k, float alpha, void* stream);
+
+/* ---- a2: chunk top-k and landmark-id gather ---------------------------------------------------
+ * Replaces torch.topk(scores, k).indices + k_landmark_idx.gather (models/kvcache/shadow.py:571-573):
+ *   out_ids[r, j] = landmark_idx[r*idx_stride + sel_j],
+ * where sel_0..sel_{k-1} are the k largest of scores[r*score_stride + 0..n-1] under the total
+ * order (value descending, index ascending), emitted in that order. k in [1, 4096], k <= n. */
+int skv_topk_gather(const uint16_t* scores, int64_t score_stride, const int64_t* landmark_idx,
+                    int64_t idx_stride, int rows, int n, int k, int64_t* out_ids, void* stream);
+
+/* ---- a8: sparse decode attention ----------------------------------------------------------------
+ * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, causal=True) for one query token
+ * (models/attention/shadow.py:48): for b, query head hq, kv head h = hq / (q_heads/kv_heads):
+ *   out[b, hq] = softmax(scale * q[b,hq] . K[b,h,:kv_len]^T) . V[b,h,:kv_len]   (fp32 math, bf16 out)
+ * q row: q + b*q_stride_b + hq*q_stride_h; K/V row s of (b,h): base + b*kv_stride_b + h*kv_stride_h
+ * + s*kv_stride_s; out row: out + b*o_stride_b + hq*o_stride_h. head_dim must be 128.
+ * workspace: caller-provided device scratch of skv_sparse_attn_workspace_bytes(...) bytes. */
+int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, int kv_len);
+int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+                           const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
+                           int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
+                           int kv_len, float scale, void* workspace, int64_t workspace_bytes, uint16_t* out,
+                           int64_t o_stride_b, int64_t o_stride_h, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHADOWKV_AMD_H */

@@ -1,0 +1,212 @@
+// a4/a5: chunk copies into the GPU-resident sparse K/V region.
+//
+// The reference moves 2 KB chunks with one 128-thread block per (b,h) and a pair of blocks
+// coupled by a spin flag (kernels/copy.cuh:438-498). Here the work is split into two
+// stream-ordered kernels, so no workgroup ever waits on another:
+//   compact_hits_kernel  — one workgroup per row performs the in-place forward compaction
+//                          slot[i] <- slot[offsets[i]] for i < cnt (offsets ascending, offsets[i] >= i);
+//   gather_chunks_kernel — many workgroups per row fetch the miss chunks i >= cnt straight from
+//                          the pinned host store (zero-copy 16-byte loads over the host link),
+//                          each workgroup keeping 8 loads per lane in flight.
+// The copy unit is a chunk of chunk_elems bf16 values, moved as 16-byte vectors.
+#include "skv_common.h"
+
+namespace {
+
+using skv::u32x4;
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;             // 16-byte vectors in flight per lane
+constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch workgroup
+
+// In-place forward compaction of the hit chunks of one row. Offsets are strictly ascending
+// with offsets[i] >= i, so the hits whose offset equals their index form a prefix that is
+// already in place; the rest are moved in batches. Within a batch every load is drained
+// before any store (a source slot of one chunk can be the destination of another chunk of
+// the same batch); a later batch only reads slots beyond every destination of earlier ones.
+__global__ void __launch_bounds__(kThreads) compact_hits_kernel(u32x4* __restrict__ buf, const int32_t* __restrict__ offsets,
+                                                                 const int32_t* __restrict__ cnts, int64_t row_stride_vec,
+                                                                 int64_t row_offset_vec, int S, int chunk_vec) {
+  __shared__ int first_moved;
+  const int row = blockIdx.x;
+  const int cnt = min(cnts[row], S);
+  if (cnt <= 0) return;
+  const int32_t* offs = offsets + static_cast<int64_t>(row) * S;
+  if (threadIdx.x == 0) first_moved = cnt;
+  __syncthreads();
+  for (int j = threadIdx.x; j < cnt; j += blockDim.x)
+    if (offs[j] != j) atomicMin(&first_moved, j);
+  __syncthreads();
+  const int p = first_moved;
+  u32x4* base = buf + static_cast<int64_t>(row) * row_stride_vec + row_offset_vec;
+  const int64_t total = static_cast<int64_t>(cnt - p) * chunk_vec;
+  for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(blockDim.x) * kUnroll) {
+    u32x4 r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      if (v < total) {
+        int j = p + static_cast<int>(v / chunk_vec);
+        int e = static_cast<int>(v % chunk_vec);
+        int src = offs[j];
+        if (src >= 0 && src < S) r[u] = base[static_cast<int64_t>(src) * chunk_vec + e];
+      }
+    }
+    skv::drain_and_barrier();
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      if (v < total) {
+        int j = p + static_cast<int>(v / chunk_vec);
+        int e = static_cast<int>(v % chunk_vec);
+        int src = offs[j];
+        if (src >= 0 && src < S) base[static_cast<int64_t>(j) * chunk_vec + e] = r[u];
+      }
+    }
+  }
+}
+
+// dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where
+// start = cnts[row] (or 0 without cnts). Grid = rows * tiles; tile t covers
+// kChunksPerFetchWG consecutive slots starting at start + t*kChunksPerFetchWG.
+// Ids outside [0, src_chunks) are skipped, so a bad id can never read past the source row.
+template <typename IdxT>
+__global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __restrict__ src, int64_t src_row_vec,
+                                                                  u32x4* __restrict__ dst, int64_t dst_row_vec,
+                                                                  int64_t dst_offset_vec, const IdxT* __restrict__ ids,
+                                                                  const int32_t* __restrict__ cnts, int S, int chunk_vec,
+                                                                  int64_t src_chunks, int tiles) {
+  const int row = blockIdx.x / tiles;
+  const int t = blockIdx.x - row * tiles;
+  const int start = cnts ? max(0, cnts[row]) : 0;
+  const int i0 = start + t * kChunksPerFetchWG;
+  if (i0 >= S) return;
+  const int i1 = min(i0 + kChunksPerFetchWG, S);
+  const int64_t total = static_cast<int64_t>(i1 - i0) * chunk_vec;
+  const u32x4* s = src + static_cast<int64_t>(row) * src_row_vec;
+  u32x4* d = dst + static_cast<int64_t>(row) * dst_row_vec + dst_offset_vec;
+  const IdxT* id = ids + static_cast<int64_t>(row) * S;
+  for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(blockDim.x) * kUnroll) {
+    u32x4 r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      if (v < total) {
+        int i = i0 + static_cast<int>(v / chunk_vec);
+        int e = static_cast<int>(v % chunk_vec);
+        int64_t c = static_cast<int64_t>(id[i]);
+        if (c >= 0 && c < src_chunks) r[u] = s[c * chunk_vec + e];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      if (v < total) {
+        int i = i0 + static_cast<int>(v / chunk_vec);
+        int e = static_cast<int>(v % chunk_vec);
+        int64_t c = static_cast<int64_t>(id[i]);
+        if (c >= 0 && c < src_chunks) d[static_cast<int64_t>(i) * chunk_vec + e] = r[u];
+      }
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(const char* what, const void* a, const void* b, int batch_size, int heads, int map_size,
+                 int chunk_elems) {
+  if ((a != nullptr && !aligned16(a)) || (b != nullptr && !aligned16(b))) {
+    skv_set_error("%s: buffers must be 16-byte aligned", what);
+    return SKV_EINVAL;
+  }
+  if (batch_size <= 0 || heads <= 0 || map_size <= 0) {
+    skv_set_error("%s: batch_size=%d heads=%d map_size=%d", what, batch_size, heads, map_size);
+    return SKV_EINVAL;
+  }
+  if (chunk_elems <= 0 || chunk_elems % 8 != 0) {
+    skv_set_error("%s: chunk_elems=%d must be a positive multiple of 8 (16-byte units)", what, chunk_elems);
+    return SKV_EUNSUPPORTED;
+  }
+  return SKV_OK;
+}
+
+}  // namespace
+
+extern "C" int skv_gather_copy_d2d_with_offsets(void* keys, const int32_t* offsets, const int32_t* cnts,
+                                                int batch_size, int heads, int64_t gpu_k_length,
+                                                int64_t gpu_k_offset, int64_t gpu_k_stride, int map_size,
+                                                int chunk_elems, void* stream) {
+  const char* what = "gather_copy_d2d_with_offsets";
+  if (!keys || !offsets || !cnts) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  int rc = check_common(what, keys, nullptr, batch_size, heads, map_size, chunk_elems);
+  if (rc) return rc;
+  if (gpu_k_offset % 8 || gpu_k_stride % 8 || gpu_k_length != static_cast<int64_t>(map_size) * chunk_elems) {
+    skv_set_error("%s: offset=%lld stride=%lld must be multiples of 8, length=%lld must be map_size*chunk_elems", what,
+                  (long long)gpu_k_offset, (long long)gpu_k_stride, (long long)gpu_k_length);
+    return SKV_EINVAL;
+  }
+  hipLaunchKernelGGL(compact_hits_kernel, dim3(batch_size * heads), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<u32x4*>(keys), offsets, cnts, gpu_k_stride / 8, gpu_k_offset / 8, map_size,
+                     chunk_elems / 8);
+  return skv_check_launch(what);
+}
+
+extern "C" int skv_gather_copy_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
+                                            const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length,
+                                            int64_t gpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
+                                            int map_size, int chunk_elems, void* stream) {
+  const char* what = "gather_copy_with_offsets";
+  if (!values || !v_cache_buffer || !offsets || !cnts) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  int rc = check_common(what, values, v_cache_buffer, batch_size, heads, map_size, chunk_elems);
+  if (rc) return rc;
+  if (cpu_v_length % 8 || gpu_v_offset % 8 || gpu_v_stride % 8 ||
+      gpu_v_length != static_cast<int64_t>(map_size) * chunk_elems) {
+    skv_set_error("%s: cpu_v_length=%lld offset=%lld stride=%lld must be multiples of 8, gpu_v_length=%lld must be "
+                  "map_size*chunk_elems", what, (long long)cpu_v_length, (long long)gpu_v_offset,
+                  (long long)gpu_v_stride, (long long)gpu_v_length);
+    return SKV_EINVAL;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rows = batch_size * heads;
+  hipLaunchKernelGGL(compact_hits_kernel, dim3(rows), dim3(kThreads), 0, s, static_cast<u32x4*>(v_cache_buffer), offsets,
+                     cnts, gpu_v_stride / 8, gpu_v_offset / 8, map_size, chunk_elems / 8);
+  rc = skv_check_launch(what);
+  if (rc) return rc;
+  const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
+  hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(rows * tiles), dim3(kThreads), 0, s,
+                     static_cast<const u32x4*>(values), cpu_v_length / 8, static_cast<u32x4*>(v_cache_buffer),
+                     gpu_v_stride / 8, gpu_v_offset / 8, offsets, cnts, map_size, chunk_elems / 8,
+                     cpu_v_length / chunk_elems, tiles);
+  return skv_check_launch(what);
+}
+
+extern "C" int skv_gather_copy(const void* values, void* v_cache_buffer, const int64_t* position_ids, int batch_size,
+                               int heads, int64_t cpu_v_length, int64_t gpu_v_length, int map_size, int chunk_elems,
+                               void* stream) {
+  const char* what = "gather_copy";
+  if (!values || !v_cache_buffer || !position_ids) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  int rc = check_common(what, values, v_cache_buffer, batch_size, heads, map_size, chunk_elems);
+  if (rc) return rc;
+  if (cpu_v_length % 8 || gpu_v_length % 8 || gpu_v_length < static_cast<int64_t>(map_size) * chunk_elems) {
+    skv_set_error("%s: cpu_v_length=%lld gpu_v_length=%lld invalid", what, (long long)cpu_v_length,
+                  (long long)gpu_v_length);
+    return SKV_EINVAL;
+  }
+  const int rows = batch_size * heads;
+  const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
+  hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(rows * tiles), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(values), cpu_v_length / 8,
+                     static_cast<u32x4*>(v_cache_buffer), gpu_v_length / 8, int64_t(0), position_ids,
+                     static_cast<const int32_t*>(nullptr), map_size, chunk_elems / 8, cpu_v_length / chunk_elems,
+                     tiles);
+  return skv_check_launch(what);
+}

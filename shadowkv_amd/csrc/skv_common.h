@@ -1,0 +1,113 @@
+// Shared device helpers for the ShadowKV sparse-decode kernels (gfx950 / CDNA4).
+//
+// bf16 values are carried as raw uint16_t bit patterns. Every bf16 arithmetic step
+// is done in fp32 and rounded to nearest-even, which is exactly what torch's CPU
+// bf16 operators do (they widen to fp32, compute, and narrow with RNE); products and
+// sums of two bf16 values are exact or correctly rounded in fp32, so one fp32 op
+// followed by RNE equals the single-rounded bf16 op of the reference kernels
+// (kernels/rope_new.cu:262-269 uses __hmul/__hadd).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/shadowkv_amd.h"
+
+namespace skv {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // canonical quiet NaN, as c10::BFloat16
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t bmul(uint16_t a, uint16_t b) { return f2bf(bf2f(a) * bf2f(b)); }
+__device__ __forceinline__ uint16_t badd(uint16_t a, uint16_t b) { return f2bf(bf2f(a) + bf2f(b)); }
+__device__ __forceinline__ uint16_t bneg(uint16_t a) { return a ^ 0x8000u; }
+
+// Order-preserving map of a bf16 bit pattern to an unsigned key: larger float -> larger key.
+__device__ __forceinline__ uint32_t bf16_order_key(uint16_t h) {
+  return (h & 0x8000u) ? (static_cast<uint32_t>(~h) & 0xffffu) : (static_cast<uint32_t>(h) | 0x8000u);
+}
+
+// Wave-wide reductions over all 64 lanes (result valid in every lane).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Sum within aligned groups of 16 lanes (result valid in every lane of the group).
+__device__ __forceinline__ float group16_sum(float v) {
+  v += __shfl_xor(v, 8, kWave);
+  v += __shfl_xor(v, 4, kWave);
+  v += __shfl_xor(v, 2, kWave);
+  v += __shfl_xor(v, 1, kWave);
+  return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    int n = __shfl_up(v, o, kWave);
+    if (lane >= o) v += n;
+  }
+  return v;
+}
+
+// Exclusive prefix sum over the whole workgroup. `scratch` needs blockDim.x/64 + 1 ints of LDS.
+// Returns the exclusive prefix for this thread; *total receives the workgroup sum.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = (blockDim.x + kWave - 1) / kWave;
+  int inc = wave_inclusive_scan(v);
+  if (lane == kWave - 1) scratch[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < nwaves; ++w) {
+      int t = scratch[w];
+      scratch[w] = run;
+      run += t;
+    }
+    scratch[nwaves] = run;
+  }
+  __syncthreads();
+  int excl = scratch[wave] + inc - v;
+  *total = scratch[nwaves];
+  __syncthreads();
+  return excl;
+}
+
+// Wait for every outstanding memory operation of this wave (vector loads included),
+// then barrier. Used where a later store by another wave must not overtake a load.
+__device__ __forceinline__ void drain_and_barrier() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+// 16-byte vector type for chunk copies.
+struct alignas(16) u32x4 {
+  uint32_t x, y, z, w;
+};
+
+}  // namespace skv
+
+// Host-side error reporting shared by every entry point (defined in skv_api.cpp).
+void skv_set_error(const char* fmt, ...);
+int skv_check_launch(const char* what);

@@ -1,0 +1,376 @@
+"""Drop-in for the reference's native module `kernels.shadowkv` (kernels/main.cu:24-36).
+
+Every function keeps the reference's name, argument order and in-place output contract
+(kernels/functions.h:23-121) and runs a hand-written gfx950 HIP kernel from
+libshadowkv_amd.so on torch's current HIP stream. Differences from the reference, all of
+them loud instead of silent:
+  * unsupported sizes raise ValueError (the reference launches nothing for a map_size
+    outside {128, 256, 512, 1024}, kernels/gather_copy.cu:132-323);
+  * the host value store is addressed with the stride of the tensor actually passed
+    (`values.stride(1)` of the [B, H, chunks, chunk*D] layer view) — the reference's
+    `cpu_v_length` argument is checked against it but not used to address memory;
+  * `temp` and `signals` are accepted for signature compatibility and ignored: the kernels
+    need neither a staging buffer nor inter-workgroup flags.
+Functions without a reference counterpart (score_gqa_max, topk_gather, rebuild_k_rope,
+sparse_attn_decode) expose the fused kernels used by the decode path.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+__all__ = [
+    "gather_copy", "gather_copy_d2d_with_offsets", "reorder_keys_and_compute_offsets", "gather_copy_with_offsets",
+    "apply_rotary_pos_emb_new", "apply_rotary_pos_emb_push_cache_opt", "apply_rotary_pos_emb_push_cache_opt_glm",
+    "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "topk_gather", "rebuild_k_rope",
+    "sparse_attn_workspace_bytes", "sparse_attn_decode", "device_address",
+]
+
+
+def _stream() -> int:
+    return int(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> int:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.data_ptr()
+
+
+def _span(t: torch.Tensor) -> int:
+    """Elements addressable from t.data_ptr() to the end of its storage."""
+    return t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+
+
+def _need(t: torch.Tensor, elems: int, name: str) -> None:
+    if _span(t) < elems:
+        raise ValueError(f"{name} holds {_span(t)} elements from its start, {elems} are addressed")
+
+
+_host_base_cache: dict[int, int] = {}
+
+
+def device_address(t: torch.Tensor) -> int:
+    """Device address of a device tensor, or of a pinned host tensor (zero-copy access)."""
+    if t.is_cuda:
+        return t.data_ptr()
+    if not t.is_pinned():
+        raise ValueError("host tensors passed to the kernels must be pinned (pin_memory=True)")
+    base = t.untyped_storage().data_ptr()
+    dev = _host_base_cache.get(base)
+    if dev is None:
+        dev = _lib.host_device_pointer(base)
+        _host_base_cache[base] = dev
+    return dev + (t.data_ptr() - base)
+
+
+def _check_map(map_size: int) -> None:
+    if not 1 <= map_size <= 2048:
+        raise ValueError(f"map_size (select_sets) must be in [1, 2048], got {map_size}")
+
+
+# ---------------------------------------------------------------------------------------------
+# a3: reorder (kernels/gather_copy.cu:189-235)
+
+def reorder_keys_and_compute_offsets(cached_pos_ids, cur_pos_ids, offsets, cnts, batch_size, heads, map_size=256):
+    _check_map(map_size)
+    rows = batch_size * heads
+    for t, n, dt in ((cached_pos_ids, "cached_pos_ids", torch.int64), (cur_pos_ids, "cur_pos_ids", torch.int64),
+                     (offsets, "offsets", torch.int32), (cnts, "cnts", torch.int32)):
+        _dev(t, n, dt)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    for t, n, e in ((cached_pos_ids, "cached_pos_ids", rows * map_size), (cur_pos_ids, "cur_pos_ids", rows * map_size),
+                    (offsets, "offsets", rows * map_size), (cnts, "cnts", rows)):
+        _need(t, e, n)
+    _lib.call("skv_reorder_keys_and_compute_offsets", cached_pos_ids.data_ptr(), cur_pos_ids.data_ptr(),
+              offsets.data_ptr(), cnts.data_ptr(), batch_size, heads, map_size, _stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# a4/a5: chunk copies (kernels/gather_copy.cu:47-185, 239-324)
+
+def _host_row_stride(values: torch.Tensor, rows: int, cpu_v_length: int) -> int:
+    """Per-(b,h) element stride of the host store [B, H, chunks, chunk*D] (or a flat buffer)."""
+    if values.dim() == 4:
+        if values.stride(0) != values.shape[1] * values.stride(1) or values.stride(3) != 1 or \
+                values.stride(2) != values.shape[3]:
+            raise ValueError("host value store must be contiguous per layer: [B, H, chunks, chunk*D]")
+        stride = values.stride(1)
+        if cpu_v_length > stride:
+            raise ValueError(f"cpu_v_length={cpu_v_length} exceeds the host row stride {stride}")
+        return stride
+    if not values.is_contiguous():
+        raise ValueError("host value store must be contiguous")
+    return cpu_v_length
+
+
+def gather_copy_with_offsets(values, v_cache_buffer, temp, offsets, cnts, signals, batch_size, heads, cpu_v_length,
+                             gpu_v_length, gpu_v_offset, gpu_v_stride, map_size=256):
+    del temp, signals  # no staging buffer or flags are needed
+    _check_map(map_size)
+    if gpu_v_length % map_size:
+        raise ValueError(f"gpu_v_length={gpu_v_length} is not map_size*chunk_elems")
+    chunk_elems = gpu_v_length // map_size
+    rows = batch_size * heads
+    row_stride = _host_row_stride(values, rows, cpu_v_length)
+    _need(values, (rows - 1) * row_stride + row_stride, "values")
+    _dev(v_cache_buffer, "v_cache_buffer", torch.bfloat16)
+    _need(v_cache_buffer, (rows - 1) * gpu_v_stride + gpu_v_offset + gpu_v_length, "v_cache_buffer")
+    _dev(offsets, "offsets", torch.int32)
+    _dev(cnts, "cnts", torch.int32)
+    _need(offsets, rows * map_size, "offsets")
+    _need(cnts, rows, "cnts")
+    if values.dtype != torch.bfloat16:
+        raise ValueError("values must be bf16")
+    _lib.call("skv_gather_copy_with_offsets", device_address(values), v_cache_buffer.data_ptr(), offsets.data_ptr(),
+              cnts.data_ptr(), batch_size, heads, row_stride, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size,
+              chunk_elems, _stream())
+
+
+def gather_copy_d2d_with_offsets(keys, offsets, cnts, batch_size, heads, gpu_v_length, gpu_v_offset, gpu_v_stride,
+                                 map_size=256):
+    _check_map(map_size)
+    if gpu_v_length % map_size:
+        raise ValueError(f"gpu_v_length={gpu_v_length} is not map_size*chunk_elems")
+    rows = batch_size * heads
+    _dev(keys, "keys", torch.bfloat16)
+    _need(keys, (rows - 1) * gpu_v_stride + gpu_v_offset + gpu_v_length, "keys")
+    _dev(offsets, "offsets", torch.int32)
+    _dev(cnts, "cnts", torch.int32)
+    _need(offsets, rows * map_size, "offsets")
+    _need(cnts, rows, "cnts")
+    _lib.call("skv_gather_copy_d2d_with_offsets", keys.data_ptr(), offsets.data_ptr(), cnts.data_ptr(), batch_size,
+              heads, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size, gpu_v_length // map_size, _stream())
+
+
+def gather_copy(values, v_cache_buffer, position_ids, batch_size, heads, cpu_v_length, gpu_v_length, map_size=256):
+    _check_map(map_size)
+    if gpu_v_length % map_size:
+        raise ValueError(f"gpu_v_length={gpu_v_length} is not map_size*chunk_elems")
+    rows = batch_size * heads
+    row_stride = _host_row_stride(values, rows, cpu_v_length)
+    _need(values, rows * row_stride, "values")
+    _dev(v_cache_buffer, "v_cache_buffer", torch.bfloat16)
+    _need(v_cache_buffer, rows * gpu_v_length, "v_cache_buffer")
+    _dev(position_ids, "position_ids", torch.int64)
+    _need(position_ids, rows * map_size, "position_ids")
+    _lib.call("skv_gather_copy", device_address(values), v_cache_buffer.data_ptr(), position_ids.data_ptr(),
+              batch_size, heads, row_stride, gpu_v_length, map_size, gpu_v_length // map_size, _stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# a7: RoPE (kernels/rope_new.cu)
+
+def apply_rotary_pos_emb_new(x, cos_sin, position_ids, output, batch_size, heads, seq_len, embed_dim, stride_xb,
+                             stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s,
+                             half_dim):
+    _dev(x, "x", torch.bfloat16)
+    _dev(cos_sin, "cos_sin", torch.bfloat16)
+    _dev(position_ids, "position_ids", torch.int64)
+    _dev(output, "output", torch.bfloat16)
+    if position_ids.numel() and int(position_ids.max()) >= cos_sin.shape[0]:
+        raise ValueError("position_ids exceed the cos_sin table")
+    _lib.call("skv_apply_rotary_pos_emb_new", x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(),
+              output.data_ptr(), batch_size, heads, seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe,
+              stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, _stream())
+
+
+def _push(name, x, cos_sin, position_ids, output, cnts, *ints):
+    _dev(x, "x", torch.bfloat16)
+    _dev(cos_sin, "cos_sin", torch.bfloat16)
+    _dev(position_ids, "position_ids", torch.int32)
+    _dev(output, "output", torch.bfloat16)
+    _dev(cnts, "cnts", torch.int32)
+    chunk_size = ints[-1]
+    if position_ids.numel() and (int(position_ids.max()) + 1) * chunk_size > cos_sin.shape[0]:
+        raise ValueError("position_ids exceed the cos_sin table")
+    _lib.call(name, x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(), output.data_ptr(), cnts.data_ptr(),
+              *ints, _stream())
+
+
+def apply_rotary_pos_emb_push_cache_opt(x, cos_sin, position_ids, output, cnts, batch_size, heads, seq_len, embed_dim,
+                                        stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b,
+                                        stride_pid_h, stride_pid_s, stride_output_b, stride_output_h, stride_output_s,
+                                        offset_output_s_start, offset_output_s_end, half_dim, chunk_size):
+    _push("skv_apply_rotary_pos_emb_push_cache_opt", x, cos_sin, position_ids, output, cnts, batch_size, heads,
+          seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h,
+          stride_pid_s, stride_output_b, stride_output_h, stride_output_s, offset_output_s_start, offset_output_s_end,
+          half_dim, chunk_size)
+
+
+def apply_rotary_pos_emb_push_cache_opt_glm(x, cos_sin, position_ids, output, cnts, batch_size, heads, seq_len,
+                                            embed_dim, stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin,
+                                            stride_pid_b, stride_pid_h, stride_pid_s, stride_output_b, stride_output_h,
+                                            stride_output_s, offset_output_s_start, offset_output_s_end, half_dim,
+                                            chunk_size):
+    _push("skv_apply_rotary_pos_emb_push_cache_opt_glm", x, cos_sin, position_ids, output, cnts, batch_size, heads,
+          seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h,
+          stride_pid_s, stride_output_b, stride_output_h, stride_output_s, offset_output_s_start, offset_output_s_end,
+          half_dim, chunk_size)
+
+
+# ---------------------------------------------------------------------------------------------
+# a6: gathered low-rank GEMM (kernels/batch_gather_gemm.cu:136-213)
+
+def batch_gather_gemm(a, b, cos, sin, position_ids, output, batch_size, heads, seq_len, embed_dim, rank,
+                      sparse_budget, max_seq_len, chunk_size, offset_array):
+    del cos, sin  # the reference's RoPE epilogue is disabled; rebuild_k_rope fuses it instead
+    for t, n in ((a, "a"), (b, "b"), (output, "output")):
+        _dev(t, n, torch.bfloat16)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    _dev(position_ids, "position_ids", torch.int32)
+    _dev(offset_array, "offset_array", torch.int32)
+    _need(a, batch_size * seq_len * rank, "a")
+    _need(b, batch_size * heads * embed_dim * rank, "b")
+    _need(output, batch_size * heads * sparse_budget * embed_dim, "output")
+    _need(position_ids, batch_size * heads * (sparse_budget // chunk_size), "position_ids")
+    _lib.call("skv_batch_gather_gemm", a.data_ptr(), b.data_ptr(), position_ids.data_ptr(), output.data_ptr(),
+              batch_size, heads, seq_len, embed_dim, rank, sparse_budget, max_seq_len, chunk_size,
+              offset_array.data_ptr(), _stream())
+
+
+def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chunk_size):
+    """Fused a6+a7: rebuild the miss rows of every (b, h) and push them, rotated, into `cache`.
+
+    u: [B, ctx, R] (head-shared, the reference layout) or [B, H, ctx, R] (per-head);
+    sv: [B, H, 128, R] (reference layout) or [H, 128, R] (shared across the batch);
+    position_ids: [B, H, S] int64 chunk ids; cnts: [B*H] int32 hit counts;
+    cos_sin: [rows, 128] ([cos|sin], half-split RoPE) or [rows, 64] (GLM interleaved);
+    cache: [B, H, buf_len, 128] key buffer; rows sparse_start + r are written.
+    """
+    B, H, S = position_ids.shape
+    _dev(u, "u", torch.bfloat16)
+    _dev(sv, "sv", torch.bfloat16)
+    _dev(position_ids, "position_ids", torch.int64)
+    _dev(cnts, "cnts", torch.int32)
+    _dev(cos_sin, "cos_sin", torch.bfloat16)
+    _dev(cache, "cache", torch.bfloat16)
+    if u.dim() == 3:
+        u_sb, u_sh, u_sr, u_rows = u.stride(0), 0, u.stride(1), u.shape[1]
+        if u.shape[0] != B:
+            raise ValueError("u batch mismatch")
+    elif u.dim() == 4:
+        u_sb, u_sh, u_sr, u_rows = u.stride(0), u.stride(1), u.stride(2), u.shape[2]
+        if u.shape[0] != B or u.shape[1] != H:
+            raise ValueError("u batch/head mismatch")
+    else:
+        raise ValueError("u must be [B, ctx, R] or [B, H, ctx, R]")
+    rank = u.shape[-1]
+    if u.stride(-1) != 1:
+        raise ValueError("u rows must be contiguous")
+    if sv.dim() == 4:
+        sv_sb, sv_sh, sv_sn = sv.stride(0), sv.stride(1), sv.stride(2)
+    elif sv.dim() == 3:
+        sv_sb, sv_sh, sv_sn = 0, sv.stride(0), sv.stride(1)
+    else:
+        raise ValueError("sv must be [B, H, 128, R] or [H, 128, R]")
+    if sv.shape[-1] != rank or sv.shape[-2] != 128 or sv.stride(-1) != 1:
+        raise ValueError("sv must end in a contiguous [128, rank] block")
+    if cos_sin.shape[-1] == 128:
+        mode = 0
+    elif cos_sin.shape[-1] == 64:
+        mode = 1
+    else:
+        raise ValueError(f"Invalid cos_sin shape {tuple(cos_sin.shape)}")
+    if cache.dim() != 4 or cache.shape[-1] != 128 or cache.stride(-1) != 1:
+        raise ValueError("cache must be [B, H, buf_len, 128]")
+    if sparse_start + S * chunk_size > cache.shape[2]:
+        raise ValueError("sparse region exceeds the cache buffer")
+    if position_ids.stride(2) != 1:
+        raise ValueError("position_ids must be contiguous along the chunk axis")
+    _need(cnts, B * H, "cnts")
+    _lib.call("skv_rebuild_k_rope", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh, sv_sn,
+              position_ids.data_ptr(), position_ids.stride(0), position_ids.stride(1), cnts.data_ptr(),
+              cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0),
+              cache.stride(1), cache.stride(2), sparse_start, B, H, S, chunk_size, rank, 128, _stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# a1/a2: scoring, GQA max, top-k
+
+def _check_scoring(A, B, D, Norm, Sum, batch_count, m, n, k):
+    for t, nm in ((A, "A"), (B, "B"), (D, "D")):
+        _dev(t, nm, torch.bfloat16)
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+    _dev(Norm, "Norm", torch.float32)
+    _dev(Sum, "Sum", torch.float32)
+    tiles = (n + 255) // 256
+    _need(A, batch_count * m * k, "A")
+    _need(B, batch_count * n * k, "B")
+    _need(D, batch_count * m * n, "D")
+    _need(Norm, batch_count * m * tiles, "Norm")
+    _need(Sum, batch_count * m * tiles, "Sum")
+
+
+def batch_gemm_softmax(A, B, D, Norm, Sum, Softmax, batch_count, m, n, k, alpha=1.0, beta=0.0):
+    _check_scoring(A, B, D, Norm, Sum, batch_count, m, n, k)
+    _dev(Softmax, "Softmax", torch.bfloat16)
+    _need(Softmax, batch_count * m * n, "Softmax")
+    _lib.call("skv_batch_gemm_softmax", A.data_ptr(), B.data_ptr(), D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(),
+              Softmax.data_ptr(), batch_count, m, n, k, float(alpha), float(beta), _stream())
+
+
+def score_gqa_max(A, B, D, Norm, Sum, out, batch_count, m, n, k, alpha=1.0 / math.sqrt(128)):
+    """out[z, j] = max_i softmax(alpha * A[z] . B[z]^T)[i, j] in bf16; D/Norm/Sum are scratch."""
+    _check_scoring(A, B, D, Norm, Sum, batch_count, m, n, k)
+    _dev(out, "out", torch.bfloat16)
+    _need(out, batch_count * n, "out")
+    _lib.call("skv_score_gqa_max", A.data_ptr(), B.data_ptr(), D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(),
+              out.data_ptr(), batch_count, m, n, k, float(alpha), _stream())
+
+
+def topk_gather(scores, landmark_idx, k, out_ids):
+    """out_ids[r] = landmark_idx[r, top-k of scores[r] by (value desc, index asc)]; 2-D row views."""
+    _dev(scores, "scores", torch.bfloat16)
+    _dev(landmark_idx, "landmark_idx", torch.int64)
+    _dev(out_ids, "out_ids", torch.int64)
+    if scores.dim() != 2 or landmark_idx.shape != scores.shape or scores.stride(1) != 1 or landmark_idx.stride(1) != 1:
+        raise ValueError("scores and landmark_idx must be [rows, n] with contiguous rows")
+    rows, n = scores.shape
+    if not 1 <= k <= min(n, 4096):
+        raise ValueError(f"k={k} must be in [1, min(n={n}, 4096)]")
+    if not out_ids.is_contiguous():
+        raise ValueError("out_ids must be contiguous")
+    _need(out_ids, rows * k, "out_ids")
+    _lib.call("skv_topk_gather", scores.data_ptr(), scores.stride(0), landmark_idx.data_ptr(), landmark_idx.stride(0),
+              rows, n, k, out_ids.data_ptr(), _stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# a8: sparse decode attention
+
+def sparse_attn_workspace_bytes(batch_size: int, q_heads: int, kv_len: int) -> int:
+    return int(_lib.lib().skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len))
+
+
+def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None):
+    """out[b, hq] = softmax(scale q[b,hq] K[b,h,:kv_len]^T) V[b,h,:kv_len], h = hq // (Hq/Hkv).
+
+    q: [B, Hq, 128] view; k_cache/v_cache: [B, Hkv, >=kv_len, 128] views; out: [B, Hq, 128];
+    workspace: uint8 device tensor of sparse_attn_workspace_bytes(B, Hq, kv_len) bytes.
+    """
+    _dev(q, "q", torch.bfloat16)
+    _dev(k_cache, "k_cache", torch.bfloat16)
+    _dev(v_cache, "v_cache", torch.bfloat16)
+    _dev(out, "out", torch.bfloat16)
+    _dev(workspace, "workspace")
+    B, Hq, D = q.shape
+    if k_cache.shape[:2] != v_cache.shape[:2] or k_cache.stride() != v_cache.stride() or k_cache.shape[0] != B:
+        raise ValueError("k_cache and v_cache must be [B, Hkv, L, 128] with identical strides")
+    if kv_len > k_cache.shape[2] or kv_len < 1:
+        raise ValueError(f"kv_len={kv_len} outside the cache length {k_cache.shape[2]}")
+    if q.stride(2) != 1 or k_cache.stride(3) != 1 or out.stride(2) != 1:
+        raise ValueError("the head dimension must be contiguous")
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    _lib.call("skv_sparse_attn_decode", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+              k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1], D, kv_len,
+              float(scale), workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
+              out.stride(0), out.stride(1), _stream())

@@ -1,0 +1,68 @@
+"""ShadowKV attention handler (reference: models/attention/shadow.py:6-50).
+
+decode() keeps the reference's order of operations and its two-stream overlap:
+RoPE -> append the new token -> select chunks (score, top-k, reorder) -> [copy stream: value
+fetch from host] || [current stream: key compaction + low-rank rebuild + RoPE] -> join ->
+sparse attention. The attention is the gfx950 split-L decode kernel in place of
+flash_attn_with_kvcache; prefill attention (not on the decode path) is plain fp32 torch.
+"""
+import math
+
+import torch
+
+from ...kernels import shadowkv
+from ..tensor_op import repeat_kv
+from .base import AttentionBase
+
+
+def causal_attention_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block: int = 1024) -> torch.Tensor:
+    """Causal GQA attention in fp32, query-blocked; q [B, Hq, L, D], k/v [B, Hkv, L, D] -> [B, L, Hq, D]."""
+    B, Hq, L, D = q.shape
+    k = repeat_kv(k, Hq // k.shape[1]).float()
+    v = repeat_kv(v, Hq // v.shape[1]).float()
+    kt = k.transpose(-1, -2).contiguous()
+    out = torch.empty(B, L, Hq, D, dtype=q.dtype, device=q.device)
+    for s in range(0, L, block):
+        e = min(L, s + block)
+        scores = torch.matmul(q[:, :, s:e].float(), kt[..., :e]) / math.sqrt(D)
+        mask = torch.arange(e, device=q.device)[None, :] > torch.arange(s, e, device=q.device)[:, None]
+        scores.masked_fill_(mask, float("-inf"))
+        p = torch.softmax(scores, dim=-1)
+        out[:, s:e] = torch.matmul(p, v[:, :, :e]).transpose(1, 2).to(q.dtype)
+    return out
+
+
+class ShadowAttention(AttentionBase):
+
+    def prefill(self, query_states, key_states, value_states, position_ids, layer_idx):
+        kv_cache = self.kv_cache
+        kv_cache.get_svd(key_states, layer_idx=layer_idx)
+        query_states, key_states = self.apply_rotary_pos_emb(query_states, key_states, position_ids)
+        kv_cache.prefill_kv_cache(value_states, layer_idx, key_states, query_states[:, :, -1:])
+        return causal_attention_fp32(query_states, key_states, value_states)
+
+    def decode(self, query_states, key_states, value_states, position_ids, layer_idx):
+        kv_cache = self.kv_cache
+        query_states, key_states = self.apply_rotary_pos_emb(query_states, key_states, position_ids)
+        kv_cache.update_kv_cache(key_states, value_states, layer_idx)
+        position_ids = kv_cache.get_retrieval_position_ids(layer_idx=layer_idx, query_states=query_states)
+
+        curr_stream = torch.cuda.current_stream()
+        copy_stream = kv_cache.copy_stream
+        with torch.cuda.stream(copy_stream):
+            copy_stream.wait_stream(curr_stream)
+            value_states = kv_cache.get_value_cache(layer_idx, position_ids)
+        key_states = kv_cache.get_key_cache(layer_idx=layer_idx, position_ids=position_ids,
+                                            rope_func=self.apply_rotary_pos_emb_single,
+                                            cos_sin_cache=self.cos_sin_cache)
+        curr_stream.wait_stream(copy_stream)
+
+        if kv_cache.attn_workspace is None:
+            kv_cache._alloc_attention()
+        B, Hq = query_states.shape[0], query_states.shape[1]
+        q = query_states.reshape(B, Hq, -1) if query_states.shape[2] == 1 else None
+        if q is None:
+            raise ValueError("decode attention takes one query token per step")
+        out = torch.empty(B, Hq, query_states.shape[-1], dtype=query_states.dtype, device=query_states.device)
+        shadowkv.sparse_attn_decode(q, key_states, value_states, key_states.shape[2], out, kv_cache.attn_workspace)
+        return out.view(B, 1, Hq, -1)

@@ -1,0 +1,61 @@
+"""Runs one decode step of one layer through the product classes (ShadowKVCache_CPU +
+ShadowAttention) on a GPU, starting from the prompt tensors of a make_golden case."""
+from __future__ import annotations
+
+import types
+
+import torch
+
+from shadowkv_amd.models.attention import ShadowAttention
+from shadowkv_amd.models.kvcache import ShadowKVCache_CPU
+
+
+def rope_tokens_cpu(x, cos_sin, pos):
+    half = x.shape[-1] // 2
+    cs = cos_sin[pos]
+    c = torch.cat((cs[:, :half], cs[:, :half]), dim=-1)
+    s = torch.cat((cs[:, half:], cs[:, half:]), dim=-1)
+    rot = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    return (x * c) + (rot * s)
+
+
+def build_cache(case, device, max_decode_len=None, num_layers=1):
+    d = case["dims"]
+    B, H, G, D, ctx = d["B"], d["H"], d["G"], d["D"], d["ctx"]
+    cfg = types.SimpleNamespace(num_attention_heads=H * G, num_key_value_heads=H, hidden_size=H * G * D,
+                                num_hidden_layers=num_layers)
+    cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device=str(device), sparse_budget=d["budget"],
+                              chunk_size=d["chunk"], rank=d["rank"], max_decode_len=max_decode_len)
+    cos_sin = case["cos_sin"]
+    k_roped = rope_tokens_cpu(case["k_pre"], cos_sin, torch.arange(ctx))
+    q_last = rope_tokens_cpu(case["q_last"], cos_sin, torch.tensor([ctx - 1]))
+    for layer in range(num_layers):
+        cache.get_svd(case["k_pre"], layer)
+        cache.prefill_kv_cache(case["v"], layer, k_roped, q_last)
+    cache.H2D()
+    return cache
+
+
+def identity_rope(B, Hq, H, D):
+    """Stands in for the model's RoPE: inputs are already rotated; only the reference's view/transpose."""
+    def f(q, k, position_ids):
+        return q.view(B, -1, Hq, D).transpose(1, 2), k.view(B, -1, H, D).transpose(1, 2)
+    return f
+
+
+def run_decode_step_gpu(case, device, cache=None):
+    d = case["dims"]
+    B, H, G, D = d["B"], d["H"], d["G"], d["D"]
+    cache = cache or build_cache(case, device)
+    cos_sin = case["cos_sin"].to(device)
+    attn = ShadowAttention(cache, G, D, H * G * D, identity_rope(B, H * G, H, D), None, cos_sin)
+    q = case["q"].to(device).reshape(B, 1, H * G * D)
+    k = case["k_new"].to(device).reshape(B, 1, H * D)
+    v = case["v_new"].to(device).reshape(B, H, 1, D)
+    out = attn.decode(q, k, v, None, 0)
+    torch.cuda.synchronize()
+    L = cache.sparse_end + cache.gen_offset
+    return dict(out=out.view(B, H * G, D).cpu(), cnts=cache.cnts.cpu().numpy(),
+                offsets=cache.offsets.view(B * H, -1).cpu().numpy(), position_ids=cache.position_ids[0].cpu().numpy(),
+                kbuf=cache.k_cache_buffer[0, :, :, :L].cpu(), vbuf=cache.v_cache_buffer[0, :, :, :L].cpu(),
+                scores=cache.chunk_attn.cpu(), selected=cache.selected_chunks.cpu(), cache=cache)

@@ -1,0 +1,85 @@
+"""End-to-end decode steps through the drop-in classes (ShadowKVCache_CPU + ShadowAttention)
+against the oracle's composition of the same reference steps."""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.decode_harness import build_cache, run_decode_step_gpu
+from tests.golden import make_golden
+
+pytestmark = pytest.mark.gpu
+
+
+def test_single_layer_decode_step(gpu):
+    print("decode small fixture, one step", flush=True)
+    case = make_golden.decode_small_case()
+    d = np.load(make_golden.HERE / "decode_small.npz")
+    got = run_decode_step_gpu(case, gpu)
+    res, st = case["res"], case["st"]
+    scores_ok = torch.equal(got["scores"], res["scores"])
+    # Scores agree to one bf16 ulp at worst (fp32 accumulation order); on this case exactly.
+    assert scores_ok
+    assert torch.equal(got["selected"], res["selected"])
+    assert np.array_equal(got["cnts"], d["out_cnts"])
+    assert np.array_equal(got["offsets"], d["out_offsets"])
+    assert np.array_equal(got["position_ids"], d["out_position_ids"])
+    L = res["L"]
+    assert torch.equal(got["vbuf"], st.vbuf[:, :, :L])
+    torch.testing.assert_close(got["kbuf"].float(), st.kbuf[:, :, :L].float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(got["out"].float(), res["out"].float(), rtol=2e-2, atol=2e-2)
+
+
+def test_multi_layer_multi_step_decode(gpu):
+    print("decode small fixture, 2 layers x 4 steps", flush=True)
+    case = make_golden.decode_small_case()
+    d = case["dims"]
+    B, H, G, D = d["B"], d["H"], d["G"], d["D"]
+    steps, layers = 4, 2
+    cache = build_cache(case, gpu, max_decode_len=steps, num_layers=layers)
+    # oracle states: one per layer, fresh copies of the encoded state
+    base = copy.deepcopy(case["state_in"])
+    states = []
+    for _ in range(layers):
+        kw = {k: v.clone() for k, v in base.items()}
+        st = oracle.LayerState(**kw, prefill_local=case["st"].prefill_local, sparse_start=case["st"].sparse_start,
+                               sparse_end=case["st"].sparse_end, chunk=d["chunk"], budget=d["budget"], ctx=d["ctx"],
+                               buf_len=case["st"].buf_len)
+        states.append(st)
+    from shadowkv_amd.models.attention import ShadowAttention
+    from tests.decode_harness import identity_rope
+    cos_sin = case["cos_sin"]
+    attn = ShadowAttention(cache, G, D, H * G * D, identity_rope(B, H * G, H, D), None, cos_sin.to(gpu))
+    g = torch.Generator().manual_seed(77)
+    for t in range(steps):
+        for layer in range(layers):
+            q = torch.randn(B, H * G, D, generator=g).to(torch.bfloat16)
+            k = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+            v = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+            out = attn.decode(q.to(gpu).reshape(B, 1, -1), k.to(gpu).reshape(B, 1, -1), v.to(gpu).reshape(B, H, 1, D),
+                              None, layer)
+            torch.cuda.synchronize()
+            res = oracle.decode_layer_step(states[layer], q, k, v, cos_sin, gen_offset=t)
+            assert torch.equal(cache.chunk_attn.cpu(), res["scores"]), (t, layer)
+            assert np.array_equal(cache.cnts.cpu().numpy(), res["cnts"]), (t, layer)
+            assert np.array_equal(cache.position_ids[layer].cpu().numpy(), states[layer].position_ids.numpy())
+            L = res["L"]
+            assert torch.equal(cache.v_cache_buffer[layer, :, :, :L].cpu(), states[layer].vbuf[:, :, :L])
+            torch.testing.assert_close(cache.k_cache_buffer[layer, :, :, :L].cpu().float(),
+                                       states[layer].kbuf[:, :, :L].float(), rtol=2e-2, atol=2e-2)
+            torch.testing.assert_close(out.view(B, H * G, D).cpu().float(), res["out"].float(), rtol=2e-2, atol=2e-2)
+    assert cache.gen_offset == steps
+
+
+def test_decode_capacity_is_an_error(gpu):
+    case = make_golden.decode_small_case()
+    cache = build_cache(case, gpu)
+    cap = cache.buf_len - cache.sparse_end
+    d = case["dims"]
+    k = torch.zeros(d["B"], d["H"], 1, d["D"], dtype=torch.bfloat16, device=gpu)
+    for _ in range(cap):
+        cache.update_kv_cache(k, k, 0)
+    with pytest.raises(RuntimeError, match="decode capacity"):
+        cache.update_kv_cache(k, k, 0)

@@ -1,0 +1,200 @@
+"""GPU parity of the floating-point kernels against the CPU oracle.
+
+RoPE alone is bit-exact (same bf16 rounding sequence). The rebuild, scoring and attention
+accumulate in fp32 in a different order than the CPU, so they are checked to the bf16
+tolerance of the contract (rtol 2e-2, atol 2e-2) plus tighter, scale-aware bounds where
+atol would be vacuous (softmax probabilities are ~1/n).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from shadowkv_amd.kernels import shadowkv
+from shadowkv_amd.models import tensor_op
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-2
+ATOL = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> int:
+    """Largest distance in bf16 units in the last place between two same-sign-or-zero tensors."""
+    ai = a.contiguous().view(torch.int16).int()
+    bi = b.contiguous().view(torch.int16).int()
+    ai = torch.where(ai < 0, -(ai & 0x7FFF), ai)
+    bi = torch.where(bi < 0, -(bi & 0x7FFF), bi)
+    return int((ai - bi).abs().max()) if ai.numel() else 0
+
+
+@pytest.mark.parametrize("glm", [False, True])
+def test_rope_push_bit_exact(gpu, glm):
+    B, H, S, c, D = 2, 8, 32, 8, 128
+    _say(f"rope push glm={glm}")
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, H, S * c, D, generator=g).to(torch.bfloat16)
+    cs = oracle.build_glm_cos_sin_cache(4096, 5e6) if glm else oracle.build_cos_sin_cache(4096, 5e5)
+    ids = torch.stack([torch.stack([torch.randperm(500, generator=g)[:S].sort().values for _ in range(H)])
+                       for _ in range(B)]).to(torch.int32)
+    cnts = torch.randint(0, S + 1, (B * H,), generator=g, dtype=torch.int32)
+    start, buf = 100, 100 + S * c + 20
+    cache = torch.randn(B, H, buf, D, generator=g).to(torch.bfloat16)
+    want = (oracle.rope_push_glm if glm else oracle.rope_push)(x, cs, ids, cnts, c, cache.clone(), start,
+                                                               start + S * c - 5)
+    cg = cache.to(gpu)
+    tensor_op.apply_rotary_pos_emb_cuda_push_cache(x.to(gpu), cs.to(gpu), ids.to(gpu), c, cg, start,
+                                                   start + S * c - 5, cnts.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(cg.cpu(), want)
+
+
+def test_rope_plain_bit_exact(gpu):
+    B, H, L, D = 2, 4, 50, 128
+    cs = oracle.build_cos_sin_cache(1000, 5e5)
+    x = torch.randn(B, H, L, D).to(torch.bfloat16)
+    pos = torch.randint(0, 1000, (B, H, L))
+    out = tensor_op.apply_rotary_pos_emb_cuda(x.to(gpu), cs.to(gpu), pos.to(gpu))
+    torch.cuda.synchronize()
+    c = cs[pos]
+    want = oracle.rope_half_split(x, c[..., :64], c[..., 64:])
+    assert torch.equal(out.cpu(), want)
+
+
+def _rebuild_case(B, H, ctx, R, S, c, seed, per_head_u=False, shared_sv=False):
+    g = torch.Generator().manual_seed(seed)
+    U = torch.randn(B, H, ctx, R, generator=g) if per_head_u else torch.randn(B, ctx, R, generator=g)
+    U = (U / math.sqrt(R)).to(torch.bfloat16)
+    SV = torch.randn(H, 128, R, generator=g) if shared_sv else torch.randn(B, H, 128, R, generator=g)
+    SV = SV.to(torch.bfloat16)
+    ids = torch.stack([torch.stack([torch.randperm(ctx // c, generator=g)[:S].sort().values for _ in range(H)])
+                       for _ in range(B)])
+    cnts = torch.randint(0, S + 1, (B * H,), generator=g, dtype=torch.int32)
+    return U, SV, ids, cnts
+
+
+def test_batch_gather_gemm_plain(gpu):
+    B, H, ctx, R, S, c = 2, 8, 4096, 160, 256, 8
+    _say("batch_gather_gemm plain")
+    U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 1)
+    want = oracle.rebuild_k(U, SV, ids, c)
+    out = torch.zeros(B * H, S * c, 128, dtype=torch.bfloat16, device=gpu)
+    shadowkv.batch_gather_gemm(U.to(gpu), SV.to(gpu), None, None, ids.to(torch.int32).to(gpu), out, B, H, ctx, 128, R,
+                               S * c, ctx, c, cnts.to(gpu))
+    torch.cuda.synchronize()
+    got = out.cpu().view(B, H, S * c, 128)
+    for bh in range(B * H):
+        b, h = divmod(bh, H)
+        miss = int(cnts[bh]) * c
+        assert (got[b, h, :miss] == 0).all()  # hit rows untouched
+        torch.testing.assert_close(got[b, h, miss:].float(), want[b, h, miss:].float(), rtol=RTOL, atol=ATOL)
+        assert _bf16_ulps(got[b, h, miss:], want[b, h, miss:]) <= 2
+
+
+@pytest.mark.parametrize("glm,per_head_u,shared_sv,R", [(False, False, False, 160), (True, False, False, 160),
+                                                       (False, True, True, 160), (False, False, False, 96),
+                                                       (False, False, False, 168)])
+def test_rebuild_k_rope_fused(gpu, glm, per_head_u, shared_sv, R):
+    B, H, ctx, S, c = 2, 8, 4096, 256, 8
+    _say(f"rebuild_k_rope glm={glm} per_head_u={per_head_u} shared_sv={shared_sv} R={R}")
+    U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 2, per_head_u, shared_sv)
+    cs = oracle.build_glm_cos_sin_cache(ctx, 5e6) if glm else oracle.build_cos_sin_cache(ctx, 5e5)
+    start, buf = 448, 448 + S * c + 96
+    cache = torch.randn(B, H, buf, 128).to(torch.bfloat16)
+    SVf = SV.unsqueeze(0).expand(B, -1, -1, -1) if shared_sv else SV
+    want = oracle.rebuild_k_rope(U, SVf, ids, cnts, cs, c, cache.clone(), start, glm=glm)
+    cg = cache.to(gpu)
+    shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
+    torch.cuda.synchronize()
+    got = cg.cpu()
+    assert torch.equal(got[:, :, :start], cache[:, :, :start])
+    assert torch.equal(got[:, :, start + S * c:], cache[:, :, start + S * c:])
+    for bh in range(B * H):
+        b, h = divmod(bh, H)
+        miss = start + int(cnts[bh]) * c
+        assert torch.equal(got[b, h, start:miss], cache[b, h, start:miss])  # hit rows untouched
+        torch.testing.assert_close(got[b, h, miss:start + S * c].float(), want[b, h, miss:start + S * c].float(),
+                                   rtol=RTOL, atol=ATOL)
+
+
+def test_rebuild_basis_rows_exact(gpu):
+    # U rows that are basis vectors make every K row an SV column: exact through MFMA and RoPE.
+    B, H, ctx, R, S, c = 1, 8, 1024, 160, 64, 8
+    SV = torch.randn(B, H, 128, R).to(torch.bfloat16)
+    U = torch.zeros(B, ctx, R, dtype=torch.bfloat16)
+    U[0, torch.arange(ctx), torch.arange(ctx) % R] = 1.0
+    g = torch.Generator().manual_seed(9)
+    ids = torch.stack([torch.randperm(ctx // c, generator=g)[:S].sort().values for _ in range(H)]).unsqueeze(0)
+    cnts = torch.zeros(H, dtype=torch.int32)
+    cs = oracle.build_cos_sin_cache(ctx, 5e5)
+    cache = torch.zeros(B, H, S * c, 128, dtype=torch.bfloat16)
+    want = oracle.rebuild_k_rope(U, SV, ids, cnts, cs, c, cache.clone(), 0)
+    cg = cache.to(gpu)
+    shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, 0, c)
+    torch.cuda.synchronize()
+    assert torch.equal(cg.cpu(), want)
+
+
+@pytest.mark.parametrize("Z,m,n", [(8, 4, 968), (64, 4, 15304), (8, 16, 32712), (4, 1, 300), (2, 8, 257)])
+def test_scoring(gpu, Z, m, n):
+    _say(f"scoring Z={Z} m={m} n={n}")
+    g = torch.Generator().manual_seed(n)
+    q = torch.randn(Z, m, 128, generator=g).to(torch.bfloat16)
+    L = torch.randn(Z, n, 128, generator=g).to(torch.bfloat16)
+    alpha = 1.0 / math.sqrt(128)
+    Dw, Pw = oracle.score_logits_softmax(q, L, alpha)
+    tiles = (n + 255) // 256
+    Dg = torch.empty(Z, m, n, dtype=torch.bfloat16, device=gpu)
+    Pg = torch.empty_like(Dg)
+    norm = torch.empty(Z, m, tiles, device=gpu)
+    ssum = torch.empty_like(norm)
+    qg, Lg = q.to(gpu), L.to(gpu)
+    shadowkv.batch_gemm_softmax(qg, Lg, Dg, norm, ssum, Pg, Z, m, n, 128, alpha, 0.0)
+    out = torch.empty(Z, n, dtype=torch.bfloat16, device=gpu)
+    shadowkv.score_gqa_max(qg, Lg, Dg, norm, ssum, out, Z, m, n, 128, alpha)
+    torch.cuda.synchronize()
+    assert _bf16_ulps(Dg.cpu(), Dw) <= 1
+    Pc = Pg.cpu().float()
+    rel = ((Pc - Pw.float()).abs() / Pw.float().clamp_min(1e-30)).max().item()
+    assert rel <= 2e-2, rel
+    torch.testing.assert_close(Pc, Pw.float(), rtol=RTOL, atol=ATOL)
+    assert torch.equal(out.cpu(), Pg.cpu().max(dim=1).values)  # GQA max of the kernel's own probabilities
+
+
+@pytest.mark.parametrize("B,Hq,Hk,L,strided", [(1, 32, 8, 2497, True), (8, 32, 8, 2600, True), (2, 32, 2, 2497, True),
+                                               (1, 8, 8, 1, False), (3, 16, 4, 300, False)])
+def test_sparse_attention(gpu, B, Hq, Hk, L, strided):
+    _say(f"attention B={B} Hq={Hq} Hk={Hk} L={L}")
+    g = torch.Generator().manual_seed(L)
+    buf = L + 37 if strided else L
+    K = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
+    V = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16)
+    want = oracle.sparse_attention(q, K, V, L)
+    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+    out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
+    shadowkv.sparse_attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), L, out, ws)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), want.float(), rtol=RTOL, atol=ATOL)
+    if L == 1:
+        for hq in range(Hq):
+            assert torch.equal(out.cpu()[:, hq], V[:, hq // (Hq // Hk), 0])
+
+
+def test_attention_identical_keys_is_mean_of_values(gpu):
+    B, Hq, Hk, L = 2, 32, 8, 777
+    K = torch.randn(B, Hk, 1, 128).to(torch.bfloat16).expand(-1, -1, L, -1).contiguous()
+    V = torch.randn(B, Hk, L, 128).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 128).to(torch.bfloat16)
+    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+    out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
+    shadowkv.sparse_attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), L, out, ws)
+    torch.cuda.synchronize()
+    mean = V.float().mean(dim=2).repeat_interleave(Hq // Hk, dim=1)
+    torch.testing.assert_close(out.cpu().float(), mean, rtol=1e-2, atol=1e-2)

@@ -1,0 +1,146 @@
+"""GPU parity of the index/copy kernels (a3 reorder, a4/a5 chunk copies, a2 top-k): bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from shadowkv_amd.kernels import shadowkv
+from tests.golden import make_golden
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def test_reorder_reference_kat(gpu):
+    d = np.load(make_golden.HERE / "reorder_kat.npz")
+    rows, S = d["orig_keys"].shape
+    _say(f"reorder KAT rows={rows} S={S}")
+    cached = torch.from_numpy(d["orig_keys"].astype(np.int64)).to(gpu)
+    cur = torch.from_numpy(d["query_keys"].astype(np.int64)).to(gpu)
+    offs = torch.zeros(rows * S, dtype=torch.int32, device=gpu)
+    cnts = torch.zeros(rows, dtype=torch.int32, device=gpu)
+    shadowkv.reorder_keys_and_compute_offsets(cached, cur, offs, cnts, rows // 8, 8, S)
+    torch.cuda.synchronize()
+    assert np.array_equal(cached.cpu().numpy(), d["expected_keys"].astype(np.int64))
+    assert np.array_equal(offs.view(rows, S).cpu().numpy(), d["expected_offsets"].astype(np.int32))
+    assert np.array_equal(cnts.cpu().numpy(), d["expected_cnts"].astype(np.int32))
+
+
+@pytest.mark.parametrize("S", [1, 7, 128, 256, 1000, 2048])
+def test_reorder_random_unsorted(gpu, S):
+    rng = np.random.default_rng(S)
+    B, H = 2, 4
+    rows = B * H
+    _say(f"reorder random S={S}")
+    old = np.stack([rng.permutation(4 * S + 3)[:S] for _ in range(rows)]).astype(np.int64)
+    old[rng.random(old.shape) < 0.05] = -1
+    new = np.stack([rng.permutation(4 * S + 3)[:S] for _ in range(rows)]).astype(np.int64)
+    valid = old[0][old[0] >= 0]  # row 0: every valid old id is selected again
+    fresh = np.setdiff1d(np.arange(10 * S + 10), old[0])[:S - len(valid)]
+    new[0] = rng.permutation(np.concatenate([valid, fresh]))
+    ids, offs, cnts = oracle.reorder(old, new)
+    cached = torch.from_numpy(old).to(gpu)
+    o = torch.zeros(rows * S, dtype=torch.int32, device=gpu)
+    c = torch.zeros(rows, dtype=torch.int32, device=gpu)
+    shadowkv.reorder_keys_and_compute_offsets(cached, torch.from_numpy(new).to(gpu), o, c, B, H, S)
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), cnts)
+    assert np.array_equal(cached.cpu().numpy(), ids)
+    assert np.array_equal(o.view(rows, S).cpu().numpy(), offs)
+
+
+def _setup_cache(gpu, B, H, S, chunk_elems, nchunks, hit_frac, seed, pinned=True):
+    rng = np.random.default_rng(seed)
+    rows = B * H
+    host = torch.from_numpy(oracle_coded(rows, nchunks, chunk_elems, seed)).view(torch.bfloat16)
+    host = host.view(B, H, nchunks, chunk_elems)
+    if pinned:
+        host = host.pin_memory()
+    else:
+        host = host.to(gpu)
+    old = np.stack([rng.permutation(nchunks)[:S] for _ in range(rows)]).astype(np.int64)
+    new = np.empty_like(old)
+    for r in range(rows):
+        nh = int(round(hit_frac * S))
+        keep = rng.permutation(old[r])[:nh]
+        rest = rng.permutation(np.setdiff1d(np.arange(nchunks), old[r]))[:S - nh]
+        new[r] = rng.permutation(np.concatenate([keep, rest]))
+    ids, offs, cnts = oracle.reorder(old, new)
+    return host, old, new, ids, offs, cnts
+
+
+def oracle_coded(rows, n, E, tag):
+    r = np.arange(rows)[:, None, None]
+    c = np.arange(n)[None, :, None]
+    w = np.arange(E)[None, None, :]
+    return ((tag * 7919 + r * 1543 + c * 131 + w) % 65521 - 32760).astype(np.int16)
+
+
+@pytest.mark.parametrize("hit_frac,chunk,S,pinned", [(0.6, 8, 256, True), (0.0, 8, 256, True), (1.0, 8, 256, True),
+                                                     (0.3, 4, 512, True), (0.6, 8, 2048, True), (0.5, 8, 256, False)])
+def test_cached_gather_copy(gpu, hit_frac, chunk, S, pinned):
+    B, H, D = 2, 8, 128
+    E = chunk * D
+    nchunks = 4 * S + 5
+    _say(f"gather_copy_with_offsets hit={hit_frac} chunk={chunk} S={S} pinned={pinned}")
+    host, old, new, ids, offs, cnts = _setup_cache(gpu, B, H, S, E, nchunks, hit_frac, 17, pinned)
+    rows = B * H
+    prefix = 3 * chunk  # device slots before the sparse region
+    buf_len = prefix + S * chunk + 40
+    hostn = host.cpu().view(torch.int16).numpy().reshape(rows, nchunks, E)
+    dev = torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16)
+    sparse = np.stack([hostn[r, old[r]] for r in range(rows)])  # slot i holds old[i]
+    dev[:, :, prefix:prefix + S * chunk] = torch.from_numpy(sparse).view(torch.bfloat16).view(B, H, S * chunk, D)
+    dev[:, :, :prefix] = 1.5
+    dev_g = dev.to(gpu)
+    offs_g = torch.from_numpy(offs.reshape(-1)).to(gpu)
+    cnts_g = torch.from_numpy(cnts).to(gpu)
+    shadowkv.gather_copy_with_offsets(host, dev_g, None, offs_g, cnts_g, None, B, H, nchunks * E, S * E,
+                                      prefix * D, buf_len * D, S)
+    torch.cuda.synchronize()
+    got = dev_g.cpu()
+    want = oracle.cached_gather_copy(hostn, sparse, offs, cnts)
+    assert torch.equal(got[:, :, :prefix], dev[:, :, :prefix])
+    assert torch.equal(got[:, :, prefix + S * chunk:], dev[:, :, prefix + S * chunk:])
+    assert np.array_equal(got[:, :, prefix:prefix + S * chunk].reshape(rows, S, E).view(torch.int16).numpy(), want)
+    # key-side compaction on the same layout
+    kdev = dev.to(gpu)
+    shadowkv.gather_copy_d2d_with_offsets(kdev, offs_g, cnts_g, B, H, S * E, prefix * D, buf_len * D, S)
+    torch.cuda.synchronize()
+    wantk = oracle.compact_hits(sparse, offs, cnts)
+    assert np.array_equal(kdev.cpu()[:, :, prefix:prefix + S * chunk].reshape(rows, S, E).view(torch.int16).numpy(),
+                          wantk)
+
+
+def test_gather_copy_plain(gpu):
+    B, H, S, chunk, D = 2, 4, 128, 8, 128
+    E = chunk * D
+    nchunks = 600
+    host, old, new, *_ = _setup_cache(gpu, B, H, S, E, nchunks, 0.0, 5)
+    dst = torch.zeros(B * H, S * E, dtype=torch.bfloat16, device=gpu)
+    shadowkv.gather_copy(host, dst, torch.from_numpy(new).to(gpu), B, H, nchunks * E, S * E, S)
+    torch.cuda.synchronize()
+    hostn = host.view(torch.int16).numpy().reshape(B * H, nchunks, E)
+    want = oracle.gather_copy_plain(hostn, new)
+    assert np.array_equal(dst.cpu().view(torch.int16).numpy().reshape(B * H, S, E), want)
+
+
+@pytest.mark.parametrize("n,k,ties", [(968, 256, False), (15304, 256, False), (15304, 256, True), (1000, 1000, True),
+                                      (130680, 2048, False), (5, 1, True)])
+def test_topk_gather_bit_exact(gpu, n, k, ties):
+    rows = 8
+    g = torch.Generator().manual_seed(n + k)
+    _say(f"topk n={n} k={k} ties={ties}")
+    x = torch.softmax(torch.randn(rows, n, generator=g) * 3, dim=-1)
+    if ties:
+        x = (x * 50).round() / 50  # heavy ties, including many zeros
+    x = x.to(torch.bfloat16)
+    lidx = torch.stack([torch.randperm(10 * n, generator=g)[:n].sort().values for _ in range(rows)])
+    want = oracle.topk_gather(x, lidx, k)
+    out = torch.empty(rows, k, dtype=torch.int64, device=gpu)
+    shadowkv.topk_gather(x.to(gpu), lidx.to(gpu), k, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
