@@ -79,23 +79,25 @@ int skv_gather_copy(const void* values, void* v_cache_buffer, const int64_t* pos
 /* ---- a7: RoPE ---------------------------------------------------------------------------
  * Replaces apply_rotary_pos_emb_new (kernels/functions.h:61-67, kernels/rope_new.cu:26-84):
  * output[b,h,s] = rope(x[b,h,s], cos_sin[position_ids[b,h,s]]) with the half-split layout,
- * cos_sin row = [cos(half_dim) | sin(half_dim)], per-op bf16 rounding. */
+ * cos_sin row = [cos(half_dim) | sin(half_dim)], per-op bf16 rounding. Rows whose position is outside
+ * [0, cos_sin_rows) are left unwritten (no counterpart argument in the reference). */
 int skv_apply_rotary_pos_emb_new(const uint16_t* x, const uint16_t* cos_sin, const int64_t* position_ids,
                                  uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
                                  int64_t stride_xb, int64_t stride_xh, int64_t stride_xs, int64_t stride_xe,
                                  int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h,
-                                 int64_t stride_pid_s, int half_dim, void* stream);
+                                 int64_t stride_pid_s, int half_dim, int64_t cos_sin_rows, void* stream);
 
 /* Replaces apply_rotary_pos_emb_push_cache_opt (kernels/functions.h:88-97, kernels/rope_new.cu:224-302):
  * for rows s with s/chunk_size >= cnts[b*heads+h] and start+s < end, writes
- * rope(x[b,h,s], cos_sin[position_ids[b,h,s/chunk]*chunk + s%chunk]) to output[b,h,start+s]. */
+ * rope(x[b,h,s], cos_sin[position_ids[b,h,s/chunk]*chunk + s%chunk]) to output[b,h,start+s];
+ * rows whose table row falls outside [0, cos_sin_rows) are skipped. */
 int skv_apply_rotary_pos_emb_push_cache_opt(
     const uint16_t* x, const uint16_t* cos_sin, const int32_t* position_ids, uint16_t* output,
     const int32_t* cnts, int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb,
     int64_t stride_xh, int64_t stride_xs, int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b,
     int64_t stride_pid_h, int64_t stride_pid_s, int64_t stride_output_b, int64_t stride_output_h,
     int64_t stride_output_s, int offset_output_s_start, int offset_output_s_end, int half_dim,
-    int chunk_size, void* stream);
+    int chunk_size, int64_t cos_sin_rows, void* stream);
 
 /* Replaces apply_rotary_pos_emb_push_cache_opt_glm (kernels/functions.h:99-108,
  * kernels/rope_new.cu:305-404): GLM interleaved pairs (2i, 2i+1), i < 32, with
@@ -106,7 +108,7 @@ int skv_apply_rotary_pos_emb_push_cache_opt_glm(
     int64_t stride_xh, int64_t stride_xs, int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b,
     int64_t stride_pid_h, int64_t stride_pid_s, int64_t stride_output_b, int64_t stride_output_h,
     int64_t stride_output_s, int offset_output_s_start, int offset_output_s_end, int half_dim,
-    int chunk_size, void* stream);
+    int chunk_size, int64_t cos_sin_rows, void* stream);
 
 /* ---- a6: low-rank key rebuild ------------------------------------------------------------
  * Replaces batch_gather_gemm (kernels/functions.h:110-116, kernels/batch_gather_gemm.cu:136-213):
@@ -154,6 +156,14 @@ int skv_batch_gemm_softmax(const uint16_t* A, const uint16_t* B, uint16_t* D, fl
  * (models/kvcache/shadow.py:553-568). D/norm/sum are caller-provided scratch as above. */
 int skv_score_gqa_max(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
                       uint16_t* out, int batch_count, int m, int n, int k, float alpha, void* stream);
+
+/* The two kernels of the scoring above, callable separately: logits + per-tile partials, then
+ * the softmax normalisation with the optional per-row probabilities (softmax, [batch][m][n])
+ * and/or the GQA max (out_max, [batch][n]); at least one output must be non-null. */
+int skv_score_logits(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum, int batch_count,
+                     int m, int n, int k, float alpha, void* stream);
+int skv_softmax_gqa_max(const uint16_t* D, const float* norm, const float* sum, uint16_t* softmax, uint16_t* out_max,
+                        int batch_count, int m, int n, void* stream);
 
 /* ---- a2: chunk top-k and landmark-id gather ---------------------------------------------------
  * Replaces torch.topk(scores, k).indices + k_landmark_idx.gather (models/kvcache/shadow.py:571-573):

@@ -29,19 +29,22 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_gather_copy_d2d_with_offsets": (_i32, [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
     "skv_gather_copy": (_i32, [_p, _p, _p, _i32, _i32, _i64, _i64, _i32, _i32, _p]),
     "skv_apply_rotary_pos_emb_new": (
-        _i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p]),
+        _i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
+               _p]),
     "skv_apply_rotary_pos_emb_push_cache_opt": (
         _i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-               _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p]),
+               _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _p]),
     "skv_apply_rotary_pos_emb_push_cache_opt_glm": (
         _i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-               _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p]),
+               _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _p]),
     "skv_batch_gather_gemm": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
     "skv_rebuild_k_rope": (
         _i32, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i32,
                _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "skv_batch_gemm_softmax": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _f32, _f32, _p]),
     "skv_score_gqa_max": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _f32, _p]),
+    "skv_score_logits": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _f32, _p]),
+    "skv_softmax_gqa_max": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "skv_topk_gather": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p]),
     "skv_sparse_attn_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "skv_sparse_attn_decode": (

@@ -15,7 +15,7 @@ __global__ void __launch_bounds__(kThreads) rope_plain_kernel(const uint16_t* __
                                                               const int64_t* __restrict__ pid, uint16_t* __restrict__ out,
                                                               int heads, int seq_len, int half, int64_t sxb, int64_t sxh,
                                                               int64_t sxs, int64_t sxe, int64_t scs, int64_t spb,
-                                                              int64_t sph, int64_t sps, int64_t total) {
+                                                              int64_t sph, int64_t sps, int64_t cs_rows, int64_t total) {
   int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (g >= total) return;
   const int d = static_cast<int>(g % half);
@@ -25,6 +25,7 @@ __global__ void __launch_bounds__(kThreads) rope_plain_kernel(const uint16_t* __
   const int h = static_cast<int>(row % heads);
   const int b = static_cast<int>(row / heads);
   const int64_t p = pid[b * spb + h * sph + s * sps];
+  if (p < 0 || p >= cs_rows) return;  // positions outside the table leave the row unwritten
   const uint16_t* c = cs + p * scs;
   const int64_t xo = b * sxb + h * sxh + s * sxs;
   uint16_t y1, y2;
@@ -40,7 +41,7 @@ __global__ void __launch_bounds__(kThreads) rope_push_kernel(const uint16_t* __r
                                                              const int32_t* __restrict__ cnts, int heads, int seq_len, int half,
                                                              int64_t sxb, int64_t sxh, int64_t sxs, int64_t scs, int64_t spb,
                                                              int64_t sph, int64_t sps, int64_t sob, int64_t soh, int64_t sos,
-                                                             int start, int end, int chunk, int64_t total) {
+                                                             int start, int end, int chunk, int64_t cs_rows, int64_t total) {
   int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (g >= total) return;
   const int d = static_cast<int>(g % half);
@@ -52,6 +53,7 @@ __global__ void __launch_bounds__(kThreads) rope_push_kernel(const uint16_t* __r
   if (s / chunk < cnts[b * heads + h]) return;
   if (start + s >= end) return;
   const int64_t p = static_cast<int64_t>(pid[b * spb + h * sph + (s / chunk) * sps]) * chunk + s % chunk;
+  if (p < 0 || p >= cs_rows) return;  // positions outside the table leave the row unwritten
   const uint16_t* c = cs + p * scs;
   const uint16_t* xr = x + b * sxb + h * sxh + s * sxs;
   uint16_t* o = out + b * sob + h * soh + static_cast<int64_t>(start + s) * sos;
@@ -79,7 +81,8 @@ int launch_push(bool glm, const uint16_t* x, const uint16_t* cos_sin, const int3
                 const int32_t* cnts, int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb,
                 int64_t stride_xh, int64_t stride_xs, int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b,
                 int64_t stride_pid_h, int64_t stride_pid_s, int64_t stride_output_b, int64_t stride_output_h,
-                int64_t stride_output_s, int start, int end, int half_dim, int chunk_size, void* stream) {
+                int64_t stride_output_s, int start, int end, int half_dim, int chunk_size, int64_t cos_sin_rows,
+                void* stream) {
   const char* what = glm ? "apply_rotary_pos_emb_push_cache_opt_glm" : "apply_rotary_pos_emb_push_cache_opt";
   if (!x || !cos_sin || !position_ids || !output || !cnts) {
     skv_set_error("%s: null pointer", what);
@@ -101,11 +104,13 @@ int launch_push(bool glm, const uint16_t* x, const uint16_t* cos_sin, const int3
   if (glm)
     hipLaunchKernelGGL(rope_push_kernel<true>, grid, dim3(kThreads), 0, s, x, cos_sin, position_ids, output, cnts, heads,
                        seq_len, half_dim, stride_xb, stride_xh, stride_xs, stride_cos_sin, stride_pid_b, stride_pid_h,
-                       stride_pid_s, stride_output_b, stride_output_h, stride_output_s, start, end, chunk_size, total);
+                       stride_pid_s, stride_output_b, stride_output_h, stride_output_s, start, end, chunk_size,
+                       cos_sin_rows, total);
   else
     hipLaunchKernelGGL(rope_push_kernel<false>, grid, dim3(kThreads), 0, s, x, cos_sin, position_ids, output, cnts, heads,
                        seq_len, half_dim, stride_xb, stride_xh, stride_xs, stride_cos_sin, stride_pid_b, stride_pid_h,
-                       stride_pid_s, stride_output_b, stride_output_h, stride_output_s, start, end, chunk_size, total);
+                       stride_pid_s, stride_output_b, stride_output_h, stride_output_s, start, end, chunk_size,
+                       cos_sin_rows, total);
   return skv_check_launch(what);
 }
 
@@ -115,7 +120,7 @@ extern "C" int skv_apply_rotary_pos_emb_new(const uint16_t* x, const uint16_t* c
                                             uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
                                             int64_t stride_xb, int64_t stride_xh, int64_t stride_xs, int64_t stride_xe,
                                             int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h,
-                                            int64_t stride_pid_s, int half_dim, void* stream) {
+                                            int64_t stride_pid_s, int half_dim, int64_t cos_sin_rows, void* stream) {
   const char* what = "apply_rotary_pos_emb_new";
   if (!x || !cos_sin || !position_ids || !output) {
     skv_set_error("%s: null pointer", what);
@@ -130,7 +135,7 @@ extern "C" int skv_apply_rotary_pos_emb_new(const uint16_t* x, const uint16_t* c
   hipLaunchKernelGGL(rope_plain_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), x, cos_sin, position_ids, output, heads, seq_len, half_dim,
                      stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s,
-                     total);
+                     cos_sin_rows, total);
   return skv_check_launch(what);
 }
 
@@ -139,11 +144,11 @@ extern "C" int skv_apply_rotary_pos_emb_push_cache_opt(
     int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb, int64_t stride_xh, int64_t stride_xs,
     int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h, int64_t stride_pid_s,
     int64_t stride_output_b, int64_t stride_output_h, int64_t stride_output_s, int offset_output_s_start,
-    int offset_output_s_end, int half_dim, int chunk_size, void* stream) {
+    int offset_output_s_end, int half_dim, int chunk_size, int64_t cos_sin_rows, void* stream) {
   return launch_push(false, x, cos_sin, position_ids, output, cnts, batch_size, heads, seq_len, embed_dim, stride_xb,
                      stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s,
                      stride_output_b, stride_output_h, stride_output_s, offset_output_s_start, offset_output_s_end,
-                     half_dim, chunk_size, stream);
+                     half_dim, chunk_size, cos_sin_rows, stream);
 }
 
 extern "C" int skv_apply_rotary_pos_emb_push_cache_opt_glm(
@@ -151,9 +156,9 @@ extern "C" int skv_apply_rotary_pos_emb_push_cache_opt_glm(
     int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb, int64_t stride_xh, int64_t stride_xs,
     int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h, int64_t stride_pid_s,
     int64_t stride_output_b, int64_t stride_output_h, int64_t stride_output_s, int offset_output_s_start,
-    int offset_output_s_end, int half_dim, int chunk_size, void* stream) {
+    int offset_output_s_end, int half_dim, int chunk_size, int64_t cos_sin_rows, void* stream) {
   return launch_push(true, x, cos_sin, position_ids, output, cnts, batch_size, heads, seq_len, embed_dim, stride_xb,
                      stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s,
                      stride_output_b, stride_output_h, stride_output_s, offset_output_s_start, offset_output_s_end,
-                     half_dim, chunk_size, stream);
+                     half_dim, chunk_size, cos_sin_rows, stream);
 }

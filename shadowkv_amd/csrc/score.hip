@@ -159,18 +159,23 @@ __global__ void __launch_bounds__(kThreads) softmax_kernel(const uint16_t* __res
   if (kWriteMax) out_max[static_cast<int64_t>(z) * n + j] = skv::f2bf(best);
 }
 
-int launch_scoring(const char* what, const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
-                   uint16_t* softmax, uint16_t* out_max, int batch_count, int m, int n, int k, float alpha,
-                   hipStream_t stream) {
-  if (!A || !B || !D || !norm || !sum || (!softmax && !out_max)) {
-    skv_set_error("%s: null pointer", what);
-    return SKV_EINVAL;
-  }
+int check_scoring_shape(const char* what, int batch_count, int m, int n, int k) {
   if (k != kHeadDim || m < 1 || m > kMaxM || n < 1 || batch_count < 1) {
     skv_set_error("%s: unsupported shape batch=%d m=%d n=%d k=%d (k must be 128, m in [1,16])", what, batch_count, m, n,
                   k);
     return SKV_EUNSUPPORTED;
   }
+  return SKV_OK;
+}
+
+int launch_logits(const char* what, const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
+                  int batch_count, int m, int n, int k, float alpha, hipStream_t stream) {
+  if (!A || !B || !D || !norm || !sum) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  int rc = check_scoring_shape(what, batch_count, m, n, k);
+  if (rc) return rc;
   if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15u) {
     skv_set_error("%s: A and B must be 16-byte aligned", what);
     return SKV_EINVAL;
@@ -182,8 +187,19 @@ int launch_scoring(const char* what, const uint16_t* A, const uint16_t* B, uint1
   else if (m <= 4) hipLaunchKernelGGL(logits_kernel<4>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
   else if (m <= 8) hipLaunchKernelGGL(logits_kernel<8>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
   else hipLaunchKernelGGL(logits_kernel<16>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
-  int rc = skv_check_launch(what);
+  return skv_check_launch(what);
+}
+
+int launch_softmax(const char* what, const uint16_t* D, const float* norm, const float* sum, uint16_t* softmax,
+                   uint16_t* out_max, int batch_count, int m, int n, hipStream_t stream) {
+  if (!D || !norm || !sum || (!softmax && !out_max)) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  int rc = check_scoring_shape(what, batch_count, m, n, kHeadDim);
   if (rc) return rc;
+  const int tiles = (n + kTile - 1) / kTile;
+  const dim3 grid(tiles, batch_count);
   if (softmax && out_max)
     hipLaunchKernelGGL((softmax_kernel<true, true>), grid, dim3(kThreads), 0, stream, D, norm, sum, softmax, out_max, m, n, tiles);
   else if (softmax)
@@ -194,6 +210,17 @@ int launch_scoring(const char* what, const uint16_t* A, const uint16_t* B, uint1
 }
 
 }  // namespace
+
+extern "C" int skv_score_logits(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
+                                int batch_count, int m, int n, int k, float alpha, void* stream) {
+  return launch_logits("score_logits", A, B, D, norm, sum, batch_count, m, n, k, alpha, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_softmax_gqa_max(const uint16_t* D, const float* norm, const float* sum, uint16_t* softmax,
+                                   uint16_t* out_max, int batch_count, int m, int n, void* stream) {
+  return launch_softmax("softmax_gqa_max", D, norm, sum, softmax, out_max, batch_count, m, n,
+                        static_cast<hipStream_t>(stream));
+}
 
 extern "C" int skv_batch_gemm_softmax(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
                                       uint16_t* softmax, int batch_count, int m, int n, int k, float alpha, float beta,
@@ -206,8 +233,10 @@ extern "C" int skv_batch_gemm_softmax(const uint16_t* A, const uint16_t* B, uint
     skv_set_error("batch_gemm_softmax: null softmax output");
     return SKV_EINVAL;
   }
-  return launch_scoring("batch_gemm_softmax", A, B, D, norm, sum, softmax, nullptr, batch_count, m, n, k, alpha,
-                        static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = launch_logits("batch_gemm_softmax", A, B, D, norm, sum, batch_count, m, n, k, alpha, s);
+  if (rc) return rc;
+  return launch_softmax("batch_gemm_softmax", D, norm, sum, softmax, nullptr, batch_count, m, n, s);
 }
 
 extern "C" int skv_score_gqa_max(const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
@@ -216,6 +245,8 @@ extern "C" int skv_score_gqa_max(const uint16_t* A, const uint16_t* B, uint16_t*
     skv_set_error("score_gqa_max: null output");
     return SKV_EINVAL;
   }
-  return launch_scoring("score_gqa_max", A, B, D, norm, sum, nullptr, out, batch_count, m, n, k, alpha,
-                        static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = launch_logits("score_gqa_max", A, B, D, norm, sum, batch_count, m, n, k, alpha, s);
+  if (rc) return rc;
+  return launch_softmax("score_gqa_max", D, norm, sum, nullptr, out, batch_count, m, n, s);
 }

@@ -1,0 +1,189 @@
+"""Random-init decoder that drives the sparse decode path end to end (throughput measurement).
+
+It reproduces the decode loop of the reference's model wrappers (models/base.py:85-176,
+models/llama.py:183-218): per layer RMSNorm -> fused QKV projection -> RoPE ->
+ShadowAttention.decode -> o_proj + residual -> RMSNorm -> gate/up -> SiLU*up -> down +
+residual; final norm, lm_head, greedy argmax. Weights are random (no checkpoint is
+available), dense products go to torch (hipBLASLt), RoPE and everything inside the attention
+handler run the gfx950 kernels of libshadowkv_amd.so.
+
+`synthesize_state` fills a ShadowKVCache_CPU with the decode-time state a long prefill would
+produce — low-rank factors, landmarks, landmark ids, the pinned host value store, the
+selected/local/outlier regions — from seeded random tensors of the right shapes, without
+running the prefill (a 122K-token SVD per layer and sequence). The sparse value region is
+filled from the host store by the chunk-gather kernel and the sparse key region by the
+rebuild kernel, so the cache starts consistent.
+"""
+from __future__ import annotations
+
+import math
+import types
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .kernels import shadowkv
+from .models.attention import ShadowAttention
+from .models.kvcache import ShadowKVCache_CPU
+from .models.tensor_op import build_cos_sin_cache
+
+
+@dataclass(frozen=True)
+class ModelShape:
+    name: str
+    layers: int
+    hidden: int
+    ffn: int
+    heads: int
+    kv_heads: int
+    vocab: int
+    rope_theta: float
+    head_dim: int = 128
+    eps: float = 1e-5
+
+
+LLAMA31_8B = ModelShape("Llama-3.1-8B", 32, 4096, 14336, 32, 8, 128256, 500000.0)
+LLAMA3_8B_1M = ModelShape("Llama-3-8B-1M", 32, 4096, 14336, 32, 8, 128256, 3580000.0)
+
+
+def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin: torch.Tensor | None = None) -> None:
+    """Give `cache` the post-prefill state of a ctx-token prompt (random contents, exact shapes)."""
+    dev = torch.device(cache.device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    L, B, H, D, c, R = cache.num_layers, cache.batch_size, cache.num_key_value_heads, cache.head_dim, \
+        cache.chunk_size, cache.rank
+    S = cache.select_sets
+    cache.prefill = ctx
+    max_ctx_chunks = ctx // c
+    cache.max_ctx_chunks_len = max_ctx_chunks * c
+    chunks = ctx // c - cache.local_chunk
+    cache.chunks = chunks - chunks % 8
+    cache.prefill_local = ctx - cache.chunks * c
+    cache.sparse_start = cache.prefill_local + cache.outlier_chunk * c
+    cache.sparse_end = cache.sparse_start + cache.sparse_budget
+    cache.kernel_offset = cache.sparse_start * D
+    cache.kernel_stride = cache.buf_len * D
+    n = cache.chunks - cache.outlier_chunk
+    G = cache.num_key_value_groups
+    tiles = (n + 255) // 256
+
+    cache.U = torch.empty(L, B, ctx, R, dtype=cache.dtype, device=dev)
+    cache.SV = torch.empty(L, B, H, D, R, dtype=cache.dtype, device=dev)
+    cache.k_landmark = torch.empty(L, B, H, n, D, dtype=cache.dtype, device=dev)
+    cache.k_landmark_idx = torch.empty(L, B, H, n, dtype=torch.int64, device=dev)
+    cache.gemm_o = torch.zeros(B, H, G, n, dtype=torch.bfloat16, device=dev)
+    cache.chunk_attn = torch.zeros(B, H, n, dtype=torch.bfloat16, device=dev)
+    cache.norm = torch.zeros(B * H, G, tiles, dtype=torch.float32, device=dev)
+    cache.sum = torch.zeros(B * H, G, tiles, dtype=torch.float32, device=dev)
+    if cos_sin is None:
+        cos_sin = build_cos_sin_cache(ctx + 4096, 500000.0, D, device=dev)
+    zero_cnts = torch.zeros(B * H, dtype=torch.int32, device=dev)
+    host_stage = torch.empty(B, H, cache.v_cache_cpu[0].shape[2], c * D, dtype=cache.dtype, device=dev)
+    for layer in range(L):
+        # U rows ~ N(0, 1/R) and SV ~ N(0, 1): rebuilt keys are O(1), like real post-SVD factors.
+        cache.U[layer].copy_(torch.randn(B, ctx, R, generator=g, device=dev) / math.sqrt(R))
+        cache.SV[layer].copy_(torch.randn(B, H, D, R, generator=g, device=dev))
+        cache.k_landmark[layer].copy_(torch.randn(B, H, n, D, generator=g, device=dev))
+        # landmark ids: every aligned chunk except `outlier_chunk` random ones, ascending (shadow.py:513-516)
+        order = torch.rand(B * H, cache.chunks, generator=g, device=dev).argsort(dim=-1)
+        keep = torch.ones(B * H, cache.chunks, dtype=torch.bool, device=dev)
+        keep.scatter_(1, order[:, :cache.outlier_chunk], False)
+        rest = torch.arange(cache.chunks, device=dev).expand(B * H, -1).masked_select(keep).view(B, H, n)
+        cache.k_landmark_idx[layer].copy_(rest)
+        pick = torch.rand(B * H, n, generator=g, device=dev).argsort(dim=-1)[:, :S].view(B, H, S)
+        cache.position_ids[layer].copy_(rest.gather(-1, pick))
+        # host value store of this layer
+        host_stage.normal_(generator=g)
+        cache.v_cache_cpu[layer].copy_(host_stage, non_blocking=False)
+        # local + outlier regions: random rows; selected region: the selected chunks themselves
+        cache.k_cache_buffer[layer].normal_(generator=g)
+        cache.v_cache_buffer[layer].normal_(generator=g)
+        _fill_selected_values(cache, layer, host_stage)
+        shadowkv.rebuild_k_rope(cache.U[layer], cache.SV[layer], cache.position_ids[layer], zero_cnts, cos_sin,
+                                cache.k_cache_buffer[layer], cache.sparse_start, c)
+    torch.cuda.synchronize()
+    cache.kv_offset = ctx
+    cache.prefilled_batch = B
+    cache._alloc_attention()
+
+
+def _fill_selected_values(cache: ShadowKVCache_CPU, layer: int, values: torch.Tensor) -> None:
+    """Selected value region <- the chunks named by position_ids, through the cached-copy kernel
+    with zero hits (every slot is a miss)."""
+    B, H, S = cache.batch_size, cache.num_key_value_heads, cache.select_sets
+    D, c = cache.head_dim, cache.chunk_size
+    cnts = torch.zeros(B * H, dtype=torch.int32, device=cache.device)
+    offsets = cache.position_ids[layer].to(torch.int32).reshape(-1).contiguous()
+    shadowkv.gather_copy_with_offsets(values, cache.v_cache_buffer[layer], None, offsets, cnts, None, B, H,
+                                      values.shape[2] * c * D, cache.sparse_budget * D, cache.kernel_offset,
+                                      cache.kernel_stride, S)
+
+
+class SyntheticDecoder:
+    """Random-init decoder-only model (Llama layout) decoding with the ShadowKV offload cache."""
+
+    def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
+                 chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
+                 dtype=torch.bfloat16):
+        self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
+        s = shape
+        D = s.head_dim
+        g = torch.Generator(device=device).manual_seed(seed)
+
+        def w(*size, scale=0.02):
+            return (torch.randn(*size, generator=g, device=device) * scale).to(dtype)
+
+        self.embed = w(s.vocab, s.hidden, scale=1.0)
+        self.lm_head = w(s.vocab, s.hidden)
+        self.norm_w = torch.ones(s.hidden, dtype=dtype, device=device)
+        self.layers = []
+        for _ in range(s.layers):
+            self.layers.append(types.SimpleNamespace(
+                wqkv=w((s.heads + 2 * s.kv_heads) * D, s.hidden), wo=w(s.hidden, s.heads * D),
+                gate_up=w(2 * s.ffn, s.hidden), down=w(s.hidden, s.ffn),
+                in_norm=torch.ones(s.hidden, dtype=dtype, device=device),
+                post_norm=torch.ones(s.hidden, dtype=dtype, device=device)))
+        self.cos_sin = build_cos_sin_cache(ctx + decode_len, s.rope_theta, D, device=device)
+        cfg = types.SimpleNamespace(num_attention_heads=s.heads, num_key_value_heads=s.kv_heads,
+                                    hidden_size=s.heads * D, num_hidden_layers=s.layers)
+        self.cache = ShadowKVCache_CPU(cfg, batch_size=batch, max_length=ctx, device=device,
+                                       sparse_budget=sparse_budget, chunk_size=chunk_size, rank=rank,
+                                       max_decode_len=decode_len, zero_host_store=False)
+        synthesize_state(self.cache, ctx, seed=seed + 1, cos_sin=self.cos_sin)
+        self.attn = ShadowAttention(self.cache, s.heads // s.kv_heads, D, s.hidden, self._rope, None, self.cos_sin)
+        self.q_rot = torch.empty(batch, s.heads * D, dtype=dtype, device=device)
+        self.k_rot = torch.empty(batch, s.kv_heads * D, dtype=dtype, device=device)
+
+    def _rope(self, q: torch.Tensor, k: torch.Tensor, position_ids: torch.Tensor):
+        """RoPE of the new token's q [B, 1, Hq*D] and k [B, 1, Hkv*D] at position_ids [B] (HIP kernel)."""
+        s, B, D = self.shape, self.batch, self.shape.head_dim
+        for x, out, h in ((q, self.q_rot, s.heads), (k, self.k_rot, s.kv_heads)):
+            xv = x.view(B, h, 1, D)
+            shadowkv.apply_rotary_pos_emb_new(xv, self.cos_sin, position_ids, out.view(B, h, 1, D), B, h, 1, D,
+                                              xv.stride(0), xv.stride(1), xv.stride(2), xv.stride(3),
+                                              self.cos_sin.stride(0), position_ids.stride(0), 0, 0, D // 2)
+        return (self.q_rot.view(B, 1, s.heads, D).transpose(1, 2), self.k_rot.view(B, 1, s.kv_heads, D).transpose(1, 2))
+
+    def _norm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, (x.shape[-1],), w, self.shape.eps)
+
+    @torch.inference_mode()
+    def decode_step(self, tokens: torch.Tensor) -> torch.Tensor:
+        """One greedy decode step for the whole batch: tokens [B, 1] -> next tokens [B, 1]."""
+        s, B, D = self.shape, self.batch, self.shape.head_dim
+        pos = torch.full((B,), self.ctx + self.cache.gen_offset, dtype=torch.int64, device=self.device)
+        h = F.embedding(tokens, self.embed)
+        for idx, lw in enumerate(self.layers):
+            x = self._norm(h, lw.in_norm)
+            qkv = F.linear(x, lw.wqkv)
+            q, k, v = qkv.split([s.heads * D, s.kv_heads * D, s.kv_heads * D], dim=-1)
+            v = v.view(B, 1, s.kv_heads, D).transpose(1, 2)
+            a = self.attn.decode(q, k, v, pos, idx)
+            h = h + F.linear(a.reshape(B, 1, s.heads * D), lw.wo)
+            x = self._norm(h, lw.post_norm)
+            gate, up = F.linear(x, lw.gate_up).chunk(2, dim=-1)
+            h = h + F.linear(F.silu(gate) * up, lw.down)
+        h = self._norm(h, self.norm_w)
+        logits = F.linear(h[:, -1], self.lm_head).float()  # [B, vocab]
+        return logits.argmax(dim=-1, keepdim=True)  # [B, 1]

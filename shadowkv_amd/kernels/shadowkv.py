@@ -25,7 +25,7 @@ from .. import _lib
 __all__ = [
     "gather_copy", "gather_copy_d2d_with_offsets", "reorder_keys_and_compute_offsets", "gather_copy_with_offsets",
     "apply_rotary_pos_emb_new", "apply_rotary_pos_emb_push_cache_opt", "apply_rotary_pos_emb_push_cache_opt_glm",
-    "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "topk_gather", "rebuild_k_rope",
+    "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "score_logits", "softmax_gqa_max", "topk_gather", "rebuild_k_rope",
     "sparse_attn_workspace_bytes", "sparse_attn_decode", "device_address",
 ]
 
@@ -174,11 +174,9 @@ def apply_rotary_pos_emb_new(x, cos_sin, position_ids, output, batch_size, heads
     _dev(cos_sin, "cos_sin", torch.bfloat16)
     _dev(position_ids, "position_ids", torch.int64)
     _dev(output, "output", torch.bfloat16)
-    if position_ids.numel() and int(position_ids.max()) >= cos_sin.shape[0]:
-        raise ValueError("position_ids exceed the cos_sin table")
     _lib.call("skv_apply_rotary_pos_emb_new", x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(),
               output.data_ptr(), batch_size, heads, seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe,
-              stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, _stream())
+              stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, cos_sin.shape[0], _stream())
 
 
 def _push(name, x, cos_sin, position_ids, output, cnts, *ints):
@@ -187,11 +185,8 @@ def _push(name, x, cos_sin, position_ids, output, cnts, *ints):
     _dev(position_ids, "position_ids", torch.int32)
     _dev(output, "output", torch.bfloat16)
     _dev(cnts, "cnts", torch.int32)
-    chunk_size = ints[-1]
-    if position_ids.numel() and (int(position_ids.max()) + 1) * chunk_size > cos_sin.shape[0]:
-        raise ValueError("position_ids exceed the cos_sin table")
     _lib.call(name, x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(), output.data_ptr(), cnts.data_ptr(),
-              *ints, _stream())
+              *ints, cos_sin.shape[0], _stream())
 
 
 def apply_rotary_pos_emb_push_cache_opt(x, cos_sin, position_ids, output, cnts, batch_size, heads, seq_len, embed_dim,
@@ -325,6 +320,33 @@ def score_gqa_max(A, B, D, Norm, Sum, out, batch_count, m, n, k, alpha=1.0 / mat
     _need(out, batch_count * n, "out")
     _lib.call("skv_score_gqa_max", A.data_ptr(), B.data_ptr(), D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(),
               out.data_ptr(), batch_count, m, n, k, float(alpha), _stream())
+
+
+def score_logits(A, B, D, Norm, Sum, batch_count, m, n, k, alpha=1.0 / math.sqrt(128)):
+    """First scoring kernel: D = bf16(alpha A.B^T) and per-256-column max / sum(exp) partials."""
+    _check_scoring(A, B, D, Norm, Sum, batch_count, m, n, k)
+    _lib.call("skv_score_logits", A.data_ptr(), B.data_ptr(), D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(),
+              batch_count, m, n, k, float(alpha), _stream())
+
+
+def softmax_gqa_max(D, Norm, Sum, out, batch_count, m, n, softmax=None):
+    """Second scoring kernel: softmax over n from the partials, max over the m rows into out [batch, n]."""
+    for t, nm in ((D, "D"), (out, "out")):
+        _dev(t, nm, torch.bfloat16)
+    _dev(Norm, "Norm", torch.float32)
+    _dev(Sum, "Sum", torch.float32)
+    tiles = (n + 255) // 256
+    _need(D, batch_count * m * n, "D")
+    _need(Norm, batch_count * m * tiles, "Norm")
+    _need(Sum, batch_count * m * tiles, "Sum")
+    _need(out, batch_count * n, "out")
+    sm = 0
+    if softmax is not None:
+        _dev(softmax, "softmax", torch.bfloat16)
+        _need(softmax, batch_count * m * n, "softmax")
+        sm = softmax.data_ptr()
+    _lib.call("skv_softmax_gqa_max", D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), sm or None, out.data_ptr(),
+              batch_count, m, n, _stream())
 
 
 def topk_gather(scores, landmark_idx, k, out_ids):

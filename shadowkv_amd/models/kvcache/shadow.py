@@ -42,7 +42,7 @@ class ShadowKVCache_CPU(KVCacheBase):
 
     def __init__(self, config, batch_size: int = 1, max_length: int = 32 * 1024, device: str = "cuda:0",
                  dtype=torch.bfloat16, sparse_budget: int = 2048, chunk_size: int = 8, rank: int = 160,
-                 max_decode_len: int | None = None) -> None:
+                 max_decode_len: int | None = None, zero_host_store: bool = True) -> None:
         self.config = config
         self.batch_size = batch_size
         self.max_length = max_length
@@ -64,8 +64,12 @@ class ShadowKVCache_CPU(KVCacheBase):
             raise ValueError(f"sparse_budget {self.sparse_budget} is not a multiple of chunk_size {chunk_size}")
 
         L, B, H, D = self.num_layers, batch_size, self.num_key_value_heads, self.head_dim
-        self.v_cache_cpu = torch.zeros(L, B, H, max_length // chunk_size, D * chunk_size, dtype=dtype,
-                                       pin_memory=True)
+        # One pinned host buffer per layer, [B, H, max_length/c, c*D] each (indexable like the reference's
+        # [L, ...] tensor): torch's pinned allocator rounds each request up to a power of two, which a
+        # single 64 GB allocation (Llama-3-8B, batch 8, 122K) would double.
+        alloc = torch.zeros if zero_host_store else torch.empty
+        self.v_cache_cpu = [alloc(B, H, max_length // chunk_size, D * chunk_size, dtype=dtype, pin_memory=True)
+                            for _ in range(L)]
         # Sparse region ends at most at (local 4 chunks + 7 alignment chunks + 7 tokens) + outliers + budget.
         ref_len = self.sparse_budget + 128 + (self.outlier_chunk + self.local_chunk) * chunk_size
         if max_decode_len is None:
@@ -152,7 +156,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.prefill = incoming
         max_ctx_chunks = incoming // c
         self.max_ctx_chunks_len = max_ctx_chunks * c
-        if max_ctx_chunks > self.v_cache_cpu.shape[3]:
+        if max_ctx_chunks > self.v_cache_cpu[l].shape[2]:
             raise ValueError(f"prompt of {incoming} tokens exceeds max_length {self.max_length}")
         self.v_cache_cpu[l][pb:pb + bsz, :, :max_ctx_chunks].copy_(
             new_v_cache[:, :, :self.max_ctx_chunks_len].reshape(bsz, H, max_ctx_chunks, c * D))
@@ -221,8 +225,9 @@ class ShadowKVCache_CPU(KVCacheBase):
             raise ValueError("decode scoring takes one query token per step")
         n = self.k_landmark.shape[-2]
         q = query_states if query_states.is_contiguous() else query_states.contiguous()
-        shadowkv.score_gqa_max(q, self.k_landmark[layer_idx], self.gemm_o, self.norm, self.sum, self.chunk_attn,
-                               B * H, G, n, D, 1.0 / math.sqrt(128))
+        shadowkv.score_logits(q, self.k_landmark[layer_idx], self.gemm_o, self.norm, self.sum, B * H, G, n, D,
+                              1.0 / math.sqrt(128))
+        shadowkv.softmax_gqa_max(self.gemm_o, self.norm, self.sum, self.chunk_attn, B * H, G, n)
         shadowkv.topk_gather(self.chunk_attn.view(B * H, n), self.k_landmark_idx[layer_idx].view(B * H, n),
                              self.select_sets, self.selected_chunks)
         shadowkv.reorder_keys_and_compute_offsets(self.position_ids[layer_idx], self.selected_chunks, self.offsets,

@@ -25,13 +25,14 @@ def _say(msg):
     print(msg, flush=True)
 
 
-def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> int:
-    """Largest distance in bf16 units in the last place between two same-sign-or-zero tensors."""
-    ai = a.contiguous().view(torch.int16).int()
-    bi = b.contiguous().view(torch.int16).int()
-    ai = torch.where(ai < 0, -(ai & 0x7FFF), ai)
-    bi = torch.where(bi < 0, -(bi & 0x7FFF), bi)
-    return int((ai - bi).abs().max()) if ai.numel() else 0
+def _assert_rounding_close(got: torch.Tensor, want: torch.Tensor, floor: float = 1e-5):
+    """fp32 sums taken in another order then rounded to bf16: at most one bf16 ulp of the larger
+    magnitude apart, plus an absolute floor for values produced by cancellation."""
+    g, w = got.float(), want.float()
+    m = torch.maximum(g.abs(), w.abs()).clamp_min(2.0 ** -126)
+    ulp = torch.exp2(torch.floor(torch.log2(m)) - 7)
+    bad = (g - w).abs() > ulp + floor
+    assert not bad.any(), f"{int(bad.sum())} elements beyond one rounding step, max diff {(g - w).abs().max():.3e}"
 
 
 @pytest.mark.parametrize("glm", [False, True])
@@ -94,7 +95,7 @@ def test_batch_gather_gemm_plain(gpu):
         miss = int(cnts[bh]) * c
         assert (got[b, h, :miss] == 0).all()  # hit rows untouched
         torch.testing.assert_close(got[b, h, miss:].float(), want[b, h, miss:].float(), rtol=RTOL, atol=ATOL)
-        assert _bf16_ulps(got[b, h, miss:], want[b, h, miss:]) <= 2
+        _assert_rounding_close(got[b, h, miss:], want[b, h, miss:])
 
 
 @pytest.mark.parametrize("glm,per_head_u,shared_sv,R", [(False, False, False, 160), (True, False, False, 160),
@@ -159,7 +160,7 @@ def test_scoring(gpu, Z, m, n):
     out = torch.empty(Z, n, dtype=torch.bfloat16, device=gpu)
     shadowkv.score_gqa_max(qg, Lg, Dg, norm, ssum, out, Z, m, n, 128, alpha)
     torch.cuda.synchronize()
-    assert _bf16_ulps(Dg.cpu(), Dw) <= 1
+    _assert_rounding_close(Dg.cpu(), Dw)
     Pc = Pg.cpu().float()
     rel = ((Pc - Pw.float()).abs() / Pw.float().clamp_min(1e-30)).max().item()
     assert rel <= 2e-2, rel
