@@ -125,31 +125,33 @@ def breakdown(model, tok) -> dict:
     import torch
     from shadowkv_amd.kernels import shadowkv
 
-    names = ["score_logits", "softmax_gqa_max", "topk_gather", "reorder_keys_and_compute_offsets",
-             "gather_copy_with_offsets", "gather_copy_d2d_with_offsets", "rebuild_k_rope", "sparse_attn_decode"]
+    names = ["apply_rotary_pos_emb_new", "score_logits", "select_chunks", "gather_copy_with_offsets",
+             "gather_copy_d2d_with_offsets", "rebuild_k_rope", "sparse_attn_decode"]
     timers = {n: KernelTimer(shadowkv, n) for n in names}
     cache = model.cache
-    misses = []
-    orig_fetch = timers["gather_copy_with_offsets"].orig
+    snaps = []  # per-layer copies of the hit counts, taken on the device (no host sync in the step)
+    orig_select = timers["select_chunks"].orig
 
-    def counted(*a, **kw):
-        misses.append(cache.select_sets * cache.batch_size * cache.num_key_value_heads - int(cache.cnts.sum()))
-        return orig_fetch(*a, **kw)
+    def select_and_snapshot(*a, **kw):
+        out = orig_select(*a, **kw)
+        snaps.append(cache.cnts.clone())
+        return out
 
-    timers["gather_copy_with_offsets"].orig = counted
+    timers["select_chunks"].orig = select_and_snapshot
     for t in timers.values():
         t.active = True
     torch.cuda.synchronize()
     model.decode_step(tok)
     torch.cuda.synchronize()
+    timers["select_chunks"].orig = orig_select
     for t in timers.values():
         t.active = False
-        setattr(shadowkv, t.name, t.orig if t.name != "gather_copy_with_offsets" else orig_fetch)
-    ops = {n: round(t.mean_ms() * 1e3, 2) for n, t in timers.items()}
+        setattr(shadowkv, t.name, t.orig)
+    ops = {n: round(t.mean_ms() * 1e3, 2) for n, t in timers.items() if t.pairs}
     chunk_bytes = cache.chunk_size * cache.head_dim * 2
     fetch_ms = timers["gather_copy_with_offsets"].mean_ms()
-    miss_mean = statistics.fmean(misses)
     total_sel = cache.select_sets * cache.batch_size * cache.num_key_value_heads
+    miss_mean = statistics.fmean(total_sel - int(c.sum()) for c in snaps)
     return {"op_us_per_layer": ops, "hit_rate": round(1 - miss_mean / total_sel, 4),
             "host_link": {"bytes_per_layer": int(miss_mean * chunk_bytes),
                           "GBps": round(miss_mean * chunk_bytes / (fetch_ms * 1e-3) / 1e9, 2),

@@ -173,6 +173,22 @@ int skv_softmax_gqa_max(const uint16_t* D, const float* norm, const float* sum, 
 int skv_topk_gather(const uint16_t* scores, int64_t score_stride, const int64_t* landmark_idx,
                     int64_t idx_stride, int rows, int n, int k, int64_t* out_ids, void* stream);
 
+/* a1 tail + a2 + a3 fused: one launch performs the softmax normalisation of D from its partials,
+ * the GQA max over the m rows, the top-k (value desc, index asc), the landmark-id gather and the
+ * reorder of the selected ids against position_ids (in place), writing offsets and cnts exactly
+ * as skv_softmax_gqa_max + skv_topk_gather + skv_reorder_keys_and_compute_offsets would.
+ * Replaces models/kvcache/shadow.py:553-574 after the scoring GEMM. D/norm/sum as produced by
+ * skv_score_logits for `rows` batch entries of m query rows; landmark_idx rows of idx_stride;
+ * position_ids/offsets [rows][select_sets]; cnts [rows]. Chunk ids (landmark ids and previous
+ * slot ids) must lie in [0, num_chunks) (-1 marks an empty previous slot); num_chunks <= 245760.
+ * out_scores ([rows][n] bf16 GQA-max probabilities) and out_selected ([rows][select_sets] ids in
+ * top-k order) are optional, except that out_scores is required as staging when n is too large
+ * for LDS. select_sets <= 2048. */
+int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                      const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
+                      int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
+                      int64_t* out_selected, void* stream);
+
 /* ---- a8: sparse decode attention ----------------------------------------------------------------
  * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, causal=True) for one query token
  * (models/attention/shadow.py:48): for b, query head hq, kv head h = hq / (q_heads/kv_heads):

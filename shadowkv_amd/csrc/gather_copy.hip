@@ -9,6 +9,9 @@
 //                          the pinned host store (zero-copy 16-byte loads over the host link),
 //                          each workgroup keeping 8 loads per lane in flight.
 // The copy unit is a chunk of chunk_elems bf16 values, moved as 16-byte vectors.
+#include <algorithm>
+#include <cstdlib>
+
 #include "skv_common.h"
 
 namespace {
@@ -17,7 +20,21 @@ using skv::u32x4;
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 8;             // 16-byte vectors in flight per lane
-constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch workgroup
+constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch tile
+// Upper bound on fetch workgroups (environment SKV_FETCH_WGS overrides it, read once). The
+// fetch is host-link bound: a few dozen workgroups keep more than the link's bandwidth-delay
+// product in flight, and a bounded grid leaves CUs free for the key rebuild that runs
+// concurrently on the other stream.
+constexpr int kDefaultFetchWGs = 256;
+
+int fetch_workgroups() {
+  static const int wgs = [] {
+    const char* e = getenv("SKV_FETCH_WGS");
+    const int v = e ? atoi(e) : 0;
+    return (v >= 1 && v <= 65536) ? v : kDefaultFetchWGs;
+  }();
+  return wgs;
+}
 
 // In-place forward compaction of the hit chunks of one row. Offsets are strictly ascending
 // with offsets[i] >= i, so the hits whose offset equals their index form a prefix that is
@@ -66,22 +83,11 @@ __global__ void __launch_bounds__(kThreads) compact_hits_kernel(u32x4* __restric
   }
 }
 
-// dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where
-// start = cnts[row] (or 0 without cnts). Grid = rows * tiles; tile t covers
-// kChunksPerFetchWG consecutive slots starting at start + t*kChunksPerFetchWG.
-// Ids outside [0, src_chunks) are skipped, so a bad id can never read past the source row.
+// Copies slots [i0, i1) of one row, 16-byte vectors, kUnroll loads in flight per lane.
 template <typename IdxT>
-__global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __restrict__ src, int64_t src_row_vec,
-                                                                  u32x4* __restrict__ dst, int64_t dst_row_vec,
-                                                                  int64_t dst_offset_vec, const IdxT* __restrict__ ids,
-                                                                  const int32_t* __restrict__ cnts, int S, int chunk_vec,
-                                                                  int64_t src_chunks, int tiles) {
-  const int row = blockIdx.x / tiles;
-  const int t = blockIdx.x - row * tiles;
-  const int start = cnts ? max(0, cnts[row]) : 0;
-  const int i0 = start + t * kChunksPerFetchWG;
-  if (i0 >= S) return;
-  const int i1 = min(i0 + kChunksPerFetchWG, S);
+__device__ __forceinline__ void gather_tile(const u32x4* __restrict__ src, int64_t src_row_vec, u32x4* __restrict__ dst,
+                                            int64_t dst_row_vec, int64_t dst_offset_vec, const IdxT* __restrict__ ids,
+                                            int row, int i0, int i1, int S, int chunk_vec, int64_t src_chunks) {
   const int64_t total = static_cast<int64_t>(i1 - i0) * chunk_vec;
   const u32x4* s = src + static_cast<int64_t>(row) * src_row_vec;
   u32x4* d = dst + static_cast<int64_t>(row) * dst_row_vec + dst_offset_vec;
@@ -108,6 +114,29 @@ __global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __
         if (c >= 0 && c < src_chunks) d[static_cast<int64_t>(i) * chunk_vec + e] = r[u];
       }
     }
+  }
+}
+
+// dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where
+// start = cnts[row] (or 0 without cnts). The work is rows * tiles tiles; tile t of a row covers
+// kChunksPerFetchWG consecutive slots starting at start + t*kChunksPerFetchWG; workgroups walk
+// the tiles with a grid stride. Ids outside [0, src_chunks) are skipped, so a bad id can never
+// read past the source row.
+template <typename IdxT>
+__global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __restrict__ src, int64_t src_row_vec,
+                                                                  u32x4* __restrict__ dst, int64_t dst_row_vec,
+                                                                  int64_t dst_offset_vec, const IdxT* __restrict__ ids,
+                                                                  const int32_t* __restrict__ cnts, int S, int chunk_vec,
+                                                                  int64_t src_chunks, int rows, int tiles) {
+  const int total_tiles = rows * tiles;
+  for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+    const int row = tile / tiles;
+    const int t = tile - row * tiles;
+    const int start = cnts ? max(0, cnts[row]) : 0;
+    const int i0 = start + t * kChunksPerFetchWG;
+    if (i0 >= S) continue;
+    gather_tile(src, src_row_vec, dst, dst_row_vec, dst_offset_vec, ids, row, i0, min(i0 + kChunksPerFetchWG, S), S,
+                chunk_vec, src_chunks);
   }
 }
 
@@ -179,10 +208,10 @@ extern "C" int skv_gather_copy_with_offsets(const void* values, void* v_cache_bu
   rc = skv_check_launch(what);
   if (rc) return rc;
   const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
-  hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(rows * tiles), dim3(kThreads), 0, s,
+  hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0, s,
                      static_cast<const u32x4*>(values), cpu_v_length / 8, static_cast<u32x4*>(v_cache_buffer),
                      gpu_v_stride / 8, gpu_v_offset / 8, offsets, cnts, map_size, chunk_elems / 8,
-                     cpu_v_length / chunk_elems, tiles);
+                     cpu_v_length / chunk_elems, rows, tiles);
   return skv_check_launch(what);
 }
 
@@ -203,10 +232,10 @@ extern "C" int skv_gather_copy(const void* values, void* v_cache_buffer, const i
   }
   const int rows = batch_size * heads;
   const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
-  hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(rows * tiles), dim3(kThreads), 0,
+  hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const u32x4*>(values), cpu_v_length / 8,
                      static_cast<u32x4*>(v_cache_buffer), gpu_v_length / 8, int64_t(0), position_ids,
                      static_cast<const int32_t*>(nullptr), map_size, chunk_elems / 8, cpu_v_length / chunk_elems,
-                     tiles);
+                     rows, tiles);
   return skv_check_launch(what);
 }

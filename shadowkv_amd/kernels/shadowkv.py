@@ -25,7 +25,7 @@ from .. import _lib
 __all__ = [
     "gather_copy", "gather_copy_d2d_with_offsets", "reorder_keys_and_compute_offsets", "gather_copy_with_offsets",
     "apply_rotary_pos_emb_new", "apply_rotary_pos_emb_push_cache_opt", "apply_rotary_pos_emb_push_cache_opt_glm",
-    "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "score_logits", "softmax_gqa_max", "topk_gather", "rebuild_k_rope",
+    "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "score_logits", "softmax_gqa_max", "select_chunks", "topk_gather", "rebuild_k_rope",
     "sparse_attn_workspace_bytes", "sparse_attn_decode", "device_address",
 ]
 
@@ -347,6 +347,51 @@ def softmax_gqa_max(D, Norm, Sum, out, batch_count, m, n, softmax=None):
         sm = softmax.data_ptr()
     _lib.call("skv_softmax_gqa_max", D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), sm or None, out.data_ptr(),
               batch_count, m, n, _stream())
+
+
+def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunks, position_ids, offsets, cnts,
+                  out_scores=None, out_selected=None):
+    """Fused softmax + GQA max + top-k + id gather + reorder (one launch, one workgroup per row).
+
+    D/Norm/Sum: outputs of score_logits for `rows` entries of m query rows; landmark_idx: [rows, n]
+    view with contiguous rows, chunk ids in [0, num_chunks); position_ids: [rows, select_sets] int64
+    (in: previous slots, -1 = empty; out: reordered); offsets: [rows * select_sets] int32; cnts:
+    [rows] int32; out_scores: optional [rows, n] bf16 GQA-max probabilities; out_selected: optional
+    [rows, select_sets] ids in top-k order (the reference's selected_chunks; costs a sort)."""
+    _dev(D, "D", torch.bfloat16)
+    _dev(Norm, "Norm", torch.float32)
+    _dev(Sum, "Sum", torch.float32)
+    _dev(landmark_idx, "landmark_idx", torch.int64)
+    _dev(position_ids, "position_ids", torch.int64)
+    _dev(offsets, "offsets", torch.int32)
+    _dev(cnts, "cnts", torch.int32)
+    if landmark_idx.dim() != 2 or landmark_idx.shape[1] != n or landmark_idx.stride(1) != 1:
+        raise ValueError("landmark_idx must be [rows, n] with contiguous rows")
+    if not (1 <= select_sets <= min(n, 2048)):
+        raise ValueError(f"select_sets={select_sets} must be in [1, min(n={n}, 2048)]")
+    tiles = (n + 255) // 256
+    _need(D, rows * m * n, "D")
+    _need(Norm, rows * m * tiles, "Norm")
+    _need(Sum, rows * m * tiles, "Sum")
+    _need(landmark_idx, (rows - 1) * landmark_idx.stride(0) + n, "landmark_idx")
+    for t, nm, e in ((position_ids, "position_ids", rows * select_sets), (offsets, "offsets", rows * select_sets),
+                     (cnts, "cnts", rows)):
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+        _need(t, e, nm)
+    sp = None
+    if out_scores is not None:
+        _dev(out_scores, "out_scores", torch.bfloat16)
+        _need(out_scores, rows * n, "out_scores")
+        sp = out_scores.data_ptr()
+    op = None
+    if out_selected is not None:
+        _dev(out_selected, "out_selected", torch.int64)
+        _need(out_selected, rows * select_sets, "out_selected")
+        op = out_selected.data_ptr()
+    _lib.call("skv_select_chunks", D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), rows, m, n, landmark_idx.data_ptr(),
+              landmark_idx.stride(0), select_sets, num_chunks, position_ids.data_ptr(), offsets.data_ptr(),
+              cnts.data_ptr(), sp, op, _stream())
 
 
 def topk_gather(scores, landmark_idx, k, out_ids):

@@ -103,6 +103,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.cnts = torch.zeros(rows, device=device, dtype=torch.int32)
         self.position_ids = torch.full((L, B, H, self.select_sets), -1, device=device, dtype=torch.int64)
         self.selected_chunks = torch.zeros(B, H, self.select_sets, device=device, dtype=torch.int64)
+        self.keep_selected = False  # also emit the selected ids in top-k order into selected_chunks
 
         self.copy_stream = torch.cuda.Stream(device=device)
         self.attn_workspace = None
@@ -227,11 +228,12 @@ class ShadowKVCache_CPU(KVCacheBase):
         q = query_states if query_states.is_contiguous() else query_states.contiguous()
         shadowkv.score_logits(q, self.k_landmark[layer_idx], self.gemm_o, self.norm, self.sum, B * H, G, n, D,
                               1.0 / math.sqrt(128))
-        shadowkv.softmax_gqa_max(self.gemm_o, self.norm, self.sum, self.chunk_attn, B * H, G, n)
-        shadowkv.topk_gather(self.chunk_attn.view(B * H, n), self.k_landmark_idx[layer_idx].view(B * H, n),
-                             self.select_sets, self.selected_chunks)
-        shadowkv.reorder_keys_and_compute_offsets(self.position_ids[layer_idx], self.selected_chunks, self.offsets,
-                                                  self.cnts, B, H, self.select_sets)
+        # softmax + GQA max + top-k + landmark-id gather + reorder in one launch. The GQA-max scores are kept in
+        # chunk_attn; the selected ids in top-k order (selected_chunks) only when keep_selected is set.
+        shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, B * H, G, n, self.k_landmark_idx[layer_idx].view(B * H, n),
+                               self.select_sets, self.chunks, self.position_ids[layer_idx].view(B * H, -1), self.offsets,
+                               self.cnts, out_scores=self.chunk_attn,
+                               out_selected=self.selected_chunks if self.keep_selected else None)
         return self.position_ids[layer_idx]
 
     def _gen_len(self, layer_idx: int) -> int:

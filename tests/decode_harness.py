@@ -33,6 +33,7 @@ def build_cache(case, device, max_decode_len=None, num_layers=1):
         cache.get_svd(case["k_pre"], layer)
         cache.prefill_kv_cache(case["v"], layer, k_roped, q_last)
     cache.H2D()
+    cache.keep_selected = True
     return cache
 
 

@@ -144,3 +144,54 @@ def test_topk_gather_bit_exact(gpu, n, k, ties):
     shadowkv.topk_gather(x.to(gpu), lidx.to(gpu), k, out)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), want)
+
+
+@pytest.mark.parametrize("rows,m,n,S", [(64, 4, 15304, 256), (8, 16, 32712, 256), (8, 4, 130680, 2048),
+                                        (8, 4, 968, 256), (2, 1, 300, 7)])
+def test_select_chunks_fused_equals_unfused(gpu, rows, m, n, S):
+    _say(f"select_chunks rows={rows} m={m} n={n} S={S}")
+    g = torch.Generator().manual_seed(rows * n + S)
+    q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
+    L = torch.randn(rows, n, 128, generator=g).to(torch.bfloat16).to(gpu)
+    lidx = torch.stack([torch.randperm(n + n // 10, generator=g)[:n].sort().values for _ in range(rows)]).to(gpu)
+    tiles = (n + 255) // 256
+    D = torch.empty(rows, m, n, dtype=torch.bfloat16, device=gpu)
+    norm = torch.empty(rows, m, tiles, device=gpu)
+    ssum = torch.empty_like(norm)
+    shadowkv.score_logits(q, L, D, norm, ssum, rows, m, n, 128)
+    scores = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+    shadowkv.softmax_gqa_max(D, norm, ssum, scores, rows, m, n)
+    sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
+    shadowkv.topk_gather(scores, lidx, S, sel)
+    torch.cuda.synchronize()
+    # previous slots: about half of this step's selection plus other landmark ids, shuffled
+    old = []
+    for r in range(rows):
+        keep = sel[r, :S // 2].cpu()
+        pool = lidx[r].cpu()
+        others = pool[~torch.isin(pool, sel[r].cpu())]
+        others = others[torch.randperm(len(others), generator=g)[:S - len(keep)]]
+        old.append(torch.cat([keep, others])[torch.randperm(S, generator=g)])
+    old = torch.stack(old).to(gpu)
+    pos1, off1, cnt1 = old.clone(), torch.empty(rows * S, dtype=torch.int32, device=gpu), torch.empty(rows, dtype=torch.int32, device=gpu)
+    shadowkv.reorder_keys_and_compute_offsets(pos1, sel, off1, cnt1, rows, 1, S)
+    pos2, off2, cnt2 = old.clone(), torch.empty_like(off1), torch.empty_like(cnt1)
+    scores2 = torch.empty_like(scores)
+    sel2 = torch.empty_like(sel)
+    nchunks = n + n // 10
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos2, off2, cnt2, out_scores=scores2,
+                           out_selected=sel2)
+    pos3, off3, cnt3 = old.clone(), torch.empty_like(off1), torch.empty_like(cnt1)
+    staging = torch.empty_like(scores) if n > 16384 else None  # scores beyond LDS need global staging
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos3, off3, cnt3, out_scores=staging)
+    torch.cuda.synchronize()
+    assert torch.equal(pos3, pos1) and torch.equal(off3, off1) and torch.equal(cnt3, cnt1)
+    assert torch.equal(scores2, scores)
+    assert torch.equal(sel2, sel)
+    assert torch.equal(pos2, pos1) and torch.equal(off2, off1) and torch.equal(cnt2, cnt1)
+    # and both against the oracle, from the kernel's own scores
+    assert torch.equal(sel.cpu(), oracle.topk_gather(scores.cpu(), lidx.cpu(), S))
+    ids, offs, cnts = oracle.reorder(old.cpu().numpy(), sel.cpu().numpy())
+    assert np.array_equal(pos2.cpu().numpy(), ids) and np.array_equal(cnt2.cpu().numpy(), cnts)
+    assert np.array_equal(off2.view(rows, S).cpu().numpy(), offs)
+    assert (cnts >= S // 2).all()
