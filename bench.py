@@ -5,10 +5,12 @@ Workload (default): Llama-3.1-8B shape (32 layers, hidden 4096, FFN 14336, GQA 3
 ShadowKV rank 160, chunk 8, sparse budget 2048 (256 chunks), 48 outlier chunks, values of every
 layer offloaded to pinned host memory (64.4 GB). The post-prefill state is synthesized from
 seeded random tensors of the exact shapes (no 122K-token prefill/SVD is run); timing covers
-greedy decode steps only. A step = one new token for all 8 sequences through all 32 layers.
+greedy decode steps only. A step = one new token for all 8 sequences through all 32 layers;
+by default the step is captured once in a HIP graph and the timed steps are graph replays.
 
-Prints one JSON line. `roofline` is measured live on the landmark-scoring kernel (the
-largest HBM stream of the path) with HIP events on its stream during the timed steps;
+Prints one JSON line. `roofline` is measured on the landmark-scoring kernel (the largest HBM
+stream of the path) with HIP events on its stream: during the timed steps when they run
+eagerly, else over eager steps of the same decode right after the timed replays;
 `host_link` reports the value fetch from pinned host memory measured in a separate
 instrumented step; `cpu_baseline` times the CPU oracle's restatement of one layer's
 hot-path ops at the same shapes on this host (a reported baseline only).
@@ -28,6 +30,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+ROOFLINE_STEPS = 4
 
 
 def log(msg: str) -> None:
@@ -43,6 +46,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--ctx", type=int, default=122880)
     p.add_argument("--budget", type=int, default=2048)
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
+    p.add_argument("--lanes", type=int, default=1, help="independent batch slices interleaved per layer")
+    p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-breakdown", action="store_true")
@@ -72,7 +77,10 @@ class KernelTimer:
         setattr(module, name, wrapped)
 
     def mean_ms(self) -> float:
-        return statistics.fmean(s.elapsed_time(e) for s, e in self.pairs)
+        ms = [s.elapsed_time(e) for s, e in self.pairs]
+        if not ms or min(ms) <= 0.0:
+            raise RuntimeError(f"no usable event timings for {self.name}")
+        return statistics.fmean(ms)
 
 
 def logits_bytes(BH: int, G: int, n: int, D: int = 128) -> int:
@@ -87,27 +95,32 @@ def cpu_baseline(model, runs: int) -> dict:
     import torch
     import oracle
 
-    cache = model.cache
     threads = max(1, min(os.cpu_count() or 1, 16))
     torch.set_num_threads(threads)
-    B, H, D = cache.batch_size, cache.num_key_value_heads, cache.head_dim
-    Hq = cache.num_attention_heads
-    st = oracle.LayerState(
-        U=cache.U[0].cpu(), SV=cache.SV[0].cpu(), landmarks=cache.k_landmark[0].cpu(),
-        landmark_idx=cache.k_landmark_idx[0].cpu(), host_v=cache.v_cache_cpu[0], kbuf=cache.k_cache_buffer[0].cpu(),
-        vbuf=cache.v_cache_buffer[0].cpu(), position_ids=cache.position_ids[0].cpu(),
-        prefill_local=cache.prefill_local, sparse_start=cache.sparse_start, sparse_end=cache.sparse_end,
-        chunk=cache.chunk_size, budget=cache.sparse_budget, ctx=cache.prefill, buf_len=cache.buf_len)
+    states = []
+    for lane in model.lanes:  # layer-0 state of every batch slice: the whole batch
+        c = lane.cache
+        states.append(oracle.LayerState(
+            U=c.U[0].cpu(), SV=c.SV[0].cpu(), landmarks=c.k_landmark[0].cpu(), landmark_idx=c.k_landmark_idx[0].cpu(),
+            host_v=c.v_cache_cpu[0], kbuf=c.k_cache_buffer[0].cpu(), vbuf=c.v_cache_buffer[0].cpu(),
+            position_ids=c.position_ids[0].cpu(), prefill_local=c.prefill_local, sparse_start=c.sparse_start,
+            sparse_end=c.sparse_end, chunk=c.chunk_size, budget=c.sparse_budget, ctx=c.prefill, buf_len=c.buf_len))
+    cache = model.cache
+    B = model.batch
+    H, D, Hq = cache.num_key_value_heads, cache.head_dim, cache.num_attention_heads
     cos_sin = model.cos_sin.cpu()
     g = torch.Generator().manual_seed(5)
     times = []
     for i in range(3 + runs):
-        q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
-        k = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
-        v = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
-        t0 = time.perf_counter()
-        oracle.decode_layer_step(st, q, k, v, cos_sin, gen_offset=0)
-        dt = time.perf_counter() - t0
+        dt = 0.0
+        for st, lane in zip(states, model.lanes):
+            b = lane.cache.batch_size
+            q = torch.randn(b, Hq, D, generator=g).to(torch.bfloat16)
+            k = torch.randn(b, H, D, generator=g).to(torch.bfloat16)
+            v = torch.randn(b, H, D, generator=g).to(torch.bfloat16)
+            t0 = time.perf_counter()
+            oracle.decode_layer_step(st, q, k, v, cos_sin, gen_offset=0)
+            dt += time.perf_counter() - t0
         if i >= 3:
             times.append(dt)
     layer_s = statistics.median(times)
@@ -129,12 +142,12 @@ def breakdown(model, tok) -> dict:
              "gather_copy_d2d_with_offsets", "rebuild_k_rope", "sparse_attn_decode"]
     timers = {n: KernelTimer(shadowkv, n) for n in names}
     cache = model.cache
-    snaps = []  # per-layer copies of the hit counts, taken on the device (no host sync in the step)
+    snaps = []  # (selected chunks, device copy of the hit counts) per call; no host sync in the step
     orig_select = timers["select_chunks"].orig
 
     def select_and_snapshot(*a, **kw):
         out = orig_select(*a, **kw)
-        snaps.append(cache.cnts.clone())
+        snaps.append((a[3] * a[7], a[11].clone()))  # rows * select_sets, cnts
         return out
 
     timers["select_chunks"].orig = select_and_snapshot
@@ -150,8 +163,8 @@ def breakdown(model, tok) -> dict:
     ops = {n: round(t.mean_ms() * 1e3, 2) for n, t in timers.items() if t.pairs}
     chunk_bytes = cache.chunk_size * cache.head_dim * 2
     fetch_ms = timers["gather_copy_with_offsets"].mean_ms()
-    total_sel = cache.select_sets * cache.batch_size * cache.num_key_value_heads
-    miss_mean = statistics.fmean(total_sel - int(c.sum()) for c in snaps)
+    total_sel = statistics.fmean(t for t, _ in snaps)
+    miss_mean = statistics.fmean(t - int(c.sum()) for t, c in snaps)
     return {"op_us_per_layer": ops, "hit_rate": round(1 - miss_mean / total_sel, 4),
             "host_link": {"bytes_per_layer": int(miss_mean * chunk_bytes),
                           "GBps": round(miss_mean * chunk_bytes / (fetch_ms * 1e-3) / 1e9, 2),
@@ -174,8 +187,9 @@ def main() -> int:
         shape = replace(shape, layers=args.layers)
     t0 = time.time()
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
+    lanes = args.lanes if args.batch % args.lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget,
-                                          decode_len=args.warmup + args.steps + 8)
+                                          decode_len=args.warmup + args.steps + ROOFLINE_STEPS + 8, lanes=lanes)
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")
@@ -191,20 +205,41 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} steps done")
 
+    graph = not args.no_graph
+    if graph:
+        model.capture(tok)
+        torch.cuda.synchronize()
+        log("decode step captured in a HIP graph")
+
+        def step(_):
+            return model.replay()
+    else:
+        step = model.decode_step
+    # HIP events bracket every scoring launch on its stream. Inside a captured graph that takes
+    # event-record nodes, which torch refuses on ROCm, so with a graph the same kernel is timed over
+    # eager steps of the same decode right after the timed replays.
     timer = KernelTimer(shadowkv, "score_logits")
-    timer.active = True
+    timer.active = not graph
     torch.cuda.synchronize()
     start = time.perf_counter()
     for i in range(args.steps):
-        tok = model.decode_step(tok)
+        tok = step(tok)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
+    log(f"timed {args.steps} {'graph replays' if graph else 'eager steps'} in {elapsed:.3f}s")
+    if graph:
+        timer.active = True
+        for i in range(ROOFLINE_STEPS):
+            tok = model.decode_step(tok)
+        torch.cuda.synchronize()
+        timing = f"HIP events around every scoring launch of {ROOFLINE_STEPS} eager steps after the timed replays"
+    else:
+        timing = "HIP events around every scoring launch of the timed steps"
     timer.active = False
     setattr(shadowkv, "score_logits", timer.orig)
-    log(f"timed {args.steps} steps in {elapsed:.3f}s")
 
     n = cache.k_landmark.shape[-2]
-    BH = args.batch * shape.kv_heads
+    BH = cache.batch_size * shape.kv_heads  # one launch covers one lane's batch slice
     G = shape.heads // shape.kv_heads
     lb = logits_bytes(BH, G, n)
     k_ms = timer.mean_ms()
@@ -237,11 +272,14 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: random-init weights, seeded random ShadowKV state of the exact shapes, greedy tokens",
         "config": {"workload": f"{shape.name}-shape {shape.layers}-layer decode, batch {args.batch}, ctx {args.ctx}, "
-                               f"ShadowKV rank 160 chunk 8 budget {args.budget}, V in pinned host memory",
+                               f"ShadowKV rank 160 chunk 8 budget {args.budget}, V in pinned host memory, "
+                               f"{lanes} interleaved batch lane(s), "
+                               f"{'HIP-graph-captured step' if graph else 'eager step'}",
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": lb, "avg_launch_us": round(k_ms * 1e3, 2)},
+                     "traffic": traffic, "algorithmic_bytes_per_launch": lb, "avg_launch_us": round(k_ms * 1e3, 2),
+                     "timing": timing},
         "cpu_baseline": cpu,
     }
     if detail is not None:

@@ -195,13 +195,17 @@ int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, in
  *   out[b, hq] = softmax(scale * q[b,hq] . K[b,h,:kv_len]^T) . V[b,h,:kv_len]   (fp32 math, bf16 out)
  * q row: q + b*q_stride_b + hq*q_stride_h; K/V row s of (b,h): base + b*kv_stride_b + h*kv_stride_h
  * + s*kv_stride_s; out row: out + b*o_stride_b + hq*o_stride_h. head_dim must be 128.
- * workspace: caller-provided device scratch of skv_sparse_attn_workspace_bytes(...) bytes. */
+ * workspace: caller-provided device scratch of skv_sparse_attn_workspace_bytes(...) bytes.
+ * kv_len_dev (optional, no reference counterpart): device int32 holding the live length, read
+ * when the kernel runs and clamped to [1, kv_len]; kv_len is then the maximum. This keeps the
+ * call valid inside a captured HIP graph while the cache grows by one row per replay. */
 int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, int kv_len);
 int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
                            const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
                            int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
-                           int kv_len, float scale, void* workspace, int64_t workspace_bytes, uint16_t* out,
-                           int64_t o_stride_b, int64_t o_stride_h, void* stream);
+                           int kv_len, const int32_t* kv_len_dev, float scale, void* workspace,
+                           int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+                           void* stream);
 
 #ifdef __cplusplus
 }

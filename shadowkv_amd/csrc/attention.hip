@@ -33,13 +33,18 @@ struct AttnArgs {
   const uint16_t* k;
   const uint16_t* v;
   int64_t kv_sb, kv_sh, kv_ss;
-  int Hkv, G, L, splits;
+  int Hkv, G, L, splits;  // L: maximum length (grid sizing)
+  const int32_t* L_dev;   // optional device-resident length, clamped to [1, L]
   float scale;
   float* ws_o;   // [B*Hq][splits][128]
   float* ws_ml;  // [B*Hq][splits][2]
   uint16_t* out;
   int64_t o_sb, o_sh;
 };
+
+__device__ __forceinline__ int live_length(const AttnArgs& a) {
+  return a.L_dev ? min(max(*a.L_dev, 1), a.L) : a.L;
+}
 
 template <int GP>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
@@ -51,8 +56,10 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   const int bh = blockIdx.y;
   const int b = bh / a.Hkv;
   const int h = bh - b * a.Hkv;
+  const int L = live_length(a);
   const int s0 = split * kSplit;
-  const int s1 = min(s0 + kSplit, a.L);
+  if (s0 >= L) return;  // workgroup-uniform: splits past the live length do nothing
+  const int s1 = min(s0 + kSplit, L);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15;
@@ -202,10 +209,11 @@ __global__ void __launch_bounds__(kHeadDim) attn_combine_kernel(AttnArgs a) {
   const int d = threadIdx.x;
   const float* ml = a.ws_ml + static_cast<int64_t>(row) * a.splits * 2;
   const float* o = a.ws_o + static_cast<int64_t>(row) * a.splits * kHeadDim;
+  const int used = (live_length(a) + kSplit - 1) / kSplit;
   float M = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, ml[2 * s]);
+  for (int s = 0; s < used; ++s) M = fmaxf(M, ml[2 * s]);
   float l = 0.f, acc = 0.f;
-  for (int s = 0; s < a.splits; ++s) {
+  for (int s = 0; s < used; ++s) {
     const float w = expf(ml[2 * s] - M);
     l += ml[2 * s + 1] * w;
     acc += o[static_cast<int64_t>(s) * kHeadDim + d] * w;
@@ -225,7 +233,8 @@ extern "C" int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, 
 extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
                                       const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
                                       int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
-                                      int kv_len, float scale, void* workspace, int64_t workspace_bytes, uint16_t* out,
+                                      int kv_len, const int32_t* kv_len_dev, float scale, void* workspace,
+                                      int64_t workspace_bytes, uint16_t* out,
                                       int64_t o_stride_b, int64_t o_stride_h, void* stream) {
   const char* what = "sparse_attn_decode";
   if (!q || !k_cache || !v_cache || !workspace || !out) {
@@ -265,6 +274,7 @@ extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int
   a.Hkv = kv_heads;
   a.G = G;
   a.L = kv_len;
+  a.L_dev = kv_len_dev;
   a.splits = splits_for(kv_len);
   a.scale = scale;
   a.ws_o = static_cast<float*>(workspace);

@@ -5,9 +5,9 @@
 // stream-ordered kernels, so no workgroup ever waits on another:
 //   compact_hits_kernel  — one workgroup per row performs the in-place forward compaction
 //                          slot[i] <- slot[offsets[i]] for i < cnt (offsets ascending, offsets[i] >= i);
-//   gather_chunks_kernel — many workgroups per row fetch the miss chunks i >= cnt straight from
-//                          the pinned host store (zero-copy 16-byte loads over the host link),
-//                          each workgroup keeping 8 loads per lane in flight.
+//   gather_chunks_kernel — a bounded grid of workgroups fetches the miss chunks i >= cnt straight
+//                          from the pinned host store (zero-copy 16-byte non-temporal loads over
+//                          the host link), each workgroup keeping 8 loads per lane in flight.
 // The copy unit is a chunk of chunk_elems bf16 values, moved as 16-byte vectors.
 #include <algorithm>
 #include <cstdlib>
@@ -22,10 +22,11 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 8;             // 16-byte vectors in flight per lane
 constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch tile
 // Upper bound on fetch workgroups (environment SKV_FETCH_WGS overrides it, read once). The
-// fetch is host-link bound: a few dozen workgroups keep more than the link's bandwidth-delay
-// product in flight, and a bounded grid leaves CUs free for the key rebuild that runs
-// concurrently on the other stream.
-constexpr int kDefaultFetchWGs = 256;
+// fetch is host-link bound: 32 workgroups of non-temporal loads (1 MiB in flight) already hold
+// the link at its ~55 GB/s ceiling on MI355X, and every further host read in flight slows the
+// HBM traffic of kernels running concurrently (measured: a 4096x28672 GEMM 1.9x slower beside
+// 32 workgroups, 2.7x beside 256; landmark scoring 1.1x vs 3.1x).
+constexpr int kDefaultFetchWGs = 32;
 
 int fetch_workgroups() {
   static const int wgs = [] {
@@ -101,7 +102,7 @@ __device__ __forceinline__ void gather_tile(const u32x4* __restrict__ src, int64
         int i = i0 + static_cast<int>(v / chunk_vec);
         int e = static_cast<int>(v % chunk_vec);
         int64_t c = static_cast<int64_t>(id[i]);
-        if (c >= 0 && c < src_chunks) r[u] = s[c * chunk_vec + e];
+        if (c >= 0 && c < src_chunks) r[u] = skv::load_nt(s + c * chunk_vec + e);
       }
     }
 #pragma unroll

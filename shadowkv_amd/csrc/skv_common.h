@@ -106,6 +106,15 @@ struct alignas(16) u32x4 {
   uint32_t x, y, z, w;
 };
 
+// 16-byte load with the non-temporal (streaming) hint: global_load_dwordx4 ... nt. Used for reads
+// of pinned host memory over the host link, which are read once; it keeps those long-latency
+// requests from holding cache resources that concurrent kernels' HBM traffic needs.
+__device__ __forceinline__ u32x4 load_nt(const u32x4* p) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return u32x4{v.x, v.y, v.z, v.w};
+}
+
 }  // namespace skv
 
 // Host-side error reporting shared by every entry point (defined in skv_api.cpp).

@@ -120,15 +120,31 @@ def _fill_selected_values(cache: ShadowKVCache_CPU, layer: int, values: torch.Te
                                       cache.kernel_stride, S)
 
 
+class _Lane:
+    """One slice of the batch with its own ShadowKV cache (and value-fetch stream) and attention handler."""
+
+    def __init__(self, rows: slice, cache: ShadowKVCache_CPU):
+        self.rows, self.cache = rows, cache
+        self.attn = None
+
+
 class SyntheticDecoder:
-    """Random-init decoder-only model (Llama layout) decoding with the ShadowKV offload cache."""
+    """Random-init decoder-only model (Llama layout) decoding with the ShadowKV offload cache.
+
+    With lanes > 1 the batch is split into that many independent slices, each with its own
+    cache and value-fetch stream, and the layers are software-pipelined on the one compute
+    stream: while lane 0's value chunks for layer i stream in over the host link, the compute
+    stream finishes lane 1's layer i-1 and starts lane 1's layer i (and so on round the lanes).
+    """
 
     def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
-                 dtype=torch.bfloat16):
+                 dtype=torch.bfloat16, lanes: int = 1):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
         s = shape
         D = s.head_dim
+        if lanes < 1 or batch % lanes:
+            raise ValueError(f"batch {batch} is not divisible into {lanes} lanes")
         g = torch.Generator(device=device).manual_seed(seed)
 
         def w(*size, scale=0.02):
@@ -147,43 +163,133 @@ class SyntheticDecoder:
         self.cos_sin = build_cos_sin_cache(ctx + decode_len, s.rope_theta, D, device=device)
         cfg = types.SimpleNamespace(num_attention_heads=s.heads, num_key_value_heads=s.kv_heads,
                                     hidden_size=s.heads * D, num_hidden_layers=s.layers)
-        self.cache = ShadowKVCache_CPU(cfg, batch_size=batch, max_length=ctx, device=device,
-                                       sparse_budget=sparse_budget, chunk_size=chunk_size, rank=rank,
-                                       max_decode_len=decode_len, zero_host_store=False)
-        synthesize_state(self.cache, ctx, seed=seed + 1, cos_sin=self.cos_sin)
-        self.attn = ShadowAttention(self.cache, s.heads // s.kv_heads, D, s.hidden, self._rope, None, self.cos_sin)
-        self.q_rot = torch.empty(batch, s.heads * D, dtype=dtype, device=device)
-        self.k_rot = torch.empty(batch, s.kv_heads * D, dtype=dtype, device=device)
+        lb = batch // lanes
+        self.lanes = []
+        for i in range(lanes):
+            cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
+                                      chunk_size=chunk_size, rank=rank, max_decode_len=decode_len,
+                                      zero_host_store=False)
+            synthesize_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin)
+            lane = _Lane(slice(i * lb, (i + 1) * lb), cache)
+            lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
+                                        self.cos_sin)
+            cache.use_device_lengths()
+            self.lanes.append(lane)
+        self.cache = self.lanes[0].cache  # lane 0's cache (shapes are identical across lanes)
+        # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
+        self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
+        self.graph = None
+        self.static_tokens = None
 
-    def _rope(self, q: torch.Tensor, k: torch.Tensor, position_ids: torch.Tensor):
-        """RoPE of the new token's q [B, 1, Hq*D] and k [B, 1, Hkv*D] at position_ids [B] (HIP kernel)."""
-        s, B, D = self.shape, self.batch, self.shape.head_dim
-        for x, out, h in ((q, self.q_rot, s.heads), (k, self.k_rot, s.kv_heads)):
-            xv = x.view(B, h, 1, D)
-            shadowkv.apply_rotary_pos_emb_new(xv, self.cos_sin, position_ids, out.view(B, h, 1, D), B, h, 1, D,
-                                              xv.stride(0), xv.stride(1), xv.stride(2), xv.stride(3),
-                                              self.cos_sin.stride(0), position_ids.stride(0), 0, 0, D // 2)
-        return (self.q_rot.view(B, 1, s.heads, D).transpose(1, 2), self.k_rot.view(B, 1, s.kv_heads, D).transpose(1, 2))
+    def _rope_for(self, lane: _Lane):
+        s, D = self.shape, self.shape.head_dim
+
+        def rope(q: torch.Tensor, k: torch.Tensor, position_ids: torch.Tensor):
+            """RoPE of the new token's q [b, 1, Hq*D] and k [b, 1, Hkv*D] (views into the fused QKV
+            output) at position_ids [b], in place like the reference's rotary_embedding
+            (models/llama.py:149-154); each rotation pair is read and written by one thread."""
+            b = q.shape[0]
+            views = []
+            for x, h in ((q, s.heads), (k, s.kv_heads)):
+                xv = x.view(b, h, 1, D)
+                shadowkv.apply_rotary_pos_emb_new(xv, self.cos_sin, position_ids, xv, b, h, 1, D, xv.stride(0),
+                                                  xv.stride(1), xv.stride(2), xv.stride(3), self.cos_sin.stride(0),
+                                                  position_ids.stride(0), 0, 0, D // 2)
+                views.append(x.view(b, 1, h, D).transpose(1, 2))
+            return views[0], views[1]
+        return rope
 
     def _norm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         return F.rms_norm(x, (x.shape[-1],), w, self.shape.eps)
 
+    def _layer_begin(self, idx: int, h: torch.Tensor, lane: _Lane):
+        """Norm, fused QKV and the first half of the attention handler (value fetch in flight)."""
+        s, D = self.shape, self.shape.head_dim
+        b = h.shape[0]
+        lw = self.layers[idx]
+        x = self._norm(h, lw.in_norm)
+        qkv = F.linear(x, lw.wqkv)
+        q, k, v = qkv.split([s.heads * D, s.kv_heads * D, s.kv_heads * D], dim=-1)
+        v = v.view(b, 1, s.kv_heads, D).transpose(1, 2)
+        return lane.attn.decode_begin(q, k, v, self.pos[lane.rows], idx)
+
+    def _layer_end(self, idx: int, h: torch.Tensor, lane: _Lane, pending) -> torch.Tensor:
+        """Attention over the assembled buffers, o_proj + residual, norm, SwiGLU MLP + residual."""
+        s = self.shape
+        b = h.shape[0]
+        lw = self.layers[idx]
+        a = lane.attn.decode_end(pending)
+        h = h + F.linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
+        x = self._norm(h, lw.post_norm)
+        gate, up = F.linear(x, lw.gate_up).chunk(2, dim=-1)
+        return h + F.linear(F.silu(gate) * up, lw.down)
+
+    @staticmethod
+    def _greedy(logits: torch.Tensor) -> torch.Tensor:
+        """argmax over the vocabulary as two short reductions (blocks of 256, then the block maxima),
+        so no reduction spans several workgroups; first maximal index wins, as in torch.argmax."""
+        B, V = logits.shape
+        blk = 256
+        pad = -V % blk
+        if pad:
+            logits = F.pad(logits, (0, pad), value=float("-inf"))
+        vals, idx = logits.view(B, -1, blk).max(dim=-1)  # [B, V/256]
+        best = vals.argmax(dim=-1, keepdim=True)  # [B, 1]
+        return best * blk + idx.gather(1, best)
+
+    def _head(self, h: torch.Tensor, lane: _Lane) -> torch.Tensor:
+        """Final norm, lm_head, greedy token; advances the lane's RoPE positions."""
+        h = self._norm(h, self.norm_w)
+        logits = F.linear(h[:, -1], self.lm_head).float()  # [b, vocab]
+        self.pos[lane.rows].add_(1)
+        return self._greedy(logits)  # [b, 1]
+
     @torch.inference_mode()
     def decode_step(self, tokens: torch.Tensor) -> torch.Tensor:
-        """One greedy decode step for the whole batch: tokens [B, 1] -> next tokens [B, 1]."""
-        s, B, D = self.shape, self.batch, self.shape.head_dim
-        pos = torch.full((B,), self.ctx + self.cache.gen_offset, dtype=torch.int64, device=self.device)
-        h = F.embedding(tokens, self.embed)
-        for idx, lw in enumerate(self.layers):
-            x = self._norm(h, lw.in_norm)
-            qkv = F.linear(x, lw.wqkv)
-            q, k, v = qkv.split([s.heads * D, s.kv_heads * D, s.kv_heads * D], dim=-1)
-            v = v.view(B, 1, s.kv_heads, D).transpose(1, 2)
-            a = self.attn.decode(q, k, v, pos, idx)
-            h = h + F.linear(a.reshape(B, 1, s.heads * D), lw.wo)
-            x = self._norm(h, lw.post_norm)
-            gate, up = F.linear(x, lw.gate_up).chunk(2, dim=-1)
-            h = h + F.linear(F.silu(gate) * up, lw.down)
-        h = self._norm(h, self.norm_w)
-        logits = F.linear(h[:, -1], self.lm_head).float()  # [B, vocab]
-        return logits.argmax(dim=-1, keepdim=True)  # [B, 1]
+        """One greedy decode step for the whole batch: tokens [B, 1] -> next tokens [B, 1].
+
+        Every step-dependent integer (RoPE position, cache append row, attention length) lives
+        on the device and is advanced by the step itself, so the step can be captured. Issue
+        order for two lanes: begin0(0) begin1(0) end0(0) begin0(1) end1(0) begin1(1) ...; each
+        lane's value fetch overlaps the other lanes' work between its begin and its end."""
+        lanes = self.lanes
+        hs = [F.embedding(tokens[lane.rows], self.embed) for lane in lanes]
+        pending = [None] * len(lanes)
+        for idx in range(self.shape.layers):
+            for i, lane in enumerate(lanes):
+                if pending[i] is not None:
+                    hs[i] = self._layer_end(idx - 1, hs[i], lane, pending[i])
+                pending[i] = self._layer_begin(idx, hs[i], lane)
+        last = self.shape.layers - 1
+        outs = [self._head(self._layer_end(last, hs[i], lane, pending[i]), lane) for i, lane in enumerate(lanes)]
+        return torch.cat(outs) if len(outs) > 1 else outs[0]
+
+    def _caches(self):
+        return [lane.cache for lane in self.lanes]
+
+    def capture(self, tokens: torch.Tensor) -> None:
+        """Capture one decode step, reading and then overwriting a static token buffer, in a HIP
+        graph. The graph's only side streams are the lanes' value-fetch streams, each forked from
+        the capture stream and joined back to it before that lane's next fork. Nothing runs
+        during capture; host counters touched by the traced Python are restored."""
+        self.static_tokens = tokens.clone()
+        saved = [(c.gen_offset, c.kv_offset) for c in self._caches()]
+        for c in self._caches():
+            c.check_capacity(1)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.static_tokens.copy_(self.decode_step(self.static_tokens))
+        for c, (gen, kv) in zip(self._caches(), saved):
+            c.gen_offset, c.kv_offset = gen, kv
+        self.graph = g
+
+    def replay(self) -> torch.Tensor:
+        """One captured decode step; returns the static token buffer (next tokens [B, 1])."""
+        if self.graph is None:
+            raise RuntimeError("capture() a decode step first")
+        for c in self._caches():
+            c.check_capacity(1)
+        self.graph.replay()
+        for c in self._caches():
+            c.advance(1)
+        return self.static_tokens

@@ -69,6 +69,20 @@ def device_address(t: torch.Tensor) -> int:
     return dev + (t.data_ptr() - base)
 
 
+def max_offset(sizes, strides) -> int:
+    """Largest element offset addressed by an index space of `sizes` with `strides` (>= 0)."""
+    if any(sz <= 0 for sz in sizes):
+        return -1
+    if any(st < 0 for st in strides):
+        raise ValueError("negative strides are not supported")
+    return sum((sz - 1) * st for sz, st in zip(sizes, strides))
+
+
+def _need_offsets(t: torch.Tensor, sizes, strides, name: str) -> None:
+    """Every offset of the index space must fall inside t's storage (from t.data_ptr())."""
+    _need(t, max_offset(sizes, strides) + 1, name)
+
+
 def _check_map(map_size: int) -> None:
     if not 1 <= map_size <= 2048:
         raise ValueError(f"map_size (select_sets) must be in [1, 2048], got {map_size}")
@@ -174,6 +188,12 @@ def apply_rotary_pos_emb_new(x, cos_sin, position_ids, output, batch_size, heads
     _dev(cos_sin, "cos_sin", torch.bfloat16)
     _dev(position_ids, "position_ids", torch.int64)
     _dev(output, "output", torch.bfloat16)
+    # x and output are both addressed with x's strides (reference rope_new.cu:45-47)
+    xs = (batch_size, heads, seq_len, embed_dim)
+    xst = (stride_xb, stride_xh, stride_xs, stride_xe)
+    _need_offsets(x, xs, xst, "x")
+    _need_offsets(output, xs, xst, "output")
+    _need_offsets(position_ids, (batch_size, heads, seq_len), (stride_pid_b, stride_pid_h, stride_pid_s), "position_ids")
     _lib.call("skv_apply_rotary_pos_emb_new", x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(),
               output.data_ptr(), batch_size, heads, seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe,
               stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, cos_sin.shape[0], _stream())
@@ -185,6 +205,12 @@ def _push(name, x, cos_sin, position_ids, output, cnts, *ints):
     _dev(position_ids, "position_ids", torch.int32)
     _dev(output, "output", torch.bfloat16)
     _dev(cnts, "cnts", torch.int32)
+    (b, h, s, d, sxb, sxh, sxs, sxe, _scs, spb, sph, sps, sob, soh, sos, start, end, _half, chunk) = ints
+    _need_offsets(x, (b, h, s, d), (sxb, sxh, sxs, sxe), "x")
+    _need_offsets(position_ids, (b, h, (s + chunk - 1) // chunk), (spb, sph, sps), "position_ids")
+    rows = max(0, min(s, end - start))
+    _need(output, max_offset((b, h, rows, d), (sob, soh, sos, 1)) + 1 + start * sos, "output")
+    _need(cnts, b * h, "cnts")
     _lib.call(name, x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(), output.data_ptr(), cnts.data_ptr(),
               *ints, cos_sin.shape[0], _stream())
 
@@ -418,11 +444,13 @@ def sparse_attn_workspace_bytes(batch_size: int, q_heads: int, kv_len: int) -> i
     return int(_lib.lib().skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len))
 
 
-def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None):
-    """out[b, hq] = softmax(scale q[b,hq] K[b,h,:kv_len]^T) V[b,h,:kv_len], h = hq // (Hq/Hkv).
+def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, kv_len_dev=None):
+    """out[b, hq] = softmax(scale q[b,hq] K[b,h,:L]^T) V[b,h,:L], h = hq // (Hq/Hkv).
 
     q: [B, Hq, 128] view; k_cache/v_cache: [B, Hkv, >=kv_len, 128] views; out: [B, Hq, 128];
     workspace: uint8 device tensor of sparse_attn_workspace_bytes(B, Hq, kv_len) bytes.
+    L = kv_len, or, with kv_len_dev (device int32 [1]), the value it holds when the kernel runs,
+    clamped to [1, kv_len].
     """
     _dev(q, "q", torch.bfloat16)
     _dev(k_cache, "k_cache", torch.bfloat16)
@@ -437,7 +465,13 @@ def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None):
     if q.stride(2) != 1 or k_cache.stride(3) != 1 or out.stride(2) != 1:
         raise ValueError("the head dimension must be contiguous")
     scale = 1.0 / math.sqrt(D) if scale is None else scale
+    ldev = None
+    if kv_len_dev is not None:
+        _dev(kv_len_dev, "kv_len_dev", torch.int32)
+        ldev = kv_len_dev.data_ptr()
+    _need_offsets(q, (B, Hq, D), q.stride(), "q")
+    _need_offsets(out, (B, Hq, D), out.stride(), "out")
     _lib.call("skv_sparse_attn_decode", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-              k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1], D, kv_len,
+              k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1], D, kv_len, ldev,
               float(scale), workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
               out.stride(0), out.stride(1), _stream())

@@ -42,6 +42,12 @@ class ShadowAttention(AttentionBase):
         return causal_attention_fp32(query_states, key_states, value_states)
 
     def decode(self, query_states, key_states, value_states, position_ids, layer_idx):
+        return self.decode_end(self.decode_begin(query_states, key_states, value_states, position_ids, layer_idx))
+
+    def decode_begin(self, query_states, key_states, value_states, position_ids, layer_idx):
+        """First half of decode(): RoPE, append, chunk selection, the value fetch launched on the
+        cache's copy stream and the key rebuild on the current stream. Returns what decode_end()
+        needs; work issued on the current stream in between overlaps the value fetch."""
         kv_cache = self.kv_cache
         query_states, key_states = self.apply_rotary_pos_emb(query_states, key_states, position_ids)
         kv_cache.update_kv_cache(key_states, value_states, layer_idx)
@@ -55,8 +61,14 @@ class ShadowAttention(AttentionBase):
         key_states = kv_cache.get_key_cache(layer_idx=layer_idx, position_ids=position_ids,
                                             rope_func=self.apply_rotary_pos_emb_single,
                                             cos_sin_cache=self.cos_sin_cache)
-        curr_stream.wait_stream(copy_stream)
+        return query_states, key_states, value_states
 
+    def decode_end(self, pending):
+        """Second half of decode(), on the stream decode_begin() ran on: wait for the value fetch,
+        then sparse attention of the new token over the assembled buffers -> [B, 1, Hq, D]."""
+        query_states, key_states, value_states = pending
+        kv_cache = self.kv_cache
+        torch.cuda.current_stream().wait_stream(kv_cache.copy_stream)
         if kv_cache.attn_workspace is None:
             kv_cache._alloc_attention()
         B, Hq = query_states.shape[0], query_states.shape[1]
@@ -64,5 +76,6 @@ class ShadowAttention(AttentionBase):
         if q is None:
             raise ValueError("decode attention takes one query token per step")
         out = torch.empty(B, Hq, query_states.shape[-1], dtype=query_states.dtype, device=query_states.device)
-        shadowkv.sparse_attn_decode(q, key_states, value_states, key_states.shape[2], out, kv_cache.attn_workspace)
+        shadowkv.sparse_attn_decode(q, key_states, value_states, key_states.shape[2], out, kv_cache.attn_workspace,
+                                    kv_len_dev=kv_cache.kv_len_dev)
         return out.view(B, 1, Hq, -1)

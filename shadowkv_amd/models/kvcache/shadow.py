@@ -108,6 +108,9 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.copy_stream = torch.cuda.Stream(device=device)
         self.attn_workspace = None
         self.attn_out = None
+        # Device-resident append row / attention length (use_device_lengths); None = host integers.
+        self.append_row_dev = None
+        self.kv_len_dev = None
 
     def print_stats(self):
         print(f"ShadowKV_CPU | sparse budget {self.sparse_budget} | chunk size {self.chunk_size} |rank {self.rank} "
@@ -239,13 +242,18 @@ class ShadowKVCache_CPU(KVCacheBase):
     def _gen_len(self, layer_idx: int) -> int:
         return self.gen_offset if layer_idx == self.num_layers - 1 else self.gen_offset + self.incoming_q_len
 
+    def _live_view(self, buf: torch.Tensor, layer_idx: int) -> torch.Tensor:
+        if self.kv_len_dev is not None:
+            return buf[:, :, :self.buf_len]  # length read on the device (kv_len_dev)
+        return buf[:, :, :self.sparse_end + self._gen_len(layer_idx)]
+
     def get_value_cache(self, layer_idx: int, position_ids: torch.Tensor) -> torch.Tensor:
         shadowkv.gather_copy_with_offsets(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.temp,
                                           self.offsets, self.cnts, self.signals, self.batch_size,
                                           self.num_key_value_heads, int(self.max_ctx_chunks_len * self.head_dim),
                                           int(self.sparse_budget * self.head_dim), self.kernel_offset,
                                           self.kernel_stride, self.select_sets)
-        return self.v_cache_buffer[layer_idx][:, :, :self.sparse_end + self._gen_len(layer_idx)]
+        return self._live_view(self.v_cache_buffer[layer_idx], layer_idx)
 
     def get_key_cache(self, layer_idx: int, position_ids: torch.Tensor, rope_func, cos_sin_cache) -> torch.Tensor:
         shadowkv.gather_copy_d2d_with_offsets(self.k_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
@@ -254,7 +262,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         batch_gather_gemm_rotary_pos_emb_cuda(self.U[layer_idx], self.SV[layer_idx], cos_sin_cache, position_ids,
                                               self.output, self.chunk_size, self.k_cache_buffer[layer_idx],
                                               self.sparse_start, self.sparse_end, self.cnts)
-        return self.k_cache_buffer[layer_idx][:, :, :self.sparse_end + self._gen_len(layer_idx)]
+        return self._live_view(self.k_cache_buffer[layer_idx], layer_idx)
 
     def H2D(self):
         gc.collect()
@@ -276,17 +284,41 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.attn_workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         self.attn_out = torch.empty(B, Hq, self.head_dim, dtype=self.dtype, device=self.device)
 
-    def update_kv_cache(self, new_k_cache: torch.Tensor, new_v_cache: torch.Tensor, layer_idx: int):
-        incoming = new_k_cache.shape[-2]
-        start = self.sparse_end + self.gen_offset
-        if start + incoming > self.buf_len:
+    def check_capacity(self, incoming: int = 1):
+        if self.sparse_end + self.gen_offset + incoming > self.buf_len:
             raise RuntimeError(f"decode capacity exhausted: {self.gen_offset} tokens generated, buffer holds "
                                f"{self.buf_len - self.sparse_end}; construct the cache with a larger max_decode_len")
-        self.v_cache_buffer[layer_idx][:, :, start:start + incoming].copy_(new_v_cache, non_blocking=True)
-        self.k_cache_buffer[layer_idx][:, :, start:start + incoming].copy_(new_k_cache, non_blocking=True)
+
+    def advance(self, incoming: int = 1):
+        """Host bookkeeping of one decode step (the device scalars advance inside the step)."""
+        self.kv_offset += incoming
+        self.gen_offset += incoming
+
+    def use_device_lengths(self):
+        """Keep the append row and the attention length in device scalars that the decode step
+        advances itself (at layer 0), so a whole step can be captured in a HIP graph and replayed.
+        The host counters stay authoritative for the capacity check."""
+        row = self.sparse_end + self.gen_offset - 1  # advanced before the step's first append
+        self.append_row_dev = torch.full((1,), row, dtype=torch.int64, device=self.device)
+        self.kv_len_dev = torch.full((1,), row + 1, dtype=torch.int32, device=self.device)
+
+    def update_kv_cache(self, new_k_cache: torch.Tensor, new_v_cache: torch.Tensor, layer_idx: int):
+        incoming = new_k_cache.shape[-2]
+        self.check_capacity(incoming)
+        if self.append_row_dev is not None:
+            if incoming != 1:
+                raise ValueError("device-resident lengths advance one token per decode step")
+            if layer_idx == 0:
+                self.append_row_dev.add_(1)
+                self.kv_len_dev.add_(1)
+            self.v_cache_buffer[layer_idx].index_copy_(2, self.append_row_dev, new_v_cache)
+            self.k_cache_buffer[layer_idx].index_copy_(2, self.append_row_dev, new_k_cache)
+        else:
+            start = self.sparse_end + self.gen_offset
+            self.v_cache_buffer[layer_idx][:, :, start:start + incoming].copy_(new_v_cache, non_blocking=True)
+            self.k_cache_buffer[layer_idx][:, :, start:start + incoming].copy_(new_k_cache, non_blocking=True)
         if layer_idx == self.num_layers - 1:
-            self.kv_offset += incoming
-            self.gen_offset += incoming
+            self.advance(incoming)
 
     def clear(self):
         self.k_cache_buffer.zero_()
@@ -301,6 +333,8 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.gen_offset = 0
         self.prefill_local = 0
         self.prefilled_batch = 0
+        self.append_row_dev = None
+        self.kv_len_dev = None
 
     def get_kv_len(self):
         return self.kv_offset

@@ -32,13 +32,16 @@ def test_single_layer_decode_step(gpu):
     torch.testing.assert_close(got["out"].float(), res["out"].float(), rtol=2e-2, atol=2e-2)
 
 
-def test_multi_layer_multi_step_decode(gpu):
-    print("decode small fixture, 2 layers x 4 steps", flush=True)
+@pytest.mark.parametrize("device_lengths", [False, True])
+def test_multi_layer_multi_step_decode(gpu, device_lengths):
+    print(f"decode small fixture, 2 layers x 4 steps, device_lengths={device_lengths}", flush=True)
     case = make_golden.decode_small_case()
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
     steps, layers = 4, 2
     cache = build_cache(case, gpu, max_decode_len=steps, num_layers=layers)
+    if device_lengths:
+        cache.use_device_lengths()
     # oracle states: one per layer, fresh copies of the encoded state
     base = copy.deepcopy(case["state_in"])
     states = []
@@ -71,6 +74,9 @@ def test_multi_layer_multi_step_decode(gpu):
                                        states[layer].kbuf[:, :, :L].float(), rtol=2e-2, atol=2e-2)
             torch.testing.assert_close(out.view(B, H * G, D).cpu().float(), res["out"].float(), rtol=2e-2, atol=2e-2)
     assert cache.gen_offset == steps
+    if device_lengths:
+        assert int(cache.kv_len_dev) == cache.sparse_end + steps
+        assert int(cache.append_row_dev) == cache.sparse_end + steps - 1
 
 
 def test_decode_capacity_is_an_error(gpu):

@@ -199,3 +199,27 @@ def test_attention_identical_keys_is_mean_of_values(gpu):
     torch.cuda.synchronize()
     mean = V.float().mean(dim=2).repeat_interleave(Hq // Hk, dim=1)
     torch.testing.assert_close(out.cpu().float(), mean, rtol=1e-2, atol=1e-2)
+
+
+def test_attention_device_length_matches_host_length(gpu):
+    """kv_len_dev (a device int32 read when the kernel runs) gives the host-length result bit for bit,
+    including at split boundaries, and is clamped to [1, kv_len]."""
+    B, Hq, Hk, Lmax = 2, 32, 8, 1100
+    g = torch.Generator().manual_seed(3)
+    K = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
+    V = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16).to(gpu)
+    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, Lmax), dtype=torch.uint8, device=gpu)
+    ldev = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for L, eff in ((1, 1), (255, 255), (256, 256), (257, 257), (1024, 1024), (1100, 1100), (0, 1), (5000, 1100)):
+        _say(f"attention device length {L}")
+        ldev.fill_(L)
+        got = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
+        shadowkv.sparse_attn_decode(q, K, V, Lmax, got, ws, kv_len_dev=ldev)
+        want = torch.empty_like(got)
+        ws2 = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, eff), dtype=torch.uint8, device=gpu)
+        shadowkv.sparse_attn_decode(q, K, V, eff, want, ws2)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), want.cpu()), L
+        ref = oracle.sparse_attention(q.cpu(), K.cpu(), V.cpu(), eff)
+        torch.testing.assert_close(got.cpu().float(), ref.float(), rtol=RTOL, atol=ATOL)

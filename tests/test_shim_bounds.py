@@ -1,0 +1,25 @@
+"""Host-side extent checks of the shim (no GPU): every offset a kernel will address must lie in
+the tensors passed, so a stride mismatch raises instead of reaching the device."""
+import pytest
+import torch
+
+from shadowkv_amd.kernels import shadowkv
+
+
+def test_max_offset():
+    assert shadowkv.max_offset((2, 32, 1, 128), (6144, 128, 128, 1)) == 6144 + 31 * 128 + 127
+    assert shadowkv.max_offset((0, 4), (1, 1)) == -1
+    with pytest.raises(ValueError):
+        shadowkv.max_offset((2,), (-1,))
+
+
+def test_rope_output_with_smaller_extent_than_input_strides_is_rejected():
+    # q of a fused QKV row (stride 6144 per batch row) written into a compact [2, 4096] buffer:
+    # the kernel addresses the output with the input's strides, so the last row would run past it.
+    qkv = torch.empty(2, 1, 6144, dtype=torch.bfloat16, device="meta")
+    q = qkv[..., :4096].view(2, 32, 1, 128)
+    out = torch.empty(2, 4096, dtype=torch.bfloat16, device="meta").view(2, 32, 1, 128)
+    sizes, strides = (2, 32, 1, 128), q.stride()
+    need = shadowkv.max_offset(sizes, strides) + 1
+    assert need > out.numel()          # the shape that faulted
+    assert need <= qkv.numel()         # in place, inside the QKV buffer: fine
