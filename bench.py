@@ -9,8 +9,8 @@ greedy decode steps only. A step = one new token for all 8 sequences through all
 by default the step is captured once in a HIP graph and the timed steps are graph replays.
 
 Prints one JSON line. `roofline` is measured on the landmark-scoring kernel (the largest HBM
-stream of the path) with HIP events on its stream: during the timed steps when they run
-eagerly, else over eager steps of the same decode right after the timed replays;
+stream of the path) with HIP events on its stream around back-to-back launches over every
+layer's live landmarks, right after the timed steps;
 `host_link` reports the value fetch from pinned host memory measured in a separate
 instrumented step; `cpu_baseline` times the CPU oracle's restatement of one layer's
 hot-path ops at the same shapes on this host (a reported baseline only).
@@ -30,7 +30,6 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-ROOFLINE_STEPS = 4
 
 
 def log(msg: str) -> None:
@@ -88,6 +87,37 @@ def logits_bytes(BH: int, G: int, n: int, D: int = 128) -> int:
     per-256-column (max, sum) partials written."""
     tiles = (n + 255) // 256
     return BH * (n * D * 2 + G * D * 2 + G * n * 2 + G * tiles * 8)
+
+
+def scoring_launch_ms(model, rounds: int = 4):
+    """Average duration of the landmark-scoring kernel on the live decode state: HIP events on its
+    stream around back-to-back launches over every layer's landmarks (the queue stays full, so the
+    events bracket kernel time, not host launch latency). A captured step cannot carry event-record
+    nodes here (torch refuses them on ROCm), so this runs right after the timed replays."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    cache = model.cache
+    B, H, G, D = cache.batch_size, cache.num_key_value_heads, cache.num_key_value_groups, cache.head_dim
+    n = cache.k_landmark.shape[-2]
+    q = torch.randn(B, H * G, 1, D, device=cache.device).to(torch.bfloat16)
+    L = cache.num_layers
+
+    def launch_all():
+        for layer in range(L):
+            shadowkv.score_logits(q, cache.k_landmark[layer], cache.gemm_o, cache.norm, cache.sum, B * H, G, n, D,
+                                  1.0 / math.sqrt(128))
+
+    launch_all()  # warm
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(rounds):
+        launch_all()
+    e.record()
+    e.synchronize()
+    return (s.elapsed_time(e) / (rounds * L),
+            f"HIP events around {rounds * L} back-to-back launches on every layer's live landmarks, "
+            f"after the timed steps")
 
 
 def cpu_baseline(model, runs: int) -> dict:
@@ -189,7 +219,7 @@ def main() -> int:
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
     lanes = args.lanes if args.batch % args.lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget,
-                                          decode_len=args.warmup + args.steps + ROOFLINE_STEPS + 8, lanes=lanes)
+                                          decode_len=args.warmup + args.steps + 8, lanes=lanes)
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")
@@ -215,11 +245,6 @@ def main() -> int:
             return model.replay()
     else:
         step = model.decode_step
-    # HIP events bracket every scoring launch on its stream. Inside a captured graph that takes
-    # event-record nodes, which torch refuses on ROCm, so with a graph the same kernel is timed over
-    # eager steps of the same decode right after the timed replays.
-    timer = KernelTimer(shadowkv, "score_logits")
-    timer.active = not graph
     torch.cuda.synchronize()
     start = time.perf_counter()
     for i in range(args.steps):
@@ -227,26 +252,17 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     log(f"timed {args.steps} {'graph replays' if graph else 'eager steps'} in {elapsed:.3f}s")
-    if graph:
-        timer.active = True
-        for i in range(ROOFLINE_STEPS):
-            tok = model.decode_step(tok)
-        torch.cuda.synchronize()
-        timing = f"HIP events around every scoring launch of {ROOFLINE_STEPS} eager steps after the timed replays"
-    else:
-        timing = "HIP events around every scoring launch of the timed steps"
-    timer.active = False
-    setattr(shadowkv, "score_logits", timer.orig)
 
     n = cache.k_landmark.shape[-2]
     BH = cache.batch_size * shape.kv_heads  # one launch covers one lane's batch slice
     G = shape.heads // shape.kv_heads
     lb = logits_bytes(BH, G, n)
-    k_ms = timer.mean_ms()
+    k_ms, timing = scoring_launch_ms(model)
     achieved = lb / (k_ms * 1e-3) / 1e9
     traffic = None
-    tfile = ROOT / "profiles" / "score_logits_traffic.json"
-    if tfile.exists():
+    # HBM traffic per launch from FETCH_SIZE / WRITE_SIZE counter runs, valid for this workload only
+    tfile = ROOT / "profiles" / "score_logits_llama8b_b8_ctx122880_traffic.json"
+    if tfile.exists() and (args.batch, args.ctx, args.budget, lanes) == (8, 122880, 2048, 1):
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
 
     detail = None
