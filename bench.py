@@ -30,6 +30,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK = 2.5e15  # dense bf16 FLOP/s
 
 
 def log(msg: str) -> None:
@@ -47,6 +48,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=1, help="independent batch slices interleaved per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
+    p.add_argument("--workload", choices=["decode", "rebuild"], default="decode",
+                   help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone")
+    p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-breakdown", action="store_true")
@@ -201,12 +205,107 @@ def breakdown(model, tok) -> dict:
                           "note": "value fetch (hit compaction + zero-copy miss gather) per layer"}}
 
 
+def rebuild_bytes(rows_per_head: int, BH: int, S: int, R: int = 160, D: int = 128) -> int:
+    """Algorithmic HBM bytes of one rebuild launch: per miss row a U row, a cos/sin row and the
+    rotated K row; per (b,h) the SV block and the chunk ids."""
+    return BH * (rows_per_head * (R * 2 + D * 2 + D * 2) + R * D * 2 + S * 8)
+
+
+def rebuild_microbench(args) -> int:
+    """Low-rank key rebuild + RoPE alone: per-head U [B*8, 122880, 160] and SV shared across the
+    batch, 256 sorted unique chunk ids per head out of 15360 (2048 rows), hit counts 0 and 154,
+    Llama RoPE (theta 5e5). One JSON line per (batch, hits)."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+    from shadowkv_amd.models.tensor_op import build_cos_sin_cache
+
+    H, D, R, c, ctx, S = 8, 128, 160, 8, 122880, 256
+    chunks, sparse_start = ctx // c, 448
+    buf_len = sparse_start + S * c + 96
+    dev = torch.device("cuda")
+    cos_sin = build_cos_sin_cache(ctx + 1024, 500000.0, D, device=dev)
+    reps = max(args.steps, 4)
+    # A plain copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters of profiling runs.
+    cal = torch.empty(64 * 2 ** 20, dtype=torch.float32, device=dev)
+    torch.neg(cal, out=cal)
+    del cal
+    for B in args.rebuild_batches:
+        g = torch.Generator(device=dev).manual_seed(1000 + B)
+        U = torch.empty(B, H, ctx, R, dtype=torch.bfloat16, device=dev)
+        for b in range(B):
+            U[b].normal_(generator=g)
+        SV = torch.empty(H, D, R, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        ids = torch.stack([torch.randperm(chunks, generator=g, device=dev)[:S].sort().values
+                           for _ in range(B * H)]).view(B, H, S)
+        cache = torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16, device=dev)
+        for hits in (0, 154):
+            cnts = torch.full((B * H,), hits, dtype=torch.int32, device=dev)
+            for _ in range(max(args.warmup, 1)):
+                shadowkv.rebuild_k_rope(U, SV, ids, cnts, cos_sin, cache, sparse_start, c)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                shadowkv.rebuild_k_rope(U, SV, ids, cnts, cos_sin, cache, sparse_start, c)
+            e.record()
+            e.synchronize()
+            t = s.elapsed_time(e) / reps * 1e-3
+            rows = (S - hits) * c
+            nbytes = rebuild_bytes(rows, B * H, S)
+            flops = 2 * B * H * rows * R * D
+            cpu = None
+            if hits == 0 and B <= 8 and not args.no_cpu_baseline:
+                cpu = rebuild_cpu_baseline(U, SV, ids, cnts, cos_sin, cache, sparse_start, c, args.cpu_runs)
+            out = {"metric": "low-rank K rebuild + RoPE rows/s", "value": round(B * H * rows / t, 1),
+                   "unit": "rows/s", "n_gpus": 1, "steps": reps, "warmup": max(args.warmup, 1),
+                   "ms_per_step": round(t * 1e3, 4), "higher_is_better": True, "scaling": "strong",
+                   "vs_baseline": None, "dtype": "bf16",
+                   "data": "synthetic: U, SV ~ N(0,1) bf16, sorted unique random chunk ids",
+                   "config": {"workload": f"rebuild microbench batch {B}, 8 kv heads, rank 160, ctx 122880, "
+                                          f"256 chunks/head, {hits} hits", "batch": B, "hits": hits},
+                   "roofline": {"kernel": "rebuild_kernel (gather-GEMM + RoPE epilogue)", "bound": "hbm",
+                                "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                                "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(t * 1e6, 2),
+                                "mfma_tflops": round(flops / t / 1e12, 2),
+                                "mfma_util": round(flops / t / MFMA_BF16_PEAK, 5)},
+                   "cpu_baseline": cpu}
+            print(json.dumps(out), flush=True)
+        del U, SV, ids, cache
+        torch.cuda.empty_cache()
+    return 0
+
+
+def rebuild_cpu_baseline(U, SV, ids, cnts, cos_sin, cache, sparse_start, c, runs) -> dict:
+    """The CPU oracle's rebuild + RoPE push at the same batch (a reported baseline only)."""
+    import torch
+    import oracle
+
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(threads)
+    B, H, S = ids.shape
+    Uc, SVc = U.cpu(), SV.cpu().unsqueeze(0).expand(B, -1, -1, -1)
+    idc, cc, csc, kc = ids.cpu(), cnts.cpu(), cos_sin.cpu(), cache.cpu()
+    times = []
+    for i in range(3 + runs):
+        t0 = time.perf_counter()
+        oracle.rebuild_k_rope(Uc, SVc, idc, cc, csc, c, kc, sparse_start)
+        if i >= 3:
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    rows = B * H * S * c
+    return {"value": round(rows / t, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"oracle rebuild + RoPE push on CPU torch at batch {B} (all {rows} rows); median of {runs} "
+                      f"runs after 3 warmups = {t * 1e3:.1f} ms"}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the sparse decode path is not sharded "
               f"across GPUs in this build", file=sys.stderr)
         return 2
+    if args.workload == "rebuild":
+        return rebuild_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv

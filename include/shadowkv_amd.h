@@ -116,7 +116,8 @@ int skv_apply_rotary_pos_emb_push_cache_opt_glm(
  *   output[bh, r, :] = bf16( a[bh/heads, pos(r), :rank] . b[bh, :, :rank]^T ),
  *   pos(r) = position_ids[bh*(sparse_budget/chunk_size) + r/chunk_size]*chunk_size + r%chunk_size.
  * a: [batch, seq_len, rank]; b: [batch*heads, embed_dim, rank]; output [batch*heads, sparse_budget, embed_dim].
- * Hit rows (r < offset_array[bh]*chunk_size) are left untouched. embed_dim must be 128. */
+ * Hit rows (r < offset_array[bh]*chunk_size) are left untouched. embed_dim must be 128; a, b and
+ * output must be 16-byte aligned. */
 int skv_batch_gather_gemm(const uint16_t* a, const uint16_t* b, const int32_t* position_ids,
                           uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
                           int rank, int sparse_budget, int max_seq_len, int chunk_size,
@@ -131,7 +132,8 @@ int skv_batch_gather_gemm(const uint16_t* a, const uint16_t* b, const int32_t* p
  *   out row of (b,h,r): cache + b*stride_cache_b + h*stride_cache_h + (sparse_start+r)*stride_cache_s
  * rope_mode 0: half-split with cos_sin row [cos(64)|sin(64)]; 1: GLM interleaved (see above).
  * Rows whose position falls outside [0, u_rows) or [0, cos_sin_rows) are not written.
- * head_dim must be 128, rank a multiple of 8 in [8, 192]. */
+ * head_dim must be 128, rank a multiple of 8 in [8, 192]; U, SV, cache and cos_sin rows must be
+ * 16-byte aligned (base pointers, and strides multiples of 8 elements). */
 int skv_rebuild_k_rope(const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
                        int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b, int64_t sv_stride_h,
                        int64_t sv_stride_n, const int64_t* position_ids, int64_t pid_stride_b, int64_t pid_stride_h,

@@ -9,13 +9,18 @@
 // bf16 k(r) itself is written (reference batch_gather_gemm output).
 //
 // Work decomposition (gfx950, wave64):
-//   * workgroup = 4 waves, owns kTileRows consecutive rows of one head; SV of that head
-//     (128 x rank bf16, 40 KB at rank 160) is staged once into LDS;
-//   * a wave computes 32 rows x 128 columns per iteration with v_mfma_f32_16x16x32_bf16:
-//     A = 16 gathered U rows (16-byte loads straight from HBM, 4 lanes per 64-byte k-slab),
-//     B = SV from LDS, 8 column tiles x ceil(rank/32) k-steps, fp32 accumulation;
-//   * the epilogue rounds to bf16 and applies the rotation lane-locally: columns d and d+64
-//     live in column tiles t and t+4 of the same lane (GLM pairs use a 1-lane shuffle).
+//   * workgroup = 4 waves, owns kTileRows = 256 consecutive rows of one head. At entry it stages
+//     SV of that head (128 x rank bf16, 40 KB at rank 160) and the U row of each of its rows
+//     (chunk id * chunk + r % chunk) into LDS;
+//   * a wave computes 32 rows x 128 columns per iteration, two iterations, with
+//     v_mfma_f32_16x16x32_bf16 where A = SV (16 output dims x 32 k, from LDS, shared by both
+//     16-row halves) and B = the gathered U rows (16-byte loads straight from HBM). The next
+//     iteration's U rows are in flight while the current one computes;
+//   * the fp32 result of a 16-row half is rounded to bf16 and staged in a per-wave LDS tile
+//     (a lane holds 4 consecutive dims of one row: one 8-byte write per column tile); the
+//     epilogue then works in row-contiguous 16-byte units: a lane takes dims [8j, 8j+8) (and,
+//     for the half-split rotation, [64+8j, 72+8j)) of one row, with its cos/sin loaded as
+//     16-byte vectors before the MFMAs, and stores the rotated row with 16-byte stores;
 //   * blockIdx -> (head, tile) is XCD-aware: all tiles of a head land on the same XCD
 //     (workgroups are dealt round-robin over the 8 XCDs), so SV is fetched from HBM once per
 //     head and re-read from that XCD's L2.
@@ -29,10 +34,13 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
 constexpr int kTileRows = 256;  // rows per workgroup: 4 waves x 2 iterations x 32 rows
 constexpr int kHeadDim = 128;
 constexpr int kMaxRank = 192;
 constexpr int kXcds = 8;
+constexpr int kStLd = kHeadDim + 8;  // staging row (elements), padded against bank conflicts
+static_assert(kThreads == kTileRows, "the position staging gives each thread one row");
 
 enum Mode { kPlain = 0, kRopeHalf = 1, kRopeGlm = 2 };
 
@@ -52,16 +60,45 @@ struct RebuildArgs {
   int B, H, S, chunk, rank, tiles;
 };
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-template <typename IdxT>
-__device__ __forceinline__ int64_t row_pos(const RebuildArgs& a, const IdxT* ids, int row) {
-  return static_cast<int64_t>(ids[row / a.chunk]) * a.chunk + row % a.chunk;
+__device__ __forceinline__ uint16_t lo16(uint32_t w) { return static_cast<uint16_t>(w & 0xffffu); }
+__device__ __forceinline__ uint16_t hi16(uint32_t w) { return static_cast<uint16_t>(w >> 16); }
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+// 8 bf16 of a 16-byte vector as an array (element 2i in the low half of word i).
+__device__ __forceinline__ void unpack8(const u32x4& v, uint16_t* e) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    e[2 * i] = lo16(w[i]);
+    e[2 * i + 1] = hi16(w[i]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const uint16_t* e) {
+  return u32x4{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7])};
 }
 
-template <int kMode, typename IdxT>
-__global__ void __launch_bounds__(kThreads) rebuild_kernel(RebuildArgs a) {
-  extern __shared__ __align__(16) uint16_t sv_lds[];  // [128][rank + 8]
+// Rows handled by one epilogue lane-unit of a 16-row tile: a half-split unit covers dims
+// [8j, 8j+8) and [64+8j, 72+8j) (8 units per row); GLM and plain units cover [8j, 8j+8)
+// (16 units per row).
+template <int kMode>
+struct Units {
+  static constexpr int kPerRow = kMode == kRopeHalf ? 8 : 16;
+  static constexpr int kPerLane = 16 * kPerRow / 64;
+};
+
+template <int kMode, int KS, typename IdxT>
+__global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
+  using U = Units<kMode>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int ldr = a.rank + 8;  // padded SV row (elements)
+  uint16_t* sv_lds = reinterpret_cast<uint16_t*>(smem);                         // [128][ldr]
+  int32_t* pos_lds = reinterpret_cast<int32_t*>(sv_lds + kHeadDim * ldr);      // [kTileRows]
+  uint16_t* kst = reinterpret_cast<uint16_t*>(pos_lds + kTileRows);            // [kWaves][16][kStLd]
 
   const int bid = blockIdx.x;
   const int xcd = bid % kXcds;
@@ -79,113 +116,169 @@ __global__ void __launch_bounds__(kThreads) rebuild_kernel(RebuildArgs a) {
   const int row_end = min(row_begin + kTileRows, total_rows);
   if (row_end <= miss_begin || row_begin >= row_end) return;
 
-  const int ldr = a.rank + 8;  // padded LDS row (elements) against bank conflicts
+  // SV -> LDS: every load of this thread is issued before any store, so the staging costs one
+  // memory latency, not one per vector.
   const int k8 = a.rank / 8;
   const uint16_t* svp = a.sv + b * a.sv_sb + h * a.sv_sh;
-  for (int idx = threadIdx.x; idx < kHeadDim * k8; idx += kThreads) {
-    int n = idx / k8, kk = (idx - n * k8) * 8;
-    *reinterpret_cast<u32x4*>(&sv_lds[n * ldr + kk]) = *reinterpret_cast<const u32x4*>(&svp[n * a.sv_sn + kk]);
+  {
+    constexpr int kVecs = (kHeadDim * (KS * 32) / 8 + kThreads - 1) / kThreads;  // >= 128*rank/8/256
+    u32x4 v[kVecs];
+#pragma unroll
+    for (int i = 0; i < kVecs; ++i) {
+      const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+      const int n = idx / k8, kk = (idx - n * k8) * 8;
+      if (idx < kHeadDim * k8) v[i] = *reinterpret_cast<const u32x4*>(&svp[n * a.sv_sn + kk]);
+    }
+#pragma unroll
+    for (int i = 0; i < kVecs; ++i) {
+      const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+      const int n = idx / k8, kk = (idx - n * k8) * 8;
+      if (idx < kHeadDim * k8) *reinterpret_cast<u32x4*>(&sv_lds[n * ldr + kk]) = v[i];
+    }
+  }
+  const IdxT* ids = static_cast<const IdxT*>(a.ids) + b * a.id_sb + h * a.id_sh;
+  {
+    const int row = row_begin + static_cast<int>(threadIdx.x);
+    int32_t p = -1;
+    if (row < row_end) {
+      const int64_t q = static_cast<int64_t>(ids[row / a.chunk]) * a.chunk + row % a.chunk;
+      if (q >= 0 && q <= 0x7fffffff) p = static_cast<int32_t>(q);
+    }
+    pos_lds[threadIdx.x] = p;  // kThreads == kTileRows: one row per thread
   }
   __syncthreads();
 
-  const IdxT* ids = static_cast<const IdxT*>(a.ids) + b * a.id_sb + h * a.id_sh;
   const uint16_t* ubase = a.u + b * a.u_sb + h * a.u_sh;
   uint16_t* obase = a.out + b * a.o_sb + h * a.o_sh;
-
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int li = lane & 15;  // A row / B column / D column within a 16x16 tile
-  const int lk = lane >> 4;  // k-slab (A/B) and row quad (D)
-  const int ksteps = (a.rank + 31) / 32;
+  const int li = lane & 15;  // B column (row within a 16-row half) / D column
+  const int lk = lane >> 4;  // k-slab of A and B; D row quad
+  uint16_t* st = kst + wave * 16 * kStLd;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  for (int it = 0; it < 2; ++it) {
-    const int rb = row_begin + (wave + 4 * it) * 32;
-    if (rb >= row_end || rb + 32 <= miss_begin) continue;  // wave-uniform
-
-    // A fragments for the two 16-row halves.
-    bf16x8_t afrag[2][kMaxRank / 32];
+  // U fragments (B operand) of the 32 rows [lr, lr+32) of this workgroup.
+  auto load_u = [&](int lr, bf16x8_t (&uf)[2][KS]) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const int row = rb + m * 16 + li;
-      bool valid = row >= miss_begin && row < row_end;
-      int64_t pos = valid ? row_pos(a, ids, row) : 0;
-      valid = valid && pos >= 0 && pos < a.u_rows;
-      const uint16_t* up = ubase + pos * a.u_sr;
+      const int r = lr + m * 16 + li;
+      const int grow = row_begin + r;
+      const int32_t pos = pos_lds[r];
+      const bool valid = grow >= miss_begin && grow < row_end && pos >= 0 && pos < a.u_rows;
+      const uint16_t* up = ubase + static_cast<int64_t>(valid ? pos : 0) * a.u_sr;
 #pragma unroll
-      for (int ks = 0; ks < kMaxRank / 32; ++ks) {
+      for (int ks = 0; ks < KS; ++ks) {
         const int kk = ks * 32 + lk * 8;
         u32x4 v = zero4;
-        if (ks < ksteps && valid && kk < a.rank) v = *reinterpret_cast<const u32x4*>(up + kk);
-        afrag[m][ks] = as_bf16x8(v);
+        if (valid && kk < a.rank) v = *reinterpret_cast<const u32x4*>(up + kk);
+        uf[m][ks] = as_bf16x8(v);
       }
     }
+  };
+
+  bf16x8_t uf[2][2][KS];
+  const int lr0 = wave * 64;
+  bool active[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int rb = row_begin + lr0 + it * 32;
+    active[it] = rb < row_end && rb + 32 > miss_begin;  // wave-uniform
+  }
+  if (active[0]) load_u(lr0, uf[0]);
+  else if (active[1]) load_u(lr0 + 32, uf[1]);  // first block all hits: no iteration 0 to prefetch it
+
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    if (!active[it]) continue;
+    const int lr = lr0 + it * 32;
+
+    // cos/sin of this iteration's epilogue units, loaded ahead of the MFMAs.
+    u32x4 cs_c[2][U::kPerLane], cs_s[2][U::kPerLane];
+    if (kMode != kPlain) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int q = 0; q < U::kPerLane; ++q) {
+          const int unit = lane + 64 * q;
+          const int r = unit / U::kPerRow, j = unit % U::kPerRow;
+          const int32_t pos = pos_lds[lr + m * 16 + r];
+          cs_c[m][q] = zero4;
+          cs_s[m][q] = zero4;
+          if (pos >= 0 && pos < a.cs_rows) {
+            const uint16_t* c = a.cs + static_cast<int64_t>(pos) * a.cs_stride;
+            if (kMode == kRopeHalf) {
+              cs_c[m][q] = *reinterpret_cast<const u32x4*>(c + 8 * j);
+              cs_s[m][q] = *reinterpret_cast<const u32x4*>(c + 64 + 8 * j);
+            } else if (j < 8) {  // GLM: 4 pairs per unit, cos at [4j], sin at [32 + 4j]
+              const u32x2 cc = *reinterpret_cast<const u32x2*>(c + 4 * j);
+              const u32x2 ss = *reinterpret_cast<const u32x2*>(c + 32 + 4 * j);
+              cs_c[m][q] = u32x4{cc.x, cc.y, 0u, 0u};
+              cs_s[m][q] = u32x4{ss.x, ss.y, 0u, 0u};
+            }
+          }
+        }
+    }
+    if (it == 0 && active[1]) load_u(lr0 + 32, uf[1]);  // in flight during this iteration's MFMAs
 
     f32x4_t acc[2][8];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int t = 0; t < 8; ++t) acc[m][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
 #pragma unroll
-    for (int ks = 0; ks < kMaxRank / 32; ++ks) {
-      if (ks >= ksteps) break;
+    for (int ks = 0; ks < KS; ++ks) {
       const int kk = ks * 32 + lk * 8;
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        u32x4 bv = zero4;
-        if (kk < a.rank) bv = *reinterpret_cast<const u32x4*>(&sv_lds[(t * 16 + li) * ldr + kk]);
-        const bf16x8_t bfrag = as_bf16x8(bv);
-        acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[0][ks], bfrag, acc[0][t], 0, 0, 0);
-        acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[1][ks], bfrag, acc[1][t], 0, 0, 0);
+        u32x4 sv = zero4;
+        if (kk < a.rank) sv = *reinterpret_cast<const u32x4*>(&sv_lds[(t * 16 + li) * ldr + kk]);
+        const bf16x8_t svf = as_bf16x8(sv);
+        acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(svf, uf[it][0][ks], acc[0][t], 0, 0, 0);
+        acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(svf, uf[it][1][ks], acc[1][t], 0, 0, 0);
       }
     }
 
-    // Epilogue: lane holds rows rb + m*16 + lk*4 + v, column t*16 + li of tile t.
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
+      // D[dim][row]: this lane holds dims t*16 + 4*lk + v (v = 0..3) of row li.
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = rb + m * 16 + lk * 4 + v;
-        bool valid = row >= miss_begin && row < row_end;
-        int64_t pos = valid ? row_pos(a, ids, row) : 0;
+      for (int t = 0; t < 8; ++t) {
+        const u32x2 w = {skv::f2bf2(acc[m][t][0], acc[m][t][1]), skv::f2bf2(acc[m][t][2], acc[m][t][3])};
+        *reinterpret_cast<u32x2*>(&st[li * kStLd + t * 16 + 4 * lk]) = w;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS before any lane reads it
+#pragma unroll
+      for (int q = 0; q < U::kPerLane; ++q) {
+        const int unit = lane + 64 * q;
+        const int r = unit / U::kPerRow, j = unit % U::kPerRow;
+        const int grow = row_begin + lr + m * 16 + r;
+        const int32_t pos = pos_lds[lr + m * 16 + r];
+        bool valid = grow >= miss_begin && grow < row_end;
         if (kMode != kPlain) valid = valid && pos >= 0 && pos < a.cs_rows;
-        uint16_t* orow = obase + static_cast<int64_t>(a.o_start + row) * a.o_ss;
-        const uint16_t* c = a.cs + pos * a.cs_stride;
+        if (!valid) continue;
+        uint16_t* orow = obase + static_cast<int64_t>(a.o_start + grow) * a.o_ss;
+        const u32x4 x1v = *reinterpret_cast<const u32x4*>(&st[r * kStLd + 8 * j]);
         if (kMode == kPlain) {
-          if (valid) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) orow[t * 16 + li] = skv::f2bf(acc[m][t][v]);
-          }
+          *reinterpret_cast<u32x4*>(orow + 8 * j) = x1v;
         } else if (kMode == kRopeHalf) {
-          if (valid) {
+          const u32x4 x2v = *reinterpret_cast<const u32x4*>(&st[r * kStLd + 64 + 8 * j]);
+          const u32x4 cv = cs_c[m][q], sv = cs_s[m][q];
+          uint32_t y1[4], y2[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int d = t * 16 + li;
-              uint16_t y1, y2;
-              skv::rope_half_split(skv::f2bf(acc[m][t][v]), skv::f2bf(acc[m][t + 4][v]), c[d], c[d + 64], y1, y2);
-              orow[d] = y1;
-              orow[d + 64] = y2;
-            }
-          }
+          for (int e = 0; e < 4; ++e) skv::rope_half_split2(x1v[e], x2v[e], cv[e], sv[e], y1[e], y2[e]);
+          *reinterpret_cast<u32x4*>(orow + 8 * j) = u32x4{y1[0], y1[1], y1[2], y1[3]};
+          *reinterpret_cast<u32x4*>(orow + 64 + 8 * j) = u32x4{y2[0], y2[1], y2[2], y2[3]};
         } else {  // GLM: interleaved pairs on dims 0..63, dims 64..127 unchanged
+          if (j < 8) {
+            uint16_t x[8], c[8], sn[8], y[8];
+            unpack8(x1v, x);
+            unpack8(cs_c[m][q], c);
+            unpack8(cs_s[m][q], sn);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int d = t * 16 + li;
-            const uint16_t x = skv::f2bf(acc[m][t][v]);
-            const uint16_t other = static_cast<uint16_t>(__shfl_xor(static_cast<int>(x), 1, 64));
-            if (valid) {
-              const int pair = d >> 1;
-              const uint16_t xe = (d & 1) ? other : x;
-              const uint16_t xo = (d & 1) ? x : other;
-              uint16_t ye, yo;
-              skv::rope_half_split(xe, xo, c[pair], c[pair + 32], ye, yo);
-              orow[d] = (d & 1) ? yo : ye;
-            }
-          }
-          if (valid) {
-#pragma unroll
-            for (int t = 4; t < 8; ++t) orow[t * 16 + li] = skv::f2bf(acc[m][t][v]);
+            for (int p = 0; p < 4; ++p) skv::rope_half_split(x[2 * p], x[2 * p + 1], c[p], sn[p], y[2 * p], y[2 * p + 1]);
+            *reinterpret_cast<u32x4*>(orow + 8 * j) = pack8(y);
+          } else {
+            *reinterpret_cast<u32x4*>(orow + 8 * j) = x1v;
           }
         }
       }
@@ -194,6 +287,33 @@ __global__ void __launch_bounds__(kThreads) rebuild_kernel(RebuildArgs a) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int kMode, int KS, typename IdxT>
+void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
+  // Ranks above 176 need more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU): raise the
+  // kernel's limit once.
+  if (lds > 65536) {
+    static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(&rebuild_kernel<kMode, KS, IdxT>),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) +
+                                                                          kTileRows * sizeof(int32_t) +
+                                                                          kWaves * 16 * kStLd * sizeof(uint16_t)));
+    (void)raised;
+  }
+  hipLaunchKernelGGL((rebuild_kernel<kMode, KS, IdxT>), grid, dim3(kThreads), lds, stream, a);
+}
+
+template <int kMode, typename IdxT>
+void launch_mode(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
+  switch (ks) {
+    case 1: launch_ks<kMode, 1, IdxT>(grid, lds, stream, a); break;
+    case 2: launch_ks<kMode, 2, IdxT>(grid, lds, stream, a); break;
+    case 3: launch_ks<kMode, 3, IdxT>(grid, lds, stream, a); break;
+    case 4: launch_ks<kMode, 4, IdxT>(grid, lds, stream, a); break;
+    case 5: launch_ks<kMode, 5, IdxT>(grid, lds, stream, a); break;
+    default: launch_ks<kMode, 6, IdxT>(grid, lds, stream, a); break;
+  }
+}
 
 int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStream_t stream) {
   if (!a.u || !a.sv || !a.ids || !a.cnts || !a.out || (mode != kPlain && !a.cs)) {
@@ -213,22 +333,31 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
     skv_set_error("%s: U and SV rows must be 16-byte aligned (strides multiples of 8 elements)", what);
     return SKV_EINVAL;
   }
+  if (!aligned16(a.out) || a.o_sb % 8 || a.o_sh % 8 || a.o_ss % 8 ||
+      (mode != kPlain && (!aligned16(a.cs) || a.cs_stride % 8))) {
+    skv_set_error("%s: output and cos/sin rows must be 16-byte aligned (strides multiples of 8 elements)", what);
+    return SKV_EINVAL;
+  }
+  if (static_cast<int64_t>(a.S) * a.chunk > (int64_t{1} << 30)) {
+    skv_set_error("%s: %d chunks of %d rows is too many", what, a.S, a.chunk);
+    return SKV_EUNSUPPORTED;
+  }
   a.tiles = (a.S * a.chunk + kTileRows - 1) / kTileRows;
   const int BH = a.B * a.H;
   const int heads_padded = (BH + kXcds - 1) / kXcds * kXcds;
   const dim3 grid(static_cast<unsigned>(heads_padded * a.tiles));
-  const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t);
-#define SKV_LAUNCH(M, T) hipLaunchKernelGGL((rebuild_kernel<M, T>), grid, dim3(kThreads), lds, stream, a)
+  const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + kTileRows * sizeof(int32_t) +
+                     static_cast<size_t>(kWaves) * 16 * kStLd * sizeof(uint16_t);
+  const int ks = (a.rank + 31) / 32;
   if (ids64) {
-    if (mode == kPlain) SKV_LAUNCH(kPlain, int64_t);
-    else if (mode == kRopeHalf) SKV_LAUNCH(kRopeHalf, int64_t);
-    else SKV_LAUNCH(kRopeGlm, int64_t);
+    if (mode == kPlain) launch_mode<kPlain, int64_t>(ks, grid, lds, stream, a);
+    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t>(ks, grid, lds, stream, a);
+    else launch_mode<kRopeGlm, int64_t>(ks, grid, lds, stream, a);
   } else {
-    if (mode == kPlain) SKV_LAUNCH(kPlain, int32_t);
-    else if (mode == kRopeHalf) SKV_LAUNCH(kRopeHalf, int32_t);
-    else SKV_LAUNCH(kRopeGlm, int32_t);
+    if (mode == kPlain) launch_mode<kPlain, int32_t>(ks, grid, lds, stream, a);
+    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int32_t>(ks, grid, lds, stream, a);
+    else launch_mode<kRopeGlm, int32_t>(ks, grid, lds, stream, a);
   }
-#undef SKV_LAUNCH
   return skv_check_launch(what);
 }
 

@@ -21,12 +21,24 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// fp32 -> bf16, round to nearest even (gfx950 v_cvt_pk_bf16_f32); NaN -> the canonical quiet NaN
+// 0x7fc0, as c10::BFloat16 does.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // canonical quiet NaN, as c10::BFloat16
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint16_t r = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  return f != f ? static_cast<uint16_t>(0x7fc0) : r;
 }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> two bf16 in one instruction (a in the low half), round to nearest even. A NaN
+// input gives a quiet NaN whose payload is not canonicalised.
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+// The two bf16 of a packed word as fp32 (exact).
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 __device__ __forceinline__ uint16_t bmul(uint16_t a, uint16_t b) { return f2bf(bf2f(a) * bf2f(b)); }
 __device__ __forceinline__ uint16_t badd(uint16_t a, uint16_t b) { return f2bf(bf2f(a) + bf2f(b)); }
@@ -101,10 +113,9 @@ __device__ __forceinline__ void drain_and_barrier() {
   __syncthreads();
 }
 
-// 16-byte vector type for chunk copies.
-struct alignas(16) u32x4 {
-  uint32_t x, y, z, w;
-};
+// 16-byte vector type for chunk copies: a native vector (not a struct), so arrays of it stay in
+// registers (a struct is copied with memcpy, which keeps such arrays in private memory).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte load with the non-temporal (streaming) hint: global_load_dwordx4 ... nt. Used for reads
 // of pinned host memory over the host link, which are read once; it keeps those long-latency

@@ -98,12 +98,14 @@ def test_batch_gather_gemm_plain(gpu):
         _assert_rounding_close(got[b, h, miss:], want[b, h, miss:])
 
 
-@pytest.mark.parametrize("glm,per_head_u,shared_sv,R", [(False, False, False, 160), (True, False, False, 160),
-                                                       (False, True, True, 160), (False, False, False, 96),
-                                                       (False, False, False, 168)])
-def test_rebuild_k_rope_fused(gpu, glm, per_head_u, shared_sv, R):
-    B, H, ctx, S, c = 2, 8, 4096, 256, 8
-    _say(f"rebuild_k_rope glm={glm} per_head_u={per_head_u} shared_sv={shared_sv} R={R}")
+@pytest.mark.parametrize("glm,per_head_u,shared_sv,R,S,c", [
+    (False, False, False, 160, 256, 8), (True, False, False, 160, 256, 8), (False, True, True, 160, 256, 8),
+    (False, False, False, 96, 256, 8), (False, False, False, 168, 256, 8), (False, False, False, 8, 256, 8),
+    (True, True, True, 40, 256, 8), (False, False, False, 192, 256, 8), (True, False, False, 192, 256, 8),
+    (False, False, False, 160, 100, 4), (True, False, True, 104, 100, 4)])
+def test_rebuild_k_rope_fused(gpu, glm, per_head_u, shared_sv, R, S, c):
+    B, H, ctx = 2, 8, 4096
+    _say(f"rebuild_k_rope glm={glm} per_head_u={per_head_u} shared_sv={shared_sv} R={R} S={S} c={c}")
     U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 2, per_head_u, shared_sv)
     cs = oracle.build_glm_cos_sin_cache(ctx, 5e6) if glm else oracle.build_cos_sin_cache(ctx, 5e5)
     start, buf = 448, 448 + S * c + 96
