@@ -48,8 +48,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=1, help="independent batch slices interleaved per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
-    p.add_argument("--workload", choices=["decode", "rebuild"], default="decode",
-                   help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone")
+    p.add_argument("--workload", choices=["decode", "rebuild", "attention"], default="decode",
+                   help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
+                        "attention: the sparse decode attention alone")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -205,6 +206,28 @@ def breakdown(model, tok) -> dict:
                           "note": "value fetch (hit compaction + zero-copy miss gather) per layer"}}
 
 
+def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
+    """Seconds per call of `fn` on the GPU: `reps` calls captured in one HIP graph, replayed
+    `rounds` times between HIP events, so host launch cost does not enter the figure."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(rounds):
+        g.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) * 1e-3 / (rounds * reps)
+
+
 def rebuild_bytes(rows_per_head: int, BH: int, S: int, R: int = 160, D: int = 128) -> int:
     """Algorithmic HBM bytes of one rebuild launch: per miss row a U row, a cos/sin row and the
     rotated K row; per (b,h) the SV block and the chunk ids."""
@@ -240,15 +263,8 @@ def rebuild_microbench(args) -> int:
         cache = torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16, device=dev)
         for hits in (0, 154):
             cnts = torch.full((B * H,), hits, dtype=torch.int32, device=dev)
-            for _ in range(max(args.warmup, 1)):
-                shadowkv.rebuild_k_rope(U, SV, ids, cnts, cos_sin, cache, sparse_start, c)
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                shadowkv.rebuild_k_rope(U, SV, ids, cnts, cos_sin, cache, sparse_start, c)
-            e.record()
-            e.synchronize()
-            t = s.elapsed_time(e) / reps * 1e-3
+            t = gpu_time_per_call(lambda: shadowkv.rebuild_k_rope(U, SV, ids, cnts, cos_sin, cache, sparse_start, c),
+                                  reps)
             rows = (S - hits) * c
             nbytes = rebuild_bytes(rows, B * H, S)
             flops = 2 * B * H * rows * R * D
@@ -256,10 +272,11 @@ def rebuild_microbench(args) -> int:
             if hits == 0 and B <= 8 and not args.no_cpu_baseline:
                 cpu = rebuild_cpu_baseline(U, SV, ids, cnts, cos_sin, cache, sparse_start, c, args.cpu_runs)
             out = {"metric": "low-rank K rebuild + RoPE rows/s", "value": round(B * H * rows / t, 1),
-                   "unit": "rows/s", "n_gpus": 1, "steps": reps, "warmup": max(args.warmup, 1),
+                   "unit": "rows/s", "n_gpus": 1, "steps": reps, "warmup": 1,
                    "ms_per_step": round(t * 1e3, 4), "higher_is_better": True, "scaling": "strong",
                    "vs_baseline": None, "dtype": "bf16",
-                   "data": "synthetic: U, SV ~ N(0,1) bf16, sorted unique random chunk ids",
+                   "data": "synthetic: U, SV ~ N(0,1) bf16, sorted unique random chunk ids; timed as HIP-graph "
+                           "replays of back-to-back launches",
                    "config": {"workload": f"rebuild microbench batch {B}, 8 kv heads, rank 160, ctx 122880, "
                                           f"256 chunks/head, {hits} hits", "batch": B, "hits": hits},
                    "roofline": {"kernel": "rebuild_kernel (gather-GEMM + RoPE epilogue)", "bound": "hbm",
@@ -298,6 +315,42 @@ def rebuild_cpu_baseline(U, SV, ids, cnts, cos_sin, cache, sparse_start, c, runs
                       f"runs after 3 warmups = {t * 1e3:.1f} ms"}
 
 
+def attention_microbench(args) -> int:
+    """Sparse decode attention alone at the decode shapes: one query token per sequence over the
+    assembled K/V buffers (Llama-3-8B: 32/8 heads; GLM-4-9B: 32/2 heads), lengths around the
+    sparse region's 2497 rows. One JSON line per shape."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    D = 128
+    reps = max(args.steps, 4)
+    for name, B, Hq, Hk, L in (("Llama-3-8B", 8, 32, 8, 2600), ("Llama-3-8B", 24, 32, 8, 2600),
+                               ("GLM-4-9B", 4, 32, 2, 2600), ("Llama-3-8B-1M", 1, 32, 8, 19616)):
+        g = torch.Generator(device="cuda").manual_seed(L + B)
+        buf = L + 32
+        K = torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16)
+        V = torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16)
+        q = torch.randn(B, Hq, D, generator=g, device="cuda").to(torch.bfloat16)
+        out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device="cuda")
+        t = gpu_time_per_call(lambda: shadowkv.sparse_attn_decode(q, K, V, L, out, ws), reps)
+        G = Hq // Hk
+        nbytes = B * Hk * (2 * L * D * 2 + 2 * G * D * 2)  # K and V rows, q in, o out
+        out_line = {"metric": "sparse decode attention (b,h) rows/s", "value": round(B * Hq / t, 1), "unit": "rows/s",
+                    "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
+                    "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
+                    "data": "synthetic: q, K, V ~ N(0,1) bf16; timed as HIP-graph replays of back-to-back launches",
+                    "config": {"workload": f"{name} shape attention: batch {B}, {Hq}/{Hk} heads, kv length {L}",
+                               "batch": B, "q_heads": Hq, "kv_heads": Hk, "kv_len": L},
+                    "roofline": {"kernel": "attn_split_kernel + attn_combine_kernel", "bound": "hbm",
+                                 "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                                 "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(t * 1e6, 2)},
+                    "cpu_baseline": None}
+        print(json.dumps(out_line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -306,6 +359,8 @@ def main() -> int:
         return 2
     if args.workload == "rebuild":
         return rebuild_microbench(args)
+    if args.workload == "attention":
+        return attention_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv

@@ -4,9 +4,10 @@
 // (q_len = 1, so causality masks nothing). Split-L flash decoding for CDNA4:
 //   attn_split_kernel: workgroup = (kv head, split of kSplit keys); all G query heads that
 //     share the kv head are served by one pass over its K and V rows, so every K/V byte is read
-//     once from HBM. Scores: 16 lanes per 256-byte key row (16-byte loads), G dots combined with
-//     a 16-lane reduce-scatter, staged in LDS; split softmax (max, exp, sum) per query head;
-//     P.V: 16 key streams x 8 dims per lane, fp32 accumulation, reduced across streams.
+//     once from HBM. Scores on MFMA: v_mfma_f32_16x16x32_bf16 with the (up to 16) query heads as
+//     the A rows and 16 keys as the B columns, so each lane ends up holding finished scores (no
+//     cross-lane reduction); split softmax per query head with DPP/readlane wave reductions;
+//     P.V in fp32: 16 key streams x 8 dims per lane, the streams summed through LDS.
 //   attn_combine_kernel: log-sum-exp merge of the splits, bf16 output.
 #include "wave_reduce.h"
 
@@ -46,10 +47,44 @@ __device__ __forceinline__ int live_length(const AttnArgs& a) {
   return a.L_dev ? min(max(*a.L_dev, 1), a.L) : a.L;
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Reductions over a wave without LDS round trips: rotations within each 16-lane row (DPP
+// row_ror), then the four row results read back as wave-uniform values.
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 template <int GP>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
+  // Up to 4 query heads per kv head, the split's K and V rows are all requested at entry (one
+  // memory latency per workgroup); with more, V is requested right after the scores, so its
+  // latency overlaps the softmax instead.
+  constexpr bool kEarlyV = false;
+  constexpr int kRows = kSplit / 16;        // keys per P.V stream
+  constexpr int kGroups = kSplit / 4 / 16;  // 16-key MFMA groups per wave
+  constexpr int kPass = GP < 4 ? GP : 4;    // query heads per stream-reduction pass
   __shared__ float p_lds[GP][kSplit];
-  __shared__ float red[4][GP][kHeadDim];
+  __shared__ __align__(16) float red[16][kPass][kHeadDim];  // [key stream][head of the pass][dim]
   __shared__ float ml[GP][2];
 
   const int split = blockIdx.x;
@@ -65,54 +100,58 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   const int li = lane & 15;
   const int grp = lane >> 4;
   const int G = a.G;
+  const uint16_t* kh = a.k + b * a.kv_sb + h * a.kv_sh;
+  const uint16_t* vh = a.v + b * a.kv_sb + h * a.kv_sh;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  const uint16_t* kb = a.k + b * a.kv_sb + h * a.kv_sh;
-  const uint16_t* vb = a.v + b * a.kv_sb + h * a.kv_sh;
-
-  {
-    float q[GP][8];
+  // K as MFMA B operand: lane (li, grp) holds key (wave*64 + 16*kg + li), dims [32*ks + 8*grp, +8).
+  u32x4 kf[kGroups][4];
 #pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      if (g < G) {
-        const int hq = h * G + g;
-        u32x4 v = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + hq * a.q_sh + li * 8);
-        unpack8(v, q[g]);
+  for (int kg = 0; kg < kGroups; ++kg) {
+    const int s = s0 + wave * (kSplit / 4) + 16 * kg + li;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) q[g][e] *= a.scale;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) q[g][e] = 0.f;
-      }
-    }
-    const int owner = skv::rs16_owner<GP>(li);
-    const bool writer = skv::rs16_writer<GP>(li) && owner < G;
-    constexpr int kSteps = kSplit / 16;  // 4 waves x 4 key groups per step
-    for (int st = 0; st < kSteps; st += 4) {
-      u32x4 rows[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int s = s0 + (st + u) * 16 + wave * 4 + grp;
-        rows[u] = u32x4{0u, 0u, 0u, 0u};
-        if (s < s1) rows[u] = *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(s) * a.kv_ss + li * 8);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int jl = (st + u) * 16 + wave * 4 + grp;
-        float kf[8];
-        unpack8(rows[u], kf);
-        float d[GP];
-#pragma unroll
-        for (int g = 0; g < GP; ++g) {
-          float acc = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc = fmaf(q[g][e], kf[e], acc);
-          d[g] = acc;
-        }
-        const float dot = skv::reduce_scatter16<GP>(d, li);
-        if (writer) p_lds[owner][jl] = (s0 + jl < s1) ? dot : -INFINITY;
-      }
+    for (int ks = 0; ks < 4; ++ks) {
+      kf[kg][ks] = zero4;
+      if (s < s1) kf[kg][ks] = *reinterpret_cast<const u32x4*>(kh + static_cast<int64_t>(s) * a.kv_ss + 32 * ks + 8 * grp);
     }
   }
+  // V for P.V: stream (wave, grp) takes keys s0 + 16*i + stream, lane li its dims [8*li, +8).
+  const int stream = wave * 4 + grp;
+  u32x4 vr[kRows];
+  auto load_v = [&]() {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int s = s0 + i * 16 + stream;
+      vr[i] = zero4;
+      if (s < s1) vr[i] = *reinterpret_cast<const u32x4*>(vh + static_cast<int64_t>(s) * a.kv_ss + li * 8);
+    }
+  };
+  if (kEarlyV) load_v();
+
+  // Q as MFMA A operand: lane (li, grp) holds query head li (zero rows past G), same dims.
+  u32x4 qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    qf[ks] = zero4;
+    if (li < G) qf[ks] = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + (h * G + li) * a.q_sh + 32 * ks + 8 * grp);
+  }
+#pragma unroll
+  for (int kg = 0; kg < kGroups; ++kg) {
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qf[ks]),
+                                                  __builtin_bit_cast(bf16x8_t, kf[kg][ks]), d, 0, 0, 0);
+    // D[head 4*grp + v][key li]
+    const int jl = wave * (kSplit / 4) + 16 * kg + li;
+    const bool live = s0 + jl < s1;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int g = 4 * grp + v;
+      if (g < G) p_lds[g][jl] = live ? d[v] * a.scale : -INFINITY;
+    }
+  }
+  if (!kEarlyV) load_v();
   __syncthreads();
 
   for (int g = wave; g < G; g += 4) {
@@ -123,7 +162,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       x[u] = p_lds[g][lane * 4 + u];
       mx = fmaxf(mx, x[u]);
     }
-    mx = skv::wave_max(mx);
+    mx = wave_max_dpp(mx);
     float l = 0.f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -131,7 +170,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       p_lds[g][lane * 4 + u] = e;
       l += e;
     }
-    l = skv::wave_sum(l);
+    l = wave_sum_dpp(l);
     if (lane == 0) {
       ml[g][0] = mx;
       ml[g][1] = l;
@@ -144,64 +183,76 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   for (int g = 0; g < GP; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  const int stream = wave * 4 + grp;  // 16 key streams
-  for (int t = 0; t < kSplit / 16; t += 4) {
-    u32x4 rows[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int s = s0 + (t + u) * 16 + stream;
-      rows[u] = u32x4{0u, 0u, 0u, 0u};
-      if (s < s1) rows[u] = *reinterpret_cast<const u32x4*>(vb + static_cast<int64_t>(s) * a.kv_ss + li * 8);
-    }
+  for (int i = 0; i < kRows; ++i) {
+    const int jl = i * 16 + stream;
+    if (s0 + jl < s1) {
+      float vf[8];
+      unpack8(vr[i], vf);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int jl = (t + u) * 16 + stream;
-      if (s0 + jl < s1) {
-        float vf[8];
-        unpack8(rows[u], vf);
+      for (int g = 0; g < GP; ++g) {
+        if (g < G) {
+          const float p = p_lds[g][jl];
 #pragma unroll
-        for (int g = 0; g < GP; ++g) {
-          if (g < G) {
-            const float p = p_lds[g][jl];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
-          }
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
         }
       }
     }
   }
-  // Sum the 4 key streams of the wave (lane groups), then the 4 waves through LDS.
-#pragma unroll
-  for (int g = 0; g < GP; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = acc[g][e];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      acc[g][e] = x;
-    }
-  if (grp == 0) {
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) red[wave][g][li * 8 + e] = acc[g][e];
-  }
-  __syncthreads();
+
+  // Sum the 16 key streams through LDS, kPass query heads per pass.
   const int Hq = a.Hkv * G;
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kThreads) {
-    const int g = idx / kHeadDim, d = idx - g * kHeadDim;
-    const float o = red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d];
-    const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
-    a.ws_o[r * kHeadDim + d] = o;
-    if (d == 0) {
-      a.ws_ml[r * 2] = ml[g][0];
-      a.ws_ml[r * 2 + 1] = ml[g][1];
+#pragma unroll
+  for (int p0 = 0; p0 < GP; p0 += kPass) {
+    if (p0 > 0) __syncthreads();  // the previous pass has read red
+#pragma unroll
+    for (int gp = 0; gp < kPass; ++gp) {
+      float* dst = &red[stream][gp][li * 8];
+      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{acc[p0 + gp][0], acc[p0 + gp][1], acc[p0 + gp][2], acc[p0 + gp][3]};
+      *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{acc[p0 + gp][4], acc[p0 + gp][5], acc[p0 + gp][6], acc[p0 + gp][7]};
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kPass * kHeadDim; idx += kThreads) {
+      const int gp = idx / kHeadDim, d = idx - gp * kHeadDim;
+      const int g = p0 + gp;
+      if (g >= G) continue;
+      float o = 0.f;
+#pragma unroll
+      for (int st = 0; st < 16; ++st) o += red[st][gp][d];
+      const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
+      a.ws_o[r * kHeadDim + d] = o;
+      if (d == 0) {
+        a.ws_ml[r * 2] = ml[g][0];
+        a.ws_ml[r * 2 + 1] = ml[g][1];
+      }
     }
   }
 }
 
+constexpr int kMaxSplits = 1024;  // kv_len <= 262144
+
+// Block-wide (two waves) max / sum through a 2-slot LDS exchange.
+__device__ __forceinline__ float block2_max(float v, float* x) {
+  v = wave_max_dpp(v);
+  if ((threadIdx.x & 63) == 0) x[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(x[0], x[1]);
+  __syncthreads();
+  return v;
+}
+__device__ __forceinline__ float block2_sum(float v, float* x) {
+  v = wave_sum_dpp(v);
+  if ((threadIdx.x & 63) == 0) x[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = x[0] + x[1];
+  __syncthreads();
+  return v;
+}
+
 __global__ void __launch_bounds__(kHeadDim) attn_combine_kernel(AttnArgs a) {
+  static_assert(kHeadDim == 128, "two waves per row");
+  __shared__ float w_lds[kMaxSplits];
+  __shared__ float xch[2];
   const int row = blockIdx.x;  // b*Hq + hq
   const int Hq = a.Hkv * a.G;
   const int b = row / Hq;
@@ -210,15 +261,27 @@ __global__ void __launch_bounds__(kHeadDim) attn_combine_kernel(AttnArgs a) {
   const float* ml = a.ws_ml + static_cast<int64_t>(row) * a.splits * 2;
   const float* o = a.ws_o + static_cast<int64_t>(row) * a.splits * kHeadDim;
   const int used = (live_length(a) + kSplit - 1) / kSplit;
-  float M = -INFINITY;
-  for (int s = 0; s < used; ++s) M = fmaxf(M, ml[2 * s]);
-  float l = 0.f, acc = 0.f;
-  for (int s = 0; s < used; ++s) {
+  float m = -INFINITY;
+  for (int s = d; s < used; s += kHeadDim) m = fmaxf(m, ml[2 * s]);
+  const float M = block2_max(m, xch);
+  float l = 0.f;
+  for (int s = d; s < used; s += kHeadDim) {
     const float w = expf(ml[2 * s] - M);
+    w_lds[s] = w;
     l += ml[2 * s + 1] * w;
-    acc += o[static_cast<int64_t>(s) * kHeadDim + d] * w;
   }
-  a.out[b * a.o_sb + hq * a.o_sh + d] = skv::f2bf(acc / l);
+  const float inv = 1.f / block2_sum(l, xch);  // the barriers also publish w_lds
+  float acc = 0.f;
+  int s = 0;
+  for (; s + 8 <= used; s += 8) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = o[static_cast<int64_t>(s + u) * kHeadDim + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = fmaf(w_lds[s + u], x[u], acc);
+  }
+  for (; s < used; ++s) acc = fmaf(w_lds[s], o[static_cast<int64_t>(s) * kHeadDim + d], acc);
+  a.out[b * a.o_sb + hq * a.o_sh + d] = skv::f2bf(acc * inv);
 }
 
 int splits_for(int kv_len) { return (kv_len + kSplit - 1) / kSplit; }
@@ -256,6 +319,10 @@ extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int
       q_stride_b % 8 || q_stride_h % 8 || kv_stride_b % 8 || kv_stride_h % 8 || kv_stride_s % 8) {
     skv_set_error("%s: q/K/V rows must be 16-byte aligned", what);
     return SKV_EINVAL;
+  }
+  if (splits_for(kv_len) > kMaxSplits) {
+    skv_set_error("%s: kv_len=%d exceeds %d", what, kv_len, kMaxSplits * kSplit);
+    return SKV_EUNSUPPORTED;
   }
   const int64_t need = skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len);
   if (workspace_bytes < need) {
