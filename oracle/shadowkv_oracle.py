@@ -315,10 +315,12 @@ def encode_layer(k_pre: torch.Tensor, v: torch.Tensor, q_pre_last: torch.Tensor,
 
 
 def decode_layer_step(st: LayerState, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
-                      cos_sin: torch.Tensor, gen_offset: int = 0) -> dict:
+                      cos_sin: torch.Tensor, gen_offset: int = 0, scores: torch.Tensor | None = None) -> dict:
     """One decode step of one layer (models/attention/shadow.py:22-50 with the offload class).
 
     q [B, Hq, D] post-RoPE query, k_new/v_new [B, H, D] post-RoPE key and value of the new token.
+    scores: optional GQA-max chunk scores [B, H, n] to select from instead of computing them (so a
+    device implementation's selection can be checked bit for bit from identical scores).
     Mutates st (buffers, position_ids) like the cache does and returns the intermediates."""
     B, H, n, D = st.landmarks.shape
     Hq = q.shape[1]
@@ -327,7 +329,10 @@ def decode_layer_step(st: LayerState, q: torch.Tensor, k_new: torch.Tensor, v_ne
     L = st.sparse_end + gen_offset + 1
     st.kbuf[:, :, L - 1] = k_new
     st.vbuf[:, :, L - 1] = v_new
-    scores = score_gqa_max(q.reshape(B * H, G, D), st.landmarks.reshape(B * H, n, D), 1.0 / math.sqrt(128))
+    if scores is None:
+        scores = score_gqa_max(q.reshape(B * H, G, D), st.landmarks.reshape(B * H, n, D), 1.0 / math.sqrt(128))
+    else:
+        scores = scores.reshape(B * H, n).to(torch.bfloat16)
     selected = topk_gather(scores, st.landmark_idx.reshape(B * H, n), S)
     ids, offs, cnts = reorder(st.position_ids.reshape(B * H, S).numpy(), selected.numpy())
     E = st.chunk * D

@@ -50,30 +50,6 @@ __device__ __forceinline__ int live_length(const AttnArgs& a) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// Reductions over a wave without LDS round trips: rotations within each 16-lane row (DPP
-// row_ror), then the four row results read back as wave-uniform values.
-template <int N>
-__device__ __forceinline__ float row_ror(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float lane_value(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, row_ror<8>(v));
-  v = fmaxf(v, row_ror<4>(v));
-  v = fmaxf(v, row_ror<2>(v));
-  v = fmaxf(v, row_ror<1>(v));
-  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += row_ror<8>(v);
-  v += row_ror<4>(v);
-  v += row_ror<2>(v);
-  v += row_ror<1>(v);
-  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
-}
-
 template <int GP>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   // Up to 4 query heads per kv head, the split's K and V rows are all requested at entry (one
@@ -162,7 +138,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       x[u] = p_lds[g][lane * 4 + u];
       mx = fmaxf(mx, x[u]);
     }
-    mx = wave_max_dpp(mx);
+    mx = skv::wave_max_dpp(mx);
     float l = 0.f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -170,7 +146,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       p_lds[g][lane * 4 + u] = e;
       l += e;
     }
-    l = wave_sum_dpp(l);
+    l = skv::wave_sum_dpp(l);
     if (lane == 0) {
       ml[g][0] = mx;
       ml[g][1] = l;
@@ -233,7 +209,7 @@ constexpr int kMaxSplits = 1024;  // kv_len <= 262144
 
 // Block-wide (two waves) max / sum through a 2-slot LDS exchange.
 __device__ __forceinline__ float block2_max(float v, float* x) {
-  v = wave_max_dpp(v);
+  v = skv::wave_max_dpp(v);
   if ((threadIdx.x & 63) == 0) x[threadIdx.x >> 6] = v;
   __syncthreads();
   v = fmaxf(x[0], x[1]);
@@ -241,7 +217,7 @@ __device__ __forceinline__ float block2_max(float v, float* x) {
   return v;
 }
 __device__ __forceinline__ float block2_sum(float v, float* x) {
-  v = wave_sum_dpp(v);
+  v = skv::wave_sum_dpp(v);
   if ((threadIdx.x & 63) == 0) x[threadIdx.x >> 6] = v;
   __syncthreads();
   v = x[0] + x[1];

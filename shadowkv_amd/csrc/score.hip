@@ -8,11 +8,12 @@
 //
 // The landmark matrix B is the only large operand (n x 128 bf16 per z), so the design is a
 // memory-streaming one, not a GEMM tiling:
-//   logits_kernel: workgroup = 256 landmarks of one z (grid n/256 x batch); 16 lanes cover one
-//     256-byte landmark row with 16-byte loads (a wave reads 4 rows = 1 KB contiguous); the m
-//     queries sit in registers; the m partial dots are combined with a 16-lane reduce-scatter;
-//     logits are staged in LDS, written out coalesced, and the tile's max and sum(exp) partials
-//     go to norm/sum [z][i][tile] (the reference's 256-column partial layout).
+//   logits_kernel: workgroup = 256 landmarks of one z (grid n/256 x batch), every landmark byte
+//     requested at entry; the dots run on v_mfma_f32_16x16x32_bf16 with the (up to 16) queries
+//     as the A rows and 16 landmarks as the B columns, so each lane ends up holding finished
+//     dots (no cross-lane reduction); logits are staged in LDS, written out coalesced, and the
+//     tile's max and sum(exp) partials (DPP wave reductions) go to norm/sum [z][i][tile] (the
+//     reference's 256-column partial layout).
 //   softmax_kernel: each workgroup merges the partials of its z, then normalises its 256
 //     columns for every query row and keeps the running max over rows.
 #include "wave_reduce.h"
@@ -35,6 +36,9 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   }
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 template <int M>
 __global__ void __launch_bounds__(kThreads) logits_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                           uint16_t* __restrict__ D, float* __restrict__ norm,
@@ -46,48 +50,44 @@ __global__ void __launch_bounds__(kThreads) logits_kernel(const uint16_t* __rest
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15;
   const int grp = lane >> 4;
+  constexpr int kGroups = kTile / 4 / 16;  // 16-landmark MFMA groups per wave
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  float q[M][8];
+  // B operand: lane (li, grp) holds landmark wave*64 + 16*kg + li, dims [32*ks + 8*grp, +8).
+  const uint16_t* Bz = B + static_cast<int64_t>(z) * n * kHeadDim + 8 * grp;
+  u32x4 lf[kGroups][4];
 #pragma unroll
-  for (int i = 0; i < M; ++i) {
-    if (i < m) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(A + (static_cast<int64_t>(z) * m + i) * kHeadDim + li * 8);
-      unpack8(v, q[i]);
-    } else {
+  for (int kg = 0; kg < kGroups; ++kg) {
+    const int j = tile * kTile + wave * (kTile / 4) + 16 * kg + li;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) q[i][e] = 0.f;
+    for (int ks = 0; ks < 4; ++ks) {
+      lf[kg][ks] = zero4;
+      if (j < n) lf[kg][ks] = *reinterpret_cast<const u32x4*>(Bz + static_cast<int64_t>(j) * kHeadDim + 32 * ks);
     }
   }
-
-  const uint16_t* Bz = B + static_cast<int64_t>(z) * n * kHeadDim;
-  const int owner = skv::rs16_owner<M>(li);
-  const bool writer = skv::rs16_writer<M>(li) && owner < m;
-  // Each wave owns kTile/4 = 64 landmarks, 4 per step (one per 16-lane group): 16 steps.
-  constexpr int kSteps = kTile / 16;
-  u32x4 rows[kSteps];
+  // A operand: lane (li, grp) holds query li (zero rows past m), same dims.
+  u32x4 qf[4];
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) {  // issue all of this lane's row loads up front
-    const int jl = wave * (kTile / 4) + s * 4 + grp;
-    const int j = tile * kTile + jl;
-    rows[s] = u32x4{0u, 0u, 0u, 0u};
-    if (j < n) rows[s] = *reinterpret_cast<const u32x4*>(Bz + static_cast<int64_t>(j) * kHeadDim + li * 8);
+  for (int ks = 0; ks < 4; ++ks) {
+    qf[ks] = zero4;
+    if (li < m)
+      qf[ks] = *reinterpret_cast<const u32x4*>(A + (static_cast<int64_t>(z) * m + li) * kHeadDim + 32 * ks + 8 * grp);
   }
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) {
-    const int jl = wave * (kTile / 4) + s * 4 + grp;
+  for (int kg = 0; kg < kGroups; ++kg) {
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qf[ks]),
+                                                  __builtin_bit_cast(bf16x8_t, lf[kg][ks]), d, 0, 0, 0);
+    // D[query 4*grp + v][landmark li]
+    const int jl = wave * (kTile / 4) + 16 * kg + li;
     const int j = tile * kTile + jl;
-    float l[8];
-    unpack8(rows[s], l);
-    float v[M];
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-      float acc = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc = fmaf(q[i][e], l[e], acc);
-      v[i] = acc;
+    for (int v = 0; v < 4; ++v) {
+      const int i = 4 * grp + v;
+      if (i < m && i < M) s_tile[i][jl] = (j < n) ? skv::bf2f(skv::f2bf(alpha * d[v])) : -INFINITY;
     }
-    const float dot = skv::reduce_scatter16<M>(v, li);
-    if (writer) s_tile[owner][jl] = (j < n) ? skv::bf2f(skv::f2bf(alpha * dot)) : -INFINITY;
   }
   __syncthreads();
 
@@ -111,11 +111,11 @@ __global__ void __launch_bounds__(kThreads) logits_kernel(const uint16_t* __rest
       for (int u = 0; u < 4; ++u)
         if (j0 + u < n) Drow[j0 + u] = skv::f2bf(x[u]);
     }
-    mx = skv::wave_max(mx);
+    mx = skv::wave_max_dpp(mx);
     float se = 0.f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) se += (x[u] == -INFINITY) ? 0.f : expf(x[u] - mx);
-    se = skv::wave_sum(se);
+    se = skv::wave_sum_dpp(se);
     if (lane == 0) {
       norm[(static_cast<int64_t>(z) * m + i) * tiles + tile] = mx;
       sum[(static_cast<int64_t>(z) * m + i) * tiles + tile] = se;

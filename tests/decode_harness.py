@@ -60,3 +60,40 @@ def run_decode_step_gpu(case, device, cache=None):
                 offsets=cache.offsets.view(B * H, -1).cpu().numpy(), position_ids=cache.position_ids[0].cpu().numpy(),
                 kbuf=cache.k_cache_buffer[0, :, :, :L].cpu(), vbuf=cache.v_cache_buffer[0, :, :, :L].cpu(),
                 scores=cache.chunk_attn.cpu(), selected=cache.selected_chunks.cpu(), cache=cache)
+
+
+def assert_bf16_close(got: torch.Tensor, want: torch.Tensor, floor: float = 1e-5, what: str = ""):
+    """fp32 sums taken in another order then rounded to bf16: at most one bf16 ulp of the larger
+    magnitude apart, plus an absolute floor for values produced by cancellation."""
+    g, w = got.float(), want.float()
+    m = torch.maximum(g.abs(), w.abs()).clamp_min(2.0 ** -126)
+    ulp = torch.exp2(torch.floor(torch.log2(m)) - 7)
+    bad = (g - w).abs() > ulp + floor
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond one rounding step, max diff {(g - w).abs().max():.3e}"
+
+
+def check_scoring(cache, q, landmarks):
+    """The scoring stage of one decode step against the oracle: the bf16 logits (gemm_o) within one
+    rounding step of the oracle's, and the GQA-max probabilities (chunk_attn) within one rounding
+    step of the oracle's softmax taken over the device's own logits (a logit one bf16 ulp away
+    moves its exp by up to a few percent, so probabilities are compared from identical logits).
+    q [B, Hq, D] and landmarks [B, H, n, D] on the CPU."""
+    import oracle
+    B, H, n, D = landmarks.shape
+    G = q.shape[1] // H
+    logits_dev = cache.gemm_o.cpu().view(B * H, G, n)
+    logits_ref, _ = oracle.score_logits_softmax(q.reshape(B * H, G, D), landmarks.reshape(B * H, n, D),
+                                                1.0 / 128 ** 0.5)
+    assert_bf16_close(logits_dev, logits_ref, what="logits")
+    probs = torch.softmax(logits_dev.float(), dim=-1).to(torch.bfloat16).max(dim=1).values
+    assert_bf16_close(cache.chunk_attn.cpu().view(B * H, n), probs, what="gqa-max probabilities")
+
+
+def fresh_oracle_state(case):
+    """An oracle LayerState holding the fixture's post-prefill state (a copy)."""
+    import oracle
+    d, st = case["dims"], case["st"]
+    kw = {k: v.clone() for k, v in case["state_in"].items()}
+    return oracle.LayerState(**kw, prefill_local=st.prefill_local, sparse_start=st.sparse_start,
+                             sparse_end=st.sparse_end, chunk=d["chunk"], budget=d["budget"], ctx=d["ctx"],
+                             buf_len=st.buf_len)

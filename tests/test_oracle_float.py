@@ -163,3 +163,19 @@ def test_decode_small_fixture_regression():
     assert np.array_equal(st.position_ids.numpy(), d["out_position_ids"])
     assert np.array_equal(res["out"].view(torch.int16).numpy(), d["out_attn"])
     assert [make_golden.digest(st.kbuf), make_golden.digest(st.vbuf)] == d["out_digests"].tolist()
+
+
+def test_decode_step_from_given_scores_matches_computed():
+    """decode_layer_step(scores=...) with the oracle's own scores reproduces the committed fixture."""
+    import numpy as np
+    from tests.decode_harness import fresh_oracle_state
+    from tests.golden import make_golden
+    case = make_golden.decode_small_case()
+    d = np.load(make_golden.HERE / "decode_small.npz")
+    st = fresh_oracle_state(case)
+    res = oracle.decode_layer_step(st, case["q"], case["k_new"], case["v_new"], case["cos_sin"],
+                                   scores=case["res"]["scores"])
+    assert np.array_equal(res["cnts"], d["out_cnts"])
+    assert np.array_equal(res["offsets"], d["out_offsets"])
+    assert np.array_equal(st.position_ids.numpy(), d["out_position_ids"])
+    assert torch.equal(res["out"], case["res"]["out"])
