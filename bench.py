@@ -48,9 +48,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=1, help="independent batch slices interleaved per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
-    p.add_argument("--workload", choices=["decode", "rebuild", "attention"], default="decode",
+    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select"], default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
-                        "attention: the sparse decode attention alone")
+                        "attention: the sparse decode attention alone; select: the fused chunk selection alone")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -351,6 +351,57 @@ def attention_microbench(args) -> int:
     return 0
 
 
+def select_microbench(args) -> int:
+    """Fused chunk selection alone (softmax normalisation, GQA max, top-k, id gather, cache-hit
+    reorder) at the decode shapes, on logits produced by the scoring kernel. Latency-bound (few
+    rows, a serial selection per row): reported in microseconds. One JSON line per shape."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    reps = max(args.steps, 4)
+    for name, B, H, G, n, S in (("Llama-3-8B 122K", 8, 8, 4, 15304, 256), ("Llama-3-8B 122K", 24, 8, 4, 15304, 256),
+                                ("GLM-4-9B 262K", 4, 2, 16, 32712, 256), ("Llama-3-8B-1M", 1, 8, 4, 130680, 2048)):
+        g = torch.Generator(device="cuda").manual_seed(n + B)
+        rows = B * H
+        chunks = n + 48 + 8
+        q = torch.randn(rows, G, 128, generator=g, device="cuda").to(torch.bfloat16)
+        lm = torch.randn(rows, n, 128, generator=g, device="cuda").to(torch.bfloat16)
+        tiles = (n + 255) // 256
+        D = torch.empty(rows, G, n, dtype=torch.bfloat16, device="cuda")
+        norm = torch.empty(rows, G, tiles, dtype=torch.float32, device="cuda")
+        ssum = torch.empty_like(norm)
+        shadowkv.score_logits(q, lm, D, norm, ssum, rows, G, n, 128, 1.0 / math.sqrt(128))
+        del lm
+        lidx = torch.stack([torch.randperm(chunks, generator=g, device="cuda")[:n].sort().values for _ in range(rows)])
+        pos0 = torch.stack([lidx[r, torch.randperm(n, generator=g, device="cuda")[:S]] for r in range(rows)])
+        pos = pos0.clone()
+        offsets = torch.empty(rows * S, dtype=torch.int32, device="cuda")
+        cnts = torch.empty(rows, dtype=torch.int32, device="cuda")
+        scores = torch.empty(rows, n, dtype=torch.bfloat16, device="cuda")
+
+        def run():
+            pos.copy_(pos0)
+            shadowkv.select_chunks(D, norm, ssum, rows, G, n, lidx, S, chunks, pos, offsets, cnts, out_scores=scores)
+
+        t_all = gpu_time_per_call(run, reps)
+        t_copy = gpu_time_per_call(lambda: pos.copy_(pos0), reps)
+        t = t_all - t_copy
+        out_line = {"metric": "fused chunk selection latency", "value": round(t * 1e6, 2), "unit": "us",
+                    "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
+                    "higher_is_better": False, "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
+                    "data": "synthetic: logits of random q / landmarks from the scoring kernel; timed as HIP-graph "
+                            "replays (minus the replayed slot-restore copy)",
+                    "config": {"workload": f"{name} selection: {rows} rows x {G} queries x {n} landmarks, top {S}",
+                               "rows": rows, "m": G, "n": n, "select_sets": S},
+                    "roofline": {"kernel": "select_kernel", "bound": "latency", "achieved": None, "peak": None,
+                                 "unit": "us", "frac": None, "traffic": None,
+                                 "algorithmic_bytes_per_launch": rows * (G * n * 2 + n * 8 + S * 28),
+                                 "avg_launch_us": round(t * 1e6, 2)},
+                    "cpu_baseline": None}
+        print(json.dumps(out_line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -361,6 +412,8 @@ def main() -> int:
         return rebuild_microbench(args)
     if args.workload == "attention":
         return attention_microbench(args)
+    if args.workload == "select":
+        return select_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv

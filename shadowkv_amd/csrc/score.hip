@@ -137,10 +137,10 @@ __global__ void __launch_bounds__(kThreads) softmax_kernel(const uint16_t* __res
     const float* sr = sum + (static_cast<int64_t>(z) * m + i) * tiles;
     float mx = -INFINITY;
     for (int t = lane; t < tiles; t += 64) mx = fmaxf(mx, nr[t]);
-    mx = skv::wave_max(mx);
+    mx = skv::wave_max_dpp(mx);
     float s = 0.f;
     for (int t = lane; t < tiles; t += 64) s += sr[t] * expf(nr[t] - mx);
-    s = skv::wave_sum(s);
+    s = skv::wave_sum_dpp(s);
     if (lane == 0) {
       gmax[i] = mx;
       ginv[i] = 1.f / s;

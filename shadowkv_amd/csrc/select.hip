@@ -5,8 +5,9 @@
 // torch.max over the query-head group, torch.topk, the landmark-id gather, and
 // reorder_keys_and_compute_offsets (kernels/gather_copy.cu:189-235).
 //
-// One workgroup (16 wave64) per (batch, kv-head) row; thread t owns the contiguous landmarks
-// [t*E, t*E+E):
+// One workgroup (16 wave64) per (batch, kv-head) row; thread t owns a contiguous block of
+// landmarks (whole 8-landmark units when n % 8 == 0, so the logits of all m query rows arrive as
+// 16-byte vectors requested together, and keys move as 16-byte vectors):
 //   1. merge the per-256-column (max, sum exp) partials of every query row;
 //   2. p_j = max_i bf16(exp(D[i,j] - max_i) / sum_i), kept as 16-bit order keys in LDS (or in
 //      global scratch when n is too large), high-byte histogram with run-length-merged atomics;
@@ -22,12 +23,15 @@
 
 namespace {
 
+using skv::u32x4;
+
 constexpr int kThreads = 1024;
 constexpr int kMaxM = 16;
 constexpr int kMaxS = 2048;
 constexpr size_t kLdsBudget = 60 * 1024;  // dynamic LDS cap (static LDS adds ~1.4 KB)
 
 struct SelectArgs {
+  int vec;  // n % 8 == 0: 8-landmark units
   const uint16_t* D;
   const float* norm;
   const float* sum;
@@ -35,6 +39,7 @@ struct SelectArgs {
   const int64_t* lidx;
   int64_t lstride;
   int S, P, n_lds, words;  // words = bitmap words covering chunk ids [0, 32*words)
+  int keys_off;            // byte offset of the LDS key array
   int64_t* pos;
   int32_t* offsets;
   int32_t* cnts;
@@ -46,12 +51,18 @@ __device__ __forceinline__ int scan_excl(int v, int* scratch, int* total) {
   return skv::block_exclusive_scan(v, scratch, total);
 }
 
+__device__ __forceinline__ uint16_t half_of(const u32x4& v, int e) {
+  const uint32_t w = v[e >> 1];
+  return static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+template <int MP>
 __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint32_t* selmap = reinterpret_cast<uint32_t*>(smem);   // words
   uint32_t* oldmap = selmap + a.words;                     // words
   uint64_t* sorted = reinterpret_cast<uint64_t*>(oldmap + a.words);  // P, only with out_sel (8-byte aligned)
-  uint16_t* keys = reinterpret_cast<uint16_t*>(sorted + (a.out_sel ? a.P : 0));      // n_lds
+  uint16_t* keys = reinterpret_cast<uint16_t*>(smem + a.keys_off);                   // n_lds, 16-byte aligned
   __shared__ skv::TopkShared sh;
   __shared__ float gmax[kMaxM], ginv[kMaxM];
   __shared__ int sel_count;
@@ -69,10 +80,10 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
     const float* sr = a.sum + (static_cast<int64_t>(row) * m + i) * a.tiles;
     float mx = -INFINITY;
     for (int t = lane; t < a.tiles; t += 64) mx = fmaxf(mx, nr[t]);
-    mx = skv::wave_max(mx);
+    mx = skv::wave_max_dpp(mx);
     float s = 0.f;
     for (int t = lane; t < a.tiles; t += 64) s += sr[t] * expf(nr[t] - mx);
-    s = skv::wave_sum(s);
+    s = skv::wave_sum_dpp(s);
     if (lane == 0) {
       gmax[i] = mx;
       ginv[i] = 1.f / s;
@@ -88,36 +99,99 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
     if (id >= 0 && id < 32ll * a.words) atomicOr(&oldmap[id >> 5], 1u << (id & 31));
   }
 
-  const int E = (n + kThreads - 1) / kThreads;
-  const int lo = min(tid * E, n), hi = min(lo + E, n);
+  // Blocked ownership in units of kU landmarks; index order is unit order is thread order.
+  const int kU = a.vec ? 8 : 1;
+  const int nu = (n + kU - 1) / kU;
+  const int Eu = (nu + kThreads - 1) / kThreads;
+  const int ulo = min(tid * Eu, nu), uhi = min(ulo + Eu, nu);
+  const int lo = ulo * kU, hi = min(uhi * kU, n);
   const uint16_t* Drow = a.D + static_cast<int64_t>(row) * m * n;
   uint16_t* srow = a.out_scores ? a.out_scores + static_cast<int64_t>(row) * n : nullptr;
-  {
-    uint32_t run_bin = 0xffffffffu, run = 0;
-    for (int j = lo; j < hi; ++j) {
-      float best = -INFINITY;
-      for (int i = 0; i < m; ++i) {
-        const uint16_t p = skv::f2bf(expf(skv::bf2f(Drow[static_cast<int64_t>(i) * n + j]) - gmax[i]) * ginv[i]);
+  auto prob_max = [&](float (&dv)[MP]) -> uint16_t {  // bf16 of max_i bf16(softmax_i)
+    float best = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MP; ++i) {
+      if (i < m) {
+        const uint16_t p = skv::f2bf(expf(dv[i] - gmax[i]) * ginv[i]);
         best = fmaxf(best, skv::bf2f(p));
       }
-      const uint16_t b = skv::f2bf(best);
-      const uint32_t key = skv::bf16_order_key(b);
-      if (a.n_lds) keys[j] = static_cast<uint16_t>(key);
-      if (srow) srow[j] = b;
-      if ((key >> 8) != run_bin) {
+    }
+    return skv::f2bf(best);
+  };
+  {
+    uint32_t run_bin = 0xffffffffu, run = 0;
+    auto count = [&](uint32_t bin) {
+      if (bin != run_bin) {
         if (run) atomicAdd(&sh.hist[run_bin], run);
-        run_bin = key >> 8;
+        run_bin = bin;
         run = 0;
       }
       ++run;
+    };
+    if (a.vec) {
+      for (int u = ulo; u < uhi; ++u) {
+        u32x4 dv[MP];
+#pragma unroll
+        for (int i = 0; i < MP; ++i) {  // every query row's 8 logits requested before any math
+          dv[i] = u32x4{0u, 0u, 0u, 0u};
+          if (i < m) dv[i] = *reinterpret_cast<const u32x4*>(Drow + static_cast<int64_t>(i) * n + 8 * u);
+        }
+        uint32_t kw[4], bw[4];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float x[MP];
+#pragma unroll
+          for (int i = 0; i < MP; ++i) x[i] = skv::bf2f(half_of(dv[i], e));
+          const uint16_t b = prob_max(x);
+          const uint32_t key = skv::bf16_order_key(b);
+          if (e & 1) {
+            kw[e >> 1] |= key << 16;
+            bw[e >> 1] |= static_cast<uint32_t>(b) << 16;
+          } else {
+            kw[e >> 1] = key;
+            bw[e >> 1] = b;
+          }
+          count(key >> 8);
+        }
+        if (a.n_lds) *reinterpret_cast<u32x4*>(&keys[8 * u]) = u32x4{kw[0], kw[1], kw[2], kw[3]};
+        if (srow) *reinterpret_cast<u32x4*>(&srow[8 * u]) = u32x4{bw[0], bw[1], bw[2], bw[3]};
+      }
+    } else {
+      for (int j = lo; j < hi; ++j) {
+        float x[MP];
+#pragma unroll
+        for (int i = 0; i < MP; ++i) x[i] = i < m ? skv::bf2f(Drow[static_cast<int64_t>(i) * n + j]) : 0.f;
+        const uint16_t b = prob_max(x);
+        const uint32_t key = skv::bf16_order_key(b);
+        if (a.n_lds) keys[j] = static_cast<uint16_t>(key);
+        if (srow) srow[j] = b;
+        count(key >> 8);
+      }
     }
     if (run) atomicAdd(&sh.hist[run_bin], run);
   }
   __syncthreads();
-  auto key_of = [&](int j) -> uint32_t {
-    return a.n_lds ? static_cast<uint32_t>(keys[j]) : skv::bf16_order_key(srow[j]);
+  // The keys of this thread's block, 8 at a time where the unit allows: f(j, key) for j in [lo, hi).
+  auto for_keys = [&](auto&& f) {
+    if (a.vec) {
+      for (int u = ulo; u < uhi; ++u) {
+        uint32_t k8[8];
+        if (a.n_lds) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&keys[8 * u]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) k8[e] = half_of(v, e);
+        } else {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&srow[8 * u]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) k8[e] = skv::bf16_order_key(half_of(v, e));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f(8 * u + e, k8[e]);
+      }
+    } else {
+      for (int j = lo; j < hi; ++j) f(j, a.n_lds ? static_cast<uint32_t>(keys[j]) : skv::bf16_order_key(srow[j]));
+    }
   };
-
   skv::select_bin(sh.hist, S, sh.found);
   const uint32_t b1 = static_cast<uint32_t>(sh.found[0]);
   const int above1 = sh.found[1];
@@ -126,16 +200,15 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   __syncthreads();
   {
     uint32_t run_bin = 0xffffffffu, run = 0;
-    for (int j = lo; j < hi; ++j) {
-      const uint32_t kj = key_of(j);
-      if ((kj >> 8) != b1) continue;
+    for_keys([&](int, uint32_t kj) {
+      if ((kj >> 8) != b1) return;
       if ((kj & 255u) != run_bin) {
         if (run) atomicAdd(&sh.hist[run_bin], run);
         run_bin = kj & 255u;
         run = 0;
       }
       ++run;
-    }
+    });
     if (run) atomicAdd(&sh.hist[run_bin], run);
   }
   __syncthreads();
@@ -145,19 +218,18 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
 
   // Rank the ties in index order (blocked ownership makes the scan order the index order).
   int my_eq = 0;
-  for (int j = lo; j < hi; ++j) my_eq += key_of(j) == T;
+  for_keys([&](int, uint32_t kj) { my_eq += kj == T; });
   int total_eq = 0;
   int eq_rank = scan_excl(my_eq, sh.scan, &total_eq);
   const int64_t* lrow = a.lidx + static_cast<int64_t>(row) * a.lstride;
-  for (int j = lo; j < hi; ++j) {
-    const uint32_t kj = key_of(j);
+  for_keys([&](int j, uint32_t kj) {
     bool win = kj > T;
     if (kj == T) win = eq_rank++ < need_eq;
-    if (!win) continue;
+    if (!win) return;
     const int64_t id = lrow[j];
     if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
     if (a.out_sel) sorted[atomicAdd(&sel_count, 1)] = (static_cast<uint64_t>(0xffffu - kj) << 32) | static_cast<uint32_t>(j);
-  }
+  });
   __syncthreads();
 
   // Hits in previous-slot order.
@@ -239,7 +311,7 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
   int P = 64;
   while (P < select_sets) P <<= 1;
   const int words = (num_chunks + 31) / 32;
-  const size_t fixed = static_cast<size_t>(words) * 8 + (out_selected ? static_cast<size_t>(P) * 8 : 0);
+  const size_t fixed = (static_cast<size_t>(words) * 8 + (out_selected ? static_cast<size_t>(P) * 8 : 0) + 15) / 16 * 16;
   if (fixed > kLdsBudget) {
     skv_set_error("%s: %d chunks need %zu bytes of bitmap, above the LDS budget", what, num_chunks, fixed);
     return SKV_EUNSUPPORTED;
@@ -250,6 +322,9 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
     return SKV_EINVAL;
   }
   SelectArgs a{};
+  a.vec = (n % 8 == 0 && (reinterpret_cast<uintptr_t>(D) & 15u) == 0 &&
+           (!out_scores || (reinterpret_cast<uintptr_t>(out_scores) & 15u) == 0));
+  a.keys_off = static_cast<int>(fixed);
   a.D = D;
   a.norm = norm;
   a.sum = sum;
@@ -268,7 +343,10 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
   a.out_scores = out_scores;
   a.out_sel = out_selected;
   const size_t lds = fixed + static_cast<size_t>(n_lds) * 2;
-  hipLaunchKernelGGL(select_kernel, dim3(rows), dim3(kThreads), (lds + 15) / 16 * 16, static_cast<hipStream_t>(stream),
-                     a);
+  const size_t ldsb = (lds + 15) / 16 * 16;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (m <= 4) hipLaunchKernelGGL(select_kernel<4>, dim3(rows), dim3(kThreads), ldsb, st, a);
+  else if (m <= 8) hipLaunchKernelGGL(select_kernel<8>, dim3(rows), dim3(kThreads), ldsb, st, a);
+  else hipLaunchKernelGGL(select_kernel<16>, dim3(rows), dim3(kThreads), ldsb, st, a);
   return skv_check_launch(what);
 }

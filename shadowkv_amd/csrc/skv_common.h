@@ -96,13 +96,16 @@ __device__ __forceinline__ float group16_sum(float v) {
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the wave on DPP: shifts within each 16-lane row (lanes shifted in
+// from outside the row read 0), then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15), then the total of rows 0-1 into rows 2-3 (row_bcast:31).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    int n = __shfl_up(v, o, kWave);
-    if (lane >= o) v += n;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
   return v;
 }
 
@@ -115,14 +118,11 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* to
   int inc = wave_inclusive_scan(v);
   if (lane == kWave - 1) scratch[wave] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int w = 0; w < nwaves; ++w) {
-      int t = scratch[w];
-      scratch[w] = run;
-      run += t;
-    }
-    scratch[nwaves] = run;
+  if (threadIdx.x < kWave) {  // wave 0 scans the per-wave totals (nwaves <= 16)
+    const int t = lane < nwaves ? scratch[lane] : 0;
+    const int incl = wave_inclusive_scan(t);
+    if (lane < nwaves) scratch[lane] = incl - t;
+    if (lane == nwaves - 1) scratch[nwaves] = incl;
   }
   __syncthreads();
   int excl = scratch[wave] + inc - v;
