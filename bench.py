@@ -46,7 +46,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--ctx", type=int, default=122880)
     p.add_argument("--budget", type=int, default=2048)
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
-    p.add_argument("--lanes", type=int, default=1, help="independent batch slices interleaved per layer")
+    p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
     p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select"], default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "

@@ -210,6 +210,38 @@ int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stri
                            int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
                            void* stream);
 
+/* ---- new-token operations around the path (fused) ------------------------------------
+ * skv_rmsnorm replaces the residual add + flashinfer rmsnorm pair of the reference model
+ * (models/llama.py:110-112 with models/tensor_op.py:39-44): with residual non-null,
+ *   residual_out[r] = bf16(x[r] + residual[r])        (the bf16 residual add)
+ *   out[r] = bf16(h * rsqrt(mean(h^2) + eps) * weight), h = residual_out[r] in fp32;
+ * with residual null, h = x[r]. rows of `hidden` bf16 (a multiple of 8, at most 8192), all rows
+ * 16-byte aligned (strides in elements, multiples of 8). */
+int skv_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t residual_stride,
+                uint16_t* residual_out, int64_t residual_out_stride, const uint16_t* weight, uint16_t* out,
+                int64_t out_stride, int rows, int hidden, float eps, void* stream);
+
+/* Replaces vllm silu_and_mul (models/llama.py:114-118): out[r, j] = bf16(silu(x[r, j]) * x[r, d + j])
+ * in fp32, j < d (a multiple of 8); rows 16-byte aligned. */
+int skv_silu_and_mul(const uint16_t* x, int64_t x_stride, uint16_t* out, int64_t out_stride, int rows, int d,
+                     void* stream);
+
+/* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:55-56) and the
+ * KV append of update_kv_cache (models/kvcache/shadow.py:621-633) in one launch. qkv row of batch b:
+ * [q_heads*128 | kv_heads*128 (k) | kv_heads*128 (v)] at qkv + b*qkv_stride_b. q and k are rotated
+ * at positions[b] with the bf16 per-op rounding of the reference (rope_mode 0: half-split with
+ * cos_sin rows [cos(64)|sin(64)]; 1: GLM interleaved pairs on dims 0..63, cos_sin [cos(32)|sin(32)]);
+ * positions outside [0, cos_sin_rows) leave q/k unrotated. Rotated q goes to q_out[b, h, :]
+ * (row stride q_out_stride_b, head stride 128); rotated k and raw v go to row *append_row (a
+ * device int64, read when the kernel runs) of the key/value buffers
+ * (cache + b*kv_stride_b + h*kv_stride_h + row*kv_stride_s); a row outside [0, buf_len) is not
+ * written. The qkv buffer itself is not modified. */
+int skv_rope_qk_append(const uint16_t* qkv, int64_t qkv_stride_b, int batch_size, int q_heads, int kv_heads,
+                       int head_dim, const int64_t* positions, const uint16_t* cos_sin, int64_t stride_cos_sin,
+                       int64_t cos_sin_rows, int rope_mode, uint16_t* q_out, int64_t q_out_stride_b,
+                       uint16_t* k_cache, uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
+                       int64_t kv_stride_s, const int64_t* append_row, int64_t buf_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

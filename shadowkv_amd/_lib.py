@@ -48,6 +48,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_select_chunks": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p]),
     "skv_topk_gather": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p]),
     "skv_sparse_attn_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "skv_rmsnorm": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "skv_silu_and_mul": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p]),
+    "skv_rope_qk_append": (
+        _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
+               _i64, _p]),
     "skv_sparse_attn_decode": (
         _i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p, _f32, _p, _i64, _p,
                _i64, _i64, _p]),

@@ -139,8 +139,11 @@ class SyntheticDecoder:
 
     def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
-                 dtype=torch.bfloat16, lanes: int = 1):
+                 dtype=torch.bfloat16, lanes: int = 1, fused: bool = True):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
+        # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels
+        # (libshadowkv_amd), instead of separate torch operations
+        self.fused = fused
         s = shape
         D = s.head_dim
         if lanes < 1 or batch % lanes:
@@ -174,6 +177,13 @@ class SyntheticDecoder:
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
                                         self.cos_sin)
             cache.use_device_lengths()
+            if lanes > 1:
+                # All lanes share one value-fetch stream and one key-rebuild stream (their fetches
+                # follow one another on the host link anyway); taking the key rebuild off the
+                # compute stream keeps it out of the stretch between two lanes' fetches.
+                if i == 0:
+                    shared = (cache.copy_stream, torch.cuda.Stream(device=device))
+                cache.copy_stream, cache.key_stream = shared
             self.lanes.append(lane)
         self.cache = self.lanes[0].cache  # lane 0's cache (shapes are identical across lanes)
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
@@ -202,23 +212,49 @@ class SyntheticDecoder:
     def _norm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         return F.rms_norm(x, (x.shape[-1],), w, self.shape.eps)
 
-    def _layer_begin(self, idx: int, h: torch.Tensor, lane: _Lane):
-        """Norm, fused QKV and the first half of the attention handler (value fetch in flight)."""
+    def _layer_begin(self, idx: int, state, lane: _Lane):
+        """Norm, fused QKV and the first half of the attention handler (value fetch in flight).
+        state: the residual stream h, or (h, x) with x = this layer's normalised input (fused)."""
         s, D = self.shape, self.shape.head_dim
-        b = h.shape[0]
         lw = self.layers[idx]
+        if self.fused:
+            h, x = state
+            b = h.shape[0]
+            qkv = F.linear(x, lw.wqkv)
+            q_out = torch.empty(b, s.heads, D, dtype=self.dtype, device=self.device)
+            q = lane.cache.rope_and_append(qkv.view(b, -1), self.pos[lane.rows], self.cos_sin, idx, q_out)
+            return lane.attn.decode_begin_appended(q, idx)
+        h = state
+        b = h.shape[0]
         x = self._norm(h, lw.in_norm)
         qkv = F.linear(x, lw.wqkv)
         q, k, v = qkv.split([s.heads * D, s.kv_heads * D, s.kv_heads * D], dim=-1)
         v = v.view(b, 1, s.kv_heads, D).transpose(1, 2)
         return lane.attn.decode_begin(q, k, v, self.pos[lane.rows], idx)
 
-    def _layer_end(self, idx: int, h: torch.Tensor, lane: _Lane, pending) -> torch.Tensor:
-        """Attention over the assembled buffers, o_proj + residual, norm, SwiGLU MLP + residual."""
+    def _layer_end(self, idx: int, state, lane: _Lane, pending):
+        """Attention over the assembled buffers, o_proj + residual, norm, SwiGLU MLP + residual
+        (fused: the residual add travels with the following norm, the next layer's input norm or,
+        after the last layer, the final norm)."""
         s = self.shape
-        b = h.shape[0]
         lw = self.layers[idx]
         a = lane.attn.decode_end(pending)
+        if self.fused:
+            h, _ = state
+            b = h.shape[0]
+            o = F.linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
+            h2, x2 = torch.empty_like(h), torch.empty_like(h)
+            shadowkv.rmsnorm(o, lw.post_norm, s.eps, x2, residual=h, residual_out=h2)
+            gate_up = F.linear(x2, lw.gate_up)
+            act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
+            shadowkv.silu_and_mul(gate_up, act)
+            down = F.linear(act, lw.down)
+            w_next = self.layers[idx + 1].in_norm if idx + 1 < s.layers else self.norm_w
+            h3, x3 = torch.empty_like(h), torch.empty_like(h)
+            shadowkv.rmsnorm(down, w_next, s.eps, x3, residual=h2, residual_out=h3)
+            return h3, x3
+        h = state
+        b = h.shape[0]
         h = h + F.linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
         x = self._norm(h, lw.post_norm)
         gate, up = F.linear(x, lw.gate_up).chunk(2, dim=-1)
@@ -237,10 +273,10 @@ class SyntheticDecoder:
         best = vals.argmax(dim=-1, keepdim=True)  # [B, 1]
         return best * blk + idx.gather(1, best)
 
-    def _head(self, h: torch.Tensor, lane: _Lane) -> torch.Tensor:
+    def _head(self, state, lane: _Lane) -> torch.Tensor:
         """Final norm, lm_head, greedy token; advances the lane's RoPE positions."""
-        h = self._norm(h, self.norm_w)
-        logits = F.linear(h[:, -1], self.lm_head).float()  # [b, vocab]
+        x = state[1] if self.fused else self._norm(state, self.norm_w)  # fused: normalised already
+        logits = F.linear(x[:, -1], self.lm_head).float()  # [b, vocab]
         self.pos[lane.rows].add_(1)
         return self._greedy(logits)  # [b, 1]
 
@@ -254,6 +290,13 @@ class SyntheticDecoder:
         lane's value fetch overlaps the other lanes' work between its begin and its end."""
         lanes = self.lanes
         hs = [F.embedding(tokens[lane.rows], self.embed) for lane in lanes]
+        if self.fused:  # (residual, normalised input of layer 0)
+            states = []
+            for h in hs:
+                x = torch.empty_like(h)
+                shadowkv.rmsnorm(h, self.layers[0].in_norm, self.shape.eps, x)
+                states.append((h, x))
+            hs = states
         pending = [None] * len(lanes)
         for idx in range(self.shape.layers):
             for i, lane in enumerate(lanes):

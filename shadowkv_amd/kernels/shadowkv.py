@@ -475,3 +475,91 @@ def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, 
               k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1], D, kv_len, ldev,
               float(scale), workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
               out.stride(0), out.stride(1), _stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# new-token operations around the path (fused)
+
+def _rows2d(t, name):
+    if t.dim() < 2 or t.stride(-1) != 1:
+        raise ValueError(f"{name} must have contiguous rows")
+    if t.dim() > 2:
+        for d in range(t.dim() - 2):
+            if t.stride(d) != t.stride(d + 1) * t.shape[d + 1]:
+                raise ValueError(f"{name} must flatten to rows")
+    return t.numel() // t.shape[-1], t.stride(-2)
+
+
+def rmsnorm(x, weight, eps, out, residual=None, residual_out=None):
+    """out = bf16(h * rsqrt(mean(h^2) + eps) * weight) per row, h = x, or with `residual`
+    h = residual_out = bf16(x + residual) (the residual add fused in front). Rows of x / out /
+    residual / residual_out: [..., hidden] with contiguous rows."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(out, "out", torch.bfloat16)
+    _dev(weight, "weight", torch.bfloat16)
+    rows, xs = _rows2d(x, "x")
+    hidden = x.shape[-1]
+    orows, os_ = _rows2d(out, "out")
+    if orows != rows or out.shape[-1] != hidden or weight.numel() != hidden:
+        raise ValueError("rmsnorm: shape mismatch")
+    rp, rs, rop, ros = None, 0, None, 0
+    if residual is not None:
+        if residual_out is None:
+            raise ValueError("rmsnorm: residual needs residual_out")
+        _dev(residual, "residual", torch.bfloat16)
+        _dev(residual_out, "residual_out", torch.bfloat16)
+        rr, rs = _rows2d(residual, "residual")
+        ro, ros = _rows2d(residual_out, "residual_out")
+        if rr != rows or ro != rows or residual.shape[-1] != hidden or residual_out.shape[-1] != hidden:
+            raise ValueError("rmsnorm: residual shape mismatch")
+        rp, rop = residual.data_ptr(), residual_out.data_ptr()
+    _lib.call("skv_rmsnorm", x.data_ptr(), xs, rp, rs, rop, ros, weight.data_ptr(), out.data_ptr(), os_, rows, hidden,
+              float(eps), _stream())
+
+
+def silu_and_mul(x, out):
+    """out[..., j] = bf16(silu(x[..., j]) * x[..., d + j]), d = out.shape[-1] = x.shape[-1] / 2."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(out, "out", torch.bfloat16)
+    rows, xs = _rows2d(x, "x")
+    orows, os_ = _rows2d(out, "out")
+    d = out.shape[-1]
+    if orows != rows or x.shape[-1] != 2 * d:
+        raise ValueError("silu_and_mul: shape mismatch")
+    _lib.call("skv_silu_and_mul", x.data_ptr(), xs, out.data_ptr(), os_, rows, d, _stream())
+
+
+def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache, append_row):
+    """The new token's q and k rotated at positions[b] (bf16 per-op rounding; half-split for a
+    [rows, 128] cos_sin, GLM-interleaved for [rows, 64]) and the KV append in one launch:
+    q_out[b] <- rotated q; row *append_row of k_cache/v_cache [B, Hkv, buf_len, 128] <- rotated k,
+    raw v. qkv: [B, (Hq + 2 Hkv) * 128] rows (views of the fused projection are fine)."""
+    B = qkv.shape[0]
+    D = 128
+    _dev(qkv, "qkv", torch.bfloat16)
+    _dev(q_out, "q_out", torch.bfloat16)
+    _dev(positions, "positions", torch.int64)
+    _dev(cos_sin, "cos_sin", torch.bfloat16)
+    _dev(append_row, "append_row", torch.int64)
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _dev(t, nm, torch.bfloat16)
+        if t.dim() != 4 or t.shape[0] != B or t.shape[1] != kv_heads or t.shape[3] != D or t.stride(3) != 1:
+            raise ValueError(f"{nm} must be [B, Hkv, buf_len, 128]")
+    if k_cache.stride() != v_cache.stride() or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must share a layout")
+    width = (q_heads + 2 * kv_heads) * D
+    if qkv.shape[-1] != width or qkv.stride(-1) != 1 or qkv.numel() != B * width:
+        raise ValueError(f"qkv must be [B, {width}]")
+    qkv_sb = qkv.stride(0)
+    if q_out.numel() != B * q_heads * D or not q_out.is_contiguous():
+        raise ValueError("q_out must be a contiguous [B, Hq, 128]")
+    if positions.numel() < B:
+        raise ValueError("positions too short")
+    mode = 0 if cos_sin.shape[-1] == 128 else 1 if cos_sin.shape[-1] == 64 else -1
+    if mode < 0:
+        raise ValueError(f"Invalid cos_sin shape {tuple(cos_sin.shape)}")
+    _need_offsets(qkv, (B, width), (qkv_sb, 1), "qkv")
+    _lib.call("skv_rope_qk_append", qkv.data_ptr(), qkv_sb, B, q_heads, kv_heads, D, positions.data_ptr(),
+              cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, q_out.data_ptr(), q_heads * D,
+              k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+              append_row.data_ptr(), k_cache.shape[2], _stream())

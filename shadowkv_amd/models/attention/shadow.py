@@ -46,11 +46,18 @@ class ShadowAttention(AttentionBase):
 
     def decode_begin(self, query_states, key_states, value_states, position_ids, layer_idx):
         """First half of decode(): RoPE, append, chunk selection, the value fetch launched on the
-        cache's copy stream and the key rebuild on the current stream. Returns what decode_end()
-        needs; work issued on the current stream in between overlaps the value fetch."""
+        cache's copy stream and the key rebuild on the current stream (or on the cache's
+        key_stream, when it has one). Returns what decode_end() needs; work issued on the current
+        stream in between overlaps the value fetch."""
         kv_cache = self.kv_cache
         query_states, key_states = self.apply_rotary_pos_emb(query_states, key_states, position_ids)
         kv_cache.update_kv_cache(key_states, value_states, layer_idx)
+        return self.decode_begin_appended(query_states, layer_idx)
+
+    def decode_begin_appended(self, query_states, layer_idx):
+        """decode_begin() for a token already rotated and appended (ShadowKVCache_CPU.rope_and_append):
+        query_states [B, Hq, 1, 128] post-RoPE."""
+        kv_cache = self.kv_cache
         position_ids = kv_cache.get_retrieval_position_ids(layer_idx=layer_idx, query_states=query_states)
 
         curr_stream = torch.cuda.current_stream()
@@ -58,17 +65,29 @@ class ShadowAttention(AttentionBase):
         with torch.cuda.stream(copy_stream):
             copy_stream.wait_stream(curr_stream)
             value_states = kv_cache.get_value_cache(layer_idx, position_ids)
-        key_states = kv_cache.get_key_cache(layer_idx=layer_idx, position_ids=position_ids,
-                                            rope_func=self.apply_rotary_pos_emb_single,
-                                            cos_sin_cache=self.cos_sin_cache)
-        return query_states, key_states, value_states
+            done = [copy_stream.record_event()]  # this fetch only, even if the stream is shared
+        key_stream = getattr(kv_cache, "key_stream", None)
+        if key_stream is None:
+            key_states = self._key_path(layer_idx, position_ids)
+        else:  # the key rebuild on its own stream too, joined in decode_end
+            with torch.cuda.stream(key_stream):
+                key_stream.wait_stream(curr_stream)
+                key_states = self._key_path(layer_idx, position_ids)
+                done.append(key_stream.record_event())
+        return query_states, key_states, value_states, done
+
+    def _key_path(self, layer_idx, position_ids):
+        return self.kv_cache.get_key_cache(layer_idx=layer_idx, position_ids=position_ids,
+                                           rope_func=self.apply_rotary_pos_emb_single,
+                                           cos_sin_cache=self.cos_sin_cache)
 
     def decode_end(self, pending):
         """Second half of decode(), on the stream decode_begin() ran on: wait for the value fetch,
         then sparse attention of the new token over the assembled buffers -> [B, 1, Hq, D]."""
-        query_states, key_states, value_states = pending
+        query_states, key_states, value_states, done = pending
         kv_cache = self.kv_cache
-        torch.cuda.current_stream().wait_stream(kv_cache.copy_stream)
+        for event in done:
+            torch.cuda.current_stream().wait_event(event)
         if kv_cache.attn_workspace is None:
             kv_cache._alloc_attention()
         B, Hq = query_states.shape[0], query_states.shape[1]

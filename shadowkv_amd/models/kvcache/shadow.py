@@ -106,6 +106,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.keep_selected = False  # also emit the selected ids in top-k order into selected_chunks
 
         self.copy_stream = torch.cuda.Stream(device=device)
+        self.key_stream = None  # optional: run the key rebuild on this stream (joined before attention)
         self.attn_workspace = None
         self.attn_out = None
         # Device-resident append row / attention length (use_device_lengths); None = host integers.
@@ -301,6 +302,24 @@ class ShadowKVCache_CPU(KVCacheBase):
         row = self.sparse_end + self.gen_offset - 1  # advanced before the step's first append
         self.append_row_dev = torch.full((1,), row, dtype=torch.int64, device=self.device)
         self.kv_len_dev = torch.full((1,), row + 1, dtype=torch.int32, device=self.device)
+
+    def rope_and_append(self, qkv: torch.Tensor, position_ids: torch.Tensor, cos_sin: torch.Tensor, layer_idx: int,
+                        q_out: torch.Tensor) -> torch.Tensor:
+        """Fused new-token step (device-resident lengths only): q and k of the fused projection
+        rows qkv [B, (Hq + 2 Hkv) * 128] rotated at position_ids [B], rotated q written to q_out
+        [B, Hq, 128], rotated k and v appended at the device append row, in one launch (the work
+        of the rotary embedding plus update_kv_cache). Returns q_out viewed [B, Hq, 1, 128]."""
+        if self.append_row_dev is None:
+            raise RuntimeError("rope_and_append needs use_device_lengths()")
+        self.check_capacity(1)
+        if layer_idx == 0:
+            self.append_row_dev.add_(1)
+            self.kv_len_dev.add_(1)
+        shadowkv.rope_qk_append(qkv, self.num_attention_heads, self.num_key_value_heads, position_ids, cos_sin, q_out,
+                                self.k_cache_buffer[layer_idx], self.v_cache_buffer[layer_idx], self.append_row_dev)
+        if layer_idx == self.num_layers - 1:
+            self.advance(1)
+        return q_out.view(q_out.shape[0], self.num_attention_heads, 1, self.head_dim)
 
     def update_kv_cache(self, new_k_cache: torch.Tensor, new_v_cache: torch.Tensor, layer_idx: int):
         incoming = new_k_cache.shape[-2]
