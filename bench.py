@@ -467,10 +467,11 @@ def main() -> int:
     k_ms, timing = scoring_launch_ms(model)
     achieved = lb / (k_ms * 1e-3) / 1e9
     traffic = None
-    # HBM traffic per launch from FETCH_SIZE / WRITE_SIZE counter runs, valid for this workload only
-    tfile = ROOT / "profiles" / "score_logits_llama8b_b8_ctx122880_traffic.json"
-    if tfile.exists() and (args.batch, args.ctx, args.budget, lanes) == (8, 122880, 2048, 1):
-        traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+    # HBM traffic per launch from FETCH_SIZE / WRITE_SIZE counter runs of this launch shape
+    for tfile in sorted((ROOT / "profiles").glob("score_logits_*_traffic.json")):
+        rec = json.loads(tfile.read_text())
+        if rec.get("launch") == {"rows": BH, "m": G, "n": n, "k": 128}:
+            traffic = rec.get("bytes_per_launch")
 
     detail = None
     if not args.no_breakdown:
