@@ -78,18 +78,22 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   const int G = a.G;
   const uint16_t* kh = a.k + b * a.kv_sb + h * a.kv_sh;
   const uint16_t* vh = a.v + b * a.kv_sb + h * a.kv_sh;
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  // K as MFMA B operand: lane (li, grp) holds key (wave*64 + 16*kg + li), dims [32*ks + 8*grp, +8).
+  // Q as MFMA A operand: lane (li, grp) holds query head li (zero rows past G), dims
+  // [32*ks + 8*grp, +8). Loaded first; every load below is unconditional (clamped index, value
+  // zeroed), so a batch of loads is issued before any is waited on.
+  u32x4 qf[4];
+  const uint16_t* qrow = a.q + b * a.q_sb + (h * G + min(li, G - 1)) * a.q_sh + 8 * grp;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = skv::load16_or_zero(qrow + 32 * ks, li < G);
+  // K as MFMA B operand: lane (li, grp) holds key (wave*64 + 16*kg + li), same dims.
   u32x4 kf[kGroups][4];
 #pragma unroll
   for (int kg = 0; kg < kGroups; ++kg) {
     const int s = s0 + wave * (kSplit / 4) + 16 * kg + li;
+    const uint16_t* krow = kh + static_cast<int64_t>(min(s, s1 - 1)) * a.kv_ss + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      kf[kg][ks] = zero4;
-      if (s < s1) kf[kg][ks] = *reinterpret_cast<const u32x4*>(kh + static_cast<int64_t>(s) * a.kv_ss + 32 * ks + 8 * grp);
-    }
+    for (int ks = 0; ks < 4; ++ks) kf[kg][ks] = skv::load16_or_zero(krow + 32 * ks, s < s1);
   }
   // V for P.V: stream (wave, grp) takes keys s0 + 16*i + stream, lane li its dims [8*li, +8).
   const int stream = wave * 4 + grp;
@@ -98,19 +102,10 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
       const int s = s0 + i * 16 + stream;
-      vr[i] = zero4;
-      if (s < s1) vr[i] = *reinterpret_cast<const u32x4*>(vh + static_cast<int64_t>(s) * a.kv_ss + li * 8);
+      vr[i] = skv::load16_or_zero(vh + static_cast<int64_t>(min(s, s1 - 1)) * a.kv_ss + li * 8, s < s1);
     }
   };
   if (kEarlyV) load_v();
-
-  // Q as MFMA A operand: lane (li, grp) holds query head li (zero rows past G), same dims.
-  u32x4 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    qf[ks] = zero4;
-    if (li < G) qf[ks] = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + (h * G + li) * a.q_sh + 32 * ks + 8 * grp);
-  }
 #pragma unroll
   for (int kg = 0; kg < kGroups; ++kg) {
     f32x4_t d = {0.f, 0.f, 0.f, 0.f};

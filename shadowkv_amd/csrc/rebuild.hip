@@ -116,35 +116,35 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   const int row_end = min(row_begin + kTileRows, total_rows);
   if (row_end <= miss_begin || row_begin >= row_end) return;
 
-  // SV -> LDS: every load of this thread is issued before any store, so the staging costs one
-  // memory latency, not one per vector.
+  // Issue order (vector loads retire in order): this thread's chunk id, the SV tile, then, after
+  // the positions are shared, every U and cos/sin row the wave needs for both iterations; SV is
+  // written to LDS last, so its wait leaves the row loads in flight. Every load is unconditional
+  // (clamped index, value zeroed), so no branch splits the batches.
+  const IdxT* ids = static_cast<const IdxT*>(a.ids) + b * a.id_sb + h * a.id_sh;
+  int64_t my_id = 0;
+  {
+    const int row = row_begin + static_cast<int>(threadIdx.x);  // kThreads == kTileRows: one row per thread
+    my_id = ids[min(row, total_rows - 1) / a.chunk];
+  }
   const int k8 = a.rank / 8;
   const uint16_t* svp = a.sv + b * a.sv_sb + h * a.sv_sh;
-  {
-    constexpr int kVecs = (kHeadDim * (KS * 32) / 8 + kThreads - 1) / kThreads;  // >= 128*rank/8/256
-    u32x4 v[kVecs];
+  constexpr int kVecs = (kHeadDim * (KS * 32) / 8 + kThreads - 1) / kThreads;  // >= 128*rank/8/256
+  u32x4 svv[kVecs];
 #pragma unroll
-    for (int i = 0; i < kVecs; ++i) {
-      const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
-      const int n = idx / k8, kk = (idx - n * k8) * 8;
-      if (idx < kHeadDim * k8) v[i] = *reinterpret_cast<const u32x4*>(&svp[n * a.sv_sn + kk]);
-    }
-#pragma unroll
-    for (int i = 0; i < kVecs; ++i) {
-      const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
-      const int n = idx / k8, kk = (idx - n * k8) * 8;
-      if (idx < kHeadDim * k8) *reinterpret_cast<u32x4*>(&sv_lds[n * ldr + kk]) = v[i];
-    }
+  for (int i = 0; i < kVecs; ++i) {
+    const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+    const int ic = min(idx, kHeadDim * k8 - 1);
+    const int n = ic / k8, kk = (ic - n * k8) * 8;
+    svv[i] = *reinterpret_cast<const u32x4*>(&svp[n * a.sv_sn + kk]);
   }
-  const IdxT* ids = static_cast<const IdxT*>(a.ids) + b * a.id_sb + h * a.id_sh;
   {
     const int row = row_begin + static_cast<int>(threadIdx.x);
     int32_t p = -1;
     if (row < row_end) {
-      const int64_t q = static_cast<int64_t>(ids[row / a.chunk]) * a.chunk + row % a.chunk;
+      const int64_t q = my_id * a.chunk + row % a.chunk;
       if (q >= 0 && q <= 0x7fffffff) p = static_cast<int32_t>(q);
     }
-    pos_lds[threadIdx.x] = p;  // kThreads == kTileRows: one row per thread
+    pos_lds[threadIdx.x] = p;
   }
   __syncthreads();
 
@@ -157,26 +157,6 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   uint16_t* st = kst + wave * 16 * kStLd;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  // U fragments (B operand) of the 32 rows [lr, lr+32) of this workgroup.
-  auto load_u = [&](int lr, bf16x8_t (&uf)[2][KS]) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int r = lr + m * 16 + li;
-      const int grow = row_begin + r;
-      const int32_t pos = pos_lds[r];
-      const bool valid = grow >= miss_begin && grow < row_end && pos >= 0 && pos < a.u_rows;
-      const uint16_t* up = ubase + static_cast<int64_t>(valid ? pos : 0) * a.u_sr;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int kk = ks * 32 + lk * 8;
-        u32x4 v = zero4;
-        if (valid && kk < a.rank) v = *reinterpret_cast<const u32x4*>(up + kk);
-        uf[m][ks] = as_bf16x8(v);
-      }
-    }
-  };
-
-  bf16x8_t uf[2][2][KS];
   const int lr0 = wave * 64;
   bool active[2];
 #pragma unroll
@@ -184,41 +164,64 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
     const int rb = row_begin + lr0 + it * 32;
     active[it] = rb < row_end && rb + 32 > miss_begin;  // wave-uniform
   }
-  if (active[0]) load_u(lr0, uf[0]);
-  else if (active[1]) load_u(lr0 + 32, uf[1]);  // first block all hits: no iteration 0 to prefetch it
+  // U fragments (B operand) of both 32-row blocks.
+  bf16x8_t uf[2][2][KS];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int r = lr0 + it * 32 + m * 16 + li;
+      const int grow = row_begin + r;
+      const int32_t pos = pos_lds[r];
+      const bool valid = active[it] && grow >= miss_begin && grow < row_end && pos >= 0 && pos < a.u_rows;
+      const uint16_t* up = ubase + static_cast<int64_t>(valid ? pos : 0) * a.u_sr;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int kk = ks * 32 + lk * 8;
+        uf[it][m][ks] = as_bf16x8(skv::load16_or_zero(up + min(kk, a.rank - 8), valid && kk < a.rank));
+      }
+    }
+  }
+  // cos/sin of both blocks' epilogue units.
+  u32x4 cs_c[2][2][U::kPerLane], cs_s[2][2][U::kPerLane];
+#pragma unroll
+  for (int it = 0; it < 2; ++it)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int q = 0; q < U::kPerLane; ++q) {
+        cs_c[it][m][q] = zero4;
+        cs_s[it][m][q] = zero4;
+        if (kMode == kPlain) continue;
+        const int unit = lane + 64 * q;
+        const int r = unit / U::kPerRow, j = unit % U::kPerRow;
+        const int32_t pos = pos_lds[lr0 + it * 32 + m * 16 + r];
+        const bool ok = active[it] && pos >= 0 && pos < a.cs_rows;
+        const uint16_t* c = a.cs + static_cast<int64_t>(ok ? pos : 0) * a.cs_stride;
+        if (kMode == kRopeHalf) {
+          cs_c[it][m][q] = skv::load16_or_zero(c + 8 * j, ok);
+          cs_s[it][m][q] = skv::load16_or_zero(c + 64 + 8 * j, ok);
+        } else {  // GLM: 4 pairs per unit, cos at [4j], sin at [32 + 4j]; units j >= 8 pass through
+          const int jc = min(j, 7);
+          const u32x2 cc = *reinterpret_cast<const u32x2*>(c + 4 * jc);
+          const u32x2 ss = *reinterpret_cast<const u32x2*>(c + 32 + 4 * jc);
+          const bool use = ok && j < 8;
+          cs_c[it][m][q] = use ? u32x4{cc.x, cc.y, 0u, 0u} : zero4;
+          cs_s[it][m][q] = use ? u32x4{ss.x, ss.y, 0u, 0u} : zero4;
+        }
+      }
+#pragma unroll
+  for (int i = 0; i < kVecs; ++i) {
+    const int idx = static_cast<int>(threadIdx.x) + i * kThreads;
+    const int n = idx / k8, kk = (idx - n * k8) * 8;
+    if (idx < kHeadDim * k8) *reinterpret_cast<u32x4*>(&sv_lds[n * ldr + kk]) = svv[i];
+  }
+  __syncthreads();
 
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     if (!active[it]) continue;
     const int lr = lr0 + it * 32;
-
-    // cos/sin of this iteration's epilogue units, loaded ahead of the MFMAs.
-    u32x4 cs_c[2][U::kPerLane], cs_s[2][U::kPerLane];
-    if (kMode != kPlain) {
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int q = 0; q < U::kPerLane; ++q) {
-          const int unit = lane + 64 * q;
-          const int r = unit / U::kPerRow, j = unit % U::kPerRow;
-          const int32_t pos = pos_lds[lr + m * 16 + r];
-          cs_c[m][q] = zero4;
-          cs_s[m][q] = zero4;
-          if (pos >= 0 && pos < a.cs_rows) {
-            const uint16_t* c = a.cs + static_cast<int64_t>(pos) * a.cs_stride;
-            if (kMode == kRopeHalf) {
-              cs_c[m][q] = *reinterpret_cast<const u32x4*>(c + 8 * j);
-              cs_s[m][q] = *reinterpret_cast<const u32x4*>(c + 64 + 8 * j);
-            } else if (j < 8) {  // GLM: 4 pairs per unit, cos at [4j], sin at [32 + 4j]
-              const u32x2 cc = *reinterpret_cast<const u32x2*>(c + 4 * j);
-              const u32x2 ss = *reinterpret_cast<const u32x2*>(c + 32 + 4 * j);
-              cs_c[m][q] = u32x4{cc.x, cc.y, 0u, 0u};
-              cs_s[m][q] = u32x4{ss.x, ss.y, 0u, 0u};
-            }
-          }
-        }
-    }
-    if (it == 0 && active[1]) load_u(lr0 + 32, uf[1]);  // in flight during this iteration's MFMAs
 
     f32x4_t acc[2][8];
 #pragma unroll
@@ -230,9 +233,8 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
       const int kk = ks * 32 + lk * 8;
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        u32x4 sv = zero4;
-        if (kk < a.rank) sv = *reinterpret_cast<const u32x4*>(&sv_lds[(t * 16 + li) * ldr + kk]);
-        const bf16x8_t svf = as_bf16x8(sv);
+        const u32x4 sv = *reinterpret_cast<const u32x4*>(&sv_lds[(t * 16 + li) * ldr + min(kk, a.rank - 8)]);
+        const bf16x8_t svf = as_bf16x8(kk < a.rank ? sv : zero4);
         acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(svf, uf[it][0][ks], acc[0][t], 0, 0, 0);
         acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(svf, uf[it][1][ks], acc[1][t], 0, 0, 0);
       }
@@ -262,7 +264,7 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
           *reinterpret_cast<u32x4*>(orow + 8 * j) = x1v;
         } else if (kMode == kRopeHalf) {
           const u32x4 x2v = *reinterpret_cast<const u32x4*>(&st[r * kStLd + 64 + 8 * j]);
-          const u32x4 cv = cs_c[m][q], sv = cs_s[m][q];
+          const u32x4 cv = cs_c[it][m][q], sv = cs_s[it][m][q];
           uint32_t y1[4], y2[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) skv::rope_half_split2(x1v[e], x2v[e], cv[e], sv[e], y1[e], y2[e]);
@@ -272,8 +274,8 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
           if (j < 8) {
             uint16_t x[8], c[8], sn[8], y[8];
             unpack8(x1v, x);
-            unpack8(cs_c[m][q], c);
-            unpack8(cs_s[m][q], sn);
+            unpack8(cs_c[it][m][q], c);
+            unpack8(cs_s[it][m][q], sn);
 #pragma unroll
             for (int p = 0; p < 4; ++p) skv::rope_half_split(x[2 * p], x[2 * p + 1], c[p], sn[p], y[2 * p], y[2 * p + 1]);
             *reinterpret_cast<u32x4*>(orow + 8 * j) = pack8(y);
@@ -331,6 +333,11 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
   if (!aligned16(a.u) || !aligned16(a.sv) || a.u_sb % 8 || a.u_sh % 8 || a.u_sr % 8 || a.sv_sb % 8 || a.sv_sh % 8 ||
       a.sv_sn % 8) {
     skv_set_error("%s: U and SV rows must be 16-byte aligned (strides multiples of 8 elements)", what);
+    return SKV_EINVAL;
+  }
+  if (a.u_rows < 1 || (mode != kPlain && a.cs_rows < 1)) {
+    skv_set_error("%s: empty U (%lld rows) or cos/sin table (%lld rows)", what, (long long)a.u_rows,
+                  (long long)a.cs_rows);
     return SKV_EINVAL;
   }
   if (!aligned16(a.out) || a.o_sb % 8 || a.o_sh % 8 || a.o_ss % 8 ||

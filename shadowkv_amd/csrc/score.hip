@@ -51,27 +51,22 @@ __global__ void __launch_bounds__(kThreads) logits_kernel(const uint16_t* __rest
   const int li = lane & 15;
   const int grp = lane >> 4;
   constexpr int kGroups = kTile / 4 / 16;  // 16-landmark MFMA groups per wave
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  // B operand: lane (li, grp) holds landmark wave*64 + 16*kg + li, dims [32*ks + 8*grp, +8).
+  // A operand: lane (li, grp) holds query li (zero rows past m), dims [32*ks + 8*grp, +8).
+  u32x4 qf[4];
+  const uint16_t* Az = A + (static_cast<int64_t>(z) * m + min(li, m - 1)) * kHeadDim + 8 * grp;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = skv::load16_or_zero(Az + 32 * ks, li < m);
+  // B operand: lane (li, grp) holds landmark wave*64 + 16*kg + li, same dims. All 16 loads are
+  // issued before any is waited on.
   const uint16_t* Bz = B + static_cast<int64_t>(z) * n * kHeadDim + 8 * grp;
   u32x4 lf[kGroups][4];
 #pragma unroll
   for (int kg = 0; kg < kGroups; ++kg) {
     const int j = tile * kTile + wave * (kTile / 4) + 16 * kg + li;
+    const uint16_t* row = Bz + static_cast<int64_t>(min(j, n - 1)) * kHeadDim;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      lf[kg][ks] = zero4;
-      if (j < n) lf[kg][ks] = *reinterpret_cast<const u32x4*>(Bz + static_cast<int64_t>(j) * kHeadDim + 32 * ks);
-    }
-  }
-  // A operand: lane (li, grp) holds query li (zero rows past m), same dims.
-  u32x4 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    qf[ks] = zero4;
-    if (li < m)
-      qf[ks] = *reinterpret_cast<const u32x4*>(A + (static_cast<int64_t>(z) * m + li) * kHeadDim + 32 * ks + 8 * grp);
+    for (int ks = 0; ks < 4; ++ks) lf[kg][ks] = skv::load16_or_zero(row + 32 * ks, j < n);
   }
 #pragma unroll
   for (int kg = 0; kg < kGroups; ++kg) {

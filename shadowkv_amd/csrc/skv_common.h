@@ -142,6 +142,14 @@ __device__ __forceinline__ void drain_and_barrier() {
 // registers (a struct is copied with memcpy, which keeps such arrays in private memory).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// 16-byte load of *p when ok, else zero. p must be readable either way (the caller clamps an
+// out-of-range index to a valid one), so the load is issued unconditionally: no branch splits a
+// batch of loads, which would make the compiler wait for each before issuing the next.
+__device__ __forceinline__ u32x4 load16_or_zero(const void* p, bool ok) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  return ok ? v : u32x4{0u, 0u, 0u, 0u};
+}
+
 // 16-byte load with the non-temporal (streaming) hint: global_load_dwordx4 ... nt. Used for reads
 // of pinned host memory over the host link, which are read once; it keeps those long-latency
 // requests from holding cache resources that concurrent kernels' HBM traffic needs.
