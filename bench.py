@@ -206,17 +206,28 @@ def breakdown(model, tok) -> dict:
                           "note": "value fetch (hit compaction + zero-copy miss gather) per layer"}}
 
 
+# Footprint that the input sets of one timed loop must exceed, so that back-to-back launches read
+# HBM and not the 256 MB last-level cache (MALL) that sits in front of it.
+COLD_FOOTPRINT = 1 << 30
+
+
+def cold_sets(bytes_per_launch: int) -> int:
+    """Number of distinct input sets to rotate through so their total exceeds COLD_FOOTPRINT."""
+    return max(1, -(-COLD_FOOTPRINT // max(1, bytes_per_launch)))
+
+
 def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
     """Seconds per call of `fn` on the GPU: `reps` calls captured in one HIP graph, replayed
-    `rounds` times between HIP events, so host launch cost does not enter the figure."""
+    `rounds` times between HIP events, so host launch cost does not enter the figure. `fn` takes
+    the call's index, so a caller can rotate through several input sets."""
     import torch
 
-    fn()
+    fn(0)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for _ in range(reps):
-            fn()
+        for i in range(reps):
+            fn(i)
     g.replay()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -258,27 +269,34 @@ def rebuild_microbench(args) -> int:
         for b in range(B):
             U[b].normal_(generator=g)
         SV = torch.empty(H, D, R, dtype=torch.bfloat16, device=dev).normal_(generator=g)
-        ids = torch.stack([torch.randperm(chunks, generator=g, device=dev)[:S].sort().values
-                           for _ in range(B * H)]).view(B, H, S)
-        cache = torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16, device=dev)
+        # Distinct chunk-id sets and output buffers, rotated so that no launch finds its U rows
+        # or its output lines in the last-level cache.
+        sets = cold_sets(rebuild_bytes(S * c, B * H, S))
+        set_reps = -(-reps // sets) * sets
+        ids = [torch.stack([torch.randperm(chunks, generator=g, device=dev)[:S].sort().values
+                            for _ in range(B * H)]).view(B, H, S) for _ in range(sets)]
+        caches = [torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16, device=dev) for _ in range(sets)]
         for hits in (0, 154):
             cnts = torch.full((B * H,), hits, dtype=torch.int32, device=dev)
-            t = gpu_time_per_call(lambda: shadowkv.rebuild_k_rope(U, SV, ids, cnts, cos_sin, cache, sparse_start, c),
-                                  reps)
+            t = gpu_time_per_call(lambda i: shadowkv.rebuild_k_rope(U, SV, ids[i % sets], cnts, cos_sin,
+                                                                    caches[i % sets], sparse_start, c),
+                                  set_reps)
             rows = (S - hits) * c
             nbytes = rebuild_bytes(rows, B * H, S)
             flops = 2 * B * H * rows * R * D
             cpu = None
             if hits == 0 and B <= 8 and not args.no_cpu_baseline:
-                cpu = rebuild_cpu_baseline(U, SV, ids, cnts, cos_sin, cache, sparse_start, c, args.cpu_runs)
+                cpu = rebuild_cpu_baseline(U, SV, ids[0], cnts, cos_sin, caches[0], sparse_start, c, args.cpu_runs)
             out = {"metric": "low-rank K rebuild + RoPE rows/s", "value": round(B * H * rows / t, 1),
-                   "unit": "rows/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+                   "unit": "rows/s", "n_gpus": 1, "steps": set_reps, "warmup": 1,
                    "ms_per_step": round(t * 1e3, 4), "higher_is_better": True, "scaling": "strong",
                    "vs_baseline": None, "dtype": "bf16",
                    "data": "synthetic: U, SV ~ N(0,1) bf16, sorted unique random chunk ids; timed as HIP-graph "
-                           "replays of back-to-back launches",
+                           f"replays of back-to-back launches rotating over {sets} id sets / output buffers "
+                           "(> 1 GiB together, so reads come from HBM)",
                    "config": {"workload": f"rebuild microbench batch {B}, 8 kv heads, rank 160, ctx 122880, "
-                                          f"256 chunks/head, {hits} hits", "batch": B, "hits": hits},
+                                          f"256 chunks/head, {hits} hits", "batch": B, "hits": hits,
+                              "rotated_sets": sets},
                    "roofline": {"kernel": "rebuild_kernel (gather-GEMM + RoPE epilogue)", "bound": "hbm",
                                 "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
@@ -287,7 +305,7 @@ def rebuild_microbench(args) -> int:
                                 "mfma_util": round(flops / t / MFMA_BF16_PEAK, 5)},
                    "cpu_baseline": cpu}
             print(json.dumps(out), flush=True)
-        del U, SV, ids, cache
+        del U, SV, ids, caches
         torch.cuda.empty_cache()
     return 0
 
@@ -328,20 +346,24 @@ def attention_microbench(args) -> int:
                                ("GLM-4-9B", 4, 32, 2, 2600), ("Llama-3-8B-1M", 1, 32, 8, 19616)):
         g = torch.Generator(device="cuda").manual_seed(L + B)
         buf = L + 32
-        K = torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16)
-        V = torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16)
-        q = torch.randn(B, Hq, D, generator=g, device="cuda").to(torch.bfloat16)
-        out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device="cuda")
-        ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device="cuda")
-        t = gpu_time_per_call(lambda: shadowkv.sparse_attn_decode(q, K, V, L, out, ws), reps)
         G = Hq // Hk
         nbytes = B * Hk * (2 * L * D * 2 + 2 * G * D * 2)  # K and V rows, q in, o out
+        sets = cold_sets(nbytes)  # distinct K/V/q sets, rotated so reads come from HBM
+        set_reps = -(-reps // sets) * sets
+        K = [torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
+        V = [torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
+        q = [torch.randn(B, Hq, D, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
+        out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device="cuda")
+        t = gpu_time_per_call(lambda i: shadowkv.sparse_attn_decode(q[i % sets], K[i % sets], V[i % sets], L, out, ws),
+                              set_reps)
         out_line = {"metric": "sparse decode attention (b,h) rows/s", "value": round(B * Hq / t, 1), "unit": "rows/s",
-                    "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
+                    "n_gpus": 1, "steps": set_reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
                     "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
-                    "data": "synthetic: q, K, V ~ N(0,1) bf16; timed as HIP-graph replays of back-to-back launches",
+                    "data": "synthetic: q, K, V ~ N(0,1) bf16; timed as HIP-graph replays of back-to-back launches "
+                            f"rotating over {sets} q/K/V sets (> 1 GiB together, so reads come from HBM)",
                     "config": {"workload": f"{name} shape attention: batch {B}, {Hq}/{Hk} heads, kv length {L}",
-                               "batch": B, "q_heads": Hq, "kv_heads": Hk, "kv_len": L},
+                               "batch": B, "q_heads": Hq, "kv_heads": Hk, "kv_len": L, "rotated_sets": sets},
                     "roofline": {"kernel": "attn_split_kernel + attn_combine_kernel", "bound": "hbm",
                                  "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
@@ -379,12 +401,12 @@ def select_microbench(args) -> int:
         cnts = torch.empty(rows, dtype=torch.int32, device="cuda")
         scores = torch.empty(rows, n, dtype=torch.bfloat16, device="cuda")
 
-        def run():
+        def run(_):
             pos.copy_(pos0)
             shadowkv.select_chunks(D, norm, ssum, rows, G, n, lidx, S, chunks, pos, offsets, cnts, out_scores=scores)
 
         t_all = gpu_time_per_call(run, reps)
-        t_copy = gpu_time_per_call(lambda: pos.copy_(pos0), reps)
+        t_copy = gpu_time_per_call(lambda _: pos.copy_(pos0), reps)
         t = t_all - t_copy
         out_line = {"metric": "fused chunk selection latency", "value": round(t * 1e6, 2), "unit": "us",
                     "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
