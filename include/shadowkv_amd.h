@@ -61,6 +61,17 @@ int skv_gather_copy_with_offsets(const void* values, void* v_cache_buffer, const
                                  int64_t gpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
                                  int map_size, int chunk_elems, void* stream);
 
+/* The i >= cnts[r] half of skv_gather_copy_with_offsets alone: the host-link gather of the
+ * misses, no in-buffer hit move. Together with skv_gather_copy_d2d_with_offsets on the value
+ * buffer (the hit move, issued first on another stream) it does the same work as
+ * skv_gather_copy_with_offsets, split so that the host-link stream carries only host-link
+ * transfers (the reference runs both halves inside one gather_copy_with_offsets call,
+ * models/kvcache/shadow.py:578-582). */
+int skv_gather_copy_misses_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
+                                        const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length,
+                                        int64_t gpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
+                                        int map_size, int chunk_elems, void* stream);
+
 /* ---- a5: key-hit compaction ------------------------------------------------------------
  * Replaces gather_copy_d2d_with_offsets (kernels/functions.h:27-35, kernels/gather_copy.cu:112-185,
  * device kernels/copy.cuh:353-390): the i < cnts[r] part of skv_gather_copy_with_offsets on `keys`. */
@@ -225,6 +236,13 @@ int skv_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, i
  * in fp32, j < d (a multiple of 8); rows 16-byte aligned. */
 int skv_silu_and_mul(const uint16_t* x, int64_t x_stride, uint16_t* out, int64_t out_stride, int rows, int d,
                      void* stream);
+
+/* Replaces F.linear on the decoding model's weights at decode batch sizes (wqkv, wo, gate_up_proj,
+ * down_proj: models/llama.py:192,203,208,214; lm_head: models/llama.py:159):
+ * y[i, j] = bf16(sum_k x[i, k] * weight[j, k]) in fp32, i < m <= 16, j < n, k a multiple of 8.
+ * weight is row-major [n, k] (row stride weight_stride); x and weight rows 16-byte aligned. */
+int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride, uint16_t* y,
+               int64_t y_stride, int m, int n, int k, void* stream);
 
 /* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:55-56) and the
  * KV append of update_kv_cache (models/kvcache/shadow.py:621-633) in one launch. qkv row of batch b:

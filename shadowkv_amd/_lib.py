@@ -26,6 +26,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_host_device_pointer": (_i32, [_p, ctypes.POINTER(_p)]),
     "skv_reorder_keys_and_compute_offsets": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "skv_gather_copy_with_offsets": (_i32, [_p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
+    "skv_gather_copy_misses_with_offsets": (_i32, [_p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
+                                                    _p]),
     "skv_gather_copy_d2d_with_offsets": (_i32, [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _p]),
     "skv_gather_copy": (_i32, [_p, _p, _p, _i32, _i32, _i64, _i64, _i32, _i32, _p]),
     "skv_apply_rotary_pos_emb_new": (
@@ -50,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_sparse_attn_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "skv_rmsnorm": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "skv_silu_and_mul": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p]),
+    "skv_linear": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p]),
     "skv_rope_qk_append": (
         _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
                _i64, _p]),

@@ -22,11 +22,12 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 8;             // 16-byte vectors in flight per lane
 constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch tile
 // Upper bound on fetch workgroups (environment SKV_FETCH_WGS overrides it, read once). The
-// fetch is host-link bound: 32 workgroups of non-temporal loads (1 MiB in flight) already hold
-// the link at its ~55 GB/s ceiling on MI355X, and every further host read in flight slows the
-// HBM traffic of kernels running concurrently (measured: a 4096x28672 GEMM 1.9x slower beside
-// 32 workgroups, 2.7x beside 256; landmark scoring 1.1x vs 3.1x).
-constexpr int kDefaultFetchWGs = 32;
+// fetch is host-link bound, and every host read in flight also slows the HBM traffic of kernels
+// running concurrently (measured: a 4096x28672 GEMM 1.9x slower beside 32 workgroups, 2.7x
+// beside 256; landmark scoring 1.1x vs 3.1x). 48 workgroups (1.5 MiB of non-temporal loads in
+// flight) give the fastest pipelined Llama-3-8B decode step on MI355X (tokens/s at 32/40/44/48/
+// 52/56/64/96 workgroups: 354/368/375/381/376/365/344/305).
+constexpr int kDefaultFetchWGs = 48;
 
 int fetch_workgroups() {
   static const int wgs = [] {
@@ -184,11 +185,13 @@ extern "C" int skv_gather_copy_d2d_with_offsets(void* keys, const int32_t* offse
   return skv_check_launch(what);
 }
 
-extern "C" int skv_gather_copy_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
-                                            const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length,
-                                            int64_t gpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
-                                            int map_size, int chunk_elems, void* stream) {
-  const char* what = "gather_copy_with_offsets";
+namespace {
+
+// Shared by the two value-fetch entry points: argument checks, then (compact) the in-buffer hit
+// move and the host-link gather of the misses, in that order on one stream.
+int value_fetch(const char* what, bool compact, const void* values, void* v_cache_buffer, const int32_t* offsets,
+                const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length, int64_t gpu_v_length,
+                int64_t gpu_v_offset, int64_t gpu_v_stride, int map_size, int chunk_elems, void* stream) {
   if (!values || !v_cache_buffer || !offsets || !cnts) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -204,16 +207,36 @@ extern "C" int skv_gather_copy_with_offsets(const void* values, void* v_cache_bu
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows = batch_size * heads;
-  hipLaunchKernelGGL(compact_hits_kernel, dim3(rows), dim3(kThreads), 0, s, static_cast<u32x4*>(v_cache_buffer), offsets,
-                     cnts, gpu_v_stride / 8, gpu_v_offset / 8, map_size, chunk_elems / 8);
-  rc = skv_check_launch(what);
-  if (rc) return rc;
+  if (compact) {
+    hipLaunchKernelGGL(compact_hits_kernel, dim3(rows), dim3(kThreads), 0, s, static_cast<u32x4*>(v_cache_buffer),
+                       offsets, cnts, gpu_v_stride / 8, gpu_v_offset / 8, map_size, chunk_elems / 8);
+    rc = skv_check_launch(what);
+    if (rc) return rc;
+  }
   const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
   hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0, s,
                      static_cast<const u32x4*>(values), cpu_v_length / 8, static_cast<u32x4*>(v_cache_buffer),
                      gpu_v_stride / 8, gpu_v_offset / 8, offsets, cnts, map_size, chunk_elems / 8,
                      cpu_v_length / chunk_elems, rows, tiles);
   return skv_check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int skv_gather_copy_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
+                                            const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length,
+                                            int64_t gpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
+                                            int map_size, int chunk_elems, void* stream) {
+  return value_fetch("gather_copy_with_offsets", true, values, v_cache_buffer, offsets, cnts, batch_size, heads,
+                     cpu_v_length, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size, chunk_elems, stream);
+}
+
+extern "C" int skv_gather_copy_misses_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
+                                                   const int32_t* cnts, int batch_size, int heads,
+                                                   int64_t cpu_v_length, int64_t gpu_v_length, int64_t gpu_v_offset,
+                                                   int64_t gpu_v_stride, int map_size, int chunk_elems, void* stream) {
+  return value_fetch("gather_copy_misses_with_offsets", false, values, v_cache_buffer, offsets, cnts, batch_size,
+                     heads, cpu_v_length, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size, chunk_elems, stream);
 }
 
 extern "C" int skv_gather_copy(const void* values, void* v_cache_buffer, const int64_t* position_ids, int batch_size,

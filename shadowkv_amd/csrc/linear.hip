@@ -1,0 +1,200 @@
+// Skinny bf16 linear layer of the decode step: y[m, n] = bf16(sum_k x[m, k] * w[n, k]) for the
+// few token rows m of one decode step (M <= 16) against a row-major weight [N, K] — the
+// decoding model's projections (F.linear on wqkv, wo, gate_up_proj, down_proj and the lm head,
+// models/llama.py:192,203,208,214 and models/llama.py:159 with its use in the model's forward).
+//
+// At M <= 16 the call is bound by reading the weight once from HBM (2*N*K bytes), so the kernel
+// is laid out for the load path, not for the matrix cores: every wave load reads 1 KB of ONE
+// weight row (64 lanes x 16 B, fully coalesced), and the arithmetic runs on the VALU as bf16 dot2
+// with fp32 accumulation (v_dot2c_f32_bf16), which needs no operand shuffles. A workgroup owns R
+// weight rows; its waves split K into 512-element blocks (wave w takes blocks w, w+nw, ...) with
+// the next block's loads in flight while the current one is multiplied. The per-lane partial
+// sums are folded within 16-lane rows by a DPP transpose-reduce (each step halves the values a
+// lane holds), then summed across rows and waves in LDS; one rounding to bf16 at the end.
+#include "skv_common.h"
+
+namespace {
+
+using skv::u32x4;
+
+constexpr int kBlockK = 512;     // k elements per wave load (64 lanes x 8)
+constexpr int kMaxWaves = 8;     // workgroup size limit (2 waves per SIMD at 256 VGPRs)
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// One transpose-reduce step over the lane bit that the DPP pattern CTRL flips: lanes with the
+// bit set keep the upper half of their C values, the others the lower half, and each adds the
+// partner's copy of the half it keeps.
+template <int C, int CTRL>
+__device__ __forceinline__ void fold(float* v, bool upper) {
+#pragma unroll
+  for (int j = 0; j < C / 2; ++j) {
+    const float keep = upper ? v[C / 2 + j] : v[j];
+    const float send = upper ? v[j] : v[C / 2 + j];
+    v[j] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), CTRL, 0xf, 0xf, false));
+  }
+}
+
+template <int R, int MP>
+__global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* __restrict__ x, int64_t xs,
+                                                               const uint16_t* __restrict__ w, int64_t ws,
+                                                               uint16_t* __restrict__ y, int64_t ys, int M, int N,
+                                                               int K) {
+  constexpr int V = R * MP;  // partial sums per lane
+  static_assert(V >= 16 && V <= 64 && (V & (V - 1)) == 0, "R * MP must be 16, 32 or 64");
+  __shared__ float red[kMaxWaves * 4 * V];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loop control
+  const int nw = blockDim.x >> 6;
+  const int n0 = blockIdx.x * R;
+  const int nblk = (K + kBlockK - 1) / kBlockK;
+
+  // Row bases are wave-uniform (scalar registers); the lane's 32-bit byte offset is added per
+  // load, so the loads take the scalar-base + vector-offset form.
+  const char* wr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wr[r] = reinterpret_cast<const char*>(w + static_cast<int64_t>(min(n0 + r, N - 1)) * ws);
+  const char* xr[MP];
+#pragma unroll
+  for (int m = 0; m < MP; ++m) xr[m] = reinterpret_cast<const char*>(x + static_cast<int64_t>(min(m, M - 1)) * xs);
+
+  float acc[R][MP];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
+
+  // Block b's operands: lane k offset b*512 + 8*lane. A lane past K (only in a last, partial
+  // block) reads the row's first 16 bytes instead (valid for any K >= 8), and mac() zeroes its x,
+  // so it adds 0. The select sits at the use, not at the load, so a prefetch never has to wait
+  // for its own data.
+  auto load = [&](int b, u32x4* wv, u32x4* xv) {
+    const int k = b * kBlockK + 8 * lane;
+    const uint32_t boff = 2u * static_cast<uint32_t>(k < K ? k : 0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[r] = skv::load_nt(reinterpret_cast<const u32x4*>(wr[r] + boff));
+#pragma unroll
+    for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const u32x4*>(xr[m] + boff);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the multiply that follows
+  };
+  auto mac = [&](int b, const u32x4* wv, const u32x4* xv) {
+    const bool ok = b * kBlockK + 8 * lane < K;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int m = 0; m < MP; ++m) {
+        const uint32_t xe = ok ? xv[m][e] : 0u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][m] = dot2(wv[r][e], xe, acc[r][m]);
+      }
+  };
+
+  // The wave's blocks are b_j = wave + j*nw, j < nb. Two register sets alternate; inside the
+  // loop every prefetch is unconditional, so the compiler's wait before each multiply covers only
+  // that block's loads (a conditional prefetch would make it wait for both sets).
+  const int nb = wave < nblk ? (nblk - 1 - wave) / nw + 1 : 0;  // wave-uniform
+  if (nb > 0) {
+    u32x4 wa[R], xa[MP], wb[R], xb[MP];
+    load(wave, wa, xa);
+    int b = wave, i = 1;  // set a holds block b = b_{i-1}; b_i is the next block to load
+    for (; i + 1 < nb; i += 2, b += 2 * nw) {
+      load(b + nw, wb, xb);
+      mac(b, wa, xa);
+      load(b + 2 * nw, wa, xa);
+      mac(b + nw, wb, xb);
+    }
+    if (i < nb) {
+      load(b + nw, wb, xb);
+      mac(b, wa, xa);
+      mac(b + nw, wb, xb);
+    } else {
+      mac(b, wa, xa);
+    }
+  }
+
+  // Fold the R*MP partial sums within each 16-lane row: bit 3 of the lane (row_mirror), bit 2
+  // (row_half_mirror), bit 1 (quad_perm 3,2,1,0), bit 0 (quad_perm 1,0,3,2). Lane p of a row then
+  // holds values p*V/16 .. p*V/16 + V/16 - 1 of the flattened [R][MP] array, summed over the row.
+  float v[V];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MP; ++m) v[r * MP + m] = acc[r][m];
+  const int p = lane & 15;
+  fold<V, 0x140>(v, p & 8);
+  fold<V / 2, 0x141>(v, p & 4);
+  fold<V / 4, 0x1B>(v, p & 2);
+  fold<V / 8, 0xB1>(v, p & 1);
+  constexpr int kPer = V / 16;
+  float* dst = red + (wave * 4 + (lane >> 4)) * V + p * kPer;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) dst[j] = v[j];
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < V) {
+    const int t = threadIdx.x;
+    float s = 0.f;
+    for (int i = 0; i < nw * 4; ++i) s += red[i * V + t];
+    const int r = t / MP, m = t % MP;
+    if (m < M && n0 + r < N) y[static_cast<int64_t>(m) * ys + n0 + r] = skv::f2bf(s);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int g_waves_override = -1;  // SKV_LINEAR_WAVES, read once
+
+template <int R, int MP>
+void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16_t* y, int64_t ys, int M, int N, int K,
+            hipStream_t s) {
+  const int groups = (N + R - 1) / R;
+  const int nblk = (K + kBlockK - 1) / kBlockK;
+  // Waves per workgroup, from sweeps of the Llama-3-8B projections and lm head on MI355X with
+  // cold weights: at up to 4 rows four waves win on every shape; at 8 rows (twice the
+  // registers, half the resident waves) four win on the 4096-row weights, one on wider ones,
+  // two on the vocabulary-sized head. At most one wave per k block.
+  int nw = MP <= 4 ? 4 : groups <= 512 ? 4 : groups >= 8192 ? 2 : 1;
+  if (g_waves_override > 0) nw = g_waves_override;
+  while (nw > 1 && nw > nblk) nw /= 2;
+  hipLaunchKernelGGL((linear_kernel<R, MP>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y, ys, M, N, K);
+}
+
+}  // namespace
+
+extern "C" int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                          uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
+  const char* what = "linear";
+  if (!x || !weight || !y) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  if (m < 1 || m > 16 || n < 1 || k < 8 || k % 8) {
+    skv_set_error("%s: m=%d n=%d k=%d (1 <= m <= 16, k a multiple of 8)", what, m, n, k);
+    return SKV_EUNSUPPORTED;
+  }
+  if (!aligned16(x) || !aligned16(weight) || x_stride % 8 || weight_stride % 8 || x_stride < k ||
+      weight_stride < k || y_stride < n) {
+    skv_set_error("%s: x and weight rows must be 16-byte aligned and hold k elements", what);
+    return SKV_EINVAL;
+  }
+  if (g_waves_override < 0) {
+    const char* e = getenv("SKV_LINEAR_WAVES");
+    const int v = e ? atoi(e) : 0;
+    g_waves_override = (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (m == 1)
+    launch<16, 1>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  else if (m == 2)
+    launch<8, 2>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  else if (m <= 4)
+    launch<8, 4>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  else if (m <= 8)
+    launch<8, 8>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  else
+    launch<2, 16>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  return skv_check_launch(what);
+}

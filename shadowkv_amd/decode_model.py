@@ -141,8 +141,8 @@ class SyntheticDecoder:
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
                  dtype=torch.bfloat16, lanes: int = 1, fused: bool = True):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
-        # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels
-        # (libshadowkv_amd), instead of separate torch operations
+        # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels and
+        # the projections on the skinny linear kernel (libshadowkv_amd), instead of torch operations
         self.fused = fused
         s = shape
         D = s.head_dim
@@ -212,6 +212,15 @@ class SyntheticDecoder:
     def _norm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         return F.rms_norm(x, (x.shape[-1],), w, self.shape.eps)
 
+    def _linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """x @ w.T; fused: the library's skinny linear (weights streamed once) up to its row limit."""
+        rows = x.numel() // x.shape[-1]
+        if not self.fused or rows > shadowkv.LINEAR_MAX_ROWS:
+            return F.linear(x, w)
+        out = torch.empty(*x.shape[:-1], w.shape[0], dtype=self.dtype, device=self.device)
+        shadowkv.linear(x, w, out)
+        return out
+
     def _layer_begin(self, idx: int, state, lane: _Lane):
         """Norm, fused QKV and the first half of the attention handler (value fetch in flight).
         state: the residual stream h, or (h, x) with x = this layer's normalised input (fused)."""
@@ -220,7 +229,7 @@ class SyntheticDecoder:
         if self.fused:
             h, x = state
             b = h.shape[0]
-            qkv = F.linear(x, lw.wqkv)
+            qkv = self._linear(x, lw.wqkv)
             q_out = torch.empty(b, s.heads, D, dtype=self.dtype, device=self.device)
             q = lane.cache.rope_and_append(qkv.view(b, -1), self.pos[lane.rows], self.cos_sin, idx, q_out)
             return lane.attn.decode_begin_appended(q, idx)
@@ -242,13 +251,13 @@ class SyntheticDecoder:
         if self.fused:
             h, _ = state
             b = h.shape[0]
-            o = F.linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
+            o = self._linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
             h2, x2 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(o, lw.post_norm, s.eps, x2, residual=h, residual_out=h2)
-            gate_up = F.linear(x2, lw.gate_up)
+            gate_up = self._linear(x2, lw.gate_up)
             act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
             shadowkv.silu_and_mul(gate_up, act)
-            down = F.linear(act, lw.down)
+            down = self._linear(act, lw.down)
             w_next = self.layers[idx + 1].in_norm if idx + 1 < s.layers else self.norm_w
             h3, x3 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(down, w_next, s.eps, x3, residual=h2, residual_out=h3)
@@ -276,7 +285,7 @@ class SyntheticDecoder:
     def _head(self, state, lane: _Lane) -> torch.Tensor:
         """Final norm, lm_head, greedy token; advances the lane's RoPE positions."""
         x = state[1] if self.fused else self._norm(state, self.norm_w)  # fused: normalised already
-        logits = F.linear(x[:, -1], self.lm_head).float()  # [b, vocab]
+        logits = self._linear(x[:, -1], self.lm_head).float()  # [b, vocab]
         self.pos[lane.rows].add_(1)
         return self._greedy(logits)  # [b, 1]
 

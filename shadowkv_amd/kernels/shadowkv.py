@@ -125,7 +125,10 @@ def _host_row_stride(values: torch.Tensor, rows: int, cpu_v_length: int) -> int:
 
 
 def gather_copy_with_offsets(values, v_cache_buffer, temp, offsets, cnts, signals, batch_size, heads, cpu_v_length,
-                             gpu_v_length, gpu_v_offset, gpu_v_stride, map_size=256):
+                             gpu_v_length, gpu_v_offset, gpu_v_stride, map_size=256, *, misses_only=False):
+    """Value fetch: hit rows moved within v_cache_buffer to their new slots, then miss chunks
+    gathered from pinned host `values`. misses_only: the gather alone (the hit move issued
+    beforehand by gather_copy_d2d_with_offsets on the value buffer, e.g. on another stream)."""
     del temp, signals  # no staging buffer or flags are needed
     _check_map(map_size)
     if gpu_v_length % map_size:
@@ -142,9 +145,9 @@ def gather_copy_with_offsets(values, v_cache_buffer, temp, offsets, cnts, signal
     _need(cnts, rows, "cnts")
     if values.dtype != torch.bfloat16:
         raise ValueError("values must be bf16")
-    _lib.call("skv_gather_copy_with_offsets", device_address(values), v_cache_buffer.data_ptr(), offsets.data_ptr(),
-              cnts.data_ptr(), batch_size, heads, row_stride, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size,
-              chunk_elems, _stream())
+    _lib.call("skv_gather_copy_misses_with_offsets" if misses_only else "skv_gather_copy_with_offsets",
+              device_address(values), v_cache_buffer.data_ptr(), offsets.data_ptr(), cnts.data_ptr(), batch_size,
+              heads, row_stride, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size, chunk_elems, _stream())
 
 
 def gather_copy_d2d_with_offsets(keys, offsets, cnts, batch_size, heads, gpu_v_length, gpu_v_offset, gpu_v_stride,
@@ -527,6 +530,26 @@ def silu_and_mul(x, out):
     if orows != rows or x.shape[-1] != 2 * d:
         raise ValueError("silu_and_mul: shape mismatch")
     _lib.call("skv_silu_and_mul", x.data_ptr(), xs, out.data_ptr(), os_, rows, d, _stream())
+
+
+LINEAR_MAX_ROWS = 16
+
+
+def linear(x, weight, out):
+    """out = bf16(x @ weight.T) in fp32 for decode-sized x (at most 16 rows of [..., k]); weight
+    [n, k] with contiguous rows. The HBM-bound skinny form of F.linear (weights read once)."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(weight, "weight", torch.bfloat16)
+    _dev(out, "out", torch.bfloat16)
+    rows, xs = _rows2d(x, "x")
+    orows, os_ = _rows2d(out, "out")
+    if weight.dim() != 2 or weight.stride(-1) != 1:
+        raise ValueError("linear: weight must be [n, k] with contiguous rows")
+    n, k = weight.shape
+    if x.shape[-1] != k or out.shape[-1] != n or orows != rows:
+        raise ValueError(f"linear: shape mismatch x {tuple(x.shape)} weight {tuple(weight.shape)} out {tuple(out.shape)}")
+    _lib.call("skv_linear", x.data_ptr(), xs, weight.data_ptr(), weight.stride(0), out.data_ptr(), os_, rows, n, k,
+              _stream())
 
 
 def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache, append_row):

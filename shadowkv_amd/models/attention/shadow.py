@@ -62,9 +62,12 @@ class ShadowAttention(AttentionBase):
 
         curr_stream = torch.cuda.current_stream()
         copy_stream = kv_cache.copy_stream
+        # The value hits move within the GPU buffer here, so the copy stream (whose transfers
+        # follow one another on the host link) carries the host-link gather alone.
+        kv_cache.move_value_hits(layer_idx)
         with torch.cuda.stream(copy_stream):
             copy_stream.wait_stream(curr_stream)
-            value_states = kv_cache.get_value_cache(layer_idx, position_ids)
+            value_states = kv_cache.get_value_cache(layer_idx, position_ids, hits_moved=True)
             done = [copy_stream.record_event()]  # this fetch only, even if the stream is shared
         key_stream = getattr(kv_cache, "key_stream", None)
         if key_stream is None:

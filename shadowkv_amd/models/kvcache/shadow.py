@@ -248,13 +248,22 @@ class ShadowKVCache_CPU(KVCacheBase):
             return buf[:, :, :self.buf_len]  # length read on the device (kv_len_dev)
         return buf[:, :, :self.sparse_end + self._gen_len(layer_idx)]
 
-    def get_value_cache(self, layer_idx: int, position_ids: torch.Tensor) -> torch.Tensor:
+    def get_value_cache(self, layer_idx: int, position_ids: torch.Tensor, hits_moved: bool = False) -> torch.Tensor:
+        """The layer's value buffer with the selected chunks in place: cache hits moved to their
+        new slots (unless move_value_hits already did, hits_moved) and misses gathered from host."""
         shadowkv.gather_copy_with_offsets(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.temp,
                                           self.offsets, self.cnts, self.signals, self.batch_size,
                                           self.num_key_value_heads, int(self.max_ctx_chunks_len * self.head_dim),
                                           int(self.sparse_budget * self.head_dim), self.kernel_offset,
-                                          self.kernel_stride, self.select_sets)
+                                          self.kernel_stride, self.select_sets, misses_only=hits_moved)
         return self._live_view(self.v_cache_buffer[layer_idx], layer_idx)
+
+    def move_value_hits(self, layer_idx: int):
+        """The in-buffer half of the value fetch alone (hit rows to their new slots), so that a
+        later get_value_cache(..., hits_moved=True) on the copy stream is host-link work only."""
+        shadowkv.gather_copy_d2d_with_offsets(self.v_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
+                                              self.num_key_value_heads, int(self.sparse_budget * self.head_dim),
+                                              self.kernel_offset, self.kernel_stride, self.select_sets)
 
     def get_key_cache(self, layer_idx: int, position_ids: torch.Tensor, rope_func, cos_sin_cache) -> torch.Tensor:
         shadowkv.gather_copy_d2d_with_offsets(self.k_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,

@@ -113,6 +113,17 @@ def test_cached_gather_copy(gpu, hit_frac, chunk, S, pinned):
     wantk = oracle.compact_hits(sparse, offs, cnts)
     assert np.array_equal(kdev.cpu()[:, :, prefix:prefix + S * chunk].reshape(rows, S, E).view(torch.int16).numpy(),
                           wantk)
+    # the split form the decode handler issues: hit move on one stream, then the miss gather
+    # alone on another; same bytes as the combined call
+    sdev = dev.to(gpu)
+    shadowkv.gather_copy_d2d_with_offsets(sdev, offs_g, cnts_g, B, H, S * E, prefix * D, buf_len * D, S)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        shadowkv.gather_copy_with_offsets(host, sdev, None, offs_g, cnts_g, None, B, H, nchunks * E, S * E,
+                                          prefix * D, buf_len * D, S, misses_only=True)
+    torch.cuda.synchronize()
+    assert torch.equal(sdev.cpu().view(torch.int16), got.view(torch.int16))  # bit patterns (some are NaNs)
 
 
 def test_gather_copy_plain(gpu):

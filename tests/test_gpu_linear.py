@@ -1,0 +1,62 @@
+"""The skinny decode linear layer (skv_linear) against an fp32 torch reference of the same
+product: bf16 inputs, exact products, fp32 sums, one rounding to bf16."""
+import pytest
+import torch
+
+from shadowkv_amd.kernels import shadowkv
+from tests.decode_harness import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _ref(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return (x.float() @ w.float().t()).to(torch.bfloat16)
+
+
+# (rows, n, k): the Llama-3-8B projections at 4 and 8 decode rows, GLM-4-9B's down projection
+# (k = 13696 is not a multiple of the 512-element block), row counts that are not powers of two,
+# n not a multiple of a workgroup's rows, and the smallest k.
+CASES = [(4, 6144, 4096), (4, 4096, 4096), (4, 28672, 4096), (8, 4096, 14336), (1, 1000, 4096),
+         (2, 520, 1032), (3, 77, 4096), (5, 130, 13696), (8, 64, 8), (13, 333, 2048), (16, 96, 4104)]
+
+
+@pytest.mark.parametrize("rows,n,k", CASES)
+def test_linear(gpu, rows, n, k):
+    _say(f"linear rows={rows} n={n} k={k}")
+    g = torch.Generator().manual_seed(rows * 7919 + n + k)
+    x = torch.randn(rows, 1, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5).to(torch.bfloat16)
+    out = torch.full((rows, 1, n), 7.0, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear(x.to(gpu), w.to(gpu), out)
+    torch.cuda.synchronize()
+    assert_bf16_close(out.cpu(), _ref(x, w), floor=1e-4, what=f"linear {rows}x{n}x{k}")
+
+
+def test_linear_strided_views(gpu):
+    """Rows taken from wider buffers (x a column slice, out a slice of a fused output), as the
+    decode step passes views of its fused projections."""
+    rows, n, k = 4, 512, 4096
+    _say("linear strided views")
+    g = torch.Generator().manual_seed(3)
+    xb = torch.randn(rows, k + 64, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5).to(torch.bfloat16)
+    ob = torch.zeros(rows, 3 * n, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear(xb.to(gpu)[:, 64:], w.to(gpu), ob[:, n:2 * n])
+    torch.cuda.synchronize()
+    o = ob.cpu()
+    assert_bf16_close(o[:, n:2 * n], _ref(xb[:, 64:], w), floor=1e-4, what="linear views")
+    assert not o[:, :n].any() and not o[:, 2 * n:].any(), "wrote outside the output slice"
+
+
+def test_linear_rejects(gpu):
+    w = torch.zeros(8, 64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError):  # more rows than the skinny kernel takes
+        shadowkv.linear(torch.zeros(17, 64, dtype=torch.bfloat16, device=gpu), w,
+                        torch.empty(17, 8, dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError):
+        shadowkv.linear(torch.zeros(2, 32, dtype=torch.bfloat16, device=gpu), w,
+                        torch.empty(2, 8, dtype=torch.bfloat16, device=gpu))
