@@ -209,7 +209,7 @@ int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, in
  * q row: q + b*q_stride_b + hq*q_stride_h; K/V row s of (b,h): base + b*kv_stride_b + h*kv_stride_h
  * + s*kv_stride_s; out row: out + b*o_stride_b + hq*o_stride_h. head_dim must be 128.
  * workspace: caller-provided device scratch of skv_sparse_attn_workspace_bytes(...) bytes.
- * kv_len at most 262144 (1024 splits of 256 keys).
+ * kv_len at most 262144.
  * kv_len_dev (optional, no reference counterpart): device int32 holding the live length, read
  * when the kernel runs and clamped to [1, kv_len]; kv_len is then the maximum. This keeps the
  * call valid inside a captured HIP graph while the cache grows by one row per replay. */

@@ -2,13 +2,14 @@
 //
 // Replaces flash_attn_with_kvcache(q, k, v, causal=True) at models/attention/shadow.py:48
 // (q_len = 1, so causality masks nothing). Split-L flash decoding for CDNA4:
-//   attn_split_kernel: workgroup = (kv head, split of kSplit keys); all G query heads that
+//   attn_split_kernel: workgroup = (kv head, split of 128 keys); all G query heads that
 //     share the kv head are served by one pass over its K and V rows, so every K/V byte is read
 //     once from HBM. Scores on MFMA: v_mfma_f32_16x16x32_bf16 with the (up to 16) query heads as
 //     the A rows and 16 keys as the B columns, so each lane ends up holding finished scores (no
 //     cross-lane reduction); split softmax per query head with DPP/readlane wave reductions;
 //     P.V in fp32: 16 key streams x 8 dims per lane, the streams summed through LDS.
-//   attn_combine_kernel: log-sum-exp merge of the splits, bf16 output.
+//   attn_combine_kernel: log-sum-exp merge of the splits in one pass (running maximum), every
+//     load of a 32-split chunk issued before the first is used; bf16 output.
 #include "wave_reduce.h"
 
 namespace {
@@ -16,8 +17,11 @@ namespace {
 using skv::u32x4;
 
 constexpr int kThreads = 256;
-constexpr int kSplit = 256;
+// Keys per split workgroup. 128 rather than 256: twice the workgroups in flight at decode batch
+// sizes (MI355X, cold K/V, Llama-3-8B shape batch 8: 24 vs 29 us; GLM-4-9B batch 4: 19 vs 27 us).
+constexpr int kSplit = 128;
 constexpr int kHeadDim = 128;
+constexpr int kMaxKvLen = 262144;
 
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -35,6 +39,7 @@ struct AttnArgs {
   const uint16_t* v;
   int64_t kv_sb, kv_sh, kv_ss;
   int Hkv, G, L, splits;  // L: maximum length (grid sizing)
+  int split_keys;         // keys per split workgroup
   const int32_t* L_dev;   // optional device-resident length, clamped to [1, L]
   float scale;
   float* ws_o;   // [B*Hq][splits][128]
@@ -50,17 +55,18 @@ __device__ __forceinline__ int live_length(const AttnArgs& a) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// kSplit keys per workgroup; the split's V rows are requested right after the scores, so their
+// latency overlaps the softmax (requesting them with K, at entry, measured no faster and holds
+// more registers).
 template <int GP>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
-  // Up to 4 query heads per kv head, the split's K and V rows are all requested at entry (one
-  // memory latency per workgroup); with more, V is requested right after the scores, so its
-  // latency overlaps the softmax instead.
-  constexpr bool kEarlyV = false;
   constexpr int kRows = kSplit / 16;        // keys per P.V stream
   constexpr int kGroups = kSplit / 4 / 16;  // 16-key MFMA groups per wave
-  constexpr int kPass = GP < 4 ? GP : 4;    // query heads per stream-reduction pass
+  constexpr int kPerLane = kSplit / 64;     // softmax entries per lane
+  constexpr int kVals = GP * 8;              // P.V partial sums per lane: [head][8 dims]
+  constexpr int kKept = kVals / 4;           // per lane after the in-wave stream fold
   __shared__ float p_lds[GP][kSplit];
-  __shared__ __align__(16) float red[16][kPass][kHeadDim];  // [key stream][head of the pass][dim]
+  __shared__ __align__(16) float red[4][64][kKept];  // [wave][lane][value]
   __shared__ float ml[GP][2];
 
   const int split = blockIdx.x;
@@ -105,7 +111,6 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       vr[i] = skv::load16_or_zero(vh + static_cast<int64_t>(min(s, s1 - 1)) * a.kv_ss + li * 8, s < s1);
     }
   };
-  if (kEarlyV) load_v();
 #pragma unroll
   for (int kg = 0; kg < kGroups; ++kg) {
     f32x4_t d = {0.f, 0.f, 0.f, 0.f};
@@ -122,23 +127,23 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       if (g < G) p_lds[g][jl] = live ? d[v] * a.scale : -INFINITY;
     }
   }
-  if (!kEarlyV) load_v();
+  load_v();
   __syncthreads();
 
   for (int g = wave; g < G; g += 4) {
-    float x[4];
+    float x[kPerLane];
     float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      x[u] = p_lds[g][lane * 4 + u];
+    for (int u = 0; u < kPerLane; ++u) {
+      x[u] = p_lds[g][lane * kPerLane + u];
       mx = fmaxf(mx, x[u]);
     }
     mx = skv::wave_max_dpp(mx);
     float l = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kPerLane; ++u) {
       const float e = (x[u] == -INFINITY) ? 0.f : expf(x[u] - mx);
-      p_lds[g][lane * 4 + u] = e;
+      p_lds[g][lane * kPerLane + u] = e;
       l += e;
     }
     l = skv::wave_sum_dpp(l);
@@ -171,97 +176,100 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     }
   }
 
-  // Sum the 16 key streams through LDS, kPass query heads per pass.
+  // Sum the 16 key streams. The 4 streams of a wave (lane bits 5 and 4) fold in registers:
+  // v_permlane32_swap / v_permlane16_swap with the lower half of the values as one operand and
+  // the upper half as the other hand every lane its own kept value and its partner's copy of
+  // it, so each step is a swap and an add and halves the values a lane holds. Lane (grp, li)
+  // then holds flattened values [grp*kKept, +kKept) of [head][8 dims] for dims li*8..+8; the 4
+  // waves are summed through LDS.
+  float v[kVals];
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[g * 8 + e] = acc[g][e];
+#pragma unroll
+  for (int j = 0; j < kVals / 2; ++j) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[kVals / 2 + j]), false,
+                                                    false);
+    v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int j = 0; j < kKept; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[kKept + j]), false,
+                                                    false);
+    v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int j = 0; j < kKept; ++j) red[wave][lane][j] = v[j];
+  __syncthreads();
   const int Hq = a.Hkv * G;
-#pragma unroll
-  for (int p0 = 0; p0 < GP; p0 += kPass) {
-    if (p0 > 0) __syncthreads();  // the previous pass has read red
-#pragma unroll
-    for (int gp = 0; gp < kPass; ++gp) {
-      float* dst = &red[stream][gp][li * 8];
-      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{acc[p0 + gp][0], acc[p0 + gp][1], acc[p0 + gp][2], acc[p0 + gp][3]};
-      *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{acc[p0 + gp][4], acc[p0 + gp][5], acc[p0 + gp][6], acc[p0 + gp][7]};
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < kPass * kHeadDim; idx += kThreads) {
-      const int gp = idx / kHeadDim, d = idx - gp * kHeadDim;
-      const int g = p0 + gp;
-      if (g >= G) continue;
-      float o = 0.f;
-#pragma unroll
-      for (int st = 0; st < 16; ++st) o += red[st][gp][d];
-      const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
-      a.ws_o[r * kHeadDim + d] = o;
-      if (d == 0) {
-        a.ws_ml[r * 2] = ml[g][0];
-        a.ws_ml[r * 2 + 1] = ml[g][1];
-      }
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kThreads) {
+    const int g = idx / kHeadDim, d = idx - g * kHeadDim;
+    const int f = g * 8 + (d & 7);                        // flattened value index
+    const int src = (f / kKept) * 16 + (d >> 3);           // lane (grp, li) that holds it
+    const int j = f % kKept;
+    const float o = (red[0][src][j] + red[1][src][j]) + (red[2][src][j] + red[3][src][j]);
+    const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
+    a.ws_o[r * kHeadDim + d] = o;
+    if (d == 0) {
+      a.ws_ml[r * 2] = ml[g][0];
+      a.ws_ml[r * 2 + 1] = ml[g][1];
     }
   }
 }
 
-constexpr int kMaxSplits = 1024;  // kv_len <= 262144
-
-// Block-wide (two waves) max / sum through a 2-slot LDS exchange.
-__device__ __forceinline__ float block2_max(float v, float* x) {
-  v = skv::wave_max_dpp(v);
-  if ((threadIdx.x & 63) == 0) x[threadIdx.x >> 6] = v;
-  __syncthreads();
-  v = fmaxf(x[0], x[1]);
-  __syncthreads();
-  return v;
-}
-__device__ __forceinline__ float block2_sum(float v, float* x) {
-  v = skv::wave_sum_dpp(v);
-  if ((threadIdx.x & 63) == 0) x[threadIdx.x >> 6] = v;
-  __syncthreads();
-  v = x[0] + x[1];
-  __syncthreads();
-  return v;
-}
-
+// One workgroup (two waves, one lane per dim) per (b, query head). Online merge over the
+// splits in chunks of kChunk: each thread first requests its dim of the chunk's kChunk partial
+// outputs, lanes 0..kChunk-1 of wave 0 request one split's (m, l) each (vector loads, so no
+// scalar-load waits), and the chunk's maximum and weights go through LDS; the running maximum
+// M, denominator l and accumulator acc are rescaled when M grows.
 __global__ void __launch_bounds__(kHeadDim) attn_combine_kernel(AttnArgs a) {
-  static_assert(kHeadDim == 128, "two waves per row");
-  __shared__ float w_lds[kMaxSplits];
-  __shared__ float xch[2];
+  constexpr int kChunk = 32;
+  __shared__ float w_s[kChunk];
+  __shared__ float m_s, l_s;
   const int row = blockIdx.x;  // b*Hq + hq
   const int Hq = a.Hkv * a.G;
   const int b = row / Hq;
   const int hq = row - b * Hq;
   const int d = threadIdx.x;
-  const float* ml = a.ws_ml + static_cast<int64_t>(row) * a.splits * 2;
-  const float* o = a.ws_o + static_cast<int64_t>(row) * a.splits * kHeadDim;
-  const int used = (live_length(a) + kSplit - 1) / kSplit;
-  float m = -INFINITY;
-  for (int s = d; s < used; s += kHeadDim) m = fmaxf(m, ml[2 * s]);
-  const float M = block2_max(m, xch);
-  float l = 0.f;
-  for (int s = d; s < used; s += kHeadDim) {
-    const float w = expf(ml[2 * s] - M);
-    w_lds[s] = w;
-    l += ml[2 * s + 1] * w;
-  }
-  const float inv = 1.f / block2_sum(l, xch);  // the barriers also publish w_lds
-  float acc = 0.f;
-  int s = 0;
-  for (; s + 8 <= used; s += 8) {
-    float x[8];
+  const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + static_cast<int64_t>(row) * a.splits;
+  const float* o = a.ws_o + static_cast<int64_t>(row) * a.splits * kHeadDim + d;
+  const int used = (live_length(a) + a.split_keys - 1) / a.split_keys;  // >= 1
+  float M = -INFINITY, l = 0.f, acc = 0.f;
+  for (int s0 = 0; s0 < used; s0 += kChunk) {
+    float x[kChunk];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = o[static_cast<int64_t>(s + u) * kHeadDim + d];
+    for (int u = 0; u < kChunk; ++u) x[u] = o[static_cast<int64_t>(min(s0 + u, used - 1)) * kHeadDim];
+    const bool own = d < kChunk && s0 + d < used;  // this lane's split of the chunk
+    const float2 p = ml[min(s0 + d, used - 1)];
+    const float cm = skv::wave_max_dpp(own ? p.x : -INFINITY);  // wave 0 holds the chunk
+    if (d == 0) m_s = cm;
+    __syncthreads();
+    const float Mn = fmaxf(M, m_s);
+    const float w = own ? expf(p.x - Mn) : 0.f;
+    const float lw = skv::wave_sum_dpp(own ? p.y * w : 0.f);
+    if (d < kChunk) w_s[d] = w;
+    if (d == 0) l_s = lw;
+    __syncthreads();
+    const float r = expf(M - Mn);  // 0 on the first chunk (M = -inf)
+    float sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = fmaf(w_lds[s + u], x[u], acc);
+    for (int u = 0; u < kChunk; ++u) sum = fmaf(w_s[u], x[u], sum);
+    acc = fmaf(acc, r, sum);
+    l = fmaf(l, r, l_s);
+    M = Mn;
+    __syncthreads();  // w_s, m_s, l_s are rewritten by the next chunk
   }
-  for (; s < used; ++s) acc = fmaf(w_lds[s], o[static_cast<int64_t>(s) * kHeadDim + d], acc);
-  a.out[b * a.o_sb + hq * a.o_sh + d] = skv::f2bf(acc * inv);
+  a.out[b * a.o_sb + hq * a.o_sh + d] = skv::f2bf(acc / l);
 }
 
-int splits_for(int kv_len) { return (kv_len + kSplit - 1) / kSplit; }
+int splits_for(int kv_len, int split_keys) { return (kv_len + split_keys - 1) / split_keys; }
 
 }  // namespace
 
 extern "C" int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, int kv_len) {
   if (batch_size < 1 || q_heads < 1 || kv_len < 1) return 0;
-  return static_cast<int64_t>(batch_size) * q_heads * splits_for(kv_len) * (kHeadDim + 2) * sizeof(float);
+  return static_cast<int64_t>(batch_size) * q_heads * splits_for(kv_len, kSplit) * (kHeadDim + 2) * sizeof(float);
 }
 
 extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
@@ -291,8 +299,8 @@ extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int
     skv_set_error("%s: q/K/V rows must be 16-byte aligned", what);
     return SKV_EINVAL;
   }
-  if (splits_for(kv_len) > kMaxSplits) {
-    skv_set_error("%s: kv_len=%d exceeds %d", what, kv_len, kMaxSplits * kSplit);
+  if (kv_len > kMaxKvLen) {
+    skv_set_error("%s: kv_len=%d exceeds %d", what, kv_len, kMaxKvLen);
     return SKV_EUNSUPPORTED;
   }
   const int64_t need = skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len);
@@ -313,7 +321,8 @@ extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int
   a.G = G;
   a.L = kv_len;
   a.L_dev = kv_len_dev;
-  a.splits = splits_for(kv_len);
+  a.split_keys = kSplit;
+  a.splits = splits_for(kv_len, a.split_keys);
   a.scale = scale;
   a.ws_o = static_cast<float*>(workspace);
   a.ws_ml = a.ws_o + static_cast<int64_t>(batch_size) * q_heads * a.splits * kHeadDim;

@@ -29,4 +29,4 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert rc == 1 and "k=200" in _lib.last_error()
     rc = lib.skv_batch_gemm_softmax(p, p, p, p, p, p, 1, 4, 10, 64, 1.0, 0.0, None)
     assert rc == 2 and "k=64" in _lib.last_error()
-    assert lib.skv_sparse_attn_workspace_bytes(8, 32, 2600) == 8 * 32 * 11 * 130 * 4
+    assert lib.skv_sparse_attn_workspace_bytes(8, 32, 2600) == 8 * 32 * 21 * 130 * 4  # 128-key splits
