@@ -48,9 +48,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
-    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select"], default="decode",
+    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear"], default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
-                        "attention: the sparse decode attention alone; select: the fused chunk selection alone")
+                        "attention: the sparse decode attention alone; select: the fused chunk selection alone; "
+                        "linear: the skinny decode projections alone (next to torch's GEMM)")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -342,6 +343,10 @@ def attention_microbench(args) -> int:
 
     D = 128
     reps = max(args.steps, 4)
+    # A plain copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters of profiling runs.
+    cal = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
+    torch.neg(cal, out=cal)
+    del cal
     for name, B, Hq, Hk, L in (("Llama-3-8B", 8, 32, 8, 2600), ("Llama-3-8B", 24, 32, 8, 2600),
                                ("GLM-4-9B", 4, 32, 2, 2600), ("Llama-3-8B-1M", 1, 32, 8, 19616)):
         g = torch.Generator(device="cuda").manual_seed(L + B)
@@ -424,6 +429,47 @@ def select_microbench(args) -> int:
     return 0
 
 
+def linear_microbench(args) -> int:
+    """The skinny linear kernel on the Llama-3-8B decode projections (fused QKV, o, fused
+    gate/up, down, lm head) at 4 and 8 token rows, cold weights (distinct copies rotated past the
+    last-level cache), next to torch's GEMM on the same operands. One JSON line per (shape, rows)."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    shapes = (("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336),
+              ("lm_head", 128256, 4096))
+    reps = max(args.steps, 4)
+    for name, n, k in shapes:
+        wbytes = n * k * 2
+        sets = cold_sets(wbytes)
+        g = torch.Generator(device="cuda").manual_seed(n + k)
+        ws = [(torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(sets)]
+        set_reps = -(-reps // sets) * sets
+        for rows in (4, 8):
+            x = torch.randn(rows, k, generator=g, device="cuda").to(torch.bfloat16)
+            y = torch.empty(rows, n, dtype=torch.bfloat16, device="cuda")
+            t = gpu_time_per_call(lambda i: shadowkv.linear(x, ws[i % sets], y), set_reps)
+            t_torch = gpu_time_per_call(lambda i: torch.matmul(x, ws[i % sets].t(), out=y), set_reps)
+            nbytes = wbytes + rows * (k + n) * 2
+            out_line = {"metric": "skinny decode linear weight stream GB/s", "value": round(nbytes / t / 1e9, 1),
+                        "unit": "GB/s", "n_gpus": 1, "steps": set_reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
+                        "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
+                        "data": "synthetic: x ~ N(0,1), weights ~ N(0, 0.02) bf16; timed as HIP-graph replays of "
+                                f"back-to-back launches rotating over {sets} weight copies (> 1 GiB together)",
+                        "config": {"workload": f"Llama-3-8B {name} projection: {rows} rows x [{n}, {k}] weight",
+                                   "rows": rows, "n": n, "k": k, "rotated_sets": sets},
+                        "roofline": {"kernel": "linear_kernel", "bound": "hbm", "achieved": round(nbytes / t / 1e9, 1),
+                                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(t * 1e6, 2),
+                                     "torch_matmul_us": round(t_torch * 1e6, 2)},
+                        "cpu_baseline": None}
+            print(json.dumps(out_line), flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -436,6 +482,8 @@ def main() -> int:
         return attention_microbench(args)
     if args.workload == "select":
         return select_microbench(args)
+    if args.workload == "linear":
+        return linear_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv
