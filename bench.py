@@ -45,6 +45,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--batch", type=int, default=8)
     p.add_argument("--ctx", type=int, default=122880)
     p.add_argument("--budget", type=int, default=2048)
+    p.add_argument("--chunk", type=int, default=8, help="rows per chunk (the reference's default is 8)")
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
@@ -495,7 +496,7 @@ def main() -> int:
     t0 = time.time()
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
     lanes = args.lanes if args.batch % args.lanes == 0 else 1
-    model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget,
+    model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes)
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
@@ -566,7 +567,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: random-init weights, seeded random ShadowKV state of the exact shapes, greedy tokens",
         "config": {"workload": f"{shape.name}-shape {shape.layers}-layer decode, batch {args.batch}, ctx {args.ctx}, "
-                               f"ShadowKV rank 160 chunk 8 budget {args.budget}, V in pinned host memory, "
+                               f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, V in pinned host memory, "
                                f"{lanes} interleaved batch lane(s), "
                                f"{'HIP-graph-captured step' if graph else 'eager step'}",
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},

@@ -95,14 +95,15 @@ def write_kat():
                         expected_cnts=cnts.astype(np.int16))
 
 
-def decode_small_case():
-    """Seeded inputs of the small decode fixture and the oracle's results (deterministic)."""
+def decode_small_case(chunk=8):
+    """Seeded inputs of the small decode fixture and the oracle's results (deterministic). The
+    committed fixture is the chunk-8 case; other chunk sizes give the same prompt tensors."""
     sys.path.insert(0, str(HERE.parents[1]))
     import torch
     import oracle
 
     g = torch.Generator().manual_seed(1234)
-    B, H, G, D, ctx, rank, chunk, budget = 1, 2, 4, 128, 2048, 32, 8, 1024
+    B, H, G, D, ctx, rank, budget = 1, 2, 4, 128, 2048, 32, 1024
     A = torch.randn(ctx, rank, generator=g) / rank ** 0.5
     Bm = torch.randn(rank, H * D, generator=g) / rank ** 0.5
     k_pre = (A @ Bm + 0.05 * torch.randn(ctx, H * D, generator=g)).view(1, ctx, H, D).transpose(1, 2)

@@ -39,10 +39,12 @@ def test_single_layer_decode_step(gpu):
         assert np.array_equal(got["position_ids"], d["out_position_ids"])
 
 
-@pytest.mark.parametrize("device_lengths", [False, True])
-def test_multi_layer_multi_step_decode(gpu, device_lengths):
-    print(f"decode small fixture, 2 layers x 4 steps, device_lengths={device_lengths}", flush=True)
-    case = make_golden.decode_small_case()
+@pytest.mark.parametrize("device_lengths,chunk", [(False, 8), (True, 8), (True, 4), (True, 16), (False, 16)])
+def test_multi_layer_multi_step_decode(gpu, device_lengths, chunk):
+    """Also chunk sizes other than 8 (budget 1024: 256 selected chunks of 4 rows, 64 of 16 rows)
+    through every kernel of the step."""
+    print(f"decode small fixture, 2 layers x 4 steps, device_lengths={device_lengths}, chunk={chunk}", flush=True)
+    case = make_golden.decode_small_case(chunk)
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
     steps, layers = 4, 2
