@@ -49,10 +49,12 @@ def parse() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
-    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear"], default="decode",
+    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode"],
+                   default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
                         "attention: the sparse decode attention alone; select: the fused chunk selection alone; "
-                        "linear: the skinny decode projections alone (next to torch's GEMM)")
+                        "linear: the skinny decode projections alone (next to torch's GEMM); encode: the prefill "
+                        "encoder (low-rank factors, chunk statistics, outliers, landmarks, initial selection)")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -471,6 +473,112 @@ def linear_microbench(args) -> int:
     return 0
 
 
+def encode_microbench(args) -> int:
+    """The device prefill encoder per layer (ShadowKVCache_CPU.get_svd + prefill_kv_cache) at the
+    Llama-3-8B shape (8 kv heads x 4 query heads), ctx 122880, rank 160, chunk 8, budget 2048, on
+    random low-rank-plus-noise keys; components timed separately, the chunk-statistics kernel against
+    its HBM roofline. One JSON line per batch size."""
+    import types
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+    from shadowkv_amd.models.kvcache import ShadowKVCache_CPU
+    from shadowkv_amd.models.kvcache.shadow import low_rank_factors
+
+    H, G, D, R, c, budget, ctx = 8, 4, 128, 160, 8, 2048, args.ctx
+    dev = torch.device("cuda")
+    cal = torch.empty(64 * 2 ** 20, dtype=torch.float32, device=dev)
+    torch.neg(cal, out=cal)
+    del cal
+
+    def timed(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / reps
+
+    for B in (1, 8):
+        g = torch.Generator(device=dev).manual_seed(B)
+        a = torch.randn(B, ctx, 128, generator=g, device=dev) @ torch.randn(B, 128, H * D, generator=g, device=dev)
+        k_pre = (a / 12 + 0.1 * torch.randn(B, ctx, H * D, generator=g, device=dev)).to(torch.bfloat16)
+        del a
+        k_pre = k_pre.view(B, ctx, H, D).transpose(1, 2).contiguous()
+        k_roped = k_pre.clone()  # the encoder's cost does not depend on the rotation
+        v = torch.randn(B, H, ctx, D, generator=g, device=dev).to(torch.bfloat16)
+        q = torch.randn(B, H * G, 1, D, generator=g, device=dev).to(torch.bfloat16)
+        cfg = types.SimpleNamespace(num_attention_heads=H * G, num_key_value_heads=H, hidden_size=H * G * D,
+                                    num_hidden_layers=1)
+        cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device="cuda", sparse_budget=budget,
+                                  chunk_size=c, rank=R, zero_host_store=False)
+
+        def encode():
+            cache.prefilled_batch = 0
+            cache.get_svd(k_pre, 0)
+            cache.prefill_kv_cache(v, 0, k_roped, q)
+
+        t_all = timed(encode)
+        kf = k_pre.transpose(1, 2).reshape(B, ctx, H * D)
+        t_svd = timed(lambda: low_rank_factors(kf, R))
+        chunks = cache.chunks
+        cand = torch.empty(B, H, chunks, D, dtype=torch.bfloat16, device=dev)
+        mc = torch.empty(B, H, chunks, dtype=torch.float32, device=dev)
+        t_stats = timed(lambda: shadowkv.chunk_stats(k_roped, chunks, c, cand, mc), reps=20)
+        out_idx = torch.empty(B * H, cache.outlier_chunk, dtype=torch.int64, device=dev)
+        rest = torch.empty(B * H, chunks - cache.outlier_chunk, dtype=torch.int64, device=dev)
+        t_sel = timed(lambda: shadowkv.select_outliers(mc.view(B * H, chunks), cache.outlier_chunk, out_idx, rest),
+                      reps=20)
+        t_full = None
+        if B == 1:
+            t_full = timed(lambda: torch.linalg.svd(kf.float(), full_matrices=False), reps=1)
+        stats_bytes = B * H * (chunks * c * D * 2 + chunks * D * 2 + chunks * 4)
+        achieved = stats_bytes / (t_stats * 1e-3) / 1e9
+        cpu = None
+        if B == 1 and not args.no_cpu_baseline:
+            cpu = encode_cpu_baseline(k_pre, v, q, R, c, budget)
+        out = {"metric": "prefill encoder ms per layer", "value": round(t_all, 3), "unit": "ms", "n_gpus": 1,
+               "steps": 3, "warmup": 1, "ms_per_step": round(t_all, 3), "higher_is_better": False,
+               "scaling": "strong", "vs_baseline": None, "dtype": "bf16 (fp32 factors)",
+               "data": "synthetic: rank-128 keys plus noise, random values and last query, bf16",
+               "config": {"workload": f"prefill encoder, Llama-3-8B shape (8 kv heads), batch {B}, ctx {ctx}, "
+                                      f"rank {R}, chunk {c}, budget {budget}", "batch": B, "ctx": ctx},
+               "components_ms": {"low_rank_factors (Gram GEMM + eigh + GEMM)": round(t_svd, 3),
+                                 "chunk_stats": round(t_stats, 4), "select_outliers": round(t_sel, 4),
+                                 "reference full SVD on the GPU (torch.linalg.svd, fp32)":
+                                     round(t_full, 1) if t_full else None},
+               "roofline": {"kernel": "chunk_stats_kernel", "bound": "hbm", "achieved": round(achieved, 1),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                            "traffic": None, "algorithmic_bytes_per_launch": stats_bytes,
+                            "avg_launch_us": round(t_stats * 1e3, 2)},
+               "cpu_baseline": cpu}
+        print(json.dumps(out), flush=True)
+        del cache, k_pre, k_roped, v, kf
+        torch.cuda.empty_cache()
+    return 0
+
+
+def encode_cpu_baseline(k_pre, v, q, R, c, budget, sample_ctx: int = 16384) -> dict:
+    """The CPU oracle's encode_layer on the first sample_ctx tokens of batch row 0 (a reported
+    baseline only), scaled linearly to the full prompt."""
+    import torch
+    import oracle
+
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(threads)
+    ctx = k_pre.shape[2]
+    cs = oracle.build_cos_sin_cache(sample_ctx + 64, 500000.0)
+    kp, vv, qq = k_pre[:1, :, :sample_ctx].cpu(), v[:1, :, :sample_ctx].cpu(), q[:1].cpu()
+    t0 = time.perf_counter()
+    oracle.encode_layer(kp, vv, qq, cs, rank=R, chunk=c, budget=budget)
+    t = time.perf_counter() - t0
+    return {"value": round(t * 1e3 * ctx / sample_ctx, 1), "unit": "ms per layer (scaled)", "cores": threads,
+            "kind": "port", "sample": f"oracle encode_layer (full fp32 SVD, bf16 cosine, torch.topk) on batch row 0, "
+                                      f"first {sample_ctx} tokens: {t * 1e3:.0f} ms, scaled by {ctx}/{sample_ctx}"}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -485,6 +593,8 @@ def main() -> int:
         return select_microbench(args)
     if args.workload == "linear":
         return linear_microbench(args)
+    if args.workload == "encode":
+        return encode_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv

@@ -244,6 +244,28 @@ int skv_silu_and_mul(const uint16_t* x, int64_t x_stride, uint16_t* out, int64_t
 int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride, uint16_t* y,
                int64_t y_stride, int m, int n, int k, void* stream);
 
+/* ---- f1: prefill encoder ----------------------------------------------------------------
+ * Replace the chunk statistics, outlier selection and landmark compaction of prefill_kv_cache
+ * (models/kvcache/shadow.py:486-519). skv_chunk_stats: for each (b, h, chunk i < chunks) of the
+ * post-RoPE keys (row s of (b,h) at keys + b*stride_b + h*stride_h + s*stride_s, head_dim 128),
+ * candidates[(b*heads + h)*chunks + i] = bf16(mean of rows i*c .. i*c+c-1) (fp32 sum, one
+ * rounding) and min_cos[...] = min over those rows of cos(candidate, row), in fp32 with norms
+ * clamped to 1e-8 (the reference computes it with bf16 operations). */
+int skv_chunk_stats(const uint16_t* keys, int64_t stride_b, int64_t stride_h, int64_t stride_s, int batch_size,
+                    int heads, int chunks, int chunk_size, uint16_t* candidates, float* min_cos, void* stream);
+
+/* Per row r < rows of min_cos [rows, chunks]: outlier_idx[r] = the `outliers` chunk ids of smallest
+ * min_cos, in ascending (min_cos, id) order (torch.topk(largest=False) at shadow.py:490, ties to the
+ * lowest id); landmark_idx[r] = every other chunk id ascending ([rows, chunks - outliers],
+ * shadow.py:513-516). chunks <= 131072, outliers <= 512. */
+int skv_select_outliers(const float* min_cos, int rows, int chunks, int outliers, int64_t* outlier_idx,
+                        int64_t* landmark_idx, void* stream);
+
+/* dst[r][j] = src[r][idx[r][j]] for 128-element bf16 rows: src [rows, src_rows, 128], idx and dst
+ * [rows, dst_rows(, 128)] (the landmark gather, shadow.py:517-519); ids outside [0, src_rows) skip. */
+int skv_gather_rows(const uint16_t* src, int rows, int src_rows, const int64_t* idx, int dst_rows, uint16_t* dst,
+                    void* stream);
+
 /* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:55-56) and the
  * KV append of update_kv_cache (models/kvcache/shadow.py:621-633) in one launch. qkv row of batch b:
  * [q_heads*128 | kv_heads*128 (k) | kv_heads*128 (v)] at qkv + b*qkv_stride_b. q and k are rotated

@@ -261,8 +261,14 @@ def _rope_tokens(x: torch.Tensor, cos_sin: torch.Tensor, pos: torch.Tensor) -> t
 
 
 def encode_layer(k_pre: torch.Tensor, v: torch.Tensor, q_pre_last: torch.Tensor, cos_sin: torch.Tensor, *,
-                 rank: int, chunk: int, budget: int, buf_len: int | None = None) -> LayerState:
-    """k_pre/v [B, H, ctx, D] bf16 (pre-RoPE keys), q_pre_last [B, Hq, 1, D] (pre-RoPE last query)."""
+                 rank: int, chunk: int, budget: int, buf_len: int | None = None,
+                 outliers: torch.Tensor | None = None, init_scores: torch.Tensor | None = None) -> LayerState:
+    """k_pre/v [B, H, ctx, D] bf16 (pre-RoPE keys), q_pre_last [B, Hq, 1, D] (pre-RoPE last query).
+
+    outliers: optional outlier chunk ids [B, H, outlier_chunk] (in outlier-slot order) to use instead
+    of the bf16 min-cosine top-k; init_scores: optional GQA-max scores [B, H, n] for the initial
+    selection, taken with topk_gather's order (value desc, index asc) instead of torch.topk. Both let
+    a device encoder be checked from identical decisions (the reference leaves ties to torch)."""
     B, H, ctx, D = k_pre.shape
     Hq = q_pre_last.shape[1]
     G = Hq // H
@@ -293,7 +299,10 @@ def encode_layer(k_pre: torch.Tensor, v: torch.Tensor, q_pre_last: torch.Tensor,
     kctx = k[:, :, :chunks * chunk].reshape(B, H, chunks, chunk, D)
     cand = kctx.mean(dim=-2)
     cos = F.cosine_similarity(cand.unsqueeze(3).expand(-1, -1, -1, chunk, -1), kctx, dim=-1)
-    out_idx = cos.min(dim=-1).values.topk(outlier_chunk, largest=False).indices
+    if outliers is None:
+        out_idx = cos.min(dim=-1).values.topk(outlier_chunk, largest=False).indices
+    else:
+        out_idx = outliers.to(torch.int64)
     gidx = out_idx.view(B, H, -1, 1, 1).expand(-1, -1, -1, chunk, D)
     kbuf[:, :, prefill_local:sparse_start] = kctx.gather(2, gidx).reshape(B, H, -1, D)
     vctx = v[:, :, :chunks * chunk].reshape(B, H, chunks, chunk, D)
@@ -302,9 +311,13 @@ def encode_layer(k_pre: torch.Tensor, v: torch.Tensor, q_pre_last: torch.Tensor,
     keep.scatter_(-1, out_idx, False)
     rest = torch.arange(chunks).expand(B, H, -1).masked_select(keep).view(B, H, -1)
     landmarks = cand.gather(2, rest.unsqueeze(-1).expand(-1, -1, -1, D)).contiguous()
-    sc = torch.einsum("bhgd,bhcd->bhgc", q_last.reshape(B, H, G, D), landmarks) / math.sqrt(128)
-    sc = F.softmax(sc, dim=-1, dtype=torch.float32).to(torch.bfloat16).max(dim=-2).values
-    sel = rest.gather(-1, sc.topk(S, dim=-1).indices)
+    if init_scores is None:
+        sc = torch.einsum("bhgd,bhcd->bhgc", q_last.reshape(B, H, G, D), landmarks) / math.sqrt(128)
+        sc = F.softmax(sc, dim=-1, dtype=torch.float32).to(torch.bfloat16).max(dim=-2).values
+        sel = rest.gather(-1, sc.topk(S, dim=-1).indices)
+    else:
+        n = rest.shape[-1]
+        sel = topk_gather(init_scores.reshape(B * H, n).to(torch.bfloat16), rest.reshape(B * H, n), S).view(B, H, S)
     tok = (sel.unsqueeze(-1) * chunk + torch.arange(chunk)).view(B, H, -1).unsqueeze(-1).expand(-1, -1, -1, D)
     vbuf[:, :, sparse_start:sparse_end] = v.gather(2, tok)
     kbuf[:, :, sparse_start:sparse_end] = k.gather(2, tok)

@@ -586,3 +586,57 @@ def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v
               cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, q_out.data_ptr(), q_heads * D,
               k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
               append_row.data_ptr(), k_cache.shape[2], _stream())
+
+# ---------------------------------------------------------------------------------------------
+# f1: prefill encoder (chunk statistics, outlier selection, landmark gather)
+
+def chunk_stats(keys, chunks, chunk_size, candidates, min_cos):
+    """keys [B, H, >= chunks*chunk_size, 128] bf16 (rows contiguous) -> candidates [B, H, chunks, 128]
+    bf16 chunk means and min_cos [B, H, chunks] fp32 (minimum row-to-mean cosine per chunk)."""
+    _dev(keys, "keys", torch.bfloat16)
+    _dev(candidates, "candidates", torch.bfloat16)
+    _dev(min_cos, "min_cos", torch.float32)
+    if keys.dim() != 4 or keys.shape[-1] != 128 or keys.stride(-1) != 1:
+        raise ValueError("keys must be [B, H, rows, 128] with contiguous rows")
+    B, H, rows, _ = keys.shape
+    if chunks * chunk_size > rows:
+        raise ValueError(f"{chunks} chunks of {chunk_size} rows exceed the {rows} key rows")
+    if not candidates.is_contiguous() or candidates.numel() < B * H * chunks * 128:
+        raise ValueError("candidates must be contiguous [B, H, chunks, 128]")
+    if not min_cos.is_contiguous() or min_cos.numel() < B * H * chunks:
+        raise ValueError("min_cos must be contiguous [B, H, chunks]")
+    _lib.call("skv_chunk_stats", keys.data_ptr(), keys.stride(0), keys.stride(1), keys.stride(2), B, H, chunks,
+              chunk_size, candidates.data_ptr(), min_cos.data_ptr(), _stream())
+
+
+def select_outliers(min_cos, outliers, outlier_idx, landmark_idx):
+    """min_cos [rows, chunks] fp32 -> outlier_idx [rows, outliers] (ascending min_cos, ties to the
+    lowest id) and landmark_idx [rows, chunks - outliers] (the other ids ascending), int64."""
+    _dev(min_cos, "min_cos", torch.float32)
+    _dev(outlier_idx, "outlier_idx", torch.int64)
+    _dev(landmark_idx, "landmark_idx", torch.int64)
+    if min_cos.dim() != 2 or not min_cos.is_contiguous():
+        raise ValueError("min_cos must be contiguous [rows, chunks]")
+    rows, chunks = min_cos.shape
+    if tuple(outlier_idx.shape) != (rows, outliers) or not outlier_idx.is_contiguous():
+        raise ValueError("outlier_idx must be contiguous [rows, outliers]")
+    if tuple(landmark_idx.shape) != (rows, chunks - outliers) or not landmark_idx.is_contiguous():
+        raise ValueError("landmark_idx must be contiguous [rows, chunks - outliers]")
+    _lib.call("skv_select_outliers", min_cos.data_ptr(), rows, chunks, outliers, outlier_idx.data_ptr(),
+              landmark_idx.data_ptr(), _stream())
+
+
+def gather_rows(src, idx, dst):
+    """dst[r, j] = src[r, idx[r, j]] for 128-element bf16 rows; src [rows, n_src, 128], idx [rows, n]
+    int64, dst [rows, n, 128], all contiguous."""
+    _dev(src, "src", torch.bfloat16)
+    _dev(idx, "idx", torch.int64)
+    _dev(dst, "dst", torch.bfloat16)
+    for t, nm in ((src, "src"), (idx, "idx"), (dst, "dst")):
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+    if src.dim() != 3 or src.shape[-1] != 128 or idx.dim() != 2 or tuple(dst.shape) != (*idx.shape, 128) or \
+            src.shape[0] != idx.shape[0]:
+        raise ValueError("gather_rows: src [rows, n_src, 128], idx [rows, n], dst [rows, n, 128]")
+    _lib.call("skv_gather_rows", src.data_ptr(), src.shape[0], src.shape[1], idx.data_ptr(), idx.shape[1],
+              dst.data_ptr(), _stream())

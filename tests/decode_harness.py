@@ -26,12 +26,13 @@ def build_cache(case, device, max_decode_len=None, num_layers=1):
                                 num_hidden_layers=num_layers)
     cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device=str(device), sparse_budget=d["budget"],
                               chunk_size=d["chunk"], rank=d["rank"], max_decode_len=max_decode_len)
-    cos_sin = case["cos_sin"]
-    k_roped = rope_tokens_cpu(case["k_pre"], cos_sin, torch.arange(ctx))
-    q_last = rope_tokens_cpu(case["q_last"], cos_sin, torch.tensor([ctx - 1]))
+    # Every layer starts from the oracle's encoded state of the prompt (the decode path is compared
+    # with the oracle's decode from exactly that state; the device encoder has its own tests).
+    si = case["state_in"]
     for layer in range(num_layers):
-        cache.get_svd(case["k_pre"], layer)
-        cache.prefill_kv_cache(case["v"], layer, k_roped, q_last)
+        cache.load_layer_state(layer, U=si["U"], SV=si["SV"], landmarks=si["landmarks"],
+                               landmark_idx=si["landmark_idx"], host_v=si["host_v"], k_buffer=si["kbuf"],
+                               v_buffer=si["vbuf"], position_ids=si["position_ids"], ctx=ctx)
     cache.H2D()
     cache.keep_selected = True
     return cache
