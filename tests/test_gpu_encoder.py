@@ -192,3 +192,45 @@ def test_prefill_rejects_host_tensors(gpu):
                               rank=32)
     with pytest.raises(ValueError):
         cache.get_svd(torch.zeros(1, 2, 2048, 128, dtype=torch.bfloat16), 0)
+
+
+def test_attention_prefill_builds_the_same_state(gpu):
+    """ShadowAttention.prefill (get_svd, RoPE, prefill_kv_cache, causal fp32 attention) leaves the
+    same cache state as the direct calls, and returns causal attention of the rotated prompt."""
+    from shadowkv_amd.models.attention import ShadowAttention
+    _say("ShadowAttention.prefill")
+    case = make_golden.decode_small_case(8)
+    d = case["dims"]
+    B, H, G, D, ctx = d["B"], d["H"], d["G"], d["D"], d["ctx"]
+    cs = case["cos_sin"].to(gpu)
+    g = torch.Generator().manual_seed(31)
+    q_pre = torch.randn(B, H * G, ctx, D, generator=g).to(torch.bfloat16)
+    q_pre[:, :, -1:] = case["q_last"]
+
+    def rope(q, k, pos):
+        return _rope_tokens(q, cs, pos), _rope_tokens(k, cs, pos)
+
+    cfg = types.SimpleNamespace(num_attention_heads=H * G, num_key_value_heads=H, hidden_size=H * G * D,
+                                num_hidden_layers=1)
+    cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device=str(gpu), sparse_budget=d["budget"],
+                              chunk_size=8, rank=d["rank"])
+    attn = ShadowAttention(cache, G, D, H * G * D, rope, None, cs)
+    out = attn.prefill(q_pre.to(gpu), case["k_pre"].to(gpu), case["v"].to(gpu), torch.arange(ctx, device=gpu), 0)
+    torch.cuda.synchronize()
+    direct, _ = _prefill_on_gpu(gpu, case["k_pre"], case["v"], case["q_last"], case["cos_sin"], 8, d["budget"],
+                                d["rank"])
+    for name in ("U", "SV", "k_landmark", "k_landmark_idx", "position_ids", "k_cache_buffer", "v_cache_buffer"):
+        a, b = getattr(cache, name), getattr(direct, name)
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b), name
+    # causal attention of the last 16 prompt queries against the fp32 CPU restatement
+    q = _rope_tokens(q_pre, case["cos_sin"], torch.arange(ctx))
+    k = _rope_tokens(case["k_pre"], case["cos_sin"], torch.arange(ctx))
+    rows = torch.arange(ctx - 16, ctx)
+    qq = q[:, :, rows].float()
+    kk = k.float().repeat_interleave(G, dim=1)
+    vv = case["v"].float().repeat_interleave(G, dim=1)
+    sc = qq @ kk.transpose(-1, -2) / D ** 0.5
+    sc = sc.masked_fill(torch.arange(ctx)[None, :] > rows[:, None], float("-inf"))
+    want = (torch.softmax(sc, dim=-1) @ vv).transpose(1, 2)
+    torch.testing.assert_close(out[:, -16:].cpu().float(), want, rtol=2e-2, atol=2e-2)
