@@ -46,15 +46,19 @@ def parse() -> argparse.Namespace:
     p.add_argument("--ctx", type=int, default=122880)
     p.add_argument("--budget", type=int, default=2048)
     p.add_argument("--chunk", type=int, default=8, help="rows per chunk (the reference's default is 8)")
+    p.add_argument("--chunk-cache", type=int, default=None,
+                   help="device chunk pool of this many slots per (b, h) and layer (>= budget/chunk); "
+                        "default: the reference's slot reuse")
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
-    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode"],
+    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode", "pool"],
                    default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
                         "attention: the sparse decode attention alone; select: the fused chunk selection alone; "
                         "linear: the skinny decode projections alone (next to torch's GEMM); encode: the prefill "
-                        "encoder (low-rank factors, chunk statistics, outliers, landmarks, initial selection)")
+                        "encoder (low-rank factors, chunk statistics, outliers, landmarks, initial selection); "
+                        "pool: one layer's sparse step on drifting queries with and without a device chunk pool")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -177,31 +181,37 @@ def breakdown(model, tok) -> dict:
     import torch
     from shadowkv_amd.kernels import shadowkv
 
-    names = ["apply_rotary_pos_emb_new", "score_logits", "select_chunks", "gather_copy_with_offsets",
+    names = ["apply_rotary_pos_emb_new", "score_logits", "select_chunks", "softmax_gqa_max", "topk_gather",
+             "pool_assign", "gather_copy_with_offsets", "gather_copy_misses_to_slots",
              "gather_copy_d2d_with_offsets", "rebuild_k_rope", "sparse_attn_decode"]
     timers = {n: KernelTimer(shadowkv, n) for n in names}
     cache = model.cache
     snaps = []  # (selected chunks, device copy of the hit counts) per call; no host sync in the step
-    orig_select = timers["select_chunks"].orig
+    pooled = cache.pooled
+    sel_name = "pool_assign" if pooled else "select_chunks"
+    orig_select = timers[sel_name].orig
 
     def select_and_snapshot(*a, **kw):
         out = orig_select(*a, **kw)
-        snaps.append((a[3] * a[7], a[11].clone()))  # rows * select_sets, cnts
+        if pooled:  # pool_assign(selected [rows, S], ..., cnts)
+            snaps.append((a[0].numel(), a[9].clone()))
+        else:  # select_chunks(..., rows, ..., select_sets, ..., cnts)
+            snaps.append((a[3] * a[7], a[11].clone()))
         return out
 
-    timers["select_chunks"].orig = select_and_snapshot
+    timers[sel_name].orig = select_and_snapshot
     for t in timers.values():
         t.active = True
     torch.cuda.synchronize()
     model.decode_step(tok)
     torch.cuda.synchronize()
-    timers["select_chunks"].orig = orig_select
+    timers[sel_name].orig = orig_select
     for t in timers.values():
         t.active = False
         setattr(shadowkv, t.name, t.orig)
     ops = {n: round(t.mean_ms() * 1e3, 2) for n, t in timers.items() if t.pairs}
     chunk_bytes = cache.chunk_size * cache.head_dim * 2
-    fetch_ms = timers["gather_copy_with_offsets"].mean_ms()
+    fetch_ms = timers["gather_copy_misses_to_slots" if pooled else "gather_copy_with_offsets"].mean_ms()
     total_sel = statistics.fmean(t for t, _ in snaps)
     miss_mean = statistics.fmean(t - int(c.sum()) for t, c in snaps)
     return {"op_us_per_layer": ops, "hit_rate": round(1 - miss_mean / total_sel, 4),
@@ -473,6 +483,64 @@ def linear_microbench(args) -> int:
     return 0
 
 
+def pool_microbench(args) -> int:
+    """One layer's sparse decode step (selection, value fetch, key rebuild, attention) at the
+    Llama-3-8B shape, batch 8, ctx 122880, budget 2048, on queries that drift from step to step
+    (q_t = q_{t-1} + drift * noise, so consecutive selections overlap as in real decoding), without
+    and with a device chunk pool. Reports the hit rate, host-link bytes and time per step."""
+    import types
+    import torch
+    from shadowkv_amd import decode_model
+    from shadowkv_amd.models.attention import ShadowAttention
+    from shadowkv_amd.models.kvcache import ShadowKVCache_CPU
+
+    B, H, G, D, ctx, budget, c, steps, warm = 8, 8, 4, 128, args.ctx, 2048, 8, 24, 8
+    S = budget // c
+    cfg = types.SimpleNamespace(num_attention_heads=H * G, num_key_value_heads=H, hidden_size=H * G * D,
+                                num_hidden_layers=1)
+    cos_sin = decode_model.build_cos_sin_cache(ctx + 1024, 500000.0, D, device="cuda")
+    for drift in (0.05, 0.2):
+        for P in (None, 2 * S, 4 * S):
+            cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device="cuda", sparse_budget=budget,
+                                      chunk_size=c, rank=160, max_decode_len=steps + warm + 4, zero_host_store=False,
+                                      chunk_cache=P)
+            decode_model.synthesize_state(cache, ctx, seed=3, cos_sin=cos_sin)
+            attn = ShadowAttention(cache, G, D, H * G * D, None, None, cos_sin)
+            g = torch.Generator(device="cuda").manual_seed(17)
+            q = torch.randn(B, H * G, 1, D, generator=g, device="cuda")
+            hits, times = [], []
+            for t in range(warm + steps):
+                q = q + drift * torch.randn(B, H * G, 1, D, generator=g, device="cuda")
+                k = torch.randn(B, H, 1, D, generator=g, device="cuda").to(torch.bfloat16)
+                v = torch.randn(B, H, 1, D, generator=g, device="cuda").to(torch.bfloat16)
+                cache.update_kv_cache(k, v, 0)
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                attn.decode_end(attn.decode_begin_appended(q.to(torch.bfloat16), 0))
+                e.record()
+                e.synchronize()
+                if t >= warm:
+                    times.append(s.elapsed_time(e))
+                    hits.append(int(cache.cnts.sum()))
+            hit_rate = statistics.fmean(hits) / (B * H * S)
+            ms = statistics.fmean(times)
+            host = (1 - hit_rate) * B * H * S * c * D * 2
+            out = {"metric": "sparse layer step ms with a device chunk pool", "value": round(ms, 4), "unit": "ms",
+                   "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(ms, 4),
+                   "higher_is_better": False, "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
+                   "data": f"synthetic ShadowKV state; queries drifting by {drift} x N(0,1) per step",
+                   "config": {"workload": f"Llama-3-8B shape one-layer sparse step, batch {B}, ctx {ctx}, budget "
+                                          f"{budget}, chunk {c}, " + (f"chunk pool of {P} slots" if P else
+                                                                       "reference slot reuse"),
+                              "drift": drift, "pool_slots": P},
+                   "hit_rate": round(hit_rate, 4), "host_link_MB_per_step": round(host / 1e6, 2),
+                   "roofline": None, "cpu_baseline": None}
+            print(json.dumps(out), flush=True)
+            del cache, attn
+            torch.cuda.empty_cache()
+    return 0
+
+
 def encode_microbench(args) -> int:
     """The device prefill encoder per layer (ShadowKVCache_CPU.get_svd + prefill_kv_cache) at the
     Llama-3-8B shape (8 kv heads x 4 query heads), ctx 122880, rank 160, chunk 8, budget 2048, on
@@ -595,6 +663,8 @@ def main() -> int:
         return linear_microbench(args)
     if args.workload == "encode":
         return encode_microbench(args)
+    if args.workload == "pool":
+        return pool_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv
@@ -607,7 +677,8 @@ def main() -> int:
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
     lanes = args.lanes if args.batch % args.lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
-                                          decode_len=args.warmup + args.steps + 8, lanes=lanes)
+                                          decode_len=args.warmup + args.steps + 8, lanes=lanes,
+                                          chunk_cache=args.chunk_cache)
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")
@@ -678,7 +749,8 @@ def main() -> int:
         "data": "synthetic: random-init weights, seeded random ShadowKV state of the exact shapes, greedy tokens",
         "config": {"workload": f"{shape.name}-shape {shape.layers}-layer decode, batch {args.batch}, ctx {args.ctx}, "
                                f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, V in pinned host memory, "
-                               f"{lanes} interleaved batch lane(s), "
+                               + (f"device chunk pool of {args.chunk_cache} slots, " if args.chunk_cache else "")
+                               + f"{lanes} interleaved batch lane(s), "
                                f"{'HIP-graph-captured step' if graph else 'eager step'}",
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),

@@ -266,6 +266,53 @@ int skv_select_outliers(const float* min_cos, int rows, int chunks, int outliers
 int skv_gather_rows(const uint16_t* src, int rows, int src_rows, const int64_t* idx, int dst_rows, uint16_t* dst,
                     void* stream);
 
+/* ---- f3: device chunk pool (a GPU cache of P >= S chunk slots per (b, h) and layer) ------
+ * No reference counterpart: extends the slot reuse of reorder_keys_and_compute_offsets
+ * (kernels/map.cuh:475-516, models/kvcache/shadow.py:574-593) to a cache larger than the
+ * selection. skv_pool_assign, per row r < rows: selected[r] [select_sets] chunk ids (int64) are
+ * looked up in slot_of[r] [num_chunks] (slot or -1); hits keep their slot; the misses take the
+ * least recently used slots holding no selected chunk (empty first, then ascending slot_used,
+ * ties to the lowest slot), the k-th miss in selection order the k-th such slot in ascending slot
+ * order; slot_of, slot_chunk[r] [pool_slots] (chunk or -1) and slot_used[r] [pool_slots] (step of
+ * last use, -1 = never) are updated, clock[r] advanced by one. Outputs: slot_list[r] [select_sets]
+ * (slot of each selected chunk), cnts[r] = select_sets - misses, and for i in [cnts[r],
+ * select_sets): miss_ids[r][i] / miss_slot[r][i] (int32). select_sets <= 2048, select_sets <=
+ * pool_slots <= 16384. */
+int skv_pool_assign(const int64_t* selected, int rows, int select_sets, int num_chunks, int pool_slots,
+                    int32_t* slot_of, int32_t* slot_chunk, int32_t* slot_used, int32_t* clock, int32_t* slot_list,
+                    int32_t* miss_ids, int32_t* miss_slot, int32_t* cnts, void* stream);
+
+/* The miss gather of a chunk pool: for r < batch_size*heads and i in [cnts[r], map_size), chunk
+ * miss_ids[r*map_size + i] of host row r (values + r*cpu_v_length) is copied to pool slot
+ * miss_slot[r*map_size + i] at v_cache_buffer + r*gpu_v_stride + pool_offset + slot*chunk_elems. */
+int skv_gather_copy_misses_to_slots(const void* values, void* v_cache_buffer, const int32_t* miss_ids,
+                                    const int32_t* cnts, const int32_t* miss_slot, int batch_size, int heads,
+                                    int64_t cpu_v_length, int64_t pool_offset, int64_t gpu_v_stride, int map_size,
+                                    int pool_slots, int chunk_elems, void* stream);
+
+/* skv_rebuild_k_rope for a chunk pool: the rows of entries i in [cnts[r], num_chunks) (chunk
+ * miss_ids[r][i], int32) are written to cache rows pool_start + miss_slot[r][i]*chunk_size + j. */
+int skv_rebuild_k_rope_slots(const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
+                             int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b, int64_t sv_stride_h,
+                             int64_t sv_stride_n, const int32_t* miss_ids, const int32_t* miss_slot,
+                             const int32_t* cnts, const uint16_t* cos_sin, int64_t stride_cos_sin,
+                             int64_t cos_sin_rows, int rope_mode, uint16_t* cache, int64_t stride_cache_b,
+                             int64_t stride_cache_h, int64_t stride_cache_s, int pool_start, int pool_slots,
+                             int batch_size, int heads, int num_chunks, int chunk_size, int rank, int head_dim,
+                             void* stream);
+
+/* skv_sparse_attn_decode over a chunk pool: virtual keys [0, kv_len) = rows [0, sparse_start) ++
+ * the select_sets chunks of slot_list[(b*kv_heads + h)*select_sets + j] (rows sparse_start +
+ * slot*chunk_size + ...) ++ rows from sparse_start + pool_slots*chunk_size on (the generated
+ * tokens). The buffers must hold kv_len + (pool_slots - select_sets)*chunk_size rows. */
+int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
+                                 int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
+                                 int kv_len, const int32_t* kv_len_dev, float scale, void* workspace,
+                                 int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+                                 const int32_t* slot_list, int sparse_start, int select_sets, int chunk_size,
+                                 int pool_slots, void* stream);
+
 /* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:55-56) and the
  * KV append of update_kv_cache (models/kvcache/shadow.py:621-633) in one launch. qkv row of batch b:
  * [q_heads*128 | kv_heads*128 (k) | kv_heads*128 (v)] at qkv + b*qkv_stride_b. q and k are rotated

@@ -17,7 +17,7 @@ __all__ = [
     "reorder", "cached_gather_copy", "compact_hits", "gather_copy_plain", "rope_half_split", "rope_push",
     "rope_push_glm", "rebuild_k", "rebuild_k_rope", "score_logits_softmax", "score_gqa_max", "topk_total_order",
     "topk_gather", "sparse_attention", "build_cos_sin_cache", "build_glm_cos_sin_cache", "encode_layer",
-    "decode_layer_step", "LayerState",
+    "decode_layer_step", "LayerState", "pool_assign", "pool_from_layer", "decode_layer_step_pooled",
 ]
 
 
@@ -363,3 +363,126 @@ def decode_layer_step(st: LayerState, q: torch.Tensor, k_new: torch.Tensor, v_ne
                    st.sparse_start)
     out = sparse_attention(q, st.kbuf, st.vbuf, L)
     return dict(scores=scores.view(B, H, n), selected=selected.view(B, H, S), cnts=cnts, offsets=offs, out=out, L=L)
+
+
+# --------------------------------------------------------------------------------------------
+# f3: chunk pool — no reference counterpart; it extends the slot reuse of the reorder
+# (kernels/map.cuh:475-516) to a device cache of P >= S chunk slots per (b, h). The policy is this
+# build's own: a selected chunk found in the pool keeps its slot; the misses take the least
+# recently used slots holding no selected chunk (empty slots first, then ascending step of last
+# use, ties to the lowest slot), the k-th miss in selection order the k-th such slot in ascending
+# slot order. Pinned by: brute-force simulation of that rule on small random and adversarial
+# streams and by the invariants checked in tests/test_oracle_pool.py (every selected chunk
+# resident after a step, table consistency, hits = |selection ∩ pool|, P == S reduces to the
+# reference's set of buffered chunks).
+
+def pool_assign(selected, slot_of, slot_chunk, slot_used, clock):
+    """selected [rows, S] int64; tables (numpy int32, updated in place): slot_of [rows, chunks]
+    (slot or -1), slot_chunk / slot_used [rows, P] (chunk or -1; step of last use or -1), clock
+    [rows]. Returns slot_list [rows, S], miss_ids / miss_slot [rows, S] (misses at [cnts, S)) and
+    cnts [rows] (the hit counts), all int32."""
+    selected = np.asarray(selected, dtype=np.int64)
+    rows, S = selected.shape
+    P = slot_chunk.shape[1]
+    slot_list = np.zeros((rows, S), np.int32)
+    miss_ids = np.zeros((rows, S), np.int32)
+    miss_slot = np.zeros((rows, S), np.int32)
+    cnts = np.zeros(rows, np.int32)
+    for r in range(rows):
+        t = int(clock[r]) + 1
+        hit = np.zeros(P, dtype=bool)
+        misses = []
+        for j, c in enumerate(selected[r]):
+            sl = int(slot_of[r, c])
+            if sl >= 0:
+                slot_list[r, j] = sl
+                slot_used[r, sl] = t
+                hit[sl] = True
+            else:
+                misses.append(j)
+        m = len(misses)
+        free = [v for v in range(P) if not hit[v]]
+        free.sort(key=lambda v: (int(slot_used[r, v]), v))
+        victims = sorted(free[:m])
+        base = S - m
+        for k, j in enumerate(misses):
+            v, c = victims[k], int(selected[r, j])
+            old = int(slot_chunk[r, v])
+            if old >= 0:
+                slot_of[r, old] = -1
+            slot_of[r, c] = v
+            slot_chunk[r, v] = c
+            slot_used[r, v] = t
+            slot_list[r, j] = v
+            miss_ids[r, base + k] = c
+            miss_slot[r, base + k] = v
+        cnts[r] = base
+        clock[r] = t
+    return slot_list, miss_ids, miss_slot, cnts
+
+
+def pool_from_layer(st: LayerState, P: int) -> dict:
+    """A chunk pool of P slots holding the layer's initial selection in slots 0..S-1: buffers with
+    (P - S)*chunk more rows between the selected region and the generated tokens, and the tables."""
+    B, H, buf, D = st.kbuf.shape
+    S, c = st.budget // st.chunk, st.chunk
+    delta = (P - S) * c
+    rows = B * H
+    kbuf = torch.zeros(B, H, buf + delta, D, dtype=st.kbuf.dtype)
+    vbuf = torch.zeros_like(kbuf)
+    kbuf[:, :, :st.sparse_end] = st.kbuf[:, :, :st.sparse_end]
+    vbuf[:, :, :st.sparse_end] = st.vbuf[:, :, :st.sparse_end]
+    sel = st.position_ids.reshape(rows, S).numpy()
+    slot_of = np.full((rows, st.chunks), -1, np.int32)
+    slot_chunk = np.full((rows, P), -1, np.int32)
+    slot_used = np.full((rows, P), -1, np.int32)
+    for r in range(rows):
+        slot_of[r, sel[r]] = np.arange(S)
+        slot_chunk[r, :S] = sel[r]
+        slot_used[r, :S] = 0
+    return dict(P=P, delta=delta, kbuf=kbuf, vbuf=vbuf, slot_of=slot_of, slot_chunk=slot_chunk, slot_used=slot_used,
+                clock=np.zeros(rows, np.int32))
+
+
+def decode_layer_step_pooled(st: LayerState, pool: dict, q, k_new, v_new, cos_sin, gen_offset: int = 0,
+                             scores=None) -> dict:
+    """decode_layer_step with a chunk pool: the selection (top-k of the GQA-max scores, or of the
+    given scores) is mapped onto the pool by pool_assign, the misses' values copied from the host
+    store and their keys rebuilt into their slots, and attention taken over [local | outliers |
+    the selected chunks through the slot list | generated]. Mutates pool; returns the intermediates."""
+    B, H, n, D = st.landmarks.shape
+    G = q.shape[1] // H
+    S, c = st.budget // st.chunk, st.chunk
+    sp0, delta, rows = st.sparse_start, pool["delta"], B * H
+    L = st.sparse_end + gen_offset + 1  # virtual length (the new token included)
+    kbuf, vbuf = pool["kbuf"], pool["vbuf"]
+    kbuf[:, :, L - 1 + delta] = k_new
+    vbuf[:, :, L - 1 + delta] = v_new
+    if scores is None:
+        scores = score_gqa_max(q.reshape(rows, G, D), st.landmarks.reshape(rows, n, D), 1.0 / math.sqrt(128))
+    else:
+        scores = scores.reshape(rows, n).to(torch.bfloat16)
+    selected = topk_gather(scores, st.landmark_idx.reshape(rows, n), S)
+    slot_list, miss_ids, miss_slot, cnts = pool_assign(selected.numpy(), pool["slot_of"], pool["slot_chunk"],
+                                                       pool["slot_used"], pool["clock"])
+    # keys of the misses: rebuilt + rotated into a scratch [B, H, S*c, D] (rows of entries i >= cnts),
+    # then moved to their slots; values from the host store
+    scratch = torch.zeros(B, H, S * c, D, dtype=kbuf.dtype)
+    ids = torch.from_numpy(miss_ids.astype(np.int64)).view(B, H, S)
+    rebuild_k_rope(st.U, st.SV, ids, torch.from_numpy(cnts), cos_sin, c, scratch, 0)
+    for r in range(rows):
+        b, h = divmod(r, H)
+        for i in range(int(cnts[r]), S):
+            v, cid = int(miss_slot[r, i]), int(miss_ids[r, i])
+            kbuf[b, h, sp0 + v * c:sp0 + (v + 1) * c] = scratch[b, h, i * c:(i + 1) * c]
+            vbuf[b, h, sp0 + v * c:sp0 + (v + 1) * c] = st.host_v[b, h, cid].view(c, D)
+    # the virtual sequence the attention reads
+    sel_rows = (torch.from_numpy(slot_list.astype(np.int64)).view(B, H, S, 1) * c + sp0 +
+                torch.arange(c).view(1, 1, 1, c)).reshape(B, H, S * c)
+    def virtual(buf):
+        mid = buf.gather(2, sel_rows.unsqueeze(-1).expand(-1, -1, -1, D))
+        tail = buf[:, :, st.sparse_end + delta:L + delta]
+        return torch.cat([buf[:, :, :sp0], mid, tail], dim=2)
+    out = sparse_attention(q, virtual(kbuf), virtual(vbuf), L)
+    return dict(scores=scores.view(B, H, n), selected=selected.view(B, H, S), slot_list=slot_list, cnts=cnts,
+                miss_ids=miss_ids, miss_slot=miss_slot, out=out, L=L)

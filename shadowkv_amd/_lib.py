@@ -56,6 +56,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_chunk_stats": (_i32, [_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "skv_select_outliers": (_i32, [_p, _i32, _i32, _i32, _p, _p, _p]),
     "skv_gather_rows": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
+    "skv_pool_assign": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "skv_gather_copy_misses_to_slots": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32,
+                                                _p]),
+    "skv_rebuild_k_rope_slots": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64,
+                                         _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                         _p]),
+    "skv_sparse_attn_decode_paged": (_i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+                                             _p, _f32, _p, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p]),
     "skv_rope_qk_append": (
         _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
                _i64, _p]),

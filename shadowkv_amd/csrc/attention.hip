@@ -10,6 +10,8 @@
 //     P.V in fp32: 16 key streams x 8 dims per lane, the streams summed through LDS.
 //   attn_combine_kernel: log-sum-exp merge of the splits in one pass (running maximum), every
 //     load of a 32-split chunk issued before the first is used; bf16 output.
+#include <type_traits>
+
 #include "wave_reduce.h"
 
 namespace {
@@ -46,6 +48,11 @@ struct AttnArgs {
   float* ws_ml;  // [B*Hq][splits][2]
   uint16_t* out;
   int64_t o_sb, o_sh;
+  // Paged selected region (chunk pool): virtual keys [sp0, sp0 + sel*chunk) are chunk j of the
+  // selection at physical rows sp0 + slot[(b*Hkv + h)*sel + j]*chunk + ...; virtual keys past the
+  // selection sit `delta` rows further (after the pool's pool_slots chunks).
+  const int32_t* slot;
+  int sp0, sel, chunk, pool_slots, delta;
 };
 
 __device__ __forceinline__ int live_length(const AttnArgs& a) {
@@ -58,7 +65,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // kSplit keys per workgroup; the split's V rows are requested right after the scores, so their
 // latency overlaps the softmax (requesting them with K, at entry, measured no faster and holds
 // more registers).
-template <int GP>
+template <int GP, bool kPaged>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   constexpr int kRows = kSplit / 16;        // keys per P.V stream
   constexpr int kGroups = kSplit / 4 / 16;  // 16-key MFMA groups per wave
@@ -68,6 +75,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   __shared__ float p_lds[GP][kSplit];
   __shared__ __align__(16) float red[4][64][kKept];  // [wave][lane][value]
   __shared__ float ml[GP][2];
+  __shared__ int prow[kPaged ? kSplit : 1];  // physical row of each key of the split (paged)
 
   const int split = blockIdx.x;
   const int bh = blockIdx.y;
@@ -92,12 +100,31 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   const uint16_t* qrow = a.q + b * a.q_sb + (h * G + min(li, G - 1)) * a.q_sh + 8 * grp;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) qf[ks] = skv::load16_or_zero(qrow + 32 * ks, li < G);
+  // Key jl of the split (clamped to the live keys) lives at row key_row(jl).
+  if (kPaged) {
+    for (int jl = threadIdx.x; jl < kSplit; jl += kThreads) {
+      const int sk = min(s0 + jl, s1 - 1);
+      int r = sk;
+      if (sk >= a.sp0) {
+        const int j = sk - a.sp0;
+        if (j < a.sel * a.chunk) {
+          const int sl = a.slot[static_cast<int64_t>(bh) * a.sel + j / a.chunk];
+          r = a.sp0 + min(max(sl, 0), a.pool_slots - 1) * a.chunk + j % a.chunk;
+        } else {
+          r = sk + a.delta;
+        }
+      }
+      prow[jl] = r;
+    }
+    __syncthreads();
+  }
+  auto key_row = [&](int jl) -> int64_t { return kPaged ? prow[jl] : min(s0 + jl, s1 - 1); };
   // K as MFMA B operand: lane (li, grp) holds key (wave*64 + 16*kg + li), same dims.
   u32x4 kf[kGroups][4];
 #pragma unroll
   for (int kg = 0; kg < kGroups; ++kg) {
     const int s = s0 + wave * (kSplit / 4) + 16 * kg + li;
-    const uint16_t* krow = kh + static_cast<int64_t>(min(s, s1 - 1)) * a.kv_ss + 8 * grp;
+    const uint16_t* krow = kh + key_row(s - s0) * a.kv_ss + 8 * grp;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) kf[kg][ks] = skv::load16_or_zero(krow + 32 * ks, s < s1);
   }
@@ -108,7 +135,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
       const int s = s0 + i * 16 + stream;
-      vr[i] = skv::load16_or_zero(vh + static_cast<int64_t>(min(s, s1 - 1)) * a.kv_ss + li * 8, s < s1);
+      vr[i] = skv::load16_or_zero(vh + key_row(i * 16 + stream) * a.kv_ss + li * 8, s < s1);
     }
   };
 #pragma unroll
@@ -272,13 +299,13 @@ extern "C" int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, 
   return static_cast<int64_t>(batch_size) * q_heads * splits_for(kv_len, kSplit) * (kHeadDim + 2) * sizeof(float);
 }
 
-extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
-                                      const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
-                                      int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
-                                      int kv_len, const int32_t* kv_len_dev, float scale, void* workspace,
-                                      int64_t workspace_bytes, uint16_t* out,
-                                      int64_t o_stride_b, int64_t o_stride_h, void* stream) {
-  const char* what = "sparse_attn_decode";
+namespace {
+
+int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+                const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, int batch_size,
+                int q_heads, int kv_heads, int head_dim, int kv_len, const int32_t* kv_len_dev, float scale,
+                void* workspace, int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+                const int32_t* slot, int sparse_start, int select_sets, int chunk, int pool_slots, void* stream) {
   if (!q || !k_cache || !v_cache || !workspace || !out) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -302,6 +329,11 @@ extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int
   if (kv_len > kMaxKvLen) {
     skv_set_error("%s: kv_len=%d exceeds %d", what, kv_len, kMaxKvLen);
     return SKV_EUNSUPPORTED;
+  }
+  if (slot && (sparse_start < 0 || select_sets < 1 || chunk < 1 || pool_slots < select_sets)) {
+    skv_set_error("%s: paged region sparse_start=%d select_sets=%d chunk=%d pool_slots=%d", what, sparse_start,
+                  select_sets, chunk, pool_slots);
+    return SKV_EINVAL;
   }
   const int64_t need = skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len);
   if (workspace_bytes < need) {
@@ -329,15 +361,57 @@ extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int
   a.out = out;
   a.o_sb = o_stride_b;
   a.o_sh = o_stride_h;
+  a.slot = slot;
+  a.sp0 = sparse_start;
+  a.sel = select_sets;
+  a.chunk = chunk;
+  a.pool_slots = pool_slots;
+  a.delta = (pool_slots - select_sets) * chunk;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(a.splits, batch_size * kv_heads);
-  if (G == 1) hipLaunchKernelGGL(attn_split_kernel<1>, grid, dim3(kThreads), 0, s, a);
-  else if (G == 2) hipLaunchKernelGGL(attn_split_kernel<2>, grid, dim3(kThreads), 0, s, a);
-  else if (G <= 4) hipLaunchKernelGGL(attn_split_kernel<4>, grid, dim3(kThreads), 0, s, a);
-  else if (G <= 8) hipLaunchKernelGGL(attn_split_kernel<8>, grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL(attn_split_kernel<16>, grid, dim3(kThreads), 0, s, a);
+  auto go = [&](auto paged) {
+    constexpr bool P = decltype(paged)::value;
+    if (G == 1) hipLaunchKernelGGL((attn_split_kernel<1, P>), grid, dim3(kThreads), 0, s, a);
+    else if (G == 2) hipLaunchKernelGGL((attn_split_kernel<2, P>), grid, dim3(kThreads), 0, s, a);
+    else if (G <= 4) hipLaunchKernelGGL((attn_split_kernel<4, P>), grid, dim3(kThreads), 0, s, a);
+    else if (G <= 8) hipLaunchKernelGGL((attn_split_kernel<8, P>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((attn_split_kernel<16, P>), grid, dim3(kThreads), 0, s, a);
+  };
+  if (slot) go(std::true_type{});
+  else go(std::false_type{});
   int rc = skv_check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(batch_size * q_heads), dim3(kHeadDim), 0, s, a);
   return skv_check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+                                      const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
+                                      int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
+                                      int kv_len, const int32_t* kv_len_dev, float scale, void* workspace,
+                                      int64_t workspace_bytes, uint16_t* out,
+                                      int64_t o_stride_b, int64_t o_stride_h, void* stream) {
+  return attn_decode("sparse_attn_decode", q, q_stride_b, q_stride_h, k_cache, v_cache, kv_stride_b, kv_stride_h,
+                     kv_stride_s, batch_size, q_heads, kv_heads, head_dim, kv_len, kv_len_dev, scale, workspace,
+                     workspace_bytes, out, o_stride_b, o_stride_h, nullptr, 0, 0, 0, 0, stream);
+}
+
+extern "C" int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
+                                            const uint16_t* k_cache, const uint16_t* v_cache, int64_t kv_stride_b,
+                                            int64_t kv_stride_h, int64_t kv_stride_s, int batch_size, int q_heads,
+                                            int kv_heads, int head_dim, int kv_len, const int32_t* kv_len_dev,
+                                            float scale, void* workspace, int64_t workspace_bytes, uint16_t* out,
+                                            int64_t o_stride_b, int64_t o_stride_h, const int32_t* slot_list,
+                                            int sparse_start, int select_sets, int chunk_size, int pool_slots,
+                                            void* stream) {
+  if (!slot_list) {
+    skv_set_error("sparse_attn_decode_paged: null slot_list");
+    return SKV_EINVAL;
+  }
+  return attn_decode("sparse_attn_decode_paged", q, q_stride_b, q_stride_h, k_cache, v_cache, kv_stride_b,
+                     kv_stride_h, kv_stride_s, batch_size, q_heads, kv_heads, head_dim, kv_len, kv_len_dev, scale,
+                     workspace, workspace_bytes, out, o_stride_b, o_stride_h, slot_list, sparse_start, select_sets,
+                     chunk_size, pool_slots, stream);
 }

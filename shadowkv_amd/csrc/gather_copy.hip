@@ -85,15 +85,18 @@ __global__ void __launch_bounds__(kThreads) compact_hits_kernel(u32x4* __restric
   }
 }
 
-// Copies slots [i0, i1) of one row, 16-byte vectors, kUnroll loads in flight per lane.
+// Copies slots [i0, i1) of one row, 16-byte vectors, kUnroll loads in flight per lane. With
+// dst_slot, entry i goes to destination slot dst_slot[row*S + i] (skipped outside [0, pool_slots)).
 template <typename IdxT>
 __device__ __forceinline__ void gather_tile(const u32x4* __restrict__ src, int64_t src_row_vec, u32x4* __restrict__ dst,
                                             int64_t dst_row_vec, int64_t dst_offset_vec, const IdxT* __restrict__ ids,
-                                            int row, int i0, int i1, int S, int chunk_vec, int64_t src_chunks) {
+                                            const int32_t* __restrict__ dst_slot, int pool_slots, int row, int i0,
+                                            int i1, int S, int chunk_vec, int64_t src_chunks) {
   const int64_t total = static_cast<int64_t>(i1 - i0) * chunk_vec;
   const u32x4* s = src + static_cast<int64_t>(row) * src_row_vec;
   u32x4* d = dst + static_cast<int64_t>(row) * dst_row_vec + dst_offset_vec;
   const IdxT* id = ids + static_cast<int64_t>(row) * S;
+  const int32_t* ds = dst_slot ? dst_slot + static_cast<int64_t>(row) * S : nullptr;
   for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(blockDim.x) * kUnroll) {
     u32x4 r[kUnroll];
 #pragma unroll
@@ -113,7 +116,9 @@ __device__ __forceinline__ void gather_tile(const u32x4* __restrict__ src, int64
         int i = i0 + static_cast<int>(v / chunk_vec);
         int e = static_cast<int>(v % chunk_vec);
         int64_t c = static_cast<int64_t>(id[i]);
-        if (c >= 0 && c < src_chunks) d[static_cast<int64_t>(i) * chunk_vec + e] = r[u];
+        const int slot = ds ? ds[i] : i;
+        if (c >= 0 && c < src_chunks && (!ds || (slot >= 0 && slot < pool_slots)))
+          d[static_cast<int64_t>(slot) * chunk_vec + e] = r[u];
       }
     }
   }
@@ -128,8 +133,10 @@ template <typename IdxT>
 __global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __restrict__ src, int64_t src_row_vec,
                                                                   u32x4* __restrict__ dst, int64_t dst_row_vec,
                                                                   int64_t dst_offset_vec, const IdxT* __restrict__ ids,
-                                                                  const int32_t* __restrict__ cnts, int S, int chunk_vec,
-                                                                  int64_t src_chunks, int rows, int tiles) {
+                                                                  const int32_t* __restrict__ cnts,
+                                                                  const int32_t* __restrict__ dst_slot, int pool_slots,
+                                                                  int S, int chunk_vec, int64_t src_chunks, int rows,
+                                                                  int tiles) {
   const int total_tiles = rows * tiles;
   for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
     const int row = tile / tiles;
@@ -137,8 +144,8 @@ __global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __
     const int start = cnts ? max(0, cnts[row]) : 0;
     const int i0 = start + t * kChunksPerFetchWG;
     if (i0 >= S) continue;
-    gather_tile(src, src_row_vec, dst, dst_row_vec, dst_offset_vec, ids, row, i0, min(i0 + kChunksPerFetchWG, S), S,
-                chunk_vec, src_chunks);
+    gather_tile(src, src_row_vec, dst, dst_row_vec, dst_offset_vec, ids, dst_slot, pool_slots, row, i0,
+                min(i0 + kChunksPerFetchWG, S), S, chunk_vec, src_chunks);
   }
 }
 
@@ -191,7 +198,8 @@ namespace {
 // move and the host-link gather of the misses, in that order on one stream.
 int value_fetch(const char* what, bool compact, const void* values, void* v_cache_buffer, const int32_t* offsets,
                 const int32_t* cnts, int batch_size, int heads, int64_t cpu_v_length, int64_t gpu_v_length,
-                int64_t gpu_v_offset, int64_t gpu_v_stride, int map_size, int chunk_elems, void* stream) {
+                int64_t gpu_v_offset, int64_t gpu_v_stride, int map_size, int chunk_elems, void* stream,
+                const int32_t* dst_slot = nullptr, int pool_slots = 0) {
   if (!values || !v_cache_buffer || !offsets || !cnts) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -216,8 +224,8 @@ int value_fetch(const char* what, bool compact, const void* values, void* v_cach
   const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
   hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0, s,
                      static_cast<const u32x4*>(values), cpu_v_length / 8, static_cast<u32x4*>(v_cache_buffer),
-                     gpu_v_stride / 8, gpu_v_offset / 8, offsets, cnts, map_size, chunk_elems / 8,
-                     cpu_v_length / chunk_elems, rows, tiles);
+                     gpu_v_stride / 8, gpu_v_offset / 8, offsets, cnts, dst_slot, pool_slots, map_size,
+                     chunk_elems / 8, cpu_v_length / chunk_elems, rows, tiles);
   return skv_check_launch(what);
 }
 
@@ -229,6 +237,21 @@ extern "C" int skv_gather_copy_with_offsets(const void* values, void* v_cache_bu
                                             int map_size, int chunk_elems, void* stream) {
   return value_fetch("gather_copy_with_offsets", true, values, v_cache_buffer, offsets, cnts, batch_size, heads,
                      cpu_v_length, gpu_v_length, gpu_v_offset, gpu_v_stride, map_size, chunk_elems, stream);
+}
+
+extern "C" int skv_gather_copy_misses_to_slots(const void* values, void* v_cache_buffer, const int32_t* miss_ids,
+                                               const int32_t* cnts, const int32_t* miss_slot, int batch_size,
+                                               int heads, int64_t cpu_v_length, int64_t pool_offset,
+                                               int64_t gpu_v_stride, int map_size, int pool_slots, int chunk_elems,
+                                               void* stream) {
+  if (!miss_slot || pool_slots < map_size) {
+    skv_set_error("gather_copy_misses_to_slots: miss_slot=%p pool_slots=%d map_size=%d",
+                  static_cast<const void*>(miss_slot), pool_slots, map_size);
+    return SKV_EINVAL;
+  }
+  return value_fetch("gather_copy_misses_to_slots", false, values, v_cache_buffer, miss_ids, cnts, batch_size, heads,
+                     cpu_v_length, static_cast<int64_t>(map_size) * chunk_elems, pool_offset, gpu_v_stride, map_size,
+                     chunk_elems, stream, miss_slot, pool_slots);
 }
 
 extern "C" int skv_gather_copy_misses_with_offsets(const void* values, void* v_cache_buffer, const int32_t* offsets,
@@ -259,7 +282,7 @@ extern "C" int skv_gather_copy(const void* values, void* v_cache_buffer, const i
   hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const u32x4*>(values), cpu_v_length / 8,
                      static_cast<u32x4*>(v_cache_buffer), gpu_v_length / 8, int64_t(0), position_ids,
-                     static_cast<const int32_t*>(nullptr), map_size, chunk_elems / 8, cpu_v_length / chunk_elems,
-                     rows, tiles);
+                     static_cast<const int32_t*>(nullptr), static_cast<const int32_t*>(nullptr), 0, map_size,
+                     chunk_elems / 8, cpu_v_length / chunk_elems, rows, tiles);
   return skv_check_launch(what);
 }

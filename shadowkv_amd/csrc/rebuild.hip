@@ -58,6 +58,11 @@ struct RebuildArgs {
   int64_t o_sb, o_sh, o_ss;
   int o_start;
   int B, H, S, chunk, rank, tiles;
+  // Optional destination slots (chunk pool): row r of entry i goes to cache row
+  // o_start + dst_slot[i] * chunk + r % chunk; entries outside [0, pool_slots) are skipped.
+  const int32_t* dst_slot;
+  int64_t ds_sb, ds_sh;
+  int pool_slots;
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -98,7 +103,8 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   const int ldr = a.rank + 8;  // padded SV row (elements)
   uint16_t* sv_lds = reinterpret_cast<uint16_t*>(smem);                         // [128][ldr]
   int32_t* pos_lds = reinterpret_cast<int32_t*>(sv_lds + kHeadDim * ldr);      // [kTileRows]
-  uint16_t* kst = reinterpret_cast<uint16_t*>(pos_lds + kTileRows);            // [kWaves][16][kStLd]
+  int32_t* orow_lds = pos_lds + kTileRows;                                      // [kTileRows]
+  uint16_t* kst = reinterpret_cast<uint16_t*>(orow_lds + kTileRows);           // [kWaves][16][kStLd]
 
   const int bid = blockIdx.x;
   const int xcd = bid % kXcds;
@@ -139,12 +145,17 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   }
   {
     const int row = row_begin + static_cast<int>(threadIdx.x);
-    int32_t p = -1;
+    int32_t p = -1, orow = row;
     if (row < row_end) {
       const int64_t q = my_id * a.chunk + row % a.chunk;
       if (q >= 0 && q <= 0x7fffffff) p = static_cast<int32_t>(q);
     }
+    if (a.dst_slot) {  // uniform
+      const int32_t sl = a.dst_slot[b * a.ds_sb + h * a.ds_sh + min(row, total_rows - 1) / a.chunk];
+      orow = (sl >= 0 && sl < a.pool_slots) ? sl * a.chunk + row % a.chunk : -1;
+    }
     pos_lds[threadIdx.x] = p;
+    orow_lds[threadIdx.x] = orow;
   }
   __syncthreads();
 
@@ -255,10 +266,11 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
         const int r = unit / U::kPerRow, j = unit % U::kPerRow;
         const int grow = row_begin + lr + m * 16 + r;
         const int32_t pos = pos_lds[lr + m * 16 + r];
-        bool valid = grow >= miss_begin && grow < row_end;
+        const int32_t prow = orow_lds[lr + m * 16 + r];
+        bool valid = grow >= miss_begin && grow < row_end && prow >= 0;
         if (kMode != kPlain) valid = valid && pos >= 0 && pos < a.cs_rows;
         if (!valid) continue;
-        uint16_t* orow = obase + static_cast<int64_t>(a.o_start + grow) * a.o_ss;
+        uint16_t* orow = obase + static_cast<int64_t>(a.o_start + prow) * a.o_ss;
         const u32x4 x1v = *reinterpret_cast<const u32x4*>(&st[r * kStLd + 8 * j]);
         if (kMode == kPlain) {
           *reinterpret_cast<u32x4*>(orow + 8 * j) = x1v;
@@ -298,7 +310,7 @@ void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) 
     static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(&rebuild_kernel<kMode, KS, IdxT>),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                                          static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) +
-                                                                          kTileRows * sizeof(int32_t) +
+                                                                          2 * kTileRows * sizeof(int32_t) +
                                                                           kWaves * 16 * kStLd * sizeof(uint16_t)));
     (void)raised;
   }
@@ -353,7 +365,7 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
   const int BH = a.B * a.H;
   const int heads_padded = (BH + kXcds - 1) / kXcds * kXcds;
   const dim3 grid(static_cast<unsigned>(heads_padded * a.tiles));
-  const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + kTileRows * sizeof(int32_t) +
+  const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * kTileRows * sizeof(int32_t) +
                      static_cast<size_t>(kWaves) * 16 * kStLd * sizeof(uint16_t);
   const int ks = (a.rank + 31) / 32;
   if (ids64) {
@@ -449,4 +461,55 @@ extern "C" int skv_rebuild_k_rope(const uint16_t* u, int64_t u_stride_b, int64_t
   r.chunk = chunk_size;
   r.rank = rank;
   return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, true, r, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_rebuild_k_rope_slots(const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h,
+                                        int64_t u_stride_row, int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b,
+                                        int64_t sv_stride_h, int64_t sv_stride_n, const int32_t* miss_ids,
+                                        const int32_t* miss_slot, const int32_t* cnts, const uint16_t* cos_sin,
+                                        int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode, uint16_t* cache,
+                                        int64_t stride_cache_b, int64_t stride_cache_h, int64_t stride_cache_s,
+                                        int pool_start, int pool_slots, int batch_size, int heads, int num_chunks,
+                                        int chunk_size, int rank, int head_dim, void* stream) {
+  const char* what = "rebuild_k_rope_slots";
+  if (head_dim != kHeadDim || (rope_mode != 0 && rope_mode != 1)) {
+    skv_set_error("%s: head_dim=%d (must be 128), rope_mode=%d (0 half-split, 1 GLM)", what, head_dim, rope_mode);
+    return SKV_EUNSUPPORTED;
+  }
+  if (!miss_slot || pool_slots < 1) {
+    skv_set_error("%s: miss_slot=%p pool_slots=%d", what, static_cast<const void*>(miss_slot), pool_slots);
+    return SKV_EINVAL;
+  }
+  RebuildArgs r{};
+  r.u = u;
+  r.u_sb = u_stride_b;
+  r.u_sh = u_stride_h;
+  r.u_sr = u_stride_row;
+  r.u_rows = u_rows;
+  r.sv = sv;
+  r.sv_sb = sv_stride_b;
+  r.sv_sh = sv_stride_h;
+  r.sv_sn = sv_stride_n;
+  r.ids = miss_ids;
+  r.id_sh = num_chunks;
+  r.id_sb = static_cast<int64_t>(num_chunks) * heads;
+  r.cnts = cnts;
+  r.cs = cos_sin;
+  r.cs_stride = stride_cos_sin;
+  r.cs_rows = cos_sin_rows;
+  r.out = cache;
+  r.o_sb = stride_cache_b;
+  r.o_sh = stride_cache_h;
+  r.o_ss = stride_cache_s;
+  r.o_start = pool_start;
+  r.B = batch_size;
+  r.H = heads;
+  r.S = num_chunks;
+  r.chunk = chunk_size;
+  r.rank = rank;
+  r.dst_slot = miss_slot;
+  r.ds_sh = num_chunks;
+  r.ds_sb = static_cast<int64_t>(num_chunks) * heads;
+  r.pool_slots = pool_slots;
+  return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, false, r, static_cast<hipStream_t>(stream));
 }

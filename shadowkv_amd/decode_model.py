@@ -102,6 +102,7 @@ def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin:
         _fill_selected_values(cache, layer, host_stage)
         shadowkv.rebuild_k_rope(cache.U[layer], cache.SV[layer], cache.position_ids[layer], zero_cnts, cos_sin,
                                 cache.k_cache_buffer[layer], cache.sparse_start, c)
+        cache.init_pool(layer)
     torch.cuda.synchronize()
     cache.kv_offset = ctx
     cache.prefilled_batch = B
@@ -139,7 +140,7 @@ class SyntheticDecoder:
 
     def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
-                 dtype=torch.bfloat16, lanes: int = 1, fused: bool = True):
+                 dtype=torch.bfloat16, lanes: int = 1, fused: bool = True, chunk_cache: int | None = None):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
         # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels and
         # the projections on the skinny linear kernel (libshadowkv_amd), instead of torch operations
@@ -171,7 +172,7 @@ class SyntheticDecoder:
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
                                       chunk_size=chunk_size, rank=rank, max_decode_len=decode_len,
-                                      zero_host_store=False)
+                                      zero_host_store=False, chunk_cache=chunk_cache)
             synthesize_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin)
             lane = _Lane(slice(i * lb, (i + 1) * lb), cache)
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,

@@ -260,7 +260,8 @@ def batch_gather_gemm(a, b, cos, sin, position_ids, output, batch_size, heads, s
               offset_array.data_ptr(), _stream())
 
 
-def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chunk_size):
+def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chunk_size, miss_slot=None,
+                   pool_slots=None):
     """Fused a6+a7: rebuild the miss rows of every (b, h) and push them, rotated, into `cache`.
 
     u: [B, ctx, R] (head-shared, the reference layout) or [B, H, ctx, R] (per-head);
@@ -268,11 +269,13 @@ def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chun
     position_ids: [B, H, S] int64 chunk ids; cnts: [B*H] int32 hit counts;
     cos_sin: [rows, 128] ([cos|sin], half-split RoPE) or [rows, 64] (GLM interleaved);
     cache: [B, H, buf_len, 128] key buffer; rows sparse_start + r are written.
+    Chunk pool: position_ids are the int32 miss ids [B, H, S] of pool_assign and miss_slot
+    [B, H, S] int32 their slots; entry i goes to rows sparse_start + miss_slot[i]*chunk_size + j.
     """
     B, H, S = position_ids.shape
     _dev(u, "u", torch.bfloat16)
     _dev(sv, "sv", torch.bfloat16)
-    _dev(position_ids, "position_ids", torch.int64)
+    _dev(position_ids, "position_ids", torch.int32 if miss_slot is not None else torch.int64)
     _dev(cnts, "cnts", torch.int32)
     _dev(cos_sin, "cos_sin", torch.bfloat16)
     _dev(cache, "cache", torch.bfloat16)
@@ -305,11 +308,21 @@ def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chun
         raise ValueError(f"Invalid cos_sin shape {tuple(cos_sin.shape)}")
     if cache.dim() != 4 or cache.shape[-1] != 128 or cache.stride(-1) != 1:
         raise ValueError("cache must be [B, H, buf_len, 128]")
-    if sparse_start + S * chunk_size > cache.shape[2]:
+    slots = S if miss_slot is None else pool_slots
+    if sparse_start + slots * chunk_size > cache.shape[2]:
         raise ValueError("sparse region exceeds the cache buffer")
     if position_ids.stride(2) != 1:
         raise ValueError("position_ids must be contiguous along the chunk axis")
     _need(cnts, B * H, "cnts")
+    if miss_slot is not None:
+        _dev(miss_slot, "miss_slot", torch.int32)
+        if not (position_ids.is_contiguous() and miss_slot.is_contiguous()) or miss_slot.numel() != B * H * S:
+            raise ValueError("pool miss lists must be contiguous [B, H, S]")
+        _lib.call("skv_rebuild_k_rope_slots", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh,
+                  sv_sn, position_ids.data_ptr(), miss_slot.data_ptr(), cnts.data_ptr(), cos_sin.data_ptr(),
+                  cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0), cache.stride(1),
+                  cache.stride(2), sparse_start, pool_slots, B, H, S, chunk_size, rank, 128, _stream())
+        return
     _lib.call("skv_rebuild_k_rope", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh, sv_sn,
               position_ids.data_ptr(), position_ids.stride(0), position_ids.stride(1), cnts.data_ptr(),
               cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0),
@@ -447,13 +460,16 @@ def sparse_attn_workspace_bytes(batch_size: int, q_heads: int, kv_len: int) -> i
     return int(_lib.lib().skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len))
 
 
-def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, kv_len_dev=None):
+def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, kv_len_dev=None, pool=None):
     """out[b, hq] = softmax(scale q[b,hq] K[b,h,:L]^T) V[b,h,:L], h = hq // (Hq/Hkv).
 
     q: [B, Hq, 128] view; k_cache/v_cache: [B, Hkv, >=kv_len, 128] views; out: [B, Hq, 128];
     workspace: uint8 device tensor of sparse_attn_workspace_bytes(B, Hq, kv_len) bytes.
     L = kv_len, or, with kv_len_dev (device int32 [1]), the value it holds when the kernel runs,
     clamped to [1, kv_len].
+    pool: optional (slot_list [B, Hkv, S] int32, sparse_start, S, chunk, pool_slots): the keys
+    [sparse_start, sparse_start + S*chunk) are read through the slot list (a chunk pool), the
+    later keys (pool_slots - S)*chunk rows further down.
     """
     _dev(q, "q", torch.bfloat16)
     _dev(k_cache, "k_cache", torch.bfloat16)
@@ -463,7 +479,14 @@ def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, 
     B, Hq, D = q.shape
     if k_cache.shape[:2] != v_cache.shape[:2] or k_cache.stride() != v_cache.stride() or k_cache.shape[0] != B:
         raise ValueError("k_cache and v_cache must be [B, Hkv, L, 128] with identical strides")
-    if kv_len > k_cache.shape[2] or kv_len < 1:
+    delta = 0
+    if pool is not None:
+        slot_list, sp0, S, chunk, pslots = pool
+        _dev(slot_list, "slot_list", torch.int32)
+        if not slot_list.is_contiguous() or slot_list.numel() != B * k_cache.shape[1] * S or pslots < S:
+            raise ValueError("slot_list must be contiguous [B, Hkv, S] with S <= pool_slots")
+        delta = (pslots - S) * chunk
+    if kv_len + delta > k_cache.shape[2] or kv_len < 1:
         raise ValueError(f"kv_len={kv_len} outside the cache length {k_cache.shape[2]}")
     if q.stride(2) != 1 or k_cache.stride(3) != 1 or out.stride(2) != 1:
         raise ValueError("the head dimension must be contiguous")
@@ -474,6 +497,13 @@ def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, 
         ldev = kv_len_dev.data_ptr()
     _need_offsets(q, (B, Hq, D), q.stride(), "q")
     _need_offsets(out, (B, Hq, D), out.stride(), "out")
+    if pool is not None:
+        _lib.call("skv_sparse_attn_decode_paged", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
+                  v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1],
+                  D, kv_len, ldev, float(scale), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                  out.data_ptr(), out.stride(0), out.stride(1), slot_list.data_ptr(), sp0, S, chunk, pslots,
+                  _stream())
+        return
     _lib.call("skv_sparse_attn_decode", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
               k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1], D, kv_len, ldev,
               float(scale), workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
@@ -640,3 +670,49 @@ def gather_rows(src, idx, dst):
         raise ValueError("gather_rows: src [rows, n_src, 128], idx [rows, n], dst [rows, n, 128]")
     _lib.call("skv_gather_rows", src.data_ptr(), src.shape[0], src.shape[1], idx.data_ptr(), idx.shape[1],
               dst.data_ptr(), _stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# f3: device chunk pool
+
+def pool_assign(selected, num_chunks, slot_of, slot_chunk, slot_used, clock, slot_list, miss_ids, miss_slot, cnts):
+    """Map the selection onto a chunk pool (one row per (b, h)): selected [rows, S] int64; tables
+    slot_of [rows, num_chunks], slot_chunk / slot_used [rows, P], clock [rows] (int32, updated);
+    outputs slot_list [rows, S], miss_ids / miss_slot [rows, S] (misses at [cnts[r], S)), cnts [rows]."""
+    _dev(selected, "selected", torch.int64)
+    for t, nm in ((slot_of, "slot_of"), (slot_chunk, "slot_chunk"), (slot_used, "slot_used"), (clock, "clock"),
+                  (slot_list, "slot_list"), (miss_ids, "miss_ids"), (miss_slot, "miss_slot"), (cnts, "cnts")):
+        _dev(t, nm, torch.int32)
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+    if not selected.is_contiguous() or selected.dim() != 2:
+        raise ValueError("selected must be contiguous [rows, S]")
+    rows, S = selected.shape
+    P = slot_chunk.numel() // rows
+    if slot_of.numel() != rows * num_chunks or slot_chunk.numel() != rows * P or slot_used.numel() != rows * P or \
+            clock.numel() != rows or cnts.numel() < rows:
+        raise ValueError("pool tables do not match the selection's rows")
+    for t, nm in ((slot_list, "slot_list"), (miss_ids, "miss_ids"), (miss_slot, "miss_slot")):
+        _need(t, rows * S, nm)
+    _lib.call("skv_pool_assign", selected.data_ptr(), rows, S, num_chunks, P, slot_of.data_ptr(),
+              slot_chunk.data_ptr(), slot_used.data_ptr(), clock.data_ptr(), slot_list.data_ptr(), miss_ids.data_ptr(),
+              miss_slot.data_ptr(), cnts.data_ptr(), _stream())
+
+
+def gather_copy_misses_to_slots(values, v_cache_buffer, miss_ids, cnts, miss_slot, batch_size, heads, cpu_v_length,
+                                pool_offset, gpu_v_stride, map_size, pool_slots, chunk_elems):
+    """The miss gather of a chunk pool: entries i >= cnts[r] (chunk miss_ids, slot miss_slot) of every
+    row r from the pinned host store into v_cache_buffer + r*gpu_v_stride + pool_offset + slot*chunk."""
+    rows = batch_size * heads
+    row_stride = _host_row_stride(values, rows, cpu_v_length)
+    _need(values, (rows - 1) * row_stride + row_stride, "values")
+    _dev(v_cache_buffer, "v_cache_buffer", torch.bfloat16)
+    _need(v_cache_buffer, (rows - 1) * gpu_v_stride + pool_offset + pool_slots * chunk_elems, "v_cache_buffer")
+    for t, nm in ((miss_ids, "miss_ids"), (miss_slot, "miss_slot")):
+        _dev(t, nm, torch.int32)
+        _need(t, rows * map_size, nm)
+    _dev(cnts, "cnts", torch.int32)
+    _need(cnts, rows, "cnts")
+    _lib.call("skv_gather_copy_misses_to_slots", device_address(values), v_cache_buffer.data_ptr(), miss_ids.data_ptr(),
+              cnts.data_ptr(), miss_slot.data_ptr(), batch_size, heads, row_stride, pool_offset, gpu_v_stride,
+              map_size, pool_slots, chunk_elems, _stream())

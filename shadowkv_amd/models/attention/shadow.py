@@ -98,6 +98,7 @@ class ShadowAttention(AttentionBase):
         if q is None:
             raise ValueError("decode attention takes one query token per step")
         out = torch.empty(B, Hq, query_states.shape[-1], dtype=query_states.dtype, device=query_states.device)
-        shadowkv.sparse_attn_decode(q, key_states, value_states, key_states.shape[2], out, kv_cache.attn_workspace,
-                                    kv_len_dev=kv_cache.kv_len_dev)
+        kv_len, pool = kv_cache.attention_args(key_states.shape[2])
+        shadowkv.sparse_attn_decode(q, key_states, value_states, kv_len, out, kv_cache.attn_workspace,
+                                    kv_len_dev=kv_cache.kv_len_dev, pool=pool)
         return out.view(B, 1, Hq, -1)

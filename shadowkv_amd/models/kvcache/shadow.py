@@ -57,7 +57,8 @@ class ShadowKVCache_CPU(KVCacheBase):
 
     def __init__(self, config, batch_size: int = 1, max_length: int = 32 * 1024, device: str = "cuda:0",
                  dtype=torch.bfloat16, sparse_budget: int = 2048, chunk_size: int = 8, rank: int = 160,
-                 max_decode_len: int | None = None, zero_host_store: bool = True) -> None:
+                 max_decode_len: int | None = None, zero_host_store: bool = True,
+                 chunk_cache: int | None = None) -> None:
         self.config = config
         self.batch_size = batch_size
         self.max_length = max_length
@@ -78,6 +79,15 @@ class ShadowKVCache_CPU(KVCacheBase):
         if self.select_sets * self.chunk_size != self.sparse_budget:
             raise ValueError(f"sparse_budget {self.sparse_budget} is not a multiple of chunk_size {chunk_size}")
 
+        # Chunk pool (chunk_cache = P >= S slots per (b, h) and layer): the selected region becomes a
+        # pool of P chunk slots that keeps chunks across steps (least recently used replaced); the
+        # attention reads the selection through a slot list. None: the reference's slot reuse.
+        self.pooled = chunk_cache is not None
+        self.pool_slots = self.select_sets if chunk_cache is None else int(chunk_cache)
+        if self.pool_slots < self.select_sets:
+            raise ValueError(f"chunk_cache={chunk_cache} holds fewer than the {self.select_sets} selected chunks")
+        self.pool_delta = (self.pool_slots - self.select_sets) * chunk_size  # rows between selection end and tail
+
         L, B, H, D = self.num_layers, batch_size, self.num_key_value_heads, self.head_dim
         # One pinned host buffer per layer, [B, H, max_length/c, c*D] each (indexable like the reference's
         # [L, ...] tensor): torch's pinned allocator rounds each request up to a power of two, which a
@@ -93,6 +103,7 @@ class ShadowKVCache_CPU(KVCacheBase):
             worst_sparse_end = (self.local_chunk + 8) * chunk_size - 1 + self.outlier_chunk * chunk_size \
                 + self.sparse_budget
             self.buf_len = max(ref_len, worst_sparse_end + int(max_decode_len))
+        self.buf_len += self.pool_delta
         self.k_cache_buffer = torch.zeros(L, B, H, self.buf_len, D, device=device, dtype=dtype)
         self.v_cache_buffer = torch.zeros(L, B, H, self.buf_len, D, device=device, dtype=dtype)
 
@@ -127,6 +138,13 @@ class ShadowKVCache_CPU(KVCacheBase):
         # Device-resident append row / attention length (use_device_lengths); None = host integers.
         self.append_row_dev = None
         self.kv_len_dev = None
+        # Chunk pool tables (allocated with the prompt geometry) and per-step scratch.
+        self.slot_of = self.slot_chunk = self.slot_used = self.pool_clock = None
+        if self.pooled:
+            S = self.select_sets
+            self.slot_list = torch.zeros(rows, S, device=device, dtype=torch.int32)
+            self.miss_ids = torch.zeros(rows, S, device=device, dtype=torch.int32)
+            self.miss_slot = torch.zeros(rows, S, device=device, dtype=torch.int32)
 
     def print_stats(self):
         print(f"ShadowKV_CPU | sparse budget {self.sparse_budget} | chunk size {self.chunk_size} |rank {self.rank} "
@@ -261,7 +279,33 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.position_ids[l][pb:pb + bsz].copy_(selected.view(bsz, H, -1))
         self._copy_chunks(v, vbuf, selected, self.sparse_start)
         self._copy_chunks(k, kbuf, selected, self.sparse_start)
+        self.init_pool(l, pb, bsz)
         self._finish_layer(l, bsz, incoming)
+
+    def init_pool(self, layer_idx: int, pb: int = 0, bsz: int | None = None):
+        """Pool tables of one layer from its initial selection: slot j holds position_ids[j]
+        (the layout of the selected region), the other slots are empty."""
+        if not self.pooled:
+            return
+        bsz = self.batch_size if bsz is None else bsz
+        H, S, P, L = self.num_key_value_heads, self.select_sets, self.pool_slots, self.num_layers
+        rows = self.batch_size * H
+        if self.slot_of is None or self.slot_of.shape[-1] != self.chunks:
+            dev = self.device
+            self.slot_of = torch.full((L, rows, self.chunks), -1, dtype=torch.int32, device=dev)
+            self.slot_chunk = torch.full((L, rows, P), -1, dtype=torch.int32, device=dev)
+            self.slot_used = torch.full((L, rows, P), -1, dtype=torch.int32, device=dev)
+            self.pool_clock = torch.zeros(L, rows, dtype=torch.int32, device=dev)
+        r0, r1 = pb * H, (pb + bsz) * H
+        sel = self.position_ids[layer_idx][pb:pb + bsz].reshape(bsz * H, S)
+        slots = torch.arange(S, dtype=torch.int32, device=sel.device).expand(bsz * H, S)
+        self.slot_of[layer_idx, r0:r1].fill_(-1)
+        self.slot_of[layer_idx, r0:r1].scatter_(1, sel, slots)
+        self.slot_chunk[layer_idx, r0:r1].fill_(-1)
+        self.slot_chunk[layer_idx, r0:r1, :S].copy_(sel)
+        self.slot_used[layer_idx, r0:r1].fill_(-1)
+        self.slot_used[layer_idx, r0:r1, :S].fill_(0)
+        self.pool_clock[layer_idx, r0:r1].fill_(0)
 
     def _finish_layer(self, layer_idx: int, bsz: int, incoming: int):
         if layer_idx == self.num_layers - 1:
@@ -298,6 +342,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.k_cache_buffer[layer_idx][:, :, :n].copy_(k_buffer)
         self.v_cache_buffer[layer_idx][:, :, :n].copy_(v_buffer)
         self.position_ids[layer_idx].copy_(position_ids)
+        self.init_pool(layer_idx)
         if layer_idx == self.num_layers - 1:
             self.prefilled_batch = B
             self.kv_offset = ctx
@@ -313,6 +358,19 @@ class ShadowKVCache_CPU(KVCacheBase):
         q = query_states if query_states.is_contiguous() else query_states.contiguous()
         shadowkv.score_logits(q, self.k_landmark[layer_idx], self.gemm_o, self.norm, self.sum, B * H, G, n, D,
                               1.0 / math.sqrt(128))
+        if self.pooled:
+            # GQA-max scores, the selection in top-k order (kept in position_ids), then the pool's
+            # hits, victims and miss list (cnts = hits; misses at [cnts, S) of miss_ids / miss_slot).
+            rows, S = B * H, self.select_sets
+            shadowkv.softmax_gqa_max(self.gemm_o, self.norm, self.sum, self.chunk_attn.view(rows, n), rows, G, n)
+            sel = self.position_ids[layer_idx].view(rows, S)
+            shadowkv.topk_gather(self.chunk_attn.view(rows, n), self.k_landmark_idx[layer_idx].view(rows, n), S, sel)
+            shadowkv.pool_assign(sel, self.chunks, self.slot_of[layer_idx], self.slot_chunk[layer_idx],
+                                 self.slot_used[layer_idx], self.pool_clock[layer_idx], self.slot_list,
+                                 self.miss_ids, self.miss_slot, self.cnts)
+            if self.keep_selected:
+                self.selected_chunks.copy_(self.position_ids[layer_idx])
+            return self.position_ids[layer_idx]
         # softmax + GQA max + top-k + landmark-id gather + reorder in one launch. The GQA-max scores are kept in
         # chunk_attn; the selected ids in top-k order (selected_chunks) only when keep_selected is set.
         shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, B * H, G, n, self.k_landmark_idx[layer_idx].view(B * H, n),
@@ -327,11 +385,29 @@ class ShadowKVCache_CPU(KVCacheBase):
     def _live_view(self, buf: torch.Tensor, layer_idx: int) -> torch.Tensor:
         if self.kv_len_dev is not None:
             return buf[:, :, :self.buf_len]  # length read on the device (kv_len_dev)
-        return buf[:, :, :self.sparse_end + self._gen_len(layer_idx)]
+        return buf[:, :, :self.sparse_end + self._gen_len(layer_idx) + self.pool_delta]
+
+    def attention_args(self, view_len: int):
+        """(kv_len, pool) for the sparse attention over a _live_view of view_len rows: the virtual
+        length (rows minus the pool's extra slots) and, with a chunk pool, its slot list geometry."""
+        if not self.pooled:
+            return view_len, None
+        B, H = self.batch_size, self.num_key_value_heads
+        return view_len - self.pool_delta, (self.slot_list.view(B, H, -1), self.sparse_start, self.select_sets,
+                                            self.chunk_size, self.pool_slots)
 
     def get_value_cache(self, layer_idx: int, position_ids: torch.Tensor, hits_moved: bool = False) -> torch.Tensor:
         """The layer's value buffer with the selected chunks in place: cache hits moved to their
-        new slots (unless move_value_hits already did, hits_moved) and misses gathered from host."""
+        new slots (unless move_value_hits already did, hits_moved) and misses gathered from host.
+        With a chunk pool the hits stay where they are and the misses go to their assigned slots."""
+        if self.pooled:
+            B, H, D = self.batch_size, self.num_key_value_heads, self.head_dim
+            shadowkv.gather_copy_misses_to_slots(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx],
+                                                 self.miss_ids, self.cnts, self.miss_slot, B, H,
+                                                 int(self.max_ctx_chunks_len * D), self.sparse_start * D,
+                                                 self.buf_len * D, self.select_sets, self.pool_slots,
+                                                 self.chunk_size * D)
+            return self._live_view(self.v_cache_buffer[layer_idx], layer_idx)
         shadowkv.gather_copy_with_offsets(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.temp,
                                           self.offsets, self.cnts, self.signals, self.batch_size,
                                           self.num_key_value_heads, int(self.max_ctx_chunks_len * self.head_dim),
@@ -341,12 +417,21 @@ class ShadowKVCache_CPU(KVCacheBase):
 
     def move_value_hits(self, layer_idx: int):
         """The in-buffer half of the value fetch alone (hit rows to their new slots), so that a
-        later get_value_cache(..., hits_moved=True) on the copy stream is host-link work only."""
+        later get_value_cache(..., hits_moved=True) on the copy stream is host-link work only.
+        Nothing to move with a chunk pool."""
+        if self.pooled:
+            return
         shadowkv.gather_copy_d2d_with_offsets(self.v_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
                                               self.num_key_value_heads, int(self.sparse_budget * self.head_dim),
                                               self.kernel_offset, self.kernel_stride, self.select_sets)
 
     def get_key_cache(self, layer_idx: int, position_ids: torch.Tensor, rope_func, cos_sin_cache) -> torch.Tensor:
+        if self.pooled:  # the misses' keys rebuilt into their slots; hits stay in place
+            B, H, S = self.batch_size, self.num_key_value_heads, self.select_sets
+            shadowkv.rebuild_k_rope(self.U[layer_idx], self.SV[layer_idx], self.miss_ids.view(B, H, S), self.cnts,
+                                    cos_sin_cache, self.k_cache_buffer[layer_idx], self.sparse_start, self.chunk_size,
+                                    miss_slot=self.miss_slot.view(B, H, S), pool_slots=self.pool_slots)
+            return self._live_view(self.k_cache_buffer[layer_idx], layer_idx)
         shadowkv.gather_copy_d2d_with_offsets(self.k_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
                                               self.num_key_value_heads, int(self.sparse_budget * self.head_dim),
                                               self.kernel_offset, self.kernel_stride, self.select_sets)
@@ -376,7 +461,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.attn_out = torch.empty(B, Hq, self.head_dim, dtype=self.dtype, device=self.device)
 
     def check_capacity(self, incoming: int = 1):
-        if self.sparse_end + self.gen_offset + incoming > self.buf_len:
+        if self.sparse_end + self.gen_offset + incoming + self.pool_delta > self.buf_len:
             raise RuntimeError(f"decode capacity exhausted: {self.gen_offset} tokens generated, buffer holds "
                                f"{self.buf_len - self.sparse_end}; construct the cache with a larger max_decode_len")
 
@@ -390,7 +475,8 @@ class ShadowKVCache_CPU(KVCacheBase):
         advances itself (at layer 0), so a whole step can be captured in a HIP graph and replayed.
         The host counters stay authoritative for the capacity check."""
         row = self.sparse_end + self.gen_offset - 1  # advanced before the step's first append
-        self.append_row_dev = torch.full((1,), row, dtype=torch.int64, device=self.device)
+        # physical append row (after the pool's extra slots); the attention length stays virtual
+        self.append_row_dev = torch.full((1,), row + self.pool_delta, dtype=torch.int64, device=self.device)
         self.kv_len_dev = torch.full((1,), row + 1, dtype=torch.int32, device=self.device)
 
     def rope_and_append(self, qkv: torch.Tensor, position_ids: torch.Tensor, cos_sin: torch.Tensor, layer_idx: int,
@@ -423,7 +509,7 @@ class ShadowKVCache_CPU(KVCacheBase):
             self.v_cache_buffer[layer_idx].index_copy_(2, self.append_row_dev, new_v_cache)
             self.k_cache_buffer[layer_idx].index_copy_(2, self.append_row_dev, new_k_cache)
         else:
-            start = self.sparse_end + self.gen_offset
+            start = self.sparse_end + self.gen_offset + self.pool_delta
             self.v_cache_buffer[layer_idx][:, :, start:start + incoming].copy_(new_v_cache, non_blocking=True)
             self.k_cache_buffer[layer_idx][:, :, start:start + incoming].copy_(new_k_cache, non_blocking=True)
         if layer_idx == self.num_layers - 1:
@@ -444,6 +530,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.prefilled_batch = 0
         self.append_row_dev = None
         self.kv_len_dev = None
+        self.slot_of = self.slot_chunk = self.slot_used = self.pool_clock = None
 
     def get_kv_len(self):
         return self.kv_offset

@@ -19,13 +19,14 @@ def rope_tokens_cpu(x, cos_sin, pos):
     return (x * c) + (rot * s)
 
 
-def build_cache(case, device, max_decode_len=None, num_layers=1):
+def build_cache(case, device, max_decode_len=None, num_layers=1, chunk_cache=None):
     d = case["dims"]
     B, H, G, D, ctx = d["B"], d["H"], d["G"], d["D"], d["ctx"]
     cfg = types.SimpleNamespace(num_attention_heads=H * G, num_key_value_heads=H, hidden_size=H * G * D,
                                 num_hidden_layers=num_layers)
     cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device=str(device), sparse_budget=d["budget"],
-                              chunk_size=d["chunk"], rank=d["rank"], max_decode_len=max_decode_len)
+                              chunk_size=d["chunk"], rank=d["rank"], max_decode_len=max_decode_len,
+                              chunk_cache=chunk_cache)
     # Every layer starts from the oracle's encoded state of the prompt (the decode path is compared
     # with the oracle's decode from exactly that state; the device encoder has its own tests).
     si = case["state_in"]
@@ -97,4 +98,4 @@ def fresh_oracle_state(case):
     kw = {k: v.clone() for k, v in case["state_in"].items()}
     return oracle.LayerState(**kw, prefill_local=st.prefill_local, sparse_start=st.sparse_start,
                              sparse_end=st.sparse_end, chunk=d["chunk"], budget=d["budget"], ctx=d["ctx"],
-                             buf_len=st.buf_len)
+                             buf_len=st.buf_len, chunks=st.chunks)

@@ -17,15 +17,18 @@ def _state(model):
         c = lane.cache
         out += [c.position_ids.clone(), c.cnts.clone(), c.offsets.clone(), c.k_cache_buffer.clone(),
                 c.v_cache_buffer.clone(), c.append_row_dev.clone(), c.kv_len_dev.clone(), c.chunk_attn.clone()]
+        if c.pooled:
+            out += [c.slot_of.clone(), c.slot_chunk.clone(), c.slot_used.clone(), c.pool_clock.clone(),
+                    c.slot_list.clone()]
     return out
 
 
-@pytest.mark.parametrize("lanes", [1, 2])
-def test_graph_replay_matches_eager(gpu, lanes):
-    print(f"graph replay vs eager, lanes={lanes}", flush=True)
+@pytest.mark.parametrize("lanes,chunk_cache", [(1, None), (2, None), (2, 384)])
+def test_graph_replay_matches_eager(gpu, lanes, chunk_cache):
+    print(f"graph replay vs eager, lanes={lanes}, chunk_cache={chunk_cache}", flush=True)
     shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
     steps = 4
-    kw = dict(sparse_budget=2048, decode_len=steps + 4, lanes=lanes, seed=11)
+    kw = dict(sparse_budget=2048, decode_len=steps + 4, lanes=lanes, seed=11, chunk_cache=chunk_cache)
     eager = decode_model.SyntheticDecoder(shape, 4, 16384, **kw)
     graphed = decode_model.SyntheticDecoder(shape, 4, 16384, **kw)
     tok0 = torch.randint(0, shape.vocab, (4, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(1))
