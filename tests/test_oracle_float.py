@@ -179,3 +179,48 @@ def test_decode_step_from_given_scores_matches_computed():
     assert np.array_equal(res["offsets"], d["out_offsets"])
     assert np.array_equal(st.position_ids.numpy(), d["out_position_ids"])
     assert torch.equal(res["out"], case["res"]["out"])
+
+
+def test_encode_layer_overrides_reproduce_the_default_path():
+    """encode_layer(outliers=..., init_scores=...) given the default path's own outlier order and
+    GQA-max scores builds the same state (the device encoder's tests continue from its decisions)."""
+    import math
+    import torch.nn.functional as F
+    from oracle.shadowkv_oracle import _rope_tokens
+    from tests.golden import make_golden
+
+    case = make_golden.decode_small_case()
+    d = case["dims"]
+    st = case["st"]
+    B, H, D, ctx, c = d["B"], d["H"], d["D"], d["ctx"], d["chunk"]
+    k = _rope_tokens(case["k_pre"], case["cos_sin"], torch.arange(ctx))
+    kc = k[:, :, :st.chunks * c].reshape(B, H, st.chunks, c, D)
+    cand = kc.mean(dim=-2)
+    cos = F.cosine_similarity(cand.unsqueeze(3).expand(-1, -1, -1, c, -1), kc, dim=-1)
+    n_out = (d["budget"] // 1024) * 24
+    outliers = cos.min(dim=-1).values.topk(n_out, largest=False).indices
+    q = _rope_tokens(case["q_last"], case["cos_sin"], torch.tensor([ctx - 1]))
+    n = st.landmarks.shape[-2]
+    # the default path's own scores (bf16 einsum, fp32 softmax, bf16, max over the group)
+    sc = torch.einsum("bhgd,bhcd->bhgc", q.reshape(B, H, -1, D), st.landmarks) / math.sqrt(128)
+    sc = F.softmax(sc, dim=-1, dtype=torch.float32).to(torch.bfloat16).max(dim=-2).values
+    st2 = oracle.encode_layer(case["k_pre"], case["v"], case["q_last"], case["cos_sin"], rank=d["rank"], chunk=c,
+                              budget=d["budget"], outliers=outliers, init_scores=sc)
+    for name in ("landmarks", "landmark_idx", "host_v", "U", "SV"):
+        a, b = getattr(st, name), getattr(st2, name)
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b), name
+    for buf in ("kbuf", "vbuf"):  # local + outlier regions identical
+        assert torch.equal(getattr(st, buf)[:, :, :st.sparse_start].view(torch.int16),
+                           getattr(st2, buf)[:, :, :st.sparse_start].view(torch.int16)), buf
+    # the initial selection: the same chunks, up to ties at the top-S boundary (torch.topk breaks
+    # them arbitrarily, topk_gather by the lowest landmark index)
+    S = d["budget"] // c
+    for r in range(B * H):
+        b, h = divmod(r, H)
+        vals = sc[b, h].float()
+        kth = torch.sort(vals, descending=True).values[S - 1]
+        score_of = {int(i): float(v) for i, v in zip(st.landmark_idx[b, h], vals)}
+        a, bsel = set(st.position_ids[b, h].tolist()), set(st2.position_ids[b, h].tolist())
+        assert all(score_of[i] == kth for i in a ^ bsel), r
+        assert {i for i, v in score_of.items() if v > kth} <= a & bsel
