@@ -191,7 +191,7 @@ def test_encode_layer_overrides_reproduce_the_default_path():
 
     case = make_golden.decode_small_case()
     d = case["dims"]
-    st = case["st"]
+    st = oracle.LayerState(**case["state_in"], chunks=case["st"].chunks, sparse_start=case["st"].sparse_start)
     B, H, D, ctx, c = d["B"], d["H"], d["D"], d["ctx"], d["chunk"]
     k = _rope_tokens(case["k_pre"], case["cos_sin"], torch.arange(ctx))
     kc = k[:, :, :st.chunks * c].reshape(B, H, st.chunks, c, D)
