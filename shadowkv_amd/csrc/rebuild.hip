@@ -20,7 +20,8 @@
 //     (a lane holds 4 consecutive dims of one row: one 8-byte write per column tile); the
 //     epilogue then works in row-contiguous 16-byte units: a lane takes dims [8j, 8j+8) (and,
 //     for the half-split rotation, [64+8j, 72+8j)) of one row, with its cos/sin loaded as
-//     16-byte vectors before the MFMAs, and stores the rotated row with 16-byte stores;
+//     16-byte vectors before the MFMAs, and stores the rotated row with 16-byte non-temporal
+//     stores (skv::store_nt: the output is not re-read by this kernel);
 //   * blockIdx -> (head, tile) is XCD-aware: all tiles of a head land on the same XCD
 //     (workgroups are dealt round-robin over the 8 XCDs), so SV is fetched from HBM once per
 //     head and re-read from that XCD's L2.
@@ -273,15 +274,15 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
         uint16_t* orow = obase + static_cast<int64_t>(a.o_start + prow) * a.o_ss;
         const u32x4 x1v = *reinterpret_cast<const u32x4*>(&st[r * kStLd + 8 * j]);
         if (kMode == kPlain) {
-          *reinterpret_cast<u32x4*>(orow + 8 * j) = x1v;
+          skv::store_nt(orow + 8 * j, x1v);
         } else if (kMode == kRopeHalf) {
           const u32x4 x2v = *reinterpret_cast<const u32x4*>(&st[r * kStLd + 64 + 8 * j]);
           const u32x4 cv = cs_c[it][m][q], sv = cs_s[it][m][q];
           uint32_t y1[4], y2[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) skv::rope_half_split2(x1v[e], x2v[e], cv[e], sv[e], y1[e], y2[e]);
-          *reinterpret_cast<u32x4*>(orow + 8 * j) = u32x4{y1[0], y1[1], y1[2], y1[3]};
-          *reinterpret_cast<u32x4*>(orow + 64 + 8 * j) = u32x4{y2[0], y2[1], y2[2], y2[3]};
+          skv::store_nt(orow + 8 * j, u32x4{y1[0], y1[1], y1[2], y1[3]});
+          skv::store_nt(orow + 64 + 8 * j, u32x4{y2[0], y2[1], y2[2], y2[3]});
         } else {  // GLM: interleaved pairs on dims 0..63, dims 64..127 unchanged
           if (j < 8) {
             uint16_t x[8], c[8], sn[8], y[8];
@@ -290,9 +291,9 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
             unpack8(cs_s[it][m][q], sn);
 #pragma unroll
             for (int p = 0; p < 4; ++p) skv::rope_half_split(x[2 * p], x[2 * p + 1], c[p], sn[p], y[2 * p], y[2 * p + 1]);
-            *reinterpret_cast<u32x4*>(orow + 8 * j) = pack8(y);
+            skv::store_nt(orow + 8 * j, pack8(y));
           } else {
-            *reinterpret_cast<u32x4*>(orow + 8 * j) = x1v;
+            skv::store_nt(orow + 8 * j, x1v);
           }
         }
       }

@@ -159,6 +159,15 @@ __device__ __forceinline__ u32x4 load_nt(const u32x4* p) {
   return u32x4{v.x, v.y, v.z, v.w};
 }
 
+// 16-byte store with the non-temporal hint: global_store_dwordx4 ... nt. For large outputs that no
+// later instruction of the same kernel reads: they are not kept dirty in the L2, so the write-back
+// of dirty L2 lines at the kernel boundary (which the next kernel on the stream waits for) stays
+// short (rebuild at batch 8, 33 MB written: 3.2 -> 1.3 us between back-to-back launches).
+__device__ __forceinline__ void store_nt(void* p, u32x4 v) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(v4u{v.x, v.y, v.z, v.w}, reinterpret_cast<v4u*>(p));
+}
+
 }  // namespace skv
 
 // Host-side error reporting shared by every entry point (defined in skv_api.cpp).
