@@ -52,6 +52,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
     p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
+    p.add_argument("--graph-steps", type=int, default=8,
+                   help="decode steps per captured graph (one continuous lane pipeline across steps); "
+                        "reduced to a divisor of --steps")
     p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode", "pool"],
                    default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
@@ -695,10 +698,12 @@ def main() -> int:
     log(f"warmup {args.warmup} steps done")
 
     graph = not args.no_graph
+    per_call = 1
     if graph:
-        model.capture(tok)
+        per_call = math.gcd(args.steps, max(1, args.graph_steps))
+        model.capture(tok, steps=per_call)
         torch.cuda.synchronize()
-        log("decode step captured in a HIP graph")
+        log(f"{per_call} decode step(s) captured in a HIP graph")
 
         def step(_):
             return model.replay()
@@ -706,11 +711,12 @@ def main() -> int:
         step = model.decode_step
     torch.cuda.synchronize()
     start = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(args.steps // per_call):
         tok = step(tok)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
-    log(f"timed {args.steps} {'graph replays' if graph else 'eager steps'} in {elapsed:.3f}s")
+    log(f"timed {args.steps} steps as {args.steps // per_call} {'graph replays' if graph else 'eager steps'} "
+        f"in {elapsed:.3f}s")
 
     n = cache.k_landmark.shape[-2]
     BH = cache.batch_size * shape.kv_heads  # one launch covers one lane's batch slice
@@ -751,7 +757,7 @@ def main() -> int:
                                f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, V in pinned host memory, "
                                + (f"device chunk pool of {args.chunk_cache} slots, " if args.chunk_cache else "")
                                + f"{lanes} interleaved batch lane(s), "
-                               f"{'HIP-graph-captured step' if graph else 'eager step'}",
+                               + (f"HIP graphs of {per_call} step(s)" if graph else "eager steps"),
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

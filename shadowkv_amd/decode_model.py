@@ -190,6 +190,7 @@ class SyntheticDecoder:
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
         self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
         self.graph = None
+        self.graph_steps = 1
         self.static_tokens = None
 
     def _rope_for(self, lane: _Lane):
@@ -290,59 +291,81 @@ class SyntheticDecoder:
         self.pos[lane.rows].add_(1)
         return self._greedy(logits)  # [b, 1]
 
+    def _embed(self, tokens: torch.Tensor):
+        """Token embedding; fused: (residual, normalised input of layer 0)."""
+        h = F.embedding(tokens, self.embed)
+        if not self.fused:
+            return h
+        x = torch.empty_like(h)
+        shadowkv.rmsnorm(h, self.layers[0].in_norm, self.shape.eps, x)
+        return h, x
+
     @torch.inference_mode()
     def decode_step(self, tokens: torch.Tensor) -> torch.Tensor:
-        """One greedy decode step for the whole batch: tokens [B, 1] -> next tokens [B, 1].
+        """One greedy decode step for the whole batch: tokens [B, 1] -> next tokens [B, 1]."""
+        return self.decode_steps(tokens, 1)
+
+    @torch.inference_mode()
+    def decode_steps(self, tokens: torch.Tensor, steps: int) -> torch.Tensor:
+        """`steps` greedy decode steps for the whole batch: tokens [B, 1] -> the last step's tokens.
 
         Every step-dependent integer (RoPE position, cache append row, attention length) lives
-        on the device and is advanced by the step itself, so the step can be captured. Issue
-        order for two lanes: begin0(0) begin1(0) end0(0) begin0(1) end1(0) begin1(1) ...; each
-        lane's value fetch overlaps the other lanes' work between its begin and its end."""
+        on the device and is advanced by the step itself, so steps can be captured. The lanes are
+        one software pipeline over (step, layer) units: issue order for two lanes is begin0(0)
+        begin1(0) end0(0) begin0(1) end1(0) begin1(1) ..., so each lane's value fetch overlaps the
+        other lanes' work between its begin and its end. A lane's step boundary is a unit like any
+        other (end of its last layer, lm head, embedding of the new token, begin of layer 0), so
+        across steps the first lane's next fetch is issued while the second lane finishes its
+        last layer and lm head, instead of after both."""
+        if steps < 1:
+            raise ValueError(f"steps must be >= 1, got {steps}")
         lanes = self.lanes
-        hs = [F.embedding(tokens[lane.rows], self.embed) for lane in lanes]
-        if self.fused:  # (residual, normalised input of layer 0)
-            states = []
-            for h in hs:
-                x = torch.empty_like(h)
-                shadowkv.rmsnorm(h, self.layers[0].in_norm, self.shape.eps, x)
-                states.append((h, x))
-            hs = states
+        L = self.shape.layers
+        cur = [tokens[lane.rows] for lane in lanes]
+        hs = [None] * len(lanes)
         pending = [None] * len(lanes)
-        for idx in range(self.shape.layers):
+        for u in range(steps * L + 1):
+            idx = u % L
             for i, lane in enumerate(lanes):
                 if pending[i] is not None:
-                    hs[i] = self._layer_end(idx - 1, hs[i], lane, pending[i])
-                pending[i] = self._layer_begin(idx, hs[i], lane)
-        last = self.shape.layers - 1
-        outs = [self._head(self._layer_end(last, hs[i], lane, pending[i]), lane) for i, lane in enumerate(lanes)]
-        return torch.cat(outs) if len(outs) > 1 else outs[0]
+                    hs[i] = self._layer_end((u - 1) % L, hs[i], lane, pending[i])
+                    pending[i] = None
+                    if idx == 0:  # the lane's step is complete
+                        cur[i] = self._head(hs[i], lane)
+                if u < steps * L:
+                    if idx == 0:
+                        hs[i] = self._embed(cur[i])
+                    pending[i] = self._layer_begin(idx, hs[i], lane)
+        return torch.cat(cur) if len(cur) > 1 else cur[0]
 
     def _caches(self):
         return [lane.cache for lane in self.lanes]
 
-    def capture(self, tokens: torch.Tensor) -> None:
-        """Capture one decode step, reading and then overwriting a static token buffer, in a HIP
-        graph. The graph's only side streams are the lanes' value-fetch streams, each forked from
-        the capture stream and joined back to it before that lane's next fork. Nothing runs
-        during capture; host counters touched by the traced Python are restored."""
+    def capture(self, tokens: torch.Tensor, steps: int = 1) -> None:
+        """Capture `steps` decode steps (one continuous lane pipeline), reading and then
+        overwriting a static token buffer, in a HIP graph. The graph's only side streams are the
+        lanes' value-fetch and key-rebuild streams, each forked from the capture stream and joined
+        back to it. Nothing runs during capture; host counters touched by the traced Python are
+        restored."""
         self.static_tokens = tokens.clone()
         saved = [(c.gen_offset, c.kv_offset) for c in self._caches()]
         for c in self._caches():
-            c.check_capacity(1)
+            c.check_capacity(steps)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self.static_tokens.copy_(self.decode_step(self.static_tokens))
+            self.static_tokens.copy_(self.decode_steps(self.static_tokens, steps))
         for c, (gen, kv) in zip(self._caches(), saved):
             c.gen_offset, c.kv_offset = gen, kv
         self.graph = g
+        self.graph_steps = steps
 
     def replay(self) -> torch.Tensor:
-        """One captured decode step; returns the static token buffer (next tokens [B, 1])."""
+        """The captured decode steps; returns the static token buffer (the last step's tokens [B, 1])."""
         if self.graph is None:
             raise RuntimeError("capture() a decode step first")
         for c in self._caches():
-            c.check_capacity(1)
+            c.check_capacity(self.graph_steps)
         self.graph.replay()
         for c in self._caches():
-            c.advance(1)
+            c.advance(self.graph_steps)
         return self.static_tokens

@@ -59,6 +59,43 @@ def test_graph_replay_matches_eager(gpu, lanes, chunk_cache):
         assert torch.equal(a, b)
 
 
+
+@pytest.mark.parametrize("lanes,chunk_cache", [(1, None), (2, None), (2, 384)])
+def test_multi_step_graph_matches_eager(gpu, lanes, chunk_cache):
+    """A graph of 3 decode steps (one continuous lane pipeline across the step boundaries)
+    replays like 3 eager steps, twice in a row."""
+    print(f"3-step graph vs eager, lanes={lanes}, chunk_cache={chunk_cache}", flush=True)
+    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    n = 3
+    kw = dict(sparse_budget=2048, decode_len=2 * n + 4, lanes=lanes, seed=12, chunk_cache=chunk_cache)
+    eager = decode_model.SyntheticDecoder(shape, 4, 16384, **kw)
+    graphed = decode_model.SyntheticDecoder(shape, 4, 16384, **kw)
+    tok0 = torch.randint(0, shape.vocab, (4, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(2))
+    te = eager.decode_step(tok0)
+    tg = graphed.decode_step(tok0)
+    torch.cuda.synchronize()
+    assert torch.equal(te, tg)
+    graphed.capture(tg, steps=n)
+    torch.cuda.synchronize()
+    for r in range(2):
+        for _ in range(n):
+            te = eager.decode_step(te)
+        tg = graphed.replay()
+        torch.cuda.synchronize()
+        float(torch.randn(1 << 20, device=gpu).sum())  # unrelated eager work between replays
+        assert torch.equal(te, tg), r
+        for a, b in zip(_state(eager), _state(graphed)):
+            assert torch.equal(a, b), r
+        for le, lg in zip(eager.lanes, graphed.lanes):
+            assert le.cache.gen_offset == lg.cache.gen_offset == 1 + n * (r + 1)
+    # eager multi-step pipelining gives the same tokens and state as single steps
+    te2 = eager.decode_steps(te, 2)
+    tg2 = graphed.decode_step(graphed.decode_step(tg))
+    torch.cuda.synchronize()
+    assert torch.equal(te2, tg2)
+    for a, b in zip(_state(eager), _state(graphed)):
+        assert torch.equal(a, b)
+
 def test_graph_replay_respects_capacity(gpu):
     shape = replace(decode_model.LLAMA31_8B, layers=1, vocab=1000)
     model = decode_model.SyntheticDecoder(shape, 2, 16384, decode_len=2)
