@@ -5,6 +5,9 @@
 // torch.max over the query-head group, torch.topk, the landmark-id gather, and
 // reorder_keys_and_compute_offsets (kernels/gather_copy.cu:189-235).
 //
+// Few rows (rows <= 32, m*n >= 2^15): step 2's probabilities come from the many-workgroup
+// softmax + GQA-max kernel (score.hip) into out_scores first, and this kernel starts from them.
+//
 // One workgroup (16 wave64) per (batch, kv-head) row; thread t owns a contiguous block of
 // landmarks (whole 8-landmark units when n % 8 == 0, so the logits of all m query rows arrive as
 // 16-byte vectors requested together, and keys move as 16-byte vectors):
@@ -12,13 +15,16 @@
 //   2. p_j = max_i bf16(exp(D[i,j] - max_i) / sum_i), kept as 16-bit order keys in LDS (or in
 //      global scratch when n is too large), high-byte histogram with run-length-merged atomics;
 //   3. radix threshold: the k-th key T and the count of keys above it (two histogram passes);
-//   4. winners = keys > T plus the lowest-index keys == T (one block scan ranks the ties); each
-//      winner's chunk id is set in a chunk-id bitmap `sel`, the previous slots' ids in `old`;
+//   4. winners = keys > T plus the lowest-index keys == T (one block scan ranks the ties) are
+//      listed in LDS; then every winner's chunk id is loaded at once and set in a chunk-id bitmap
+//      `sel`, the previous slots' ids in `old`;
 //   5. hits: a scan over the previous slots whose id is in `sel` emits them in old-slot order;
 //      misses: a popcount scan over the words of `sel & ~old` emits them in ascending id order.
 // With out_selected requested, the winners are additionally bitonic-sorted (value desc, index
 // asc) to emit the ids in top-k order. The arithmetic of step 2 and the selection rule are those
 // of score.hip softmax_kernel and topk.hip, so the result is bit-identical to the unfused path.
+#include <cstdlib>
+
 #include "select_core.h"
 
 namespace {
@@ -44,6 +50,7 @@ struct SelectArgs {
   int32_t* offsets;
   int32_t* cnts;
   uint16_t* out_scores;  // [rows][n], required when n_lds == 0
+  int pre;               // out_scores already holds the GQA-max probabilities (split path)
   int64_t* out_sel;      // [rows][S] ids in top-k order, optional
 };
 
@@ -61,7 +68,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint32_t* selmap = reinterpret_cast<uint32_t*>(smem);   // words
   uint32_t* oldmap = selmap + a.words;                     // words
-  uint64_t* sorted = reinterpret_cast<uint64_t*>(oldmap + a.words);  // P, only with out_sel (8-byte aligned)
+  uint64_t* sorted = reinterpret_cast<uint64_t*>(oldmap + a.words);  // P winners (8-byte aligned)
   uint16_t* keys = reinterpret_cast<uint16_t*>(smem + a.keys_off);                   // n_lds, 16-byte aligned
   __shared__ skv::TopkShared sh;
   __shared__ float gmax[kMaxM], ginv[kMaxM];
@@ -75,7 +82,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const int64_t base = static_cast<int64_t>(row) * S;
   int64_t* prow = a.pos + base;
 
-  for (int i = wave; i < m; i += kThreads / 64) {
+  for (int i = wave; i < (a.pre ? 0 : m); i += kThreads / 64) {
     const float* nr = a.norm + (static_cast<int64_t>(row) * m + i) * a.tiles;
     const float* sr = a.sum + (static_cast<int64_t>(row) * m + i) * a.tiles;
     float mx = -INFINITY;
@@ -118,7 +125,55 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
     }
     return skv::f2bf(best);
   };
+  // The keys of this thread's block, 8 at a time where the unit allows: f(j, key) for j in [lo, hi).
+  auto for_keys = [&](auto&& f) {
+    if (a.vec) {
+      for (int u = ulo; u < uhi; ++u) {
+        uint32_t k8[8];
+        if (a.n_lds) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&keys[8 * u]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) k8[e] = half_of(v, e);
+        } else {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&srow[8 * u]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) k8[e] = skv::bf16_order_key(half_of(v, e));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f(8 * u + e, k8[e]);
+      }
+    } else {
+      for (int j = lo; j < hi; ++j) f(j, a.n_lds ? static_cast<uint32_t>(keys[j]) : skv::bf16_order_key(srow[j]));
+    }
+  };
+  // The same keys in any order, for the histogram passes: with the keys in global memory the
+  // workgroup reads the row interleaved (each wave load is 1 KB contiguous) with kB loads per lane
+  // requested before the first is used, so a pass costs a few memory latencies, not one per unit.
+  auto for_keys_any = [&](auto&& f) {
+    if (a.n_lds || !a.vec) {
+      for_keys(f);
+      return;
+    }
+    constexpr int kB = 4;
+    const u32x4* sv = reinterpret_cast<const u32x4*>(srow);
+    for (int u0 = tid; u0 < nu; u0 += kThreads * kB) {
+      u32x4 v[kB];
+#pragma unroll
+      for (int b = 0; b < kB; ++b) v[b] = sv[min(u0 + b * kThreads, nu - 1)];
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        if (u0 + b * kThreads < nu) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f(8 * (u0 + b * kThreads) + e, skv::bf16_order_key(half_of(v[b], e)));
+        }
+      }
+    }
+  };
   {
+    // Fused path: run-length-merged LDS atomics (a thread's consecutive keys often share a bin).
+    // Split path: the keys are read in any order, so counts go to 8 per-thread registers for the
+    // bins [wbase, wbase + 8) around the thread's first key, LDS atomics only outside that window
+    // (softmax outputs crowd into a few adjacent high-byte (exponent) bins).
     uint32_t run_bin = 0xffffffffu, run = 0;
     auto count = [&](uint32_t bin) {
       if (bin != run_bin) {
@@ -128,7 +183,21 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
       }
       ++run;
     };
-    if (a.vec) {
+    uint32_t wc[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    int wbase = -1;
+    auto count_win = [&](uint32_t bin) {
+      if (wbase < 0) wbase = max(0, static_cast<int>(bin) - 3);
+      const uint32_t d = bin - static_cast<uint32_t>(wbase);
+      if (d < 8u) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) wc[k] += d == static_cast<uint32_t>(k);
+      } else {
+        atomicAdd(&sh.hist[bin], 1u);
+      }
+    };
+    if (a.pre) {
+      for_keys_any([&](int, uint32_t kj) { count_win(kj >> 8); });
+    } else if (a.vec) {
       for (int u = ulo; u < uhi; ++u) {
         u32x4 dv[MP];
 #pragma unroll
@@ -169,29 +238,11 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
       }
     }
     if (run) atomicAdd(&sh.hist[run_bin], run);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (wc[k]) atomicAdd(&sh.hist[wbase + k], wc[k]);
   }
   __syncthreads();
-  // The keys of this thread's block, 8 at a time where the unit allows: f(j, key) for j in [lo, hi).
-  auto for_keys = [&](auto&& f) {
-    if (a.vec) {
-      for (int u = ulo; u < uhi; ++u) {
-        uint32_t k8[8];
-        if (a.n_lds) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(&keys[8 * u]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) k8[e] = half_of(v, e);
-        } else {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(&srow[8 * u]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) k8[e] = skv::bf16_order_key(half_of(v, e));
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f(8 * u + e, k8[e]);
-      }
-    } else {
-      for (int j = lo; j < hi; ++j) f(j, a.n_lds ? static_cast<uint32_t>(keys[j]) : skv::bf16_order_key(srow[j]));
-    }
-  };
   skv::select_bin(sh.hist, S, sh.found);
   const uint32_t b1 = static_cast<uint32_t>(sh.found[0]);
   const int above1 = sh.found[1];
@@ -200,7 +251,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   __syncthreads();
   {
     uint32_t run_bin = 0xffffffffu, run = 0;
-    for_keys([&](int, uint32_t kj) {
+    for_keys_any([&](int, uint32_t kj) {
       if ((kj >> 8) != b1) return;
       if ((kj & 255u) != run_bin) {
         if (run) atomicAdd(&sh.hist[run_bin], run);
@@ -225,11 +276,15 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   for_keys([&](int j, uint32_t kj) {
     bool win = kj > T;
     if (kj == T) win = eq_rank++ < need_eq;
-    if (!win) return;
-    const int64_t id = lrow[j];
-    if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
-    if (a.out_sel) sorted[atomicAdd(&sel_count, 1)] = (static_cast<uint64_t>(0xffffu - kj) << 32) | static_cast<uint32_t>(j);
+    if (win) sorted[atomicAdd(&sel_count, 1)] = (static_cast<uint64_t>(0xffffu - kj) << 32) | static_cast<uint32_t>(j);
   });
+  __syncthreads();
+  // The winners' chunk ids into the selection bitmap: every id load of the workgroup in flight
+  // together (exactly S winners).
+  for (int i = tid; i < sel_count; i += kThreads) {
+    const int64_t id = lrow[static_cast<uint32_t>(sorted[i])];
+    if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
+  }
   __syncthreads();
 
   // Hits in previous-slot order.
@@ -287,6 +342,15 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   }
 }
 
+// Split path when the rows are too few to occupy the GPU with one workgroup each and the key
+// computation is long: rows * 8 <= 256 CUs and m*n >= 2^15 (environment SKV_SELECT_SPLIT=0/1
+// forces it off/on, read per call).
+bool use_split(int rows, int m, int n) {
+  const char* e = getenv("SKV_SELECT_SPLIT");
+  if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
+  return rows <= 32 && static_cast<int64_t>(m) * n >= (int64_t{1} << 15);
+}
+
 }  // namespace
 
 extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
@@ -311,12 +375,16 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
   int P = 64;
   while (P < select_sets) P <<= 1;
   const int words = (num_chunks + 31) / 32;
-  const size_t fixed = (static_cast<size_t>(words) * 8 + (out_selected ? static_cast<size_t>(P) * 8 : 0) + 15) / 16 * 16;
+  const size_t fixed = (static_cast<size_t>(words) * 8 + static_cast<size_t>(P) * 8 + 15) / 16 * 16;
   if (fixed > kLdsBudget) {
     skv_set_error("%s: %d chunks need %zu bytes of bitmap, above the LDS budget", what, num_chunks, fixed);
     return SKV_EUNSUPPORTED;
   }
-  const int n_lds = (fixed + static_cast<size_t>(n) * 2 <= kLdsBudget) ? n : 0;
+  // Few rows: the per-row key computation (m*n exponentials) would run on as many workgroups as
+  // rows, so it moves to the many-workgroup softmax + GQA-max kernel, which writes the keys
+  // (bit-identical) into out_scores; the selection kernel then starts from them.
+  const bool split = out_scores && use_split(rows, m, n);
+  const int n_lds = (!split && fixed + static_cast<size_t>(n) * 2 <= kLdsBudget) ? n : 0;
   if (!n_lds && !out_scores) {
     skv_set_error("%s: n=%d landmarks do not fit LDS; pass out_scores as staging", what, n);
     return SKV_EINVAL;
@@ -342,9 +410,14 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
   a.cnts = cnts;
   a.out_scores = out_scores;
   a.out_sel = out_selected;
+  a.pre = split ? 1 : 0;
   const size_t lds = fixed + static_cast<size_t>(n_lds) * 2;
   const size_t ldsb = (lds + 15) / 16 * 16;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (split) {
+    const int rc = skv_softmax_gqa_max(D, norm, sum, nullptr, out_scores, rows, m, n, stream);
+    if (rc) return rc;
+  }
   if (m <= 4) hipLaunchKernelGGL(select_kernel<4>, dim3(rows), dim3(kThreads), ldsb, st, a);
   else if (m <= 8) hipLaunchKernelGGL(select_kernel<8>, dim3(rows), dim3(kThreads), ldsb, st, a);
   else hipLaunchKernelGGL(select_kernel<16>, dim3(rows), dim3(kThreads), ldsb, st, a);

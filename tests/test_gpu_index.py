@@ -157,10 +157,14 @@ def test_topk_gather_bit_exact(gpu, n, k, ties):
     assert torch.equal(out.cpu(), want)
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
 @pytest.mark.parametrize("rows,m,n,S", [(64, 4, 15304, 256), (8, 16, 32712, 256), (8, 4, 130680, 2048),
                                         (8, 4, 968, 256), (2, 1, 300, 7)])
-def test_select_chunks_fused_equals_unfused(gpu, rows, m, n, S):
-    _say(f"select_chunks rows={rows} m={m} n={n} S={S}")
+def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, split):
+    """The fused selection (keys computed per row in the selection kernel, or, on the split path,
+    by the many-workgroup softmax + GQA-max kernel first) equals the unfused sequence."""
+    monkeypatch.setenv("SKV_SELECT_SPLIT", split)
+    _say(f"select_chunks rows={rows} m={m} n={n} S={S} split={split}")
     g = torch.Generator().manual_seed(rows * n + S)
     q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
     L = torch.randn(rows, n, 128, generator=g).to(torch.bfloat16).to(gpu)
