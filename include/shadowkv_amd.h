@@ -193,10 +193,14 @@ int skv_topk_gather(const uint16_t* scores, int64_t score_stride, const int64_t*
  * Replaces models/kvcache/shadow.py:553-574 after the scoring GEMM. D/norm/sum as produced by
  * skv_score_logits for `rows` batch entries of m query rows; landmark_idx rows of idx_stride;
  * position_ids/offsets [rows][select_sets]; cnts [rows]. Chunk ids (landmark ids and previous
- * slot ids) must lie in [0, num_chunks) (-1 marks an empty previous slot); num_chunks <= 245760.
+ * slot ids) must lie in [0, num_chunks) (-1 marks an empty previous slot); num_chunks <= 237568
+ * at select_sets <= 256 and <= 180224 at 2048 (two chunk bitmaps and the winner list in LDS).
  * out_scores ([rows][n] bf16 GQA-max probabilities) and out_selected ([rows][select_sets] ids in
  * top-k order) are optional, except that out_scores is required as staging when n is too large
- * for LDS. select_sets <= 2048. */
+ * for LDS. With out_scores given and few rows (rows <= 32, m*n >= 32768) the probabilities are
+ * first computed by the many-workgroup softmax kernel (as skv_softmax_gqa_max, a second launch on
+ * the same stream) and the selection starts from them; results are identical.
+ * select_sets <= 2048. */
 int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
                       const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
                       int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,

@@ -393,7 +393,8 @@ def softmax_gqa_max(D, Norm, Sum, out, batch_count, m, n, softmax=None):
 
 def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunks, position_ids, offsets, cnts,
                   out_scores=None, out_selected=None):
-    """Fused softmax + GQA max + top-k + id gather + reorder (one launch, one workgroup per row).
+    """Fused softmax + GQA max + top-k + id gather + reorder (one workgroup per row; for few rows
+    the softmax + GQA max runs first on many workgroups into out_scores, a second launch).
 
     D/Norm/Sum: outputs of score_logits for `rows` entries of m query rows; landmark_idx: [rows, n]
     view with contiguous rows, chunk ids in [0, num_chunks); position_ids: [rows, select_sets] int64
