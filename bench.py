@@ -106,10 +106,10 @@ def logits_bytes(BH: int, G: int, n: int, D: int = 128) -> int:
 
 
 def scoring_launch_ms(model, rounds: int = 4):
-    """Average duration of the landmark-scoring kernel on the live decode state: HIP events on its
-    stream around back-to-back launches over every layer's landmarks (the queue stays full, so the
-    events bracket kernel time, not host launch latency). A captured step cannot carry event-record
-    nodes here (torch refuses them on ROCm), so this runs right after the timed replays."""
+    """Average duration of the landmark-scoring kernel on the live decode state: one launch per
+    layer over that layer's landmarks, the 32 launches captured in a HIP graph and replayed
+    `rounds` times between HIP events (no host launch cost in the figure; the events bracket the
+    replays on the stream the kernels run on). Runs right after the timed decode steps."""
     import torch
     from shadowkv_amd.kernels import shadowkv
 
@@ -119,21 +119,15 @@ def scoring_launch_ms(model, rounds: int = 4):
     q = torch.randn(B, H * G, 1, D, device=cache.device).to(torch.bfloat16)
     L = cache.num_layers
 
-    def launch_all():
-        for layer in range(L):
-            shadowkv.score_logits(q, cache.k_landmark[layer], cache.gemm_o, cache.norm, cache.sum, B * H, G, n, D,
-                                  1.0 / math.sqrt(128))
+    def launch(i):
+        layer = i % L
+        shadowkv.score_logits(q, cache.k_landmark[layer], cache.gemm_o, cache.norm, cache.sum, B * H, G, n, D,
+                              1.0 / math.sqrt(128))
 
-    launch_all()  # warm
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(rounds):
-        launch_all()
-    e.record()
-    e.synchronize()
-    return (s.elapsed_time(e) / (rounds * L),
-            f"HIP events around {rounds * L} back-to-back launches on every layer's live landmarks, "
-            f"after the timed steps")
+    t = gpu_time_per_call(launch, L, rounds)
+    return (t * 1e3,
+            f"HIP events around {rounds} replays of a HIP graph of {L} back-to-back launches (one per layer, "
+            f"on that layer's live landmarks), after the timed steps")
 
 
 def cpu_baseline(model, runs: int) -> dict:
