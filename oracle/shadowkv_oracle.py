@@ -254,9 +254,18 @@ class LayerState:
 
 
 def _rope_tokens(x: torch.Tensor, cos_sin: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-    """x [B, H, L, D] RoPE by token position pos [L] (reference model RoPE, half-split)."""
-    half = x.shape[-1] // 2
+    """x [B, H, L, D] RoPE by token position pos [L]: half-split with a [cos|sin] table of width D
+    (models/llama.py:149-154), or, with a width-64 table, GLM's interleaved pairs (2i, 2i+1) of
+    dims 0..63 and dims 64.. passed through (models/glm.py:212-235)."""
     cs = cos_sin[pos]
+    if cos_sin.shape[-1] == 64:
+        co, si = cs[:, :32], cs[:, 32:]
+        xe, xo = x[..., 0:64:2], x[..., 1:64:2]
+        y = x.clone()
+        y[..., 0:64:2] = (xe * co) - (xo * si)
+        y[..., 1:64:2] = (xo * co) + (xe * si)
+        return y
+    half = x.shape[-1] // 2
     return rope_half_split(x, cs[:, :half], cs[:, half:])
 
 
@@ -359,8 +368,9 @@ def decode_layer_step(st: LayerState, q: torch.Tensor, k_new: torch.Tensor, v_ne
     st.kbuf[:, :, st.sparse_start:st.sparse_end] = torch.from_numpy(kcomp).view(torch.bfloat16).reshape(
         B, H, S * st.chunk, D)
     st.position_ids = torch.from_numpy(ids).view(B, H, S)
+    # RoPE flavour by table width, as the reference's dispatch (models/tensor_op.py:176-204)
     rebuild_k_rope(st.U, st.SV, st.position_ids, torch.from_numpy(cnts), cos_sin, st.chunk, st.kbuf,
-                   st.sparse_start)
+                   st.sparse_start, glm=cos_sin.shape[-1] == 64)
     out = sparse_attention(q, st.kbuf, st.vbuf, L)
     return dict(scores=scores.view(B, H, n), selected=selected.view(B, H, S), cnts=cnts, offsets=offs, out=out, L=L)
 
@@ -469,7 +479,7 @@ def decode_layer_step_pooled(st: LayerState, pool: dict, q, k_new, v_new, cos_si
     # then moved to their slots; values from the host store
     scratch = torch.zeros(B, H, S * c, D, dtype=kbuf.dtype)
     ids = torch.from_numpy(miss_ids.astype(np.int64)).view(B, H, S)
-    rebuild_k_rope(st.U, st.SV, ids, torch.from_numpy(cnts), cos_sin, c, scratch, 0)
+    rebuild_k_rope(st.U, st.SV, ids, torch.from_numpy(cnts), cos_sin, c, scratch, 0, glm=cos_sin.shape[-1] == 64)
     for r in range(rows):
         b, h = divmod(r, H)
         for i in range(int(cnts[r]), S):

@@ -95,22 +95,23 @@ def write_kat():
                         expected_cnts=cnts.astype(np.int16))
 
 
-def decode_small_case(chunk=8):
+def decode_small_case(chunk=8, glm=False):
     """Seeded inputs of the small decode fixture and the oracle's results (deterministic). The
-    committed fixture is the chunk-8 case; other chunk sizes give the same prompt tensors."""
+    committed fixture is the chunk-8 case; other chunk sizes give the same prompt tensors. glm:
+    the GLM-4-9B head layout (2 kv heads of 16 query heads) with GLM's interleaved RoPE table."""
     sys.path.insert(0, str(HERE.parents[1]))
     import torch
     import oracle
 
     g = torch.Generator().manual_seed(1234)
-    B, H, G, D, ctx, rank, budget = 1, 2, 4, 128, 2048, 32, 1024
+    B, H, G, D, ctx, rank, budget = 1, 2, (16 if glm else 4), 128, 2048, 32, 1024
     A = torch.randn(ctx, rank, generator=g) / rank ** 0.5
     Bm = torch.randn(rank, H * D, generator=g) / rank ** 0.5
     k_pre = (A @ Bm + 0.05 * torch.randn(ctx, H * D, generator=g)).view(1, ctx, H, D).transpose(1, 2)
     k_pre = k_pre.to(torch.bfloat16).contiguous()
     v = torch.randn(B, H, ctx, D, generator=g).to(torch.bfloat16)
     q_last = torch.randn(B, H * G, 1, D, generator=g).to(torch.bfloat16)
-    cos_sin = oracle.build_cos_sin_cache(ctx + 64, 500000.0)
+    cos_sin = oracle.build_glm_cos_sin_cache(ctx + 64, 10000.0) if glm else oracle.build_cos_sin_cache(ctx + 64, 500000.0)
     st = oracle.encode_layer(k_pre, v, q_last, cos_sin, rank=rank, chunk=chunk, budget=budget)
     q = torch.randn(B, H * G, D, generator=g).to(torch.bfloat16)
     k_new = torch.randn(B, H, D, generator=g).to(torch.bfloat16)

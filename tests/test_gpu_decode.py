@@ -39,12 +39,19 @@ def test_single_layer_decode_step(gpu):
         assert np.array_equal(got["position_ids"], d["out_position_ids"])
 
 
-@pytest.mark.parametrize("device_lengths,chunk", [(False, 8), (True, 8), (True, 4), (True, 16), (False, 16)])
-def test_multi_layer_multi_step_decode(gpu, device_lengths, chunk):
+@pytest.mark.parametrize("device_lengths,chunk,split,glm", [(False, 8, None, False), (True, 8, None, False),
+                                                           (True, 4, None, False), (True, 16, None, False),
+                                                           (False, 16, None, False), (True, 8, "1", False),
+                                                           (True, 8, None, True), (False, 16, "1", True)])
+def test_multi_layer_multi_step_decode(gpu, monkeypatch, device_lengths, chunk, split, glm):
     """Also chunk sizes other than 8 (budget 1024: 256 selected chunks of 4 rows, 64 of 16 rows)
-    through every kernel of the step."""
-    print(f"decode small fixture, 2 layers x 4 steps, device_lengths={device_lengths}, chunk={chunk}", flush=True)
-    case = make_golden.decode_small_case(chunk)
+    through every kernel of the step, the selection's few-row split path forced on, and the
+    GLM-4-9B head layout (16 query heads per kv head) with GLM's interleaved RoPE table."""
+    if split is not None:
+        monkeypatch.setenv("SKV_SELECT_SPLIT", split)
+    print(f"decode small fixture, 2 layers x 4 steps, device_lengths={device_lengths}, chunk={chunk}, split={split}, "
+          f"glm={glm}", flush=True)
+    case = make_golden.decode_small_case(chunk, glm=glm)
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
     steps, layers = 4, 2

@@ -224,3 +224,19 @@ def test_encode_layer_overrides_reproduce_the_default_path():
         a, bsel = set(st.position_ids[b, h].tolist()), set(st2.position_ids[b, h].tolist())
         assert all(score_of[i] == kth for i in a ^ bsel), r
         assert {i for i, v in score_of.items() if v > kth} <= a & bsel
+
+
+def test_glm_token_rope_matches_glm_push():
+    """The oracle's token RoPE with a GLM (width-64) table equals its GLM cache push (pinned against
+    an independent numpy restatement above) row for row, and position 0 is the identity."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 2, 16, 128, generator=g).to(torch.bfloat16)
+    cs = oracle.build_glm_cos_sin_cache(64, 10000.0)
+    from oracle import shadowkv_oracle
+    got = shadowkv_oracle._rope_tokens(x, cs, torch.arange(16))
+    cache = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
+    ids = torch.arange(16).view(1, 1, 16).expand(1, 2, 16).contiguous()
+    oracle.rope_push_glm(x, cs, ids, torch.zeros(2, dtype=torch.int32), 1, cache, 0, 16)
+    assert torch.equal(got, cache)
+    assert torch.equal(got[:, :, 0], x[:, :, 0])
+    assert torch.equal(got[..., 64:], x[..., 64:])
