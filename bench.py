@@ -397,7 +397,7 @@ def select_microbench(args) -> int:
 
     reps = max(args.steps, 4)
     for name, B, H, G, n, S in (("Llama-3-8B 122K", 8, 8, 4, 15304, 256), ("Llama-3-8B 122K", 24, 8, 4, 15304, 256),
-                                ("Llama-3-8B 122K", 1, 8, 4, 15304, 256),
+                                ("Llama-3-8B 122K", 4, 8, 4, 15304, 256), ("Llama-3-8B 122K", 1, 8, 4, 15304, 256),
                                 ("GLM-4-9B 262K", 4, 2, 16, 32712, 256), ("Llama-3-8B-1M", 1, 8, 4, 130680, 2048)):
         g = torch.Generator(device="cuda").manual_seed(n + B)
         rows = B * H
@@ -416,15 +416,18 @@ def select_microbench(args) -> int:
         offsets = torch.empty(rows * S, dtype=torch.int32, device="cuda")
         cnts = torch.empty(rows, dtype=torch.int32, device="cuda")
         scores = torch.empty(rows, n, dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device="cuda")
 
         def run(_):
             pos.copy_(pos0)
-            shadowkv.select_chunks(D, norm, ssum, rows, G, n, lidx, S, chunks, pos, offsets, cnts, out_scores=scores)
+            shadowkv.select_chunks(D, norm, ssum, rows, G, n, lidx, S, chunks, pos, offsets, cnts, out_scores=scores,
+                                   workspace=ws)
 
         t_all = gpu_time_per_call(run, reps)
         t_copy = gpu_time_per_call(lambda _: pos.copy_(pos0), reps)
         env = os.environ.get("SKV_SELECT_SPLIT")
-        split = env == "1" if env in ("0", "1") else (rows <= 32 and G * n >= 1 << 15)
+        few = rows <= 32 and G * n >= 1 << 15
+        path = {"0": "fused", "1": "split", "2": "parts"}.get(env, ("parts" if n >= 65536 else "split") if few else "fused")
         t = t_all - t_copy
         out_line = {"metric": "fused chunk selection latency", "value": round(t * 1e6, 2), "unit": "us",
                     "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(t * 1e3, 4),
@@ -433,7 +436,10 @@ def select_microbench(args) -> int:
                             "replays (minus the replayed slot-restore copy)",
                     "config": {"workload": f"{name} selection: {rows} rows x {G} queries x {n} landmarks, top {S}",
                                "rows": rows, "m": G, "n": n, "select_sets": S},
-                    "roofline": {"kernel": "select_kernel" + (" (after softmax_kernel: split path)" if split else ""),
+                    "roofline": {"kernel": {"fused": "select_kernel",
+                                            "split": "softmax_kernel + select_kernel (keys on many workgroups)",
+                                            "parts": "softmax_kernel + part_*_kernel + select_finish_kernel "
+                                                     "(many workgroups per row)"}[path],
                                  "bound": "latency", "achieved": None, "peak": None,
                                  "unit": "us", "frac": None, "traffic": None,
                                  "algorithmic_bytes_per_launch": rows * (G * n * 2 + n * 8 + S * 28),

@@ -206,6 +206,23 @@ int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, in
                       int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
                       int64_t* out_selected, void* stream);
 
+/* Bytes of the workspace skv_select_chunks_ws needs for `rows` rows of n landmarks and
+ * select_sets winners (0 for invalid arguments). */
+int64_t skv_select_workspace_bytes(int rows, int n, int select_sets);
+
+/* skv_select_chunks with a caller-owned device workspace (skv_select_workspace_bytes; no
+ * initialisation needed; calls that overlap on one workspace race). With out_scores given and few
+ * rows (rows <= 32, m*n >= 32768) each row's selection is spread over many workgroups: the
+ * softmax kernel writes the keys, then per-slice histograms of the high and low key bytes, the
+ * per-slice counts above and at the threshold, the winners at their rank positions, and one
+ * workgroup per row for the id bitmap and the reorder (six launches on the stream). Otherwise it
+ * behaves as skv_select_chunks. Results are identical. Variant of skv_select_chunks (same
+ * reference lines: models/kvcache/shadow.py:553-574). */
+int skv_select_chunks_ws(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                         const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
+                         int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
+                         int64_t* out_selected, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- a8: sparse decode attention ----------------------------------------------------------------
  * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, causal=True) for one query token
  * (models/attention/shadow.py:48): for b, query head hq, kv head h = hq / (q_heads/kv_heads):

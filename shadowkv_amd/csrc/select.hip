@@ -23,6 +23,7 @@
 // With out_selected requested, the winners are additionally bitonic-sorted (value desc, index
 // asc) to emit the ids in top-k order. The arithmetic of step 2 and the selection rule are those
 // of score.hip softmax_kernel and topk.hip, so the result is bit-identical to the unfused path.
+#include <algorithm>
 #include <cstdlib>
 
 #include "select_core.h"
@@ -61,6 +62,56 @@ __device__ __forceinline__ int scan_excl(int v, int* scratch, int* total) {
 __device__ __forceinline__ uint16_t half_of(const u32x4& v, int e) {
   const uint32_t w = v[e >> 1];
   return static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// Hits in previous-slot order, then misses in ascending id order, from the selection bitmap
+// `selmap` (every winner's chunk id) and `oldmap` (the previous slots' ids), both in LDS:
+// prow[0, S) and offs[0, S) rewritten in place, *cnt = number of hits (the reorder of
+// kernels/map.cuh:475-516). Called by every thread of a kThreads workgroup.
+__device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* oldmap, int words, int64_t* prow,
+                                     int32_t* offs, int32_t* cnt, int S, int* scan) {
+  const int tid = threadIdx.x;
+  const int Es = (S + kThreads - 1) / kThreads;
+  const int slo = min(tid * Es, S), shi = min(slo + Es, S);
+  int my_hits = 0;
+  for (int j = slo; j < shi; ++j) {
+    const int64_t id = prow[j];
+    my_hits += id >= 0 && id < 32ll * words && ((selmap[id >> 5] >> (id & 31)) & 1u);
+  }
+  const int Ew = (words + kThreads - 1) / kThreads;
+  const int wlo = min(tid * Ew, words), whi = min(wlo + Ew, words);
+  int my_miss = 0;
+  for (int w = wlo; w < whi; ++w) my_miss += __popc(selmap[w] & ~oldmap[w]);
+  int total_hits = 0, total_miss = 0;
+  int hrank = scan_excl(my_hits, scan, &total_hits);
+  int mrank = scan_excl(my_miss, scan, &total_miss);
+  // All previous-slot ids were read above (scan barriers separate reads from these writes).
+  int64_t hit_ids[kMaxS / kThreads + 1];
+  int nh = 0;
+  for (int j = slo; j < shi; ++j) {
+    const int64_t id = prow[j];
+    if (id >= 0 && id < 32ll * words && ((selmap[id >> 5] >> (id & 31)) & 1u)) hit_ids[nh++] = id | (static_cast<int64_t>(j) << 40);
+  }
+  __syncthreads();
+  for (int h = 0; h < nh; ++h) {
+    const int64_t id = hit_ids[h] & ((1ll << 40) - 1);
+    const int j = static_cast<int>(hit_ids[h] >> 40);
+    prow[hrank] = id;
+    offs[hrank] = j;
+    ++hrank;
+  }
+  for (int w = wlo; w < whi; ++w) {
+    uint32_t bits = selmap[w] & ~oldmap[w];
+    while (bits) {
+      const int b = __ffs(bits) - 1;
+      bits &= bits - 1;
+      const int id = w * 32 + b;
+      prow[total_hits + mrank] = id;
+      offs[total_hits + mrank] = id;
+      ++mrank;
+    }
+  }
+  if (tid == 0) *cnt = total_hits;
 }
 
 template <int MP>
@@ -287,49 +338,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   }
   __syncthreads();
 
-  // Hits in previous-slot order.
-  const int Es = (S + kThreads - 1) / kThreads;
-  const int slo = min(tid * Es, S), shi = min(slo + Es, S);
-  int my_hits = 0;
-  for (int j = slo; j < shi; ++j) {
-    const int64_t id = prow[j];
-    my_hits += id >= 0 && id < 32ll * a.words && ((selmap[id >> 5] >> (id & 31)) & 1u);
-  }
-  // Misses in ascending id order.
-  const int Ew = (a.words + kThreads - 1) / kThreads;
-  const int wlo = min(tid * Ew, a.words), whi = min(wlo + Ew, a.words);
-  int my_miss = 0;
-  for (int w = wlo; w < whi; ++w) my_miss += __popc(selmap[w] & ~oldmap[w]);
-  int total_hits = 0, total_miss = 0;
-  int hrank = scan_excl(my_hits, sh.scan, &total_hits);
-  int mrank = scan_excl(my_miss, sh.scan, &total_miss);
-  // All previous-slot ids were read above (scan barriers separate reads from these writes).
-  int64_t hit_ids[kMaxS / kThreads + 1];
-  int nh = 0;
-  for (int j = slo; j < shi; ++j) {
-    const int64_t id = prow[j];
-    if (id >= 0 && id < 32ll * a.words && ((selmap[id >> 5] >> (id & 31)) & 1u)) hit_ids[nh++] = id | (static_cast<int64_t>(j) << 40);
-  }
-  __syncthreads();
-  for (int h = 0; h < nh; ++h) {
-    const int64_t id = hit_ids[h] & ((1ll << 40) - 1);
-    const int j = static_cast<int>(hit_ids[h] >> 40);
-    prow[hrank] = id;
-    a.offsets[base + hrank] = j;
-    ++hrank;
-  }
-  for (int w = wlo; w < whi; ++w) {
-    uint32_t bits = selmap[w] & ~oldmap[w];
-    while (bits) {
-      const int b = __ffs(bits) - 1;
-      bits &= bits - 1;
-      const int id = w * 32 + b;
-      prow[total_hits + mrank] = id;
-      a.offsets[base + total_hits + mrank] = id;
-      ++mrank;
-    }
-  }
-  if (tid == 0) a.cnts[row] = total_hits;
+  reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan);
 
   if (a.out_sel) {
     for (int i = S + tid; i < a.P; i += kThreads) sorted[i] = ~0ull;
@@ -342,22 +351,324 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   }
 }
 
-// Split path when the rows are too few to occupy the GPU with one workgroup each and the key
-// computation is long: rows * 8 <= 256 CUs and m*n >= 2^15 (environment SKV_SELECT_SPLIT=0/1
-// forces it off/on, read per call).
-bool use_split(int rows, int m, int n) {
-  const char* e = getenv("SKV_SELECT_SPLIT");
-  if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
-  return rows <= 32 && static_cast<int64_t>(m) * n >= (int64_t{1} << 15);
+// ---------------------------------------------------------------------------------------------
+// Few rows over many workgroups (skv_select_chunks_ws): after the softmax kernel has written the
+// GQA-max probabilities (keys) of every row, each row is cut into `parts` slices of part_len keys,
+// one workgroup per (slice, row):
+//   part_hist_kernel<1>: high-byte histogram of the slice            -> h1[row][part][256]
+//   part_hist_kernel<2>: bin b1 of the S-th largest key from sum(h1); low-byte histogram of the
+//                        slice's keys in bin b1                      -> h2[row][part][256]
+//   part_count_kernel:   threshold T (S-th largest key) from sum(h1), sum(h2); the slice's counts
+//                        of keys > T and == T                        -> cnt[row][part]
+//   part_emit_kernel:    the slice's winners (keys > T, and keys == T ranked by index among all
+//                        ties, the lowest need_eq indices winning) at their rank positions
+//                                                                    -> win[row][0, S)
+//   select_finish_kernel (one workgroup per row): winners' chunk ids into the selection bitmap,
+//                        the reorder, and the top-k order when requested.
+// The selection rule, key order and outputs are those of select_kernel (bit-identical).
+constexpr int kPartThreads = 256;
+constexpr int kMaxPartLen = 4096;  // 16 keys per thread in part_emit_kernel
+
+struct PartArgs {
+  const uint16_t* scores;  // [rows][n] bf16 GQA-max probabilities
+  int n, S, parts, part_len;
+  uint32_t* h1;   // [rows][parts][256]
+  uint32_t* h2;   // [rows][parts][256]
+  int32_t* cnt;   // [rows][parts][2]: keys > T, keys == T
+  int32_t* thr;   // [rows][4]: T, keys > T over the row, ties that win
+  uint64_t* win;  // [rows][S]: (0xffff - key) << 32 | landmark index
+};
+
+// Sums the rows' partial histograms h[parts][256] into tot and finds the bin of the want-th
+// largest key: out[0] = bin, out[1] = keys in higher bins. Thread t adds bins [4(t%64), +4) of
+// parts t/64, t/64 + 4, ... with 16-byte loads, 16 requested before the first is used; the four
+// part groups meet in LDS (part_tot). Every thread of the kPartThreads workgroup calls it.
+__device__ void sum_select(const uint32_t* h, int parts, int want, uint32_t* tot, uint32_t (*part_tot)[256],
+                           int* out) {
+  const int quad = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int q0 = grp; q0 < parts; q0 += 64) {
+    u32x4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int q = min(q0 + 4 * u, parts - 1);
+      v[u] = *reinterpret_cast<const u32x4*>(&h[q * 256 + 4 * quad]);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (q0 + 4 * u < parts) acc += v[u];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) part_tot[grp][4 * quad + e] = acc[e];
+  __syncthreads();
+  for (int b = threadIdx.x; b < 256; b += blockDim.x)
+    tot[b] = (part_tot[0][b] + part_tot[1][b]) + (part_tot[2][b] + part_tot[3][b]);
+  __syncthreads();
+  skv::select_bin(tot, want, out);
 }
 
-}  // namespace
+constexpr int kPartE = kMaxPartLen / kPartThreads;  // keys per thread, at most
 
-extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
-                                 const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
-                                 int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
-                                 int64_t* out_selected, void* stream) {
-  const char* what = "select_chunks";
+// This thread's block of the slice: keys [lo, lo + E) of the row (blocked ownership, index order),
+// all requested before the first is used; entries past the slice are marked invalid (valid bit).
+__device__ __forceinline__ void load_part_keys(const PartArgs& a, int row, int part, uint32_t (&kv)[kPartE],
+                                               uint32_t* valid, int* lo_out) {
+  const int j0 = part * a.part_len, j1 = min(a.n, j0 + a.part_len);
+  const int E = (a.part_len + kPartThreads - 1) / kPartThreads;
+  const int lo = min(j1, j0 + static_cast<int>(threadIdx.x) * E), hi = min(j1, lo + E);
+  const uint16_t* sr = a.scores + static_cast<int64_t>(row) * a.n;
+  uint32_t v = 0;
+#pragma unroll
+  for (int u = 0; u < kPartE; ++u) {
+    const bool ok = u < E && lo + u < hi;
+    kv[u] = skv::bf16_order_key(sr[ok ? lo + u : 0]);
+    v |= static_cast<uint32_t>(ok) << u;
+  }
+  *valid = v;
+  *lo_out = lo;
+}
+
+template <int kPass>
+__global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t tot[256];
+  __shared__ uint32_t part_tot[kPartThreads / 64][256];
+  __shared__ int found[2];
+  const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  for (int b = tid; b < 256; b += kPartThreads) hist[b] = 0;
+  uint32_t b1 = 0;
+  if (kPass == 2) {
+    sum_select(a.h1 + static_cast<int64_t>(row) * a.parts * 256, a.parts, a.S, tot, part_tot, found);
+    b1 = static_cast<uint32_t>(found[0]);
+  } else {
+    __syncthreads();
+  }
+  uint32_t kv[kPartE], valid;
+  int lo;
+  load_part_keys(a, row, part, kv, &valid, &lo);
+  // Pass 1 counts in 8 per-thread registers around the thread's first bin (keys crowd into a few
+  // adjacent high-byte bins), LDS atomics outside that window; pass 2 spreads over 256 bins.
+  uint32_t wc[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  int wbase = -1;
+#pragma unroll
+  for (int u = 0; u < kPartE; ++u) {
+    if (!((valid >> u) & 1u)) continue;
+    const uint32_t k = kv[u];
+    if (kPass == 1) {
+      const uint32_t bin = k >> 8;
+      if (wbase < 0) wbase = max(0, static_cast<int>(bin) - 3);
+      const uint32_t d = bin - static_cast<uint32_t>(wbase);
+      if (d < 8u) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wc[q] += d == static_cast<uint32_t>(q);
+      } else {
+        atomicAdd(&hist[bin], 1u);
+      }
+    } else if ((k >> 8) == b1) {
+      atomicAdd(&hist[k & 255u], 1u);
+    }
+  }
+  if (kPass == 1) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (wc[q]) atomicAdd(&hist[wbase + q], wc[q]);
+  }
+  __syncthreads();
+  uint32_t* out = (kPass == 1 ? a.h1 : a.h2) + (static_cast<int64_t>(row) * a.parts + part) * 256;
+  for (int b = tid; b < 256; b += kPartThreads) out[b] = hist[b];
+}
+
+// T, keys > T over the row (c_gt) and the ties that win (need_eq), from the summed histograms.
+__device__ void row_threshold(const PartArgs& a, int row, uint32_t* tot, uint32_t (*part_tot)[256], int* found,
+                              uint32_t* T, int* c_gt, int* need_eq) {
+  sum_select(a.h1 + static_cast<int64_t>(row) * a.parts * 256, a.parts, a.S, tot, part_tot, found);
+  const uint32_t b1 = static_cast<uint32_t>(found[0]);
+  const int above1 = found[1];
+  __syncthreads();  // tot and found are rewritten below
+  sum_select(a.h2 + static_cast<int64_t>(row) * a.parts * 256, a.parts, a.S - above1, tot, part_tot, found);
+  *T = (b1 << 8) | static_cast<uint32_t>(found[0]);
+  *c_gt = above1 + found[1];
+  *need_eq = a.S - *c_gt;
+}
+
+__global__ void __launch_bounds__(kPartThreads) part_count_kernel(PartArgs a) {
+  __shared__ uint32_t tot[256];
+  __shared__ uint32_t part_tot[kPartThreads / 64][256];
+  __shared__ int found[2];
+  __shared__ int scan[kPartThreads / 64 + 1];
+  const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  uint32_t T;
+  int c_gt, need_eq;
+  row_threshold(a, row, tot, part_tot, found, &T, &c_gt, &need_eq);
+  uint32_t kv[kPartE], valid;
+  int lo;
+  load_part_keys(a, row, part, kv, &valid, &lo);
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int u = 0; u < kPartE; ++u) {
+    const bool ok = (valid >> u) & 1u;
+    gt += ok && kv[u] > T;
+    eq += ok && kv[u] == T;
+  }
+  int gt_total, eq_total;
+  skv::block_exclusive_scan(gt, scan, &gt_total);
+  skv::block_exclusive_scan(eq, scan, &eq_total);
+  if (tid == 0) {
+    int32_t* c = a.cnt + (static_cast<int64_t>(row) * a.parts + part) * 2;
+    c[0] = gt_total;
+    c[1] = eq_total;
+    if (part == 0) {
+      int32_t* t = a.thr + static_cast<int64_t>(row) * 4;
+      t[0] = static_cast<int32_t>(T);
+      t[1] = c_gt;
+      t[2] = need_eq;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kPartThreads) part_emit_kernel(PartArgs a) {
+  __shared__ int scan[kPartThreads / 64 + 1];
+  __shared__ int bases[2];
+  const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int32_t* t = a.thr + static_cast<int64_t>(row) * 4;
+  const uint32_t T = static_cast<uint32_t>(t[0]);
+  const int c_gt = t[1], need_eq = t[2];
+  if (tid < 64) {  // this slice's first ranks: the counts of the slices before it
+    const int32_t* c = a.cnt + static_cast<int64_t>(row) * a.parts * 2;
+    int g = 0, e = 0;
+    for (int q = tid; q < part; q += 64) {
+      g += c[2 * q];
+      e += c[2 * q + 1];
+    }
+    g = __builtin_amdgcn_readlane(skv::wave_inclusive_scan(g), 63);
+    e = __builtin_amdgcn_readlane(skv::wave_inclusive_scan(e), 63);
+    if (tid == 0) {
+      bases[0] = g;
+      bases[1] = e;
+    }
+  }
+  // Blocked ownership: thread t holds keys [lo, lo + E) of the slice in index order.
+  uint32_t kv[kPartE], valid;
+  int lo;
+  load_part_keys(a, row, part, kv, &valid, &lo);
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int u = 0; u < kPartE; ++u) {
+    const bool ok = (valid >> u) & 1u;
+    gt += ok && kv[u] > T;
+    eq += ok && kv[u] == T;
+  }
+  int gt_total, eq_total;
+  int gr = skv::block_exclusive_scan(gt, scan, &gt_total);
+  int er = skv::block_exclusive_scan(eq, scan, &eq_total);
+  gr += bases[0];
+  er += bases[1];
+  uint64_t* w = a.win + static_cast<int64_t>(row) * a.S;
+#pragma unroll
+  for (int u = 0; u < kPartE; ++u) {
+    const int j = lo + u;
+    if (!((valid >> u) & 1u)) continue;
+    const uint64_t comp = (static_cast<uint64_t>(0xffffu - kv[u]) << 32) | static_cast<uint32_t>(j);
+    if (kv[u] > T) {
+      if (gr < a.S) w[gr] = comp;  // gr < c_gt <= S by construction; the guard keeps a bad count in bounds
+      ++gr;
+    } else if (kv[u] == T) {
+      if (er < need_eq && c_gt + er < a.S) w[c_gt + er] = comp;
+      ++er;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) select_finish_kernel(SelectArgs a, PartArgs pa) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* selmap = reinterpret_cast<uint32_t*>(smem);
+  uint32_t* oldmap = selmap + a.words;
+  uint64_t* sorted = reinterpret_cast<uint64_t*>(oldmap + a.words);  // P
+  __shared__ int scan[kThreads / 64 + 1];
+  const int row = blockIdx.x, tid = threadIdx.x, S = a.S;
+  const int64_t base = static_cast<int64_t>(row) * S;
+  int64_t* prow = a.pos + base;
+  const int64_t* lrow = a.lidx + static_cast<int64_t>(row) * a.lstride;
+  for (int w = tid; w < 2 * a.words; w += kThreads) selmap[w] = 0;
+  __syncthreads();
+  for (int j = tid; j < S; j += kThreads) {
+    const int64_t id = prow[j];
+    if (id >= 0 && id < 32ll * a.words) atomicOr(&oldmap[id >> 5], 1u << (id & 31));
+  }
+  const uint64_t* w = pa.win + base;
+  for (int i = tid; i < S; i += kThreads) {
+    const uint64_t c = w[i];
+    sorted[i] = c;
+    const int64_t id = lrow[min(static_cast<uint32_t>(c), static_cast<uint32_t>(a.n - 1))];
+    if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
+  }
+  __syncthreads();
+  reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan);
+  if (a.out_sel) {
+    for (int i = S + tid; i < a.P; i += kThreads) sorted[i] = ~0ull;
+    __syncthreads();
+    skv::block_bitonic_sort(sorted, a.P);
+    for (int i = tid; i < S; i += kThreads) {
+      const uint32_t j = static_cast<uint32_t>(sorted[i]);
+      a.out_sel[base + i] = (j < static_cast<uint32_t>(a.n)) ? lrow[j] : -1;
+    }
+  }
+}
+
+// Slices of part_len keys (a multiple of 256, at most kMaxPartLen), about 256 / rows per row.
+void part_plan(int rows, int n, int* parts, int* part_len) {
+  const int target = std::max(1, std::min(64, 256 / std::max(1, rows)));
+  int len = (n + target - 1) / target;
+  len = std::max(256, std::min(kMaxPartLen, (len + 255) / 256 * 256));
+  *part_len = len;
+  *parts = (n + len - 1) / len;
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace layout of skv_select_chunks_ws: h1, h2, cnt, thr, win.
+size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws) {
+  int parts, len;
+  part_plan(rows, n, &parts, &len);
+  const size_t h = align256(static_cast<size_t>(rows) * parts * 256 * 4);
+  const size_t c = align256(static_cast<size_t>(rows) * parts * 2 * 4);
+  const size_t t = align256(static_cast<size_t>(rows) * 4 * 4);
+  const size_t wn = align256(static_cast<size_t>(rows) * S * 8);
+  if (pa) {
+    unsigned char* p = static_cast<unsigned char*>(ws);
+    pa->parts = parts;
+    pa->part_len = len;
+    pa->h1 = reinterpret_cast<uint32_t*>(p);
+    pa->h2 = reinterpret_cast<uint32_t*>(p + h);
+    pa->cnt = reinterpret_cast<int32_t*>(p + 2 * h);
+    pa->thr = reinterpret_cast<int32_t*>(p + 2 * h + c);
+    pa->win = reinterpret_cast<uint64_t*>(p + 2 * h + c + t);
+  }
+  return 2 * h + c + t + wn;
+}
+
+// Path of a selection call. kFused: the selection kernel computes the keys itself (one workgroup
+// per row). kSplit: few rows (rows * 8 <= 256 CUs) and m*n >= 2^15, so the keys come from the
+// many-workgroup softmax kernel first. kParts: as kSplit, and long rows (n >= 65536) with a
+// workspace, so the selection passes also run over many workgroups per row. Environment
+// SKV_SELECT_SPLIT=0/1/2 forces fused / split / parts (parts only with a workspace), read per call.
+enum SelectPath { kFused = 0, kSplitPath = 1, kParts = 2 };
+
+SelectPath select_path(int rows, int m, int n, bool has_scores, bool has_ws) {
+  if (!has_scores) return kFused;
+  const char* e = getenv("SKV_SELECT_SPLIT");
+  if (e && e[0] >= '0' && e[0] <= '2' && e[1] == 0) {
+    const int v = e[0] - '0';
+    return v == 2 ? (has_ws ? kParts : kSplitPath) : static_cast<SelectPath>(v);
+  }
+  if (rows > 32 || static_cast<int64_t>(m) * n < (int64_t{1} << 15)) return kFused;
+  return (has_ws && n >= 65536) ? kParts : kSplitPath;
+}
+
+int select_impl(const char* what, const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks, int64_t* position_ids,
+                int32_t* offsets, int32_t* cnts, uint16_t* out_scores, int64_t* out_selected, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   if (!D || !norm || !sum || !landmark_idx || !position_ids || !offsets || !cnts) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -383,7 +694,16 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
   // Few rows: the per-row key computation (m*n exponentials) would run on as many workgroups as
   // rows, so it moves to the many-workgroup softmax + GQA-max kernel, which writes the keys
   // (bit-identical) into out_scores; the selection kernel then starts from them.
-  const bool split = out_scores && use_split(rows, m, n);
+  const SelectPath path = select_path(rows, m, n, out_scores != nullptr, workspace != nullptr);
+  const bool split = path != kFused;
+  const bool parts = path == kParts;
+  if (parts) {
+    const size_t need = part_workspace(rows, n, select_sets, nullptr, nullptr);
+    if (workspace_bytes < static_cast<int64_t>(need)) {
+      skv_set_error("%s: workspace of %lld bytes, %zu needed", what, (long long)workspace_bytes, need);
+      return SKV_EINVAL;
+    }
+  }
   const int n_lds = (!split && fixed + static_cast<size_t>(n) * 2 <= kLdsBudget) ? n : 0;
   if (!n_lds && !out_scores) {
     skv_set_error("%s: n=%d landmarks do not fit LDS; pass out_scores as staging", what, n);
@@ -418,8 +738,50 @@ extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const flo
     const int rc = skv_softmax_gqa_max(D, norm, sum, nullptr, out_scores, rows, m, n, stream);
     if (rc) return rc;
   }
+  if (parts) {
+    PartArgs pa{};
+    pa.scores = out_scores;
+    pa.n = n;
+    pa.S = select_sets;
+    part_workspace(rows, n, select_sets, &pa, workspace);
+    const dim3 pg(pa.parts, rows);
+    hipLaunchKernelGGL(part_hist_kernel<1>, pg, dim3(kPartThreads), 0, st, pa);
+    hipLaunchKernelGGL(part_hist_kernel<2>, pg, dim3(kPartThreads), 0, st, pa);
+    hipLaunchKernelGGL(part_count_kernel, pg, dim3(kPartThreads), 0, st, pa);
+    hipLaunchKernelGGL(part_emit_kernel, pg, dim3(kPartThreads), 0, st, pa);
+    const size_t fb = (fixed + 15) / 16 * 16;
+    hipLaunchKernelGGL(select_finish_kernel, dim3(rows), dim3(kThreads), fb, st, a, pa);
+    return skv_check_launch(what);
+  }
   if (m <= 4) hipLaunchKernelGGL(select_kernel<4>, dim3(rows), dim3(kThreads), ldsb, st, a);
   else if (m <= 8) hipLaunchKernelGGL(select_kernel<8>, dim3(rows), dim3(kThreads), ldsb, st, a);
   else hipLaunchKernelGGL(select_kernel<16>, dim3(rows), dim3(kThreads), ldsb, st, a);
   return skv_check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                                 const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
+                                 int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
+                                 int64_t* out_selected, void* stream) {
+  return select_impl("select_chunks", D, norm, sum, rows, m, n, landmark_idx, idx_stride, select_sets, num_chunks,
+                     position_ids, offsets, cnts, out_scores, out_selected, nullptr, 0, stream);
+}
+
+extern "C" int64_t skv_select_workspace_bytes(int rows, int n, int select_sets) {
+  if (rows < 1 || n < 1 || select_sets < 1) return 0;
+  return static_cast<int64_t>(part_workspace(rows, n, select_sets, nullptr, nullptr));
+}
+
+extern "C" int skv_select_chunks_ws(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                                    const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
+                                    int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
+                                    int64_t* out_selected, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!workspace) {
+    skv_set_error("select_chunks_ws: null workspace");
+    return SKV_EINVAL;
+  }
+  return select_impl("select_chunks_ws", D, norm, sum, rows, m, n, landmark_idx, idx_stride, select_sets, num_chunks,
+                     position_ids, offsets, cnts, out_scores, out_selected, workspace, workspace_bytes, stream);
 }

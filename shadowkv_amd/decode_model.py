@@ -76,6 +76,8 @@ def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin:
     cache.chunk_attn = torch.zeros(B, H, n, dtype=torch.bfloat16, device=dev)
     cache.norm = torch.zeros(B * H, G, tiles, dtype=torch.float32, device=dev)
     cache.sum = torch.zeros(B * H, G, tiles, dtype=torch.float32, device=dev)
+    cache.select_workspace = torch.empty(shadowkv.select_workspace_bytes(B * H, n, cache.select_sets),
+                                         dtype=torch.uint8, device=dev)
     if cos_sin is None:
         cos_sin = build_cos_sin_cache(ctx + 4096, 500000.0, D, device=dev)
     zero_cnts = torch.zeros(B * H, dtype=torch.int32, device=dev)

@@ -26,7 +26,7 @@ __all__ = [
     "gather_copy", "gather_copy_d2d_with_offsets", "reorder_keys_and_compute_offsets", "gather_copy_with_offsets",
     "apply_rotary_pos_emb_new", "apply_rotary_pos_emb_push_cache_opt", "apply_rotary_pos_emb_push_cache_opt_glm",
     "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "score_logits", "softmax_gqa_max", "select_chunks", "topk_gather", "rebuild_k_rope",
-    "sparse_attn_workspace_bytes", "sparse_attn_decode", "device_address",
+    "sparse_attn_workspace_bytes", "sparse_attn_decode", "device_address", "select_workspace_bytes",
 ]
 
 
@@ -391,8 +391,12 @@ def softmax_gqa_max(D, Norm, Sum, out, batch_count, m, n, softmax=None):
               batch_count, m, n, _stream())
 
 
+def select_workspace_bytes(rows: int, n: int, select_sets: int) -> int:
+    return int(_lib.lib().skv_select_workspace_bytes(rows, n, select_sets))
+
+
 def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunks, position_ids, offsets, cnts,
-                  out_scores=None, out_selected=None):
+                  out_scores=None, out_selected=None, workspace=None):
     """Fused softmax + GQA max + top-k + id gather + reorder (one workgroup per row; for few rows
     the softmax + GQA max runs first on many workgroups into out_scores, a second launch).
 
@@ -400,7 +404,9 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
     view with contiguous rows, chunk ids in [0, num_chunks); position_ids: [rows, select_sets] int64
     (in: previous slots, -1 = empty; out: reordered); offsets: [rows * select_sets] int32; cnts:
     [rows] int32; out_scores: optional [rows, n] bf16 GQA-max probabilities; out_selected: optional
-    [rows, select_sets] ids in top-k order (the reference's selected_chunks; costs a sort)."""
+    [rows, select_sets] ids in top-k order (the reference's selected_chunks; costs a sort);
+    workspace: optional device buffer of select_workspace_bytes(rows, n, select_sets) bytes, with
+    which few rows (<= 32) are each selected by many workgroups."""
     _dev(D, "D", torch.bfloat16)
     _dev(Norm, "Norm", torch.float32)
     _dev(Sum, "Sum", torch.float32)
@@ -432,9 +438,17 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
         _dev(out_selected, "out_selected", torch.int64)
         _need(out_selected, rows * select_sets, "out_selected")
         op = out_selected.data_ptr()
-    _lib.call("skv_select_chunks", D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), rows, m, n, landmark_idx.data_ptr(),
-              landmark_idx.stride(0), select_sets, num_chunks, position_ids.data_ptr(), offsets.data_ptr(),
-              cnts.data_ptr(), sp, op, _stream())
+    args = (D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), rows, m, n, landmark_idx.data_ptr(),
+            landmark_idx.stride(0), select_sets, num_chunks, position_ids.data_ptr(), offsets.data_ptr(),
+            cnts.data_ptr(), sp, op)
+    if workspace is None:
+        _lib.call("skv_select_chunks", *args, _stream())
+    else:
+        _dev(workspace, "workspace")
+        nbytes = workspace.numel() * workspace.element_size()
+        if nbytes < select_workspace_bytes(rows, n, select_sets):
+            raise ValueError(f"workspace of {nbytes} bytes, {select_workspace_bytes(rows, n, select_sets)} needed")
+        _lib.call("skv_select_chunks_ws", *args, workspace.data_ptr(), nbytes, _stream())
 
 
 def topk_gather(scores, landmark_idx, k, out_ids):

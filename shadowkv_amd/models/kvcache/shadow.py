@@ -135,6 +135,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.key_stream = None  # optional: run the key rebuild on this stream (joined before attention)
         self.attn_workspace = None
         self.attn_out = None
+        self.select_workspace = None  # allocated with the landmarks
         # Device-resident append row / attention length (use_device_lengths); None = host integers.
         self.append_row_dev = None
         self.kv_len_dev = None
@@ -188,6 +189,9 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.chunk_attn = torch.zeros(B, H, n, dtype=torch.bfloat16, device=dev)
         self.norm = torch.zeros(B * H, G, tiles, dtype=torch.float32, device=dev)
         self.sum = torch.zeros(B * H, G, tiles, dtype=torch.float32, device=dev)
+        # scratch of the selection, which spreads each row over many workgroups when rows are few
+        nbytes = shadowkv.select_workspace_bytes(B * H, n, self.select_sets)
+        self.select_workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
 
     def register_k_landmark(self, k_landmark: torch.Tensor, k_landmark_idx: torch.Tensor, layer_idx: int):
         n = k_landmark.shape[-2]
@@ -376,7 +380,8 @@ class ShadowKVCache_CPU(KVCacheBase):
         shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, B * H, G, n, self.k_landmark_idx[layer_idx].view(B * H, n),
                                self.select_sets, self.chunks, self.position_ids[layer_idx].view(B * H, -1), self.offsets,
                                self.cnts, out_scores=self.chunk_attn,
-                               out_selected=self.selected_chunks if self.keep_selected else None)
+                               out_selected=self.selected_chunks if self.keep_selected else None,
+                               workspace=self.select_workspace)
         return self.position_ids[layer_idx]
 
     def _gen_len(self, layer_idx: int) -> int:

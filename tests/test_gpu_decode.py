@@ -42,10 +42,12 @@ def test_single_layer_decode_step(gpu):
 @pytest.mark.parametrize("device_lengths,chunk,split,glm", [(False, 8, None, False), (True, 8, None, False),
                                                            (True, 4, None, False), (True, 16, None, False),
                                                            (False, 16, None, False), (True, 8, "1", False),
-                                                           (True, 8, None, True), (False, 16, "1", True)])
+                                                           (True, 8, None, True), (False, 16, "1", True),
+                                                           (True, 8, "2", False), (True, 4, "2", True)])
 def test_multi_layer_multi_step_decode(gpu, monkeypatch, device_lengths, chunk, split, glm):
     """Also chunk sizes other than 8 (budget 1024: 256 selected chunks of 4 rows, 64 of 16 rows)
-    through every kernel of the step, the selection's few-row split path forced on, and the
+    through every kernel of the step, the selection's few-row paths forced on (keys from the softmax
+    kernel; also the radix passes over many workgroups per row), and the
     GLM-4-9B head layout (16 query heads per kv head) with GLM's interleaved RoPE table."""
     if split is not None:
         monkeypatch.setenv("SKV_SELECT_SPLIT", split)

@@ -157,13 +157,14 @@ def test_topk_gather_bit_exact(gpu, n, k, ties):
     assert torch.equal(out.cpu(), want)
 
 
-@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("split", ["0", "1", "ws"])
 @pytest.mark.parametrize("rows,m,n,S", [(64, 4, 15304, 256), (8, 16, 32712, 256), (8, 4, 130680, 2048),
                                         (8, 4, 968, 256), (2, 1, 300, 7)])
 def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, split):
-    """The fused selection (keys computed per row in the selection kernel, or, on the split path,
-    by the many-workgroup softmax + GQA-max kernel first) equals the unfused sequence."""
-    monkeypatch.setenv("SKV_SELECT_SPLIT", split)
+    """The fused selection (keys computed per row in the selection kernel; on the split path by
+    the many-workgroup softmax + GQA-max kernel first; on the parts path ("ws") also the radix
+    passes over many workgroups per row, with a caller workspace) equals the unfused sequence."""
+    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
     _say(f"select_chunks rows={rows} m={m} n={n} S={S} split={split}")
     g = torch.Generator().manual_seed(rows * n + S)
     q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
@@ -194,11 +195,17 @@ def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, spl
     scores2 = torch.empty_like(scores)
     sel2 = torch.empty_like(sel)
     nchunks = n + n // 10
+    ws = None
+    if split == "ws":  # each row's selection over many workgroups (scratch from the caller)
+        ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu)
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos2, off2, cnt2, out_scores=scores2,
-                           out_selected=sel2)
+                           out_selected=sel2, workspace=ws)
     pos3, off3, cnt3 = old.clone(), torch.empty_like(off1), torch.empty_like(cnt1)
     staging = torch.empty_like(scores) if n > 16384 else None  # scores beyond LDS need global staging
-    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos3, off3, cnt3, out_scores=staging)
+    if split == "ws" and staging is None:
+        staging = torch.empty_like(scores)  # the many-workgroup path needs the keys in global memory
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos3, off3, cnt3, out_scores=staging,
+                           workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(pos3, pos1) and torch.equal(off3, off1) and torch.equal(cnt3, cnt1)
     assert torch.equal(scores2, scores)
