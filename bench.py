@@ -105,11 +105,12 @@ def logits_bytes(BH: int, G: int, n: int, D: int = 128) -> int:
     return BH * (n * D * 2 + G * D * 2 + G * n * 2 + G * tiles * 8)
 
 
-def scoring_launch_ms(model, rounds: int = 4):
-    """Average duration of the landmark-scoring kernel on the live decode state: one launch per
-    layer over that layer's landmarks, the 32 launches captured in a HIP graph and replayed
-    `rounds` times between HIP events (no host launch cost in the figure; the events bracket the
-    replays on the stream the kernels run on). Runs right after the timed decode steps."""
+def scoring_launch_ms(model, rounds: int = 8, sweeps: int = 4):
+    """Average duration of the landmark-scoring kernel on the live decode state: `sweeps` passes
+    over the layers, one launch per layer over that layer's landmarks, captured in a HIP graph and
+    replayed `rounds` times between HIP events (no host launch cost in the figure; the events
+    bracket the replays on the stream the kernels run on). Runs right after the timed decode
+    steps."""
     import torch
     from shadowkv_amd.kernels import shadowkv
 
@@ -124,10 +125,10 @@ def scoring_launch_ms(model, rounds: int = 4):
         shadowkv.score_logits(q, cache.k_landmark[layer], cache.gemm_o, cache.norm, cache.sum, B * H, G, n, D,
                               1.0 / math.sqrt(128))
 
-    t = gpu_time_per_call(launch, L, rounds)
+    t = gpu_time_per_call(launch, sweeps * L, rounds)
     return (t * 1e3,
-            f"HIP events around {rounds} replays of a HIP graph of {L} back-to-back launches (one per layer, "
-            f"on that layer's live landmarks), after the timed steps")
+            f"HIP events around {rounds} replays of a HIP graph of {sweeps * L} back-to-back launches ({sweeps} "
+            f"sweeps over the layers, each launch on its layer's live landmarks), after the timed steps")
 
 
 def cpu_baseline(model, runs: int) -> dict:
