@@ -10,6 +10,7 @@
 //     P.V in fp32: 16 key streams x 8 dims per lane, the streams summed through LDS.
 //   attn_combine_kernel: log-sum-exp merge of the splits in one pass (running maximum), every
 //     load of a 32-split chunk issued before the first is used; bf16 output.
+#include <algorithm>
 #include <type_traits>
 
 #include "wave_reduce.h"
@@ -245,47 +246,80 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   }
 }
 
-// One workgroup (two waves, one lane per dim) per (b, query head). Online merge over the
-// splits in chunks of kChunk: each thread first requests its dim of the chunk's kChunk partial
-// outputs, lanes 0..kChunk-1 of wave 0 request one split's (m, l) each (vector loads, so no
-// scalar-load waits), and the chunk's maximum and weights go through LDS; the running maximum
-// M, denominator l and accumulator acc are rescaled when M grows.
-__global__ void __launch_bounds__(kHeadDim) attn_combine_kernel(AttnArgs a) {
+// One workgroup per (b, query head): `groups` groups of 128 threads (one lane per dim), group g
+// merging chunks g, g + groups, ... of kChunk splits. Online merge per chunk: each thread first
+// requests its dim of the chunk's kChunk partial outputs, lanes 0..kChunk-1 of the group's first
+// wave request one split's (m, l) each (vector loads, so no scalar-load waits), and the chunk's
+// maximum and weights go through LDS; the running maximum M, denominator l and accumulator acc
+// are rescaled when M grows. The groups' (M, l, acc) are merged the same way at the end. Several
+// groups serve long rows (many splits), whose chunks would otherwise be merged one after another.
+constexpr int kMaxCombineGroups = 4;
+
+__global__ void __launch_bounds__(kHeadDim * kMaxCombineGroups) attn_combine_kernel(AttnArgs a) {
   constexpr int kChunk = 32;
-  __shared__ float w_s[kChunk];
-  __shared__ float m_s, l_s;
+  __shared__ float w_s[kMaxCombineGroups][kChunk];
+  __shared__ float m_s[kMaxCombineGroups], l_s[kMaxCombineGroups];
+  __shared__ float acc_s[kMaxCombineGroups][kHeadDim];
+  const int groups = blockDim.x / kHeadDim;
+  const int g = threadIdx.x / kHeadDim;
   const int row = blockIdx.x;  // b*Hq + hq
   const int Hq = a.Hkv * a.G;
   const int b = row / Hq;
   const int hq = row - b * Hq;
-  const int d = threadIdx.x;
+  const int d = threadIdx.x - g * kHeadDim;
   const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + static_cast<int64_t>(row) * a.splits;
   const float* o = a.ws_o + static_cast<int64_t>(row) * a.splits * kHeadDim + d;
   const int used = (live_length(a) + a.split_keys - 1) / a.split_keys;  // >= 1
+  // Groups in use follow the live split count only (not the launch), so a device length and the
+  // same host length merge in the same order; groups beyond it stay idle.
+  const int eg = min(groups, (used + kChunk - 1) / kChunk);
+  const int iters = (used + kChunk * eg - 1) / (kChunk * eg);  // the same for every group
   float M = -INFINITY, l = 0.f, acc = 0.f;
-  for (int s0 = 0; s0 < used; s0 += kChunk) {
+  for (int it = 0; it < iters; ++it) {
+    const int s0 = (it * eg + g) * kChunk;
+    const bool live = g < eg && s0 < used;  // group-uniform: this group has a chunk this round
     float x[kChunk];
 #pragma unroll
     for (int u = 0; u < kChunk; ++u) x[u] = o[static_cast<int64_t>(min(s0 + u, used - 1)) * kHeadDim];
     const bool own = d < kChunk && s0 + d < used;  // this lane's split of the chunk
     const float2 p = ml[min(s0 + d, used - 1)];
-    const float cm = skv::wave_max_dpp(own ? p.x : -INFINITY);  // wave 0 holds the chunk
-    if (d == 0) m_s = cm;
+    const float cm = skv::wave_max_dpp(own ? p.x : -INFINITY);  // the group's first wave holds the chunk
+    if (d == 0) m_s[g] = cm;
     __syncthreads();
-    const float Mn = fmaxf(M, m_s);
+    const float Mn = live ? fmaxf(M, m_s[g]) : M;
     const float w = own ? expf(p.x - Mn) : 0.f;
     const float lw = skv::wave_sum_dpp(own ? p.y * w : 0.f);
-    if (d < kChunk) w_s[d] = w;
-    if (d == 0) l_s = lw;
+    if (d < kChunk) w_s[g][d] = w;
+    if (d == 0) l_s[g] = lw;
     __syncthreads();
-    const float r = expf(M - Mn);  // 0 on the first chunk (M = -inf)
-    float sum = 0.f;
+    if (live) {
+      const float r = expf(M - Mn);  // 0 on the group's first chunk (M = -inf)
+      float sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < kChunk; ++u) sum = fmaf(w_s[u], x[u], sum);
-    acc = fmaf(acc, r, sum);
-    l = fmaf(l, r, l_s);
-    M = Mn;
-    __syncthreads();  // w_s, m_s, l_s are rewritten by the next chunk
+      for (int u = 0; u < kChunk; ++u) sum = fmaf(w_s[g][u], x[u], sum);
+      acc = fmaf(acc, r, sum);
+      l = fmaf(l, r, l_s[g]);
+      M = Mn;
+    }
+    __syncthreads();  // w_s, m_s, l_s are rewritten by the next round
+  }
+  if (groups > 1) {
+    acc_s[g][d] = acc;
+    if (d == 0) {
+      m_s[g] = M;
+      l_s[g] = l;
+    }
+    __syncthreads();
+    if (g != 0) return;
+    float Mt = m_s[0];
+    for (int q = 1; q < groups; ++q) Mt = fmaxf(Mt, m_s[q]);  // group 0 always merged a chunk
+    l = 0.f;
+    acc = 0.f;
+    for (int q = 0; q < groups; ++q) {
+      const float r = expf(m_s[q] - Mt);  // 0 for a group without chunks (M = -inf)
+      l = fmaf(l_s[q], r, l);
+      acc = fmaf(acc_s[q][d], r, acc);
+    }
   }
   a.out[b * a.o_sb + hq * a.o_sh + d] = skv::f2bf(acc / l);
 }
@@ -381,7 +415,9 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
   else go(std::false_type{});
   int rc = skv_check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(batch_size * q_heads), dim3(kHeadDim), 0, s, a);
+  // Several merge groups only when there are chunks for them (the split count by the maximum length).
+  const int groups = std::min(kMaxCombineGroups, (a.splits + 31) / 32);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(batch_size * q_heads), dim3(kHeadDim * groups), 0, s, a);
   return skv_check_launch(what);
 }
 

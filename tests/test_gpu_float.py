@@ -171,7 +171,8 @@ def test_scoring(gpu, Z, m, n):
 
 
 @pytest.mark.parametrize("B,Hq,Hk,L,strided", [(1, 32, 8, 2497, True), (8, 32, 8, 2600, True), (2, 32, 2, 2497, True),
-                                               (1, 8, 8, 1, False), (3, 16, 4, 300, False)])
+                                               (1, 8, 8, 1, False), (3, 16, 4, 300, False), (1, 32, 8, 19521, True),
+                                               (1, 32, 8, 8193, False)])
 def test_sparse_attention(gpu, B, Hq, Hk, L, strided):
     _say(f"attention B={B} Hq={Hq} Hk={Hk} L={L}")
     g = torch.Generator().manual_seed(L)
@@ -224,4 +225,28 @@ def test_attention_device_length_matches_host_length(gpu):
         torch.cuda.synchronize()
         assert torch.equal(got.cpu(), want.cpu()), L
         ref = oracle.sparse_attention(q.cpu(), K.cpu(), V.cpu(), eff)
+        torch.testing.assert_close(got.cpu().float(), ref.float(), rtol=RTOL, atol=ATOL)
+
+
+def test_attention_device_length_long_rows(gpu):
+    """Rows long enough for several merge groups (more than 32 splits): a device length below the
+    maximum merges in the same order as the same host length (bit for bit)."""
+    B, Hq, Hk, Lmax = 1, 32, 8, 12000
+    g = torch.Generator().manual_seed(4)
+    K = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
+    V = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16).to(gpu)
+    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, Lmax), dtype=torch.uint8, device=gpu)
+    ldev = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for L in (3000, 4096, 4097, 8300, 12000):
+        _say(f"attention long rows, device length {L}")
+        ldev.fill_(L)
+        got = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
+        shadowkv.sparse_attn_decode(q, K, V, Lmax, got, ws, kv_len_dev=ldev)
+        want = torch.empty_like(got)
+        ws2 = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+        shadowkv.sparse_attn_decode(q, K, V, L, want, ws2)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), want.cpu()), L
+        ref = oracle.sparse_attention(q.cpu(), K.cpu(), V.cpu(), L)
         torch.testing.assert_close(got.cpu().float(), ref.float(), rtol=RTOL, atol=ATOL)
