@@ -217,3 +217,37 @@ def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, spl
     assert np.array_equal(pos2.cpu().numpy(), ids) and np.array_equal(cnt2.cpu().numpy(), cnts)
     assert np.array_equal(off2.view(rows, S).cpu().numpy(), offs)
     assert (cnts >= S // 2).all()
+
+
+@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("rows,m,n,S", [(8, 4, 130680, 2048), (8, 16, 32712, 256), (4, 4, 15304, 256)])
+def test_select_chunks_all_ties(gpu, monkeypatch, rows, m, n, S, split):
+    """Zero queries: every logit 0, every probability 1/n, so all keys tie and the selection is
+    the S lowest landmark indices (ties broken by index across every slice of a row)."""
+    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    _say(f"select_chunks all ties rows={rows} m={m} n={n} S={S} split={split}")
+    g = torch.Generator().manual_seed(n + S)
+    q = torch.zeros(rows, m, 128, dtype=torch.bfloat16, device=gpu)
+    L = torch.randn(rows, n, 128, generator=g).to(torch.bfloat16).to(gpu)
+    lidx = torch.stack([torch.randperm(n + n // 10, generator=g)[:n].sort().values for _ in range(rows)]).to(gpu)
+    tiles = (n + 255) // 256
+    D = torch.empty(rows, m, n, dtype=torch.bfloat16, device=gpu)
+    norm = torch.empty(rows, m, tiles, device=gpu)
+    ssum = torch.empty_like(norm)
+    shadowkv.score_logits(q, L, D, norm, ssum, rows, m, n, 128)
+    nchunks = n + n // 10
+    pos = torch.full((rows, S), -1, dtype=torch.int64, device=gpu)
+    off = torch.empty(rows * S, dtype=torch.int32, device=gpu)
+    cnt = torch.empty(rows, dtype=torch.int32, device=gpu)
+    scores = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+    sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
+    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split == "ws" else None
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos, off, cnt, out_scores=scores,
+                           out_selected=sel, workspace=ws)
+    torch.cuda.synchronize()
+    assert (scores == scores[0, 0]).all()
+    want = lidx[:, :S].cpu()  # lowest indices, ids ascending (previous slots empty: all misses)
+    assert torch.equal(sel.cpu(), want)
+    assert torch.equal(pos.cpu(), want)
+    assert (cnt.cpu() == 0).all()
+    assert torch.equal(off.view(rows, S).cpu(), want.to(torch.int32))
