@@ -7,7 +7,9 @@
 //     once from HBM. Scores on MFMA: v_mfma_f32_16x16x32_bf16 with the (up to 16) query heads as
 //     the A rows and 16 keys as the B columns, so each lane ends up holding finished scores (no
 //     cross-lane reduction); split softmax per query head with DPP/readlane wave reductions;
-//     P.V in fp32: 16 key streams x 8 dims per lane, the streams summed through LDS.
+//     P.V on MFMA for 9..16 query heads (P in bf16 as the A operand, the V tile read transposed
+//     from LDS as B, each wave owning 32 dims), in fp32 for 1..8 (16 key streams x 8 dims per
+//     lane, the streams summed through LDS).
 //   attn_combine_kernel: log-sum-exp merge of the splits in one pass (running maximum), every
 //     load of a 32-split chunk issued before the first is used; bf16 output.
 #include <algorithm>
@@ -74,7 +76,14 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   constexpr int kVals = GP * 8;              // P.V partial sums per lane: [head][8 dims]
   constexpr int kKept = kVals / 4;           // per lane after the in-wave stream fold
   __shared__ float p_lds[GP][kSplit];
-  __shared__ __align__(16) float red[4][64][kKept];  // [wave][lane][value]
+  // [wave][lane][value] for the fp32 P.V path; the MFMA P.V path (GP == 16) stages the V tile here
+  // instead ([key][kVtLd] bf16, rows padded so the 4 key groups of an operand read hit disjoint
+  // banks).
+  constexpr int kVtLd = kHeadDim + 4;
+  constexpr int kRedBytes = 4 * 64 * kKept * 4;
+  constexpr int kVtBytes = GP == 16 ? kSplit * kVtLd * 2 : 0;
+  __shared__ __align__(16) unsigned char big[kRedBytes > kVtBytes ? kRedBytes : kVtBytes];
+  float (*red)[64][kKept] = reinterpret_cast<float (*)[64][kKept]>(big);
   __shared__ float ml[GP][2];
   __shared__ int prow[kPaged ? kSplit : 1];  // physical row of each key of the split (paged)
 
@@ -181,6 +190,72 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
+
+  if constexpr (GP == 16) {
+    // P.V on MFMA (9..16 query heads per kv head): O[head][dim] += P[head][32 keys] . V[32 keys][dim]
+    // with P as the A operand (rows past G zero; rounded to bf16, as flash attention does for its
+    // second product) and V as B, read transposed from an LDS copy of the split's V tile. Wave w
+    // owns dims [32w, 32w + 32) for every head, so no cross-wave sum is needed (MI355X, GLM-4-9B
+    // batch 4: 10.9 vs 18.5 us with fp32 P.V). For 4 query heads the same path measured faster
+    // alone (22.2 vs 23.6 us at Llama-3-8B batch 8) but slowed the pipelined decode step (373 vs
+    // 382 tokens/s: the V tile's 34 KB of LDS per workgroup), so 1..8 heads keep fp32 P.V.
+    uint16_t* vt = reinterpret_cast<uint16_t*>(big);
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      uint16_t* dst = vt + (i * 16 + stream) * kVtLd + li * 8;
+      *reinterpret_cast<uint32_t __attribute__((ext_vector_type(2)))*>(dst) = {vr[i].x, vr[i].y};
+      *reinterpret_cast<uint32_t __attribute__((ext_vector_type(2)))*>(dst + 4) = {vr[i].z, vr[i].w};
+    }
+    __syncthreads();
+    const int qh = lane & 15;    // A row: query head of the group; B column: dim within the tile
+    const int slab = lane >> 4;  // k-slab: keys [8*slab, +8) of each 32-key step
+    f32x4_t o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < kSplit / 32; ++ks) {
+      const int k0 = ks * 32 + 8 * slab;
+      u32x4 pa = {0u, 0u, 0u, 0u};
+      if (qh < G) {
+        const float* pr = &p_lds[qh][k0];
+        pa = u32x4{skv::f2bf2(pr[0], pr[1]), skv::f2bf2(pr[2], pr[3]), skv::f2bf2(pr[4], pr[5]),
+                   skv::f2bf2(pr[6], pr[7])};
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int dim = wave * 32 + t * 16 + qh;
+        const uint16_t* vc = vt + k0 * kVtLd + dim;
+        uint16_t e[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) e[u] = vc[u * kVtLd];
+        const u32x4 vb = {static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
+                          static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16),
+                          static_cast<uint32_t>(e[4]) | (static_cast<uint32_t>(e[5]) << 16),
+                          static_cast<uint32_t>(e[6]) | (static_cast<uint32_t>(e[7]) << 16)};
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pa),
+                                                       __builtin_bit_cast(bf16x8_t, vb), o[t], 0, 0, 0);
+      }
+    }
+    // D[head 4*slab + v][dim]: this lane holds 4 heads of one dim per tile.
+    const int Hq = a.Hkv * G;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int dim = wave * 32 + t * 16 + qh;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int g = 4 * slab + v;
+        if (g < G) {
+          const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
+          a.ws_o[r * kHeadDim + dim] = o[t][v];
+        }
+      }
+    }
+    if (threadIdx.x < G) {
+      const int g = threadIdx.x;
+      const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
+      a.ws_ml[r * 2] = ml[g][0];
+      a.ws_ml[r * 2 + 1] = ml[g][1];
+    }
+    return;
+  }
 
   float acc[GP][8];
 #pragma unroll
