@@ -30,3 +30,24 @@ def test_argument_errors_are_reported_without_a_gpu():
     rc = lib.skv_batch_gemm_softmax(p, p, p, p, p, p, 1, 4, 10, 64, 1.0, 0.0, None)
     assert rc == 2 and "k=64" in _lib.last_error()
     assert lib.skv_sparse_attn_workspace_bytes(8, 32, 2600) == 8 * 32 * 21 * 130 * 4  # 128-key splits
+
+
+def test_selection_workspace_plan():
+    """The selection workspace covers the slice histograms, counts and winners of the plan the
+    library uses (about 256 / rows slices of at most 4096 keys per row), and bad sizes give 0."""
+    lib = _lib.lib()
+    assert lib.skv_select_workspace_bytes(0, 100, 10) == 0
+    assert lib.skv_select_workspace_bytes(8, 0, 10) == 0
+    for rows, n, S in ((8, 130680, 2048), (8, 32712, 256), (32, 15304, 256), (1, 1000, 7)):
+        target = max(1, min(64, 256 // rows))
+        part_len = max(256, min(4096, -(-(-(-n // target)) // 256) * 256))
+        parts = -(-n // part_len)
+        align = lambda b: -(-b // 256) * 256
+        want = 2 * align(rows * parts * 256 * 4) + align(rows * parts * 8) + align(rows * 16) + align(rows * S * 8)
+        assert lib.skv_select_workspace_bytes(rows, n, S) == want, (rows, n, S)
+    # select_chunks_ws rejects a null workspace and a short one on the host
+    p = ctypes.c_void_p(16)
+    rc = lib.skv_select_chunks_ws(p, p, p, 8, 4, 130680, p, 130680, 2048, 131000, p, p, p, p, None, None, 0, None)
+    assert rc == 1 and "null workspace" in _lib.last_error()
+    rc = lib.skv_select_chunks_ws(p, p, p, 8, 4, 130680, p, 130680, 2048, 131000, p, p, p, p, None, p, 1, None)
+    assert rc == 1 and "workspace of 1 bytes" in _lib.last_error()
