@@ -50,6 +50,9 @@ def parse() -> argparse.Namespace:
                    help="device chunk pool of this many slots per (b, h) and layer (>= budget/chunk); "
                         "default: the reference's slot reuse")
     p.add_argument("--layers", type=int, default=None, help="override the layer count (debug only)")
+    p.add_argument("--model", choices=["llama31_8b", "glm4_9b", "llama3_8b_1m"], default="llama31_8b",
+                   help="model shape of the decode workload (random weights): Llama-3.1-8B (the headline), "
+                        "GLM-4-9B (2 kv heads of 16 query heads, GLM RoPE), Llama-3-8B-1M (RoPE theta 3.58e6)")
     p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
     p.add_argument("--graph-steps", type=int, default=8,
@@ -678,7 +681,8 @@ def main() -> int:
     from shadowkv_amd.kernels import shadowkv
     from dataclasses import replace
 
-    shape = decode_model.LLAMA31_8B
+    shape = {"llama31_8b": decode_model.LLAMA31_8B, "glm4_9b": decode_model.GLM4_9B,
+             "llama3_8b_1m": decode_model.LLAMA3_8B_1M}[args.model]
     if args.layers:
         shape = replace(shape, layers=args.layers)
     t0 = time.time()
@@ -746,7 +750,8 @@ def main() -> int:
         cpu = cpu_baseline(model, args.cpu_runs)
 
     out = {
-        "metric": "decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util",
+        "metric": ("decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util"
+                   if args.model == "llama31_8b" else f"decode tokens/sec, {shape.name} shape"),
         "value": round(args.batch * args.steps / elapsed, 3),
         "unit": "tokens/s",
         "n_gpus": 1,

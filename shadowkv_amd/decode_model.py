@@ -26,7 +26,7 @@ import torch.nn.functional as F
 from .kernels import shadowkv
 from .models.attention import ShadowAttention
 from .models.kvcache import ShadowKVCache_CPU
-from .models.tensor_op import build_cos_sin_cache
+from .models.tensor_op import build_cos_sin_cache, build_glm_cos_sin_cache
 
 
 @dataclass(frozen=True)
@@ -41,10 +41,12 @@ class ModelShape:
     rope_theta: float
     head_dim: int = 128
     eps: float = 1e-5
+    rope: str = "half"  # "half": Llama half-split; "glm": interleaved pairs on the first 64 dims
 
 
 LLAMA31_8B = ModelShape("Llama-3.1-8B", 32, 4096, 14336, 32, 8, 128256, 500000.0)
 LLAMA3_8B_1M = ModelShape("Llama-3-8B-1M", 32, 4096, 14336, 32, 8, 128256, 3580000.0)
+GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="glm")
 
 
 def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin: torch.Tensor | None = None) -> None:
@@ -166,7 +168,12 @@ class SyntheticDecoder:
                 gate_up=w(2 * s.ffn, s.hidden), down=w(s.hidden, s.ffn),
                 in_norm=torch.ones(s.hidden, dtype=dtype, device=device),
                 post_norm=torch.ones(s.hidden, dtype=dtype, device=device)))
-        self.cos_sin = build_cos_sin_cache(ctx + decode_len, s.rope_theta, D, device=device)
+        if s.rope == "glm":  # [rows, 64] table: the kernels take GLM's interleaved rotation from its width
+            if not fused:
+                raise ValueError("the GLM rotary embedding runs in the fused new-token kernel (fused=True)")
+            self.cos_sin = build_glm_cos_sin_cache(ctx + decode_len, s.rope_theta, device=device)
+        else:
+            self.cos_sin = build_cos_sin_cache(ctx + decode_len, s.rope_theta, D, device=device)
         cfg = types.SimpleNamespace(num_attention_heads=s.heads, num_key_value_heads=s.kv_heads,
                                     hidden_size=s.heads * D, num_hidden_layers=s.layers)
         lb = batch // lanes

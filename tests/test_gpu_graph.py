@@ -60,12 +60,14 @@ def test_graph_replay_matches_eager(gpu, lanes, chunk_cache):
 
 
 
-@pytest.mark.parametrize("lanes,chunk_cache", [(1, None), (2, None), (2, 384)])
-def test_multi_step_graph_matches_eager(gpu, lanes, chunk_cache):
+@pytest.mark.parametrize("lanes,chunk_cache,glm", [(1, None, False), (2, None, False), (2, 384, False),
+                                                  (2, None, True)])
+def test_multi_step_graph_matches_eager(gpu, lanes, chunk_cache, glm):
     """A graph of 3 decode steps (one continuous lane pipeline across the step boundaries)
-    replays like 3 eager steps, twice in a row."""
-    print(f"3-step graph vs eager, lanes={lanes}, chunk_cache={chunk_cache}", flush=True)
-    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    replays like 3 eager steps, twice in a row; also the GLM-4-9B shape (2 kv heads of 16 query
+    heads, GLM's interleaved RoPE table through the fused new-token kernel and the rebuild)."""
+    print(f"3-step graph vs eager, lanes={lanes}, chunk_cache={chunk_cache}, glm={glm}", flush=True)
+    shape = replace(decode_model.GLM4_9B if glm else decode_model.LLAMA31_8B, layers=2, vocab=1000)
     n = 3
     kw = dict(sparse_budget=2048, decode_len=2 * n + 4, lanes=lanes, seed=12, chunk_cache=chunk_cache)
     eager = decode_model.SyntheticDecoder(shape, 4, 16384, **kw)
