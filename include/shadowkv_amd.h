@@ -200,6 +200,9 @@ int skv_topk_gather(const uint16_t* scores, int64_t score_stride, const int64_t*
  * for LDS. With out_scores given and few rows (rows <= 32, m*n >= 32768) the probabilities are
  * first computed by the many-workgroup softmax kernel (as skv_softmax_gqa_max, a second launch on
  * the same stream) and the selection starts from them; results are identical.
+ * position_ids, offsets and cnts all null: selection only (no previous slots, no reorder, no
+ * num_chunks limit); out_selected is then required and receives the ids in top-k order, as
+ * skv_softmax_gqa_max + skv_topk_gather would (the selection of a device chunk pool).
  * select_sets <= 2048. */
 int skv_select_chunks(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
                       const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,

@@ -21,7 +21,9 @@
 //   5. hits: a scan over the previous slots whose id is in `sel` emits them in old-slot order;
 //      misses: a popcount scan over the words of `sel & ~old` emits them in ascending id order.
 // With out_selected requested, the winners are additionally bitonic-sorted (value desc, index
-// asc) to emit the ids in top-k order. The arithmetic of step 2 and the selection rule are those
+// asc) to emit the ids in top-k order. Without previous slots (position_ids null: the selection
+// of a chunk pool, which does its own hit lookup) steps 4's bitmaps and 5 are skipped and only the
+// ids in top-k order are written. The arithmetic of step 2 and the selection rule are those
 // of score.hip softmax_kernel and topk.hip, so the result is bit-identical to the unfused path.
 #include <algorithm>
 #include <cstdlib>
@@ -47,7 +49,7 @@ struct SelectArgs {
   int64_t lstride;
   int S, P, n_lds, words;  // words = bitmap words covering chunk ids [0, 32*words)
   int keys_off;            // byte offset of the LDS key array
-  int64_t* pos;
+  int64_t* pos;  // previous slots, reordered in place; null: selection only (out_sel required)
   int32_t* offsets;
   int32_t* cnts;
   uint16_t* out_scores;  // [rows][n], required when n_lds == 0
@@ -131,7 +133,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const int wave = tid >> 6;
   const int m = a.m, n = a.n, S = a.S;
   const int64_t base = static_cast<int64_t>(row) * S;
-  int64_t* prow = a.pos + base;
+  int64_t* prow = a.pos ? a.pos + base : nullptr;
 
   for (int i = wave; i < (a.pre ? 0 : m); i += kThreads / 64) {
     const float* nr = a.norm + (static_cast<int64_t>(row) * m + i) * a.tiles;
@@ -152,7 +154,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   if (tid == 0) sel_count = 0;
   __syncthreads();
   // previous slots into the old-id bitmap (ids outside the bitmap can never be hits)
-  for (int j = tid; j < S; j += kThreads) {
+  for (int j = tid; j < (a.pos ? S : 0); j += kThreads) {
     const int64_t id = prow[j];
     if (id >= 0 && id < 32ll * a.words) atomicOr(&oldmap[id >> 5], 1u << (id & 31));
   }
@@ -330,15 +332,16 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
     if (win) sorted[atomicAdd(&sel_count, 1)] = (static_cast<uint64_t>(0xffffu - kj) << 32) | static_cast<uint32_t>(j);
   });
   __syncthreads();
-  // The winners' chunk ids into the selection bitmap: every id load of the workgroup in flight
-  // together (exactly S winners).
-  for (int i = tid; i < sel_count; i += kThreads) {
-    const int64_t id = lrow[static_cast<uint32_t>(sorted[i])];
-    if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
+  if (a.pos) {
+    // The winners' chunk ids into the selection bitmap: every id load of the workgroup in flight
+    // together (exactly S winners).
+    for (int i = tid; i < sel_count; i += kThreads) {
+      const int64_t id = lrow[static_cast<uint32_t>(sorted[i])];
+      if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+    reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan);
   }
-  __syncthreads();
-
-  reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan);
 
   if (a.out_sel) {
     for (int i = S + tid; i < a.P; i += kThreads) sorted[i] = ~0ull;
@@ -587,11 +590,12 @@ __global__ void __launch_bounds__(kThreads) select_finish_kernel(SelectArgs a, P
   __shared__ int scan[kThreads / 64 + 1];
   const int row = blockIdx.x, tid = threadIdx.x, S = a.S;
   const int64_t base = static_cast<int64_t>(row) * S;
-  int64_t* prow = a.pos + base;
+  int64_t* prow = a.pos ? a.pos + base : nullptr;
   const int64_t* lrow = a.lidx + static_cast<int64_t>(row) * a.lstride;
+  const bool reorder = a.pos != nullptr;
   for (int w = tid; w < 2 * a.words; w += kThreads) selmap[w] = 0;
   __syncthreads();
-  for (int j = tid; j < S; j += kThreads) {
+  for (int j = tid; j < (reorder ? S : 0); j += kThreads) {
     const int64_t id = prow[j];
     if (id >= 0 && id < 32ll * a.words) atomicOr(&oldmap[id >> 5], 1u << (id & 31));
   }
@@ -599,11 +603,12 @@ __global__ void __launch_bounds__(kThreads) select_finish_kernel(SelectArgs a, P
   for (int i = tid; i < S; i += kThreads) {
     const uint64_t c = w[i];
     sorted[i] = c;
+    if (!reorder) continue;
     const int64_t id = lrow[min(static_cast<uint32_t>(c), static_cast<uint32_t>(a.n - 1))];
     if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
   }
   __syncthreads();
-  reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan);
+  if (reorder) reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan);
   if (a.out_sel) {
     for (int i = S + tid; i < a.P; i += kThreads) sorted[i] = ~0ull;
     __syncthreads();
@@ -669,7 +674,9 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
                 const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks, int64_t* position_ids,
                 int32_t* offsets, int32_t* cnts, uint16_t* out_scores, int64_t* out_selected, void* workspace,
                 int64_t workspace_bytes, void* stream) {
-  if (!D || !norm || !sum || !landmark_idx || !position_ids || !offsets || !cnts) {
+  // No previous slots: selection only, the ids in top-k order into out_selected.
+  const bool reorder = position_ids != nullptr;
+  if (!D || !norm || !sum || !landmark_idx || (reorder && (!offsets || !cnts)) || (!reorder && !out_selected)) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
   }
@@ -685,7 +692,7 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
   }
   int P = 64;
   while (P < select_sets) P <<= 1;
-  const int words = (num_chunks + 31) / 32;
+  const int words = reorder ? (num_chunks + 31) / 32 : 0;
   const size_t fixed = (static_cast<size_t>(words) * 8 + static_cast<size_t>(P) * 8 + 15) / 16 * 16;
   if (fixed > kLdsBudget) {
     skv_set_error("%s: %d chunks need %zu bytes of bitmap, above the LDS budget", what, num_chunks, fixed);

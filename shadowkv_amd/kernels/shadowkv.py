@@ -406,14 +406,20 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
     [rows] int32; out_scores: optional [rows, n] bf16 GQA-max probabilities; out_selected: optional
     [rows, select_sets] ids in top-k order (the reference's selected_chunks; costs a sort);
     workspace: optional device buffer of select_workspace_bytes(rows, n, select_sets) bytes, with
-    which few rows (<= 32) are each selected by many workgroups."""
+    which few rows (<= 32) are each selected by many workgroups. position_ids, offsets and cnts
+    None: selection only (no previous slots, no reorder), the ids in top-k order into the then
+    required out_selected (what a chunk pool selects before its own hit lookup)."""
     _dev(D, "D", torch.bfloat16)
     _dev(Norm, "Norm", torch.float32)
     _dev(Sum, "Sum", torch.float32)
     _dev(landmark_idx, "landmark_idx", torch.int64)
-    _dev(position_ids, "position_ids", torch.int64)
-    _dev(offsets, "offsets", torch.int32)
-    _dev(cnts, "cnts", torch.int32)
+    reorder = position_ids is not None
+    if reorder:
+        _dev(position_ids, "position_ids", torch.int64)
+        _dev(offsets, "offsets", torch.int32)
+        _dev(cnts, "cnts", torch.int32)
+    elif offsets is not None or cnts is not None or out_selected is None:
+        raise ValueError("without position_ids, offsets and cnts must be None and out_selected given")
     if landmark_idx.dim() != 2 or landmark_idx.shape[1] != n or landmark_idx.stride(1) != 1:
         raise ValueError("landmark_idx must be [rows, n] with contiguous rows")
     if not (1 <= select_sets <= min(n, 2048)):
@@ -423,11 +429,12 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
     _need(Norm, rows * m * tiles, "Norm")
     _need(Sum, rows * m * tiles, "Sum")
     _need(landmark_idx, (rows - 1) * landmark_idx.stride(0) + n, "landmark_idx")
-    for t, nm, e in ((position_ids, "position_ids", rows * select_sets), (offsets, "offsets", rows * select_sets),
-                     (cnts, "cnts", rows)):
-        if not t.is_contiguous():
-            raise ValueError(f"{nm} must be contiguous")
-        _need(t, e, nm)
+    if reorder:
+        for t, nm, e in ((position_ids, "position_ids", rows * select_sets), (offsets, "offsets", rows * select_sets),
+                         (cnts, "cnts", rows)):
+            if not t.is_contiguous():
+                raise ValueError(f"{nm} must be contiguous")
+            _need(t, e, nm)
     sp = None
     if out_scores is not None:
         _dev(out_scores, "out_scores", torch.bfloat16)
@@ -439,8 +446,8 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
         _need(out_selected, rows * select_sets, "out_selected")
         op = out_selected.data_ptr()
     args = (D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), rows, m, n, landmark_idx.data_ptr(),
-            landmark_idx.stride(0), select_sets, num_chunks, position_ids.data_ptr(), offsets.data_ptr(),
-            cnts.data_ptr(), sp, op)
+            landmark_idx.stride(0), select_sets, num_chunks, position_ids.data_ptr() if reorder else None,
+            offsets.data_ptr() if reorder else None, cnts.data_ptr() if reorder else None, sp, op)
     if workspace is None:
         _lib.call("skv_select_chunks", *args, _stream())
     else:

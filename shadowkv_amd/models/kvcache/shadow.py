@@ -366,9 +366,10 @@ class ShadowKVCache_CPU(KVCacheBase):
             # GQA-max scores, the selection in top-k order (kept in position_ids), then the pool's
             # hits, victims and miss list (cnts = hits; misses at [cnts, S) of miss_ids / miss_slot).
             rows, S = B * H, self.select_sets
-            shadowkv.softmax_gqa_max(self.gemm_o, self.norm, self.sum, self.chunk_attn.view(rows, n), rows, G, n)
             sel = self.position_ids[layer_idx].view(rows, S)
-            shadowkv.topk_gather(self.chunk_attn.view(rows, n), self.k_landmark_idx[layer_idx].view(rows, n), S, sel)
+            shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, rows, G, n,
+                                   self.k_landmark_idx[layer_idx].view(rows, n), S, self.chunks, None, None, None,
+                                   out_scores=self.chunk_attn, out_selected=sel, workspace=self.select_workspace)
             shadowkv.pool_assign(sel, self.chunks, self.slot_of[layer_idx], self.slot_chunk[layer_idx],
                                  self.slot_used[layer_idx], self.pool_clock[layer_idx], self.slot_list,
                                  self.miss_ids, self.miss_slot, self.cnts)

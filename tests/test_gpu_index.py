@@ -206,7 +206,12 @@ def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, spl
         staging = torch.empty_like(scores)  # the many-workgroup path needs the keys in global memory
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos3, off3, cnt3, out_scores=staging,
                            workspace=ws)
+    # selection only (no previous slots; a chunk pool's selection): the ids in top-k order
+    sel4 = torch.full_like(sel, -7)
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, None, None, None,
+                           out_scores=torch.empty_like(scores), out_selected=sel4, workspace=ws)
     torch.cuda.synchronize()
+    assert torch.equal(sel4, sel)
     assert torch.equal(pos3, pos1) and torch.equal(off3, off1) and torch.equal(cnt3, cnt1)
     assert torch.equal(scores2, scores)
     assert torch.equal(sel2, sel)

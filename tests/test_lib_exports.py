@@ -51,3 +51,14 @@ def test_selection_workspace_plan():
     assert rc == 1 and "null workspace" in _lib.last_error()
     rc = lib.skv_select_chunks_ws(p, p, p, 8, 4, 130680, p, 130680, 2048, 131000, p, p, p, p, None, p, 1, None)
     assert rc == 1 and "workspace of 1 bytes" in _lib.last_error()
+
+
+def test_selection_only_needs_an_output():
+    """Selection without previous slots (null position_ids, offsets, cnts) writes only the ids in
+    top-k order, so out_selected must be given; a half-given reorder triple is rejected too."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    rc = lib.skv_select_chunks(p, p, p, 8, 4, 1000, p, 1000, 256, 1100, None, None, None, p, None, None)
+    assert rc == 1 and "null pointer" in _lib.last_error()
+    rc = lib.skv_select_chunks(p, p, p, 8, 4, 1000, p, 1000, 256, 1100, p, None, p, p, None, None)
+    assert rc == 1 and "null pointer" in _lib.last_error()
