@@ -13,11 +13,32 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 constexpr int kMaxPool = 16384;  // slots per row (LDS bitmap of 2 KB)
 constexpr int kMaxSel = 2048;
-constexpr int kSelPerThread = kMaxSel / kThreads;
+constexpr int kSelPer = kMaxSel / kThreads;    // selection entries per thread
+constexpr int kSlotPer = kMaxPool / kThreads;  // slots per thread
 
+// One histogram count per lane where `count` holds. Last-use keys cluster on a few recent steps,
+// so a wave's bins are often all equal: then one atomic adds the wave's count (instead of up to 64
+// atomics on one LDS address); otherwise every counting lane adds its own. Called by whole waves.
+__device__ __forceinline__ void hist_add(int* hist, uint32_t bin, bool count) {
+  const uint64_t act = __ballot(count);
+  if (act == 0) return;
+  const int leader = __ffsll(static_cast<unsigned long long>(act)) - 1;
+  const uint32_t lb = __builtin_amdgcn_readlane(bin, leader);
+  if (__ballot(count && bin != lb) == 0) {
+    if ((threadIdx.x & 63) == static_cast<unsigned>(leader)) atomicAdd(&hist[lb], __popcll(act));
+  } else if (count) {
+    atomicAdd(&hist[bin], 1);
+  }
+}
+
+// Every thread owns a contiguous range of the selection (<= kSelPer entries) and of the slots
+// (<= kSlotPer), so block scans over the threads rank entries and slots in index order. All
+// global reads are issued up front (the selection and every slot's last use together, then the
+// selected chunks' table entries), so a row costs two dependent round trips; the victims' radix
+// select runs on the keys held in registers.
 __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __restrict__ selected, int S,
                                                                int chunks, int P, int32_t* __restrict__ slot_of,
                                                                int32_t* __restrict__ slot_chunk,
@@ -33,6 +54,7 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
   __shared__ int scan[kThreads / 64 + 1];
   __shared__ int bin_sh, need_sh;
   const int row = blockIdx.x;
+  const int tid = threadIdx.x;
   const int64_t* sel = selected + static_cast<int64_t>(row) * S;
   int32_t* so = slot_of + static_cast<int64_t>(row) * chunks;
   int32_t* sc = slot_chunk + static_cast<int64_t>(row) * P;
@@ -40,61 +62,71 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
   int32_t* sl = slot_list + static_cast<int64_t>(row) * S;
   const int32_t t = clock[row] + 1;
 
-  for (int w = threadIdx.x; w < (P + 31) / 32; w += kThreads) hit_bits[w] = 0u;
+  const int sper = (S + kThreads - 1) / kThreads;  // <= kSelPer
+  const int j0 = min(S, tid * sper), j1 = min(S, j0 + sper);
+  const int pper = (P + kThreads - 1) / kThreads;  // <= kSlotPer
+  const int v0 = min(P, tid * pper), v1 = min(P, v0 + pper);
+  int64_t c[kSelPer];
+#pragma unroll
+  for (int u = 0; u < kSelPer; ++u) c[u] = (j0 + u < j1) ? sel[j0 + u] : -1;
+  // Victim keys: last use + 1 (empty slots: 0); a hit slot's key is replaced below, so a hit's
+  // last-use update racing with this read does not matter.
+  uint32_t key[kSlotPer];
+#pragma unroll
+  for (int u = 0; u < kSlotPer; ++u) key[u] = (v0 + u < v1) ? static_cast<uint32_t>(su[v0 + u] + 1) : 0xffffffffu;
+  for (int w = tid; w < (P + 31) / 32; w += kThreads) hit_bits[w] = 0u;
   __syncthreads();
-  // Hits keep their slot. Each thread owns a contiguous range of the selection (order kept) and
-  // remembers which of its entries missed.
-  const int sper = (S + kThreads - 1) / kThreads;  // <= kSelPerThread
-  const int j0 = min(S, static_cast<int>(threadIdx.x) * sper), j1 = min(S, j0 + sper);
+  // Hits keep their slot; the thread remembers which of its entries missed.
+  int s[kSelPer];
+#pragma unroll
+  for (int u = 0; u < kSelPer; ++u) s[u] = (c[u] >= 0 && c[u] < chunks) ? so[c[u]] : -1;
   uint32_t miss_mask = 0;
   int misses = 0;
-  for (int j = j0; j < j1; ++j) {
-    const int64_t c = sel[j];
-    const int s = (c >= 0 && c < chunks) ? so[c] : -1;
-    if (s >= 0 && s < P) {
-      sl[j] = s;
-      su[s] = t;
-      atomicOr(&hit_bits[s >> 5], 1u << (s & 31));
+#pragma unroll
+  for (int u = 0; u < kSelPer; ++u) {
+    if (j0 + u >= j1) continue;
+    if (s[u] >= 0 && s[u] < P) {
+      sl[j0 + u] = s[u];
+      su[s[u]] = t;
+      atomicOr(&hit_bits[s[u] >> 5], 1u << (s[u] & 31));
     } else {
-      miss_mask |= 1u << (j - j0);
+      miss_mask |= 1u << u;
       ++misses;
     }
   }
   int m;
   int miss_rank = skv::block_exclusive_scan(misses, scan, &m);  // its barriers publish hit_bits
+#pragma unroll
+  for (int u = 0; u < kSlotPer; ++u) {
+    const int v = v0 + u;
+    if (v < v1 && ((hit_bits[v >> 5] >> (v & 31)) & 1u)) key[u] = 0xffffffffu;
+  }
 
-  // Victims: the m smallest keys over the slots, key = last use + 1 (empty slots: 0; hit slots
-  // excluded), by a 4-pass 8-bit radix select; ties to the lowest slot.
-  const int pper = (P + kThreads - 1) / kThreads;
-  const int v0 = min(P, static_cast<int>(threadIdx.x) * pper), v1 = min(P, v0 + pper);
-  auto key_of = [&](int v) -> uint32_t {
-    if ((hit_bits[v >> 5] >> (v & 31)) & 1u) return 0xffffffffu;
-    return static_cast<uint32_t>(su[v] + 1);  // last use >= -1
-  };
+  // Victims: the m smallest keys over the slots (hit slots excluded by their key), by a 4-pass
+  // 8-bit radix select; ties to the lowest slot.
   uint32_t prefix = 0, mask = 0;
   int need = m;
   if (m > 0) {  // workgroup-uniform
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
-      for (int i = threadIdx.x; i < 256; i += kThreads) hist[i] = 0;
+      for (int i = tid; i < 256; i += kThreads) hist[i] = 0;
       __syncthreads();
-      for (int v = v0; v < v1; ++v) {
-        const uint32_t kk = key_of(v);
-        if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255], 1);
-      }
+#pragma unroll
+      for (int u = 0; u < kSlotPer; ++u)
+        hist_add(hist, (key[u] >> shift) & 255u, v0 + u < v1 && (key[u] & mask) == prefix);
       __syncthreads();
-      if (threadIdx.x < 64) {
+      if (tid < 64) {
         int c4[4], tot = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          c4[u] = hist[threadIdx.x * 4 + u];
+          c4[u] = hist[tid * 4 + u];
           tot += c4[u];
         }
         int before = skv::wave_inclusive_scan(tot) - tot;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           if (before < need && need <= before + c4[u]) {
-            bin_sh = threadIdx.x * 4 + u;
+            bin_sh = tid * 4 + u;
             need_sh = need - before;
           }
           before += c4[u];
@@ -111,10 +143,11 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
   // it (lowest slots); each thread's first victim rank from two block scans over the slot ranges.
   int lt = 0, eq = 0;
   if (m > 0) {
-    for (int v = v0; v < v1; ++v) {
-      const uint32_t kk = key_of(v);
-      lt += kk < prefix;
-      eq += kk == prefix;
+#pragma unroll
+    for (int u = 0; u < kSlotPer; ++u) {
+      if (v0 + u >= v1) continue;
+      lt += key[u] < prefix;
+      eq += key[u] == prefix;
     }
   }
   int eq_total, taken_total;
@@ -123,11 +156,12 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
   int rank = skv::block_exclusive_scan(lt + my_ties, scan, &taken_total);
   if (m > 0) {
     int e = eq_before;
-    for (int v = v0; v < v1; ++v) {
-      const uint32_t kk = key_of(v);
-      bool take = kk < prefix;
-      if (kk == prefix) take = e++ < need;
-      if (take) victim[rank++] = v;
+#pragma unroll
+    for (int u = 0; u < kSlotPer; ++u) {
+      if (v0 + u >= v1) continue;
+      bool take = key[u] < prefix;
+      if (key[u] == prefix) take = e++ < need;
+      if (take) victim[rank++] = v0 + u;
     }
   }
   __syncthreads();
@@ -135,21 +169,22 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
   // selected chunk, so the entries cleared (the victim's old chunk) and set (the miss) are all
   // distinct.
   const int base = S - m;
-  for (int j = j0; j < j1; ++j) {
-    if (!((miss_mask >> (j - j0)) & 1u)) continue;
-    const int64_t c = sel[j];
+#pragma unroll
+  for (int u = 0; u < kSelPer; ++u) {
+    if (!((miss_mask >> u) & 1u)) continue;
+    const int64_t cu = c[u];
     const int v = victim[miss_rank];
     const int32_t old = sc[v];
     if (old >= 0 && old < chunks) so[old] = -1;
-    if (c >= 0 && c < chunks) so[c] = v;
-    sc[v] = static_cast<int32_t>(c);
+    if (cu >= 0 && cu < chunks) so[cu] = v;
+    sc[v] = static_cast<int32_t>(cu);
     su[v] = t;
-    sl[j] = v;
-    miss_ids[static_cast<int64_t>(row) * S + base + miss_rank] = static_cast<int32_t>(c);
+    sl[j0 + u] = v;
+    miss_ids[static_cast<int64_t>(row) * S + base + miss_rank] = static_cast<int32_t>(cu);
     miss_slot[static_cast<int64_t>(row) * S + base + miss_rank] = v;
     ++miss_rank;
   }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     cnts[row] = base;
     clock[row] = t;
   }

@@ -126,6 +126,29 @@ def test_rebuild_k_rope_fused(gpu, glm, per_head_u, shared_sv, R, S, c):
                                    rtol=RTOL, atol=ATOL)
 
 
+def test_rebuild_k_rope_long_selection(gpu):
+    """The 1M-context selection size: 2048 chunks per head (16384 rows) at positions up to 2^18,
+    RoPE theta 3.58e6, part of every head already in place (random hit counts)."""
+    B, H, ctx, R, S, c = 1, 8, 262144, 160, 2048, 8
+    _say("rebuild_k_rope long selection S=2048 ctx=262144")
+    U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 5)
+    cs = oracle.build_cos_sin_cache(ctx, 3.58e6)
+    start = 3136
+    cache = torch.randn(B, H, start + S * c + 64, 128).to(torch.bfloat16)
+    want = oracle.rebuild_k_rope(U, SV, ids, cnts, cs, c, cache.clone(), start)
+    cg = cache.to(gpu)
+    shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
+    torch.cuda.synchronize()
+    got = cg.cpu()
+    assert torch.equal(got[:, :, :start], cache[:, :, :start])
+    assert torch.equal(got[:, :, start + S * c:], cache[:, :, start + S * c:])
+    for h in range(H):
+        miss = start + int(cnts[h]) * c
+        assert torch.equal(got[0, h, start:miss], cache[0, h, start:miss])  # hit rows untouched
+        torch.testing.assert_close(got[0, h, miss:start + S * c].float(), want[0, h, miss:start + S * c].float(),
+                                   rtol=RTOL, atol=ATOL)
+
+
 def test_rebuild_basis_rows_exact(gpu):
     # U rows that are basis vectors make every K row an SV column: exact through MFMA and RoPE.
     B, H, ctx, R, S, c = 1, 8, 1024, 160, 64, 8

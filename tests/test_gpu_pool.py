@@ -21,7 +21,8 @@ def _say(msg):
 
 @pytest.mark.parametrize("rows,chunks,S,P,drift", [(16, 1000, 64, 64, 0.3), (16, 1000, 64, 96, 0.3),
                                                    (8, 4000, 256, 1024, 0.5), (4, 600, 100, 101, 1.0),
-                                                   (2, 20000, 2048, 4096, 0.2)])
+                                                   (2, 20000, 2048, 4096, 0.2), (2, 3000, 300, 1025, 0.4),
+                                                   (1, 60000, 2048, 16384, 0.3)])
 def test_pool_assign_matches_oracle(gpu, rows, chunks, S, P, drift):
     _say(f"pool_assign rows={rows} chunks={chunks} S={S} P={P} drift={drift}")
     rng = np.random.default_rng(rows + S + P)
