@@ -43,9 +43,19 @@ int fetch_workgroups() {
 // already in place; the rest are moved in batches. Within a batch every load is drained
 // before any store (a source slot of one chunk can be the destination of another chunk of
 // the same batch); a later batch only reads slots beyond every destination of earlier ones.
-__global__ void __launch_bounds__(kThreads) compact_hits_kernel(u32x4* __restrict__ buf, const int32_t* __restrict__ offsets,
-                                                                 const int32_t* __restrict__ cnts, int64_t row_stride_vec,
-                                                                 int64_t row_offset_vec, int S, int chunk_vec) {
+// One 1024-thread workgroup per row: the row's offsets are read once into LDS (map_size <=
+// kCompactLdsMap; beyond that they are read from global memory), so a batch of 64 chunks costs
+// one round trip for its loads and one for its stores.
+constexpr int kCompactThreads = 1024;
+constexpr int kCompactLdsMap = 8192;
+
+template <bool kLdsOffsets>
+__global__ void __launch_bounds__(kCompactThreads) compact_hits_kernel(u32x4* __restrict__ buf,
+                                                                        const int32_t* __restrict__ offsets,
+                                                                        const int32_t* __restrict__ cnts,
+                                                                        int64_t row_stride_vec, int64_t row_offset_vec,
+                                                                        int S, int chunk_vec) {
+  __shared__ int offs_lds[kLdsOffsets ? kCompactLdsMap : 1];
   __shared__ int first_moved;
   const int row = blockIdx.x;
   const int cnt = min(cnts[row], S);
@@ -53,36 +63,48 @@ __global__ void __launch_bounds__(kThreads) compact_hits_kernel(u32x4* __restric
   const int32_t* offs = offsets + static_cast<int64_t>(row) * S;
   if (threadIdx.x == 0) first_moved = cnt;
   __syncthreads();
-  for (int j = threadIdx.x; j < cnt; j += blockDim.x)
-    if (offs[j] != j) atomicMin(&first_moved, j);
+  for (int j = threadIdx.x; j < cnt; j += blockDim.x) {
+    const int o = offs[j];
+    if (kLdsOffsets) offs_lds[j] = o;
+    if (o != j) atomicMin(&first_moved, j);
+  }
   __syncthreads();
+  const int32_t* src_of = kLdsOffsets ? offs_lds : offs;
   const int p = first_moved;
   u32x4* base = buf + static_cast<int64_t>(row) * row_stride_vec + row_offset_vec;
-  const int64_t total = static_cast<int64_t>(cnt - p) * chunk_vec;
-  for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(blockDim.x) * kUnroll) {
+  const int total = (cnt - p) * chunk_vec;  // < 2^31: map_size * chunk_vec is bounded on the host
+  for (int v0 = 0; v0 < total; v0 += static_cast<int>(blockDim.x) * kUnroll) {
     u32x4 r[kUnroll];
+    int dst[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      const int v = v0 + u * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+      dst[u] = -1;
       if (v < total) {
-        int j = p + static_cast<int>(v / chunk_vec);
-        int e = static_cast<int>(v % chunk_vec);
-        int src = offs[j];
-        if (src >= 0 && src < S) r[u] = base[static_cast<int64_t>(src) * chunk_vec + e];
+        const int j = p + v / chunk_vec;
+        const int e = v - (j - p) * chunk_vec;
+        const int src = src_of[j];
+        if (src >= 0 && src < S) {
+          r[u] = base[static_cast<int64_t>(src) * chunk_vec + e];
+          dst[u] = j * chunk_vec + e;
+        }
       }
     }
     skv::drain_and_barrier();
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
-      if (v < total) {
-        int j = p + static_cast<int>(v / chunk_vec);
-        int e = static_cast<int>(v % chunk_vec);
-        int src = offs[j];
-        if (src >= 0 && src < S) base[static_cast<int64_t>(j) * chunk_vec + e] = r[u];
-      }
-    }
+    for (int u = 0; u < kUnroll; ++u)
+      if (dst[u] >= 0) base[dst[u]] = r[u];
   }
+}
+
+void launch_compact_hits(u32x4* buf, const int32_t* offsets, const int32_t* cnts, int rows, int64_t row_stride_vec,
+                         int64_t row_offset_vec, int S, int chunk_vec, hipStream_t s) {
+  if (S <= kCompactLdsMap)
+    hipLaunchKernelGGL(compact_hits_kernel<true>, dim3(rows), dim3(kCompactThreads), 0, s, buf, offsets, cnts,
+                       row_stride_vec, row_offset_vec, S, chunk_vec);
+  else
+    hipLaunchKernelGGL(compact_hits_kernel<false>, dim3(rows), dim3(kCompactThreads), 0, s, buf, offsets, cnts,
+                       row_stride_vec, row_offset_vec, S, chunk_vec);
 }
 
 // Copies slots [i0, i1) of one row, 16-byte vectors, kUnroll loads in flight per lane. With
@@ -165,6 +187,10 @@ int check_common(const char* what, const void* a, const void* b, int batch_size,
     skv_set_error("%s: chunk_elems=%d must be a positive multiple of 8 (16-byte units)", what, chunk_elems);
     return SKV_EUNSUPPORTED;
   }
+  if (static_cast<int64_t>(map_size) * chunk_elems > (int64_t{1} << 31)) {
+    skv_set_error("%s: map_size=%d chunks of %d elements exceed 2^31 elements per row", what, map_size, chunk_elems);
+    return SKV_EUNSUPPORTED;
+  }
   return SKV_OK;
 }
 
@@ -186,9 +212,8 @@ extern "C" int skv_gather_copy_d2d_with_offsets(void* keys, const int32_t* offse
                   (long long)gpu_k_offset, (long long)gpu_k_stride, (long long)gpu_k_length);
     return SKV_EINVAL;
   }
-  hipLaunchKernelGGL(compact_hits_kernel, dim3(batch_size * heads), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<u32x4*>(keys), offsets, cnts, gpu_k_stride / 8, gpu_k_offset / 8, map_size,
-                     chunk_elems / 8);
+  launch_compact_hits(static_cast<u32x4*>(keys), offsets, cnts, batch_size * heads, gpu_k_stride / 8, gpu_k_offset / 8,
+                      map_size, chunk_elems / 8, static_cast<hipStream_t>(stream));
   return skv_check_launch(what);
 }
 
@@ -216,8 +241,8 @@ int value_fetch(const char* what, bool compact, const void* values, void* v_cach
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows = batch_size * heads;
   if (compact) {
-    hipLaunchKernelGGL(compact_hits_kernel, dim3(rows), dim3(kThreads), 0, s, static_cast<u32x4*>(v_cache_buffer),
-                       offsets, cnts, gpu_v_stride / 8, gpu_v_offset / 8, map_size, chunk_elems / 8);
+    launch_compact_hits(static_cast<u32x4*>(v_cache_buffer), offsets, cnts, rows, gpu_v_stride / 8, gpu_v_offset / 8,
+                        map_size, chunk_elems / 8, s);
     rc = skv_check_launch(what);
     if (rc) return rc;
   }

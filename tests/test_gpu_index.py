@@ -4,6 +4,7 @@ import pytest
 import torch
 
 import oracle
+from shadowkv_amd import _lib
 from shadowkv_amd.kernels import shadowkv
 from tests.golden import make_golden
 
@@ -124,6 +125,40 @@ def test_cached_gather_copy(gpu, hit_frac, chunk, S, pinned):
                                           prefix * D, buf_len * D, S, misses_only=True)
     torch.cuda.synchronize()
     assert torch.equal(sdev.cpu().view(torch.int16), got.view(torch.int16))  # bit patterns (some are NaNs)
+
+
+@pytest.mark.parametrize("S,chunk,hit_frac", [(2048, 16, 0.9), (9000, 2, 0.95), (300, 8, 1.0)])
+def test_compact_hits_many_batches(gpu, S, chunk, hit_frac):
+    """The in-place hit compaction over rows whose moving hits span many 64-chunk batches, with
+    the offsets held in LDS (map_size <= 8192) and read from global memory (9000)."""
+    rows, D = 3, 128
+    E = chunk * D
+    _say(f"compact_hits S={S} chunk={chunk} hit={hit_frac}")
+    rng = np.random.default_rng(S + chunk)
+    sparse = rng.integers(-32768, 32767, size=(rows, S, E), dtype=np.int16)
+    offs = np.zeros((rows, S), dtype=np.int32)
+    cnts = np.zeros(rows, dtype=np.int32)
+    for r in range(rows):
+        c = int(hit_frac * S) - r  # ragged hit counts
+        hit_slots = np.sort(rng.choice(S, size=c, replace=False)).astype(np.int32)
+        offs[r, :c] = hit_slots
+        offs[r, c:] = rng.integers(0, 4 * S, size=S - c)  # miss ids: not read by the compaction
+        cnts[r] = c
+    prefix = 2 * chunk
+    buf_len = prefix + S * chunk + 8
+    dev = torch.zeros(1, rows, buf_len, D, dtype=torch.int16)
+    dev[0, :, prefix:prefix + S * chunk] = torch.from_numpy(sparse).view(rows, S * chunk, D)
+    kdev = dev.view(torch.bfloat16).to(gpu)
+    offs_g, cnts_g = torch.from_numpy(offs.reshape(-1)).to(gpu), torch.from_numpy(cnts).to(gpu)
+    # through the C ABI: the Python shim caps map_size at the selection maximum (2048)
+    _lib.call("skv_gather_copy_d2d_with_offsets", kdev.data_ptr(), offs_g.data_ptr(), cnts_g.data_ptr(), 1, rows,
+              S * E, prefix * D, buf_len * D, S, E, int(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    got = kdev.cpu().view(torch.int16)
+    assert torch.equal(got[0, :, :prefix], dev[0, :, :prefix])
+    assert torch.equal(got[0, :, prefix + S * chunk:], dev[0, :, prefix + S * chunk:])
+    want = oracle.compact_hits(sparse, offs, cnts)
+    assert np.array_equal(got[0, :, prefix:prefix + S * chunk].reshape(rows, S, E).numpy(), want)
 
 
 def test_gather_copy_plain(gpu):
