@@ -53,7 +53,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--model", choices=["llama31_8b", "glm4_9b", "llama3_8b_1m"], default="llama31_8b",
                    help="model shape of the decode workload (random weights): Llama-3.1-8B (the headline), "
                         "GLM-4-9B (2 kv heads of 16 query heads, GLM RoPE), Llama-3-8B-1M (RoPE theta 3.58e6)")
-    p.add_argument("--lanes", type=int, default=2, help="independent batch slices pipelined per layer")
+    p.add_argument("--lanes", type=int, default=None,
+                   help="independent batch slices pipelined per layer (default: 2 where the value fetch outweighs the dense layers, see decode_model.auto_lanes)")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
     p.add_argument("--graph-steps", type=int, default=8,
                    help="decode steps per captured graph (one continuous lane pipeline across steps); "
@@ -687,7 +688,8 @@ def main() -> int:
         shape = replace(shape, layers=args.layers)
     t0 = time.time()
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
-    lanes = args.lanes if args.batch % args.lanes == 0 else 1
+    lanes = args.lanes if args.lanes else decode_model.auto_lanes(shape, args.batch, args.budget)
+    lanes = lanes if args.batch % lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes,
                                           chunk_cache=args.chunk_cache)

@@ -49,6 +49,21 @@ LLAMA3_8B_1M = ModelShape("Llama-3-8B-1M", 32, 4096, 14336, 32, 8, 128256, 35800
 GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="glm")
 
 
+
+def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int) -> int:
+    """Batch lanes for the decode step: 2 when a layer's value fetch over the host link outlasts
+    three passes over the layer's dense weights, else 1. Each lane streams the dense weights once
+    per layer, so a second lane only pays off where the fetch it hides is long: measured on one
+    MI355X (tokens/s, 1 vs 2 lanes): Llama-3.1-8B ctx 122880 batch 2 197 / 160 (fetch / weights
+    2.2), batch 4 262 / 271 (4.4), batch 8 271 / 383 (8.9); GLM-4-9B ctx 262144 batch 4 393 / 261
+    (1.2). Rates: 52 GB/s host link, 6 TB/s weight stream."""
+    if batch % 2:
+        return 1
+    d = shape.head_dim
+    weights = 2 * shape.hidden * ((shape.heads + 2 * shape.kv_heads) * d + shape.heads * d + 3 * shape.ffn)
+    fetch = batch * shape.kv_heads * sparse_budget * d * 2
+    return 2 if fetch / 52e9 > 3 * weights / 6e12 else 1
+
 def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin: torch.Tensor | None = None) -> None:
     """Give `cache` the post-prefill state of a ctx-token prompt (random contents, exact shapes)."""
     dev = torch.device(cache.device)

@@ -23,3 +23,15 @@ def test_rope_output_with_smaller_extent_than_input_strides_is_rejected():
     need = shadowkv.max_offset(sizes, strides) + 1
     assert need > out.numel()          # the shape that faulted
     assert need <= qkv.numel()         # in place, inside the QKV buffer: fine
+
+
+def test_auto_lanes_follows_the_measured_choices():
+    """Two pipelined lanes only where a layer's value fetch outlasts three passes over its dense
+    weights: the faster setting measured on one MI355X for each of these shapes."""
+    from shadowkv_amd import decode_model as dm
+    assert dm.auto_lanes(dm.LLAMA31_8B, 8, 2048) == 2   # 383 vs 271 tokens/s
+    assert dm.auto_lanes(dm.LLAMA31_8B, 4, 2048) == 2   # 271 vs 262
+    assert dm.auto_lanes(dm.LLAMA31_8B, 2, 2048) == 1   # 197 vs 160
+    assert dm.auto_lanes(dm.GLM4_9B, 4, 2048) == 1      # 393 vs 261
+    assert dm.auto_lanes(dm.LLAMA3_8B_1M, 1, 16384) == 1  # one sequence: nothing to pipeline
+    assert dm.auto_lanes(dm.LLAMA31_8B, 7, 2048) == 1   # odd batch
