@@ -443,6 +443,8 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
     op = None
     if out_selected is not None:
         _dev(out_selected, "out_selected", torch.int64)
+        if not out_selected.is_contiguous():
+            raise ValueError("out_selected must be contiguous")
         _need(out_selected, rows * select_sets, "out_selected")
         op = out_selected.data_ptr()
     args = (D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), rows, m, n, landmark_idx.data_ptr(),
