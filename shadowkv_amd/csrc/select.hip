@@ -654,10 +654,15 @@ size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws) {
 
 // Path of a selection call. kFused: the selection kernel computes the keys itself (one workgroup
 // per row). kSplit: few rows (rows * 8 <= 256 CUs) and m*n >= 2^15, so the keys come from the
-// many-workgroup softmax kernel first. kParts: as kSplit, and long rows (n >= 65536) with a
+// many-workgroup softmax kernel first. kParts: as kSplit, and long rows (n >= kPartsMinKeys) with a
 // workspace, so the selection passes also run over many workgroups per row. Environment
 // SKV_SELECT_SPLIT=0/1/2 forces fused / split / parts (parts only with a workspace), read per call.
 enum SelectPath { kFused = 0, kSplitPath = 1, kParts = 2 };
+// Row length from which the few-row selection runs its radix passes over many workgroups per row.
+// Measured at 8 rows, keys-first vs many workgroups: 15304 keys 17.9 vs 23.6 µs; 32712 keys 32.5
+// vs 30.4 µs alone, but the GLM-4-9B decode step is slower with the six launches (387 vs 394
+// tokens/s); 130680 keys 93 vs 45 µs.
+constexpr int kPartsMinKeys = 65536;
 
 SelectPath select_path(int rows, int m, int n, bool has_scores, bool has_ws) {
   if (!has_scores) return kFused;
@@ -667,7 +672,7 @@ SelectPath select_path(int rows, int m, int n, bool has_scores, bool has_ws) {
     return v == 2 ? (has_ws ? kParts : kSplitPath) : static_cast<SelectPath>(v);
   }
   if (rows > 32 || static_cast<int64_t>(m) * n < (int64_t{1} << 15)) return kFused;
-  return (has_ws && n >= 65536) ? kParts : kSplitPath;
+  return (has_ws && n >= kPartsMinKeys) ? kParts : kSplitPath;
 }
 
 int select_impl(const char* what, const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
