@@ -43,13 +43,17 @@ int fetch_workgroups() {
 // already in place; the rest are moved in batches. Within a batch every load is drained
 // before any store (a source slot of one chunk can be the destination of another chunk of
 // the same batch); a later batch only reads slots beyond every destination of earlier ones.
-// One 1024-thread workgroup per row: the row's offsets are read once into LDS (map_size <=
-// kCompactLdsMap; beyond that they are read from global memory), so a batch of 64 chunks costs
-// one round trip for its loads and one for its stores.
-constexpr int kCompactThreads = 1024;
+// One workgroup per row: the row's offsets are read once into LDS (map_size <= kCompactLdsMap;
+// beyond that they are read from global memory), so a batch costs one round trip for its loads
+// and one for its stores. Long maps (>= kCompactWideMap slots) take 1024 threads (batches of 64
+// chunks of 2 KB); short ones 256, which keeps the many small rows of a batched decode step from
+// crowding the concurrent host-link fetch (Llama-3.1-8B batch 8, 256 slots: 1024 threads cost
+// 1.7 of 383 tokens/s; Llama-3-8B-1M, 2048 slots: the value-hit move takes 7 µs against 29 µs
+// with 256 threads re-reading the offsets per batch).
 constexpr int kCompactLdsMap = 8192;
+constexpr int kCompactWideMap = 1024;
 
-template <bool kLdsOffsets>
+template <bool kLdsOffsets, int kCompactThreads>
 __global__ void __launch_bounds__(kCompactThreads) compact_hits_kernel(u32x4* __restrict__ buf,
                                                                         const int32_t* __restrict__ offsets,
                                                                         const int32_t* __restrict__ cnts,
@@ -99,11 +103,14 @@ __global__ void __launch_bounds__(kCompactThreads) compact_hits_kernel(u32x4* __
 
 void launch_compact_hits(u32x4* buf, const int32_t* offsets, const int32_t* cnts, int rows, int64_t row_stride_vec,
                          int64_t row_offset_vec, int S, int chunk_vec, hipStream_t s) {
-  if (S <= kCompactLdsMap)
-    hipLaunchKernelGGL(compact_hits_kernel<true>, dim3(rows), dim3(kCompactThreads), 0, s, buf, offsets, cnts,
+  if (S < kCompactWideMap)
+    hipLaunchKernelGGL((compact_hits_kernel<true, 256>), dim3(rows), dim3(256), 0, s, buf, offsets, cnts,
+                       row_stride_vec, row_offset_vec, S, chunk_vec);
+  else if (S <= kCompactLdsMap)
+    hipLaunchKernelGGL((compact_hits_kernel<true, 1024>), dim3(rows), dim3(1024), 0, s, buf, offsets, cnts,
                        row_stride_vec, row_offset_vec, S, chunk_vec);
   else
-    hipLaunchKernelGGL(compact_hits_kernel<false>, dim3(rows), dim3(kCompactThreads), 0, s, buf, offsets, cnts,
+    hipLaunchKernelGGL((compact_hits_kernel<false, 1024>), dim3(rows), dim3(1024), 0, s, buf, offsets, cnts,
                        row_stride_vec, row_offset_vec, S, chunk_vec);
 }
 
