@@ -193,8 +193,8 @@ int skv_topk_gather(const uint16_t* scores, int64_t score_stride, const int64_t*
  * Replaces models/kvcache/shadow.py:553-574 after the scoring GEMM. D/norm/sum as produced by
  * skv_score_logits for `rows` batch entries of m query rows; landmark_idx rows of idx_stride;
  * position_ids/offsets [rows][select_sets]; cnts [rows]. Chunk ids (landmark ids and previous
- * slot ids) must lie in [0, num_chunks) (-1 marks an empty previous slot); num_chunks <= 237568
- * at select_sets <= 256 and <= 180224 at 2048 (two chunk bitmaps and the winner list in LDS).
+ * slot ids) must lie in [0, num_chunks) (-1 marks an empty previous slot); num_chunks <= 606208
+ * at select_sets <= 256 and <= 548864 at 2048 (two chunk bitmaps and the winner list in LDS).
  * out_scores ([rows][n] bf16 GQA-max probabilities) and out_selected ([rows][select_sets] ids in
  * top-k order) are optional, except that out_scores is required as staging when n is too large
  * for LDS. With out_scores given and few rows (rows <= 32, m*n >= 32768) the probabilities are

@@ -37,7 +37,7 @@ using skv::u32x4;
 constexpr int kThreads = 1024;
 constexpr int kMaxM = 16;
 constexpr int kMaxS = 2048;
-constexpr size_t kLdsBudget = 60 * 1024;  // dynamic LDS cap (static LDS adds ~1.4 KB)
+constexpr size_t kLdsBudget = 150 * 1024;  // dynamic LDS cap (static LDS adds ~1.4 KB; 160 KB per CU)
 
 struct SelectArgs {
   int vec;  // n % 8 == 0: 8-landmark units
@@ -202,11 +202,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   // The same keys in any order, for the histogram passes: with the keys in global memory the
   // workgroup reads the row interleaved (each wave load is 1 KB contiguous) with kB loads per lane
   // requested before the first is used, so a pass costs a few memory latencies, not one per unit.
-  auto for_keys_any = [&](auto&& f) {
-    if (a.n_lds || !a.vec) {
-      for_keys(f);
-      return;
-    }
+  auto for_keys_global_any = [&](auto&& f) {
     constexpr int kB = 4;
     const u32x4* sv = reinterpret_cast<const u32x4*>(srow);
     for (int u0 = tid; u0 < nu; u0 += kThreads * kB) {
@@ -221,6 +217,13 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
         }
       }
     }
+  };
+  auto for_keys_any = [&](auto&& f) {
+    if (a.n_lds || !a.vec) {
+      for_keys(f);
+      return;
+    }
+    for_keys_global_any(f);
   };
   {
     // Fused path: run-length-merged LDS atomics (a thread's consecutive keys often share a bin).
@@ -248,7 +251,20 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
         atomicAdd(&sh.hist[bin], 1u);
       }
     };
-    if (a.pre) {
+    if (a.pre && a.n_lds) {  // the keys staged in LDS on the way, for the later passes
+      if (a.vec) {
+        for_keys_global_any([&](int j, uint32_t kj) {
+          keys[j] = static_cast<uint16_t>(kj);
+          count_win(kj >> 8);
+        });
+      } else {
+        for (int j = lo; j < hi; ++j) {
+          const uint32_t kj = skv::bf16_order_key(srow[j]);
+          keys[j] = static_cast<uint16_t>(kj);
+          count_win(kj >> 8);
+        }
+      }
+    } else if (a.pre) {
       for_keys_any([&](int, uint32_t kj) { count_win(kj >> 8); });
     } else if (a.vec) {
       for (int u = ulo; u < uhi; ++u) {
@@ -716,7 +732,7 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
       return SKV_EINVAL;
     }
   }
-  const int n_lds = (!split && fixed + static_cast<size_t>(n) * 2 <= kLdsBudget) ? n : 0;
+  const int n_lds = (fixed + static_cast<size_t>(n) * 2 <= kLdsBudget) ? n : 0;
   if (!n_lds && !out_scores) {
     skv_set_error("%s: n=%d landmarks do not fit LDS; pass out_scores as staging", what, n);
     return SKV_EINVAL;
