@@ -195,7 +195,8 @@ def test_scoring(gpu, Z, m, n):
 
 @pytest.mark.parametrize("B,Hq,Hk,L,strided", [(1, 32, 8, 2497, True), (8, 32, 8, 2600, True), (2, 32, 2, 2497, True),
                                                (1, 8, 8, 1, False), (3, 16, 4, 300, False), (1, 32, 8, 19521, True),
-                                               (1, 32, 8, 8193, False), (2, 24, 2, 700, True), (1, 16, 1, 129, False)])
+                                               (1, 32, 8, 8193, False), (2, 24, 2, 700, True), (1, 16, 1, 129, False),
+                                               (1, 32, 2, 1, False), (2, 32, 2, 128, True), (1, 32, 4, 4097, False)])
 def test_sparse_attention(gpu, B, Hq, Hk, L, strided):
     _say(f"attention B={B} Hq={Hq} Hk={Hk} L={L}")
     g = torch.Generator().manual_seed(L)
