@@ -291,3 +291,35 @@ def test_select_chunks_all_ties(gpu, monkeypatch, rows, m, n, S, split):
     assert torch.equal(pos.cpu(), want)
     assert (cnt.cpu() == 0).all()
     assert torch.equal(off.view(rows, S).cpu(), want.to(torch.int32))
+
+
+@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("rows,m,n", [(4, 4, 256), (2, 16, 1000), (1, 8, 2048)])
+def test_select_chunks_selects_every_landmark(gpu, monkeypatch, rows, m, n, split):
+    """select_sets = n: every landmark is selected; with empty previous slots all are misses, so
+    the slots hold the landmark ids ascending and the top-k order is the scores' total order."""
+    S = n
+    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    _say(f"select every landmark rows={rows} m={m} n={n} split={split}")
+    g = torch.Generator().manual_seed(n + m)
+    q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
+    L = torch.randn(rows, n, 128, generator=g).to(torch.bfloat16).to(gpu)
+    lidx = torch.stack([torch.randperm(2 * n, generator=g)[:n].sort().values for _ in range(rows)]).to(gpu)
+    tiles = (n + 255) // 256
+    D = torch.empty(rows, m, n, dtype=torch.bfloat16, device=gpu)
+    norm = torch.empty(rows, m, tiles, device=gpu)
+    ssum = torch.empty_like(norm)
+    shadowkv.score_logits(q, L, D, norm, ssum, rows, m, n, 128)
+    pos = torch.full((rows, S), -1, dtype=torch.int64, device=gpu)
+    off = torch.empty(rows * S, dtype=torch.int32, device=gpu)
+    cnt = torch.empty(rows, dtype=torch.int32, device=gpu)
+    scores = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+    sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
+    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split == "ws" else None
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, 2 * n, pos, off, cnt, out_scores=scores,
+                           out_selected=sel, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(pos.cpu(), lidx.cpu())
+    assert (cnt.cpu() == 0).all()
+    assert torch.equal(off.view(rows, S).cpu(), lidx.cpu().to(torch.int32))
+    assert torch.equal(sel.cpu(), oracle.topk_gather(scores.cpu(), lidx.cpu(), S))
