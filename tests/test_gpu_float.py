@@ -149,6 +149,30 @@ def test_rebuild_k_rope_long_selection(gpu):
                                    rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("glm", [False, True])
+def test_rebuild_k_rope_extreme_hit_counts(gpu, glm):
+    """Rows with every chunk a hit (nothing rebuilt), no hit, one hit and one miss."""
+    B, H, ctx, R, S, c = 1, 4, 4096, 160, 256, 8
+    _say(f"rebuild extreme hit counts glm={glm}")
+    U, SV, ids, _ = _rebuild_case(B, H, ctx, R, S, c, 7)
+    cnts = torch.tensor([S, 0, 1, S - 1], dtype=torch.int32)
+    cs = oracle.build_glm_cos_sin_cache(ctx, 5e6) if glm else oracle.build_cos_sin_cache(ctx, 5e5)
+    start = 64
+    cache = torch.randn(B, H, start + S * c + 16, 128).to(torch.bfloat16)
+    want = oracle.rebuild_k_rope(U, SV, ids, cnts, cs, c, cache.clone(), start, glm=glm)
+    cg = cache.to(gpu)
+    shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
+    torch.cuda.synchronize()
+    got = cg.cpu()
+    assert torch.equal(got[0, 0], cache[0, 0])  # all hits: the row is untouched
+    for h in range(1, H):
+        miss = start + int(cnts[h]) * c
+        assert torch.equal(got[0, h, :miss], cache[0, h, :miss])
+        assert torch.equal(got[0, h, start + S * c:], cache[0, h, start + S * c:])
+        torch.testing.assert_close(got[0, h, miss:start + S * c].float(), want[0, h, miss:start + S * c].float(),
+                                   rtol=RTOL, atol=ATOL)
+
+
 def test_rebuild_basis_rows_exact(gpu):
     # U rows that are basis vectors make every K row an SV column: exact through MFMA and RoPE.
     B, H, ctx, R, S, c = 1, 8, 1024, 160, 64, 8
