@@ -268,6 +268,13 @@ int skv_silu_and_mul(const uint16_t* x, int64_t x_stride, uint16_t* out, int64_t
 int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride, uint16_t* y,
                int64_t y_stride, int m, int n, int k, void* stream);
 
+/* skv_linear on the SiLU-and-mul of the gate/up projection, formed as the rows are read: x rows
+ * hold [gate (k) | up (k)] (x_stride >= 2k) and the multiplied row is bf16(silu(gate) * up) as
+ * skv_silu_and_mul computes it, so the result equals skv_silu_and_mul followed by skv_linear
+ * (models/llama.py:114-118 then :214: act_fn and down_proj of the reference's MLP). */
+int skv_linear_silu_mul(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                        uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream);
+
 /* ---- f1: prefill encoder ----------------------------------------------------------------
  * Replace the chunk statistics, outlier selection and landmark compaction of prefill_kv_cache
  * (models/kvcache/shadow.py:486-519). skv_chunk_stats: for each (b, h, chunk i < chunks) of the

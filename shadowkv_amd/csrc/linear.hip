@@ -39,7 +39,15 @@ __device__ __forceinline__ void fold(float* v, bool upper) {
   }
 }
 
-template <int R, int MP>
+// bf16 pair of silu(g) * u from the bf16 pairs g2, u2 (element 0 in the low half), with the
+// arithmetic and single rounding of the SiLU-and-mul kernel (skv::silu_mul).
+__device__ __forceinline__ uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
+  return skv::f2bf2(skv::silu_mul(skv::bf_lo(g2), skv::bf_lo(u2)), skv::silu_mul(skv::bf_hi(g2), skv::bf_hi(u2)));
+}
+
+// kGated: x rows hold [gate (K) | up (K)] and the multiplied row is silu(gate) * up, formed from
+// the two halves as they are loaded (the down projection reading the gate/up projection's output).
+template <int R, int MP, bool kGated>
 __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* __restrict__ x, int64_t xs,
                                                                const uint16_t* __restrict__ w, int64_t ws,
                                                                uint16_t* __restrict__ y, int64_t ys, int M, int N,
@@ -72,22 +80,25 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
   // block) reads the row's first 16 bytes instead (valid for any K >= 8), and mac() zeroes its x,
   // so it adds 0. The select sits at the use, not at the load, so a prefetch never has to wait
   // for its own data.
-  auto load = [&](int b, u32x4* wv, u32x4* xv) {
+  auto load = [&](int b, u32x4* wv, u32x4* xv, u32x4* xu) {
     const int k = b * kBlockK + 8 * lane;
     const uint32_t boff = 2u * static_cast<uint32_t>(k < K ? k : 0);
 #pragma unroll
     for (int r = 0; r < R; ++r) wv[r] = skv::load_nt(reinterpret_cast<const u32x4*>(wr[r] + boff));
 #pragma unroll
-    for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const u32x4*>(xr[m] + boff);
+    for (int m = 0; m < MP; ++m) {
+      xv[m] = *reinterpret_cast<const u32x4*>(xr[m] + boff);
+      if (kGated) xu[m] = *reinterpret_cast<const u32x4*>(xr[m] + boff + 2u * static_cast<uint32_t>(K));
+    }
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the multiply that follows
   };
-  auto mac = [&](int b, const u32x4* wv, const u32x4* xv) {
+  auto mac = [&](int b, const u32x4* wv, const u32x4* xv, const u32x4* xu) {
     const bool ok = b * kBlockK + 8 * lane < K;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int m = 0; m < MP; ++m) {
-        const uint32_t xe = ok ? xv[m][e] : 0u;
+        const uint32_t xe = ok ? (kGated ? silu_mul2(xv[m][e], xu[m][e]) : xv[m][e]) : 0u;
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r][m] = dot2(wv[r][e], xe, acc[r][m]);
       }
@@ -98,21 +109,21 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
   // that block's loads (a conditional prefetch would make it wait for both sets).
   const int nb = wave < nblk ? (nblk - 1 - wave) / nw + 1 : 0;  // wave-uniform
   if (nb > 0) {
-    u32x4 wa[R], xa[MP], wb[R], xb[MP];
-    load(wave, wa, xa);
+    u32x4 wa[R], xa[MP], ua[MP], wb[R], xb[MP], ub[MP];
+    load(wave, wa, xa, ua);
     int b = wave, i = 1;  // set a holds block b = b_{i-1}; b_i is the next block to load
     for (; i + 1 < nb; i += 2, b += 2 * nw) {
-      load(b + nw, wb, xb);
-      mac(b, wa, xa);
-      load(b + 2 * nw, wa, xa);
-      mac(b + nw, wb, xb);
+      load(b + nw, wb, xb, ub);
+      mac(b, wa, xa, ua);
+      load(b + 2 * nw, wa, xa, ua);
+      mac(b + nw, wb, xb, ub);
     }
     if (i < nb) {
-      load(b + nw, wb, xb);
-      mac(b, wa, xa);
-      mac(b + nw, wb, xb);
+      load(b + nw, wb, xb, ub);
+      mac(b, wa, xa, ua);
+      mac(b + nw, wb, xb, ub);
     } else {
-      mac(b, wa, xa);
+      mac(b, wa, xa, ua);
     }
   }
 
@@ -147,7 +158,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int g_waves_override = -1;  // SKV_LINEAR_WAVES, read once
 
-template <int R, int MP>
+template <int R, int MP, bool kGated>
 void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16_t* y, int64_t ys, int M, int N, int K,
             hipStream_t s) {
   const int groups = (N + R - 1) / R;
@@ -159,14 +170,12 @@ void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16
   int nw = MP <= 4 ? 4 : groups <= 512 ? 4 : groups >= 8192 ? 2 : 1;
   if (g_waves_override > 0) nw = g_waves_override;
   while (nw > 1 && nw > nblk) nw /= 2;
-  hipLaunchKernelGGL((linear_kernel<R, MP>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y, ys, M, N, K);
+  hipLaunchKernelGGL((linear_kernel<R, MP, kGated>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y, ys, M, N, K);
 }
 
-}  // namespace
-
-extern "C" int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
-                          uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
-  const char* what = "linear";
+template <bool kGated>
+int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
   if (!x || !weight || !y) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -175,9 +184,11 @@ extern "C" int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* w
     skv_set_error("%s: m=%d n=%d k=%d (1 <= m <= 16, k a multiple of 8)", what, m, n, k);
     return SKV_EUNSUPPORTED;
   }
-  if (!aligned16(x) || !aligned16(weight) || x_stride % 8 || weight_stride % 8 || x_stride < k ||
+  const int64_t x_need = kGated ? 2 * static_cast<int64_t>(k) : k;
+  if (!aligned16(x) || !aligned16(weight) || x_stride % 8 || weight_stride % 8 || x_stride < x_need ||
       weight_stride < k || y_stride < n) {
-    skv_set_error("%s: x and weight rows must be 16-byte aligned and hold k elements", what);
+    skv_set_error("%s: x and weight rows must be 16-byte aligned and hold %lld and k elements", what,
+                  (long long)x_need);
     return SKV_EINVAL;
   }
   if (g_waves_override < 0) {
@@ -187,14 +198,27 @@ extern "C" int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* w
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (m == 1)
-    launch<16, 1>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<16, 1, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if (m == 2)
-    launch<8, 2>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 2, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if (m <= 4)
-    launch<8, 4>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 4, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if (m <= 8)
-    launch<8, 8>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 8, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else
-    launch<2, 16>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<2, 16, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   return skv_check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                          uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
+  return linear_impl<false>("linear", x, x_stride, weight, weight_stride, y, y_stride, m, n, k, stream);
+}
+
+extern "C" int skv_linear_silu_mul(const uint16_t* x, int64_t x_stride, const uint16_t* weight,
+                                   int64_t weight_stride, uint16_t* y, int64_t y_stride, int m, int n, int k,
+                                   void* stream) {
+  return linear_impl<true>("linear_silu_mul", x, x_stride, weight, weight_stride, y, y_stride, m, n, k, stream);
 }

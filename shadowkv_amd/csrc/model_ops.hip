@@ -88,7 +88,7 @@ __global__ void __launch_bounds__(kThreads) silu_mul_kernel(const uint16_t* __re
   unpack8(*reinterpret_cast<const u32x4*>(x + row * xs + 8 * v), g);
   unpack8(*reinterpret_cast<const u32x4*>(x + row * xs + d + 8 * v), u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = g[e] / (1.f + expf(-g[e])) * u[e];
+  for (int e = 0; e < 8; ++e) y[e] = skv::silu_mul(g[e], u[e]);
   *reinterpret_cast<u32x4*>(out + row * os + 8 * v) = pack8(y);
 }
 

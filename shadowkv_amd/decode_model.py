@@ -211,6 +211,12 @@ class SyntheticDecoder:
                 cache.copy_stream, cache.key_stream = shared
             self.lanes.append(lane)
         self.cache = self.lanes[0].cache  # lane 0's cache (shapes are identical across lanes)
+        # The down projection forming SiLU-and-mul from the gate/up rows (one launch instead of two):
+        # faster where the lanes keep the host link busy and the compute stream has slack
+        # (Llama-3.1-8B batch 8, two lanes: 384.9 vs 381.7 tokens/s), slower where the step is the
+        # one-lane compute chain, every workgroup recomputing the activations (GLM-4-9B batch 4:
+        # 385.4 vs 396.5; Llama-3-8B-1M: 37.0 vs 36.9).
+        self.gated_down = lanes > 1
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
         self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
         self.graph = None
@@ -281,9 +287,13 @@ class SyntheticDecoder:
             h2, x2 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(o, lw.post_norm, s.eps, x2, residual=h, residual_out=h2)
             gate_up = self._linear(x2, lw.gate_up)
-            act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
-            shadowkv.silu_and_mul(gate_up, act)
-            down = self._linear(act, lw.down)
+            if self.gated_down and b <= shadowkv.LINEAR_MAX_ROWS:  # SiLU-and-mul formed by the down projection
+                down = torch.empty(b, 1, s.hidden, dtype=self.dtype, device=self.device)
+                shadowkv.linear_silu_mul(gate_up, lw.down, down)
+            else:
+                act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
+                shadowkv.silu_and_mul(gate_up, act)
+                down = self._linear(act, lw.down)
             w_next = self.layers[idx + 1].in_norm if idx + 1 < s.layers else self.norm_w
             h3, x3 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(down, w_next, s.eps, x3, residual=h2, residual_out=h3)

@@ -606,6 +606,25 @@ def linear(x, weight, out):
               _stream())
 
 
+def linear_silu_mul(gate_up, weight, out):
+    """out = bf16(bf16(silu(g) * u) @ weight.T) for gate_up rows [g (k) | u (k)]: the SiLU-and-mul
+    of the gate/up projection formed while the down projection reads it (bit-identical to
+    silu_and_mul followed by linear). At most 16 rows; weight [n, k] with contiguous rows."""
+    _dev(gate_up, "gate_up", torch.bfloat16)
+    _dev(weight, "weight", torch.bfloat16)
+    _dev(out, "out", torch.bfloat16)
+    rows, xs = _rows2d(gate_up, "gate_up")
+    orows, os_ = _rows2d(out, "out")
+    if weight.dim() != 2 or weight.stride(-1) != 1:
+        raise ValueError("linear_silu_mul: weight must be [n, k] with contiguous rows")
+    n, k = weight.shape
+    if gate_up.shape[-1] != 2 * k or out.shape[-1] != n or orows != rows:
+        raise ValueError(f"linear_silu_mul: shape mismatch gate_up {tuple(gate_up.shape)} weight "
+                         f"{tuple(weight.shape)} out {tuple(out.shape)}")
+    _lib.call("skv_linear_silu_mul", gate_up.data_ptr(), xs, weight.data_ptr(), weight.stride(0), out.data_ptr(), os_,
+              rows, n, k, _stream())
+
+
 def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache, append_row):
     """The new token's q and k rotated at positions[b] (bf16 per-op rounding; half-split for a
     [rows, 128] cos_sin, GLM-interleaved for [rows, 64]) and the KV append in one launch:

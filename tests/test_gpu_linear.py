@@ -60,3 +60,24 @@ def test_linear_rejects(gpu):
     with pytest.raises(ValueError):
         shadowkv.linear(torch.zeros(2, 32, dtype=torch.bfloat16, device=gpu), w,
                         torch.empty(2, 8, dtype=torch.bfloat16, device=gpu))
+
+
+@pytest.mark.parametrize("rows,n,k", [(4, 4096, 14336), (4, 4096, 13696), (1, 4096, 14336), (8, 4096, 14336),
+                                      (3, 130, 1032), (16, 96, 4104), (2, 64, 8)])
+def test_linear_silu_mul_equals_the_two_kernels(gpu, rows, n, k):
+    """The down projection reading the gate/up output through SiLU-and-mul gives, bit for bit,
+    silu_and_mul followed by linear (same activation arithmetic and rounding, same sums)."""
+    _say(f"linear_silu_mul rows={rows} n={n} k={k}")
+    g = torch.Generator().manual_seed(rows * 131 + n + k)
+    gu = (torch.randn(rows, 1, 2 * k, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5).to(torch.bfloat16).to(gpu)
+    act = torch.empty(rows, 1, k, dtype=torch.bfloat16, device=gpu)
+    shadowkv.silu_and_mul(gu, act)
+    want = torch.empty(rows, 1, n, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear(act, w, want)
+    got = torch.full((rows, 1, n), 7.0, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear_silu_mul(gu, w, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want.cpu())
+    ref = (torch.nn.functional.silu(gu.float()[..., :k]) * gu.float()[..., k:]).to(torch.bfloat16)
+    assert_bf16_close(got.cpu(), _ref(ref.cpu(), w.cpu()), floor=1e-3, what=f"linear_silu_mul {rows}x{n}x{k}")
