@@ -489,6 +489,17 @@ def linear_microbench(args) -> int:
                                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(t * 1e6, 2),
                                      "torch_matmul_us": round(t_torch * 1e6, 2)},
                         "cpu_baseline": None}
+            if name == "down":  # the same weight read through SiLU-and-mul of [gate | up] rows
+                gu = torch.randn(rows, 2 * k, generator=g, device="cuda").to(torch.bfloat16)
+                act = torch.empty(rows, k, dtype=torch.bfloat16, device="cuda")
+                t_gated = gpu_time_per_call(lambda i: shadowkv.linear_silu_mul(gu, ws[i % sets], y), set_reps)
+
+                def two(i):
+                    shadowkv.silu_and_mul(gu, act)
+                    shadowkv.linear(act, ws[i % sets], y)
+                t_two = gpu_time_per_call(two, set_reps)
+                out_line["roofline"]["silu_mul_fused_us"] = round(t_gated * 1e6, 2)
+                out_line["roofline"]["silu_mul_then_linear_us"] = round(t_two * 1e6, 2)
             print(json.dumps(out_line), flush=True)
         del ws
         torch.cuda.empty_cache()

@@ -211,12 +211,12 @@ class SyntheticDecoder:
                 cache.copy_stream, cache.key_stream = shared
             self.lanes.append(lane)
         self.cache = self.lanes[0].cache  # lane 0's cache (shapes are identical across lanes)
-        # The down projection forming SiLU-and-mul from the gate/up rows (one launch instead of two):
-        # faster where the lanes keep the host link busy and the compute stream has slack
-        # (Llama-3.1-8B batch 8, two lanes: 384.9 vs 381.7 tokens/s), slower where the step is the
-        # one-lane compute chain, every workgroup recomputing the activations (GLM-4-9B batch 4:
-        # 385.4 vs 396.5; Llama-3-8B-1M: 37.0 vs 36.9).
-        self.gated_down = lanes > 1
+        # The down projection forming SiLU-and-mul from the gate/up rows (one launch instead of two).
+        # Alone it is slower, every workgroup recomputing the activations (4 rows: 32.5 vs 23.4 µs
+        # for the two kernels; 8 rows: 126 vs 27.7 µs), but where two lanes keep the host link busy
+        # the step gains from the launch it saves (Llama-3.1-8B batch 8: 384.9 vs 381.7 tokens/s);
+        # the one-lane compute chain loses (GLM-4-9B batch 4: 385.4 vs 396.5 tokens/s).
+        self.gated_down = lanes > 1 and lb <= 4
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
         self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
         self.graph = None
