@@ -247,7 +247,8 @@ int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stri
 
 /* ---- new-token operations around the path (fused) ------------------------------------
  * skv_rmsnorm replaces the residual add + flashinfer rmsnorm pair of the reference model
- * (models/llama.py:110-112 with models/tensor_op.py:39-44): with residual non-null,
+ * (models/llama.py:191, :204-206, :215 and models/base.py:94, through layer_norm of
+ * models/tensor_op.py:39-44): with residual non-null,
  *   residual_out[r] = bf16(x[r] + residual[r])        (the bf16 residual add)
  *   out[r] = bf16(h * rsqrt(mean(h^2) + eps) * weight), h = residual_out[r] in fp32;
  * with residual null, h = x[r]. rows of `hidden` bf16 (a multiple of 8, at most 8192), all rows
@@ -256,22 +257,25 @@ int skv_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, i
                 uint16_t* residual_out, int64_t residual_out_stride, const uint16_t* weight, uint16_t* out,
                 int64_t out_stride, int rows, int hidden, float eps, void* stream);
 
-/* Replaces vllm silu_and_mul (models/llama.py:114-118): out[r, j] = bf16(silu(x[r, j]) * x[r, d + j])
- * in fp32, j < d (a multiple of 8); rows 16-byte aligned. */
+/* Replaces vllm silu_and_mul (models/llama.py:208-214 at :212, models/glm.py:193):
+ * out[r, j] = bf16(bf16(silu(x[r, j])) * x[r, d + j]), j < d (a multiple of 8): silu in fp32 rounded
+ * to bf16, then the bf16 product, vLLM's two roundings; rows 16-byte aligned. */
 int skv_silu_and_mul(const uint16_t* x, int64_t x_stride, uint16_t* out, int64_t out_stride, int rows, int d,
                      void* stream);
 
 /* Replaces F.linear on the decoding model's weights at decode batch sizes (wqkv, wo, gate_up_proj,
- * down_proj: models/llama.py:192,203,208,214; lm_head: models/llama.py:159):
+ * down_proj: models/llama.py:192,203,208,214; lm_head: models/base.py:98):
  * y[i, j] = bf16(sum_k x[i, k] * weight[j, k]) in fp32, i < m <= 16, j < n, k a multiple of 8.
  * weight is row-major [n, k] (row stride weight_stride); x and weight rows 16-byte aligned. */
 int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride, uint16_t* y,
                int64_t y_stride, int m, int n, int k, void* stream);
 
 /* skv_linear on the SiLU-and-mul of the gate/up projection, formed as the rows are read: x rows
- * hold [gate (k) | up (k)] (x_stride >= 2k) and the multiplied row is bf16(silu(gate) * up) as
- * skv_silu_and_mul computes it, so the result equals skv_silu_and_mul followed by skv_linear
- * (models/llama.py:114-118 then :214: act_fn and down_proj of the reference's MLP). */
+ * hold [gate (k) | up (k)] (x_stride >= 2k) and the multiplied row is bf16(bf16(silu(gate)) * up)
+ * as skv_silu_and_mul computes it, so the result equals skv_silu_and_mul followed by skv_linear
+ * (models/llama.py:212 then :214, models/glm.py:193-195: the activation and down_proj of the
+ * reference's MLP). m <= 4 (SKV_EUNSUPPORTED above: every workgroup recomputes the activations of
+ * its rows, which only pays off for a few rows). */
 int skv_linear_silu_mul(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
                         uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream);
 
@@ -344,7 +348,8 @@ int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_b, int64_t 
                                  const int32_t* slot_list, int sparse_start, int select_sets, int chunk_size,
                                  int pool_slots, void* stream);
 
-/* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:55-56) and the
+/* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:149-150,
+ * models/glm.py:200-201) and the
  * KV append of update_kv_cache (models/kvcache/shadow.py:621-633) in one launch. qkv row of batch b:
  * [q_heads*128 | kv_heads*128 (k) | kv_heads*128 (v)] at qkv + b*qkv_stride_b. q and k are rotated
  * at positions[b] with the bf16 per-op rounding of the reference (rope_mode 0: half-split with

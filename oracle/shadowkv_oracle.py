@@ -17,7 +17,7 @@ __all__ = [
     "reorder", "cached_gather_copy", "compact_hits", "gather_copy_plain", "rope_half_split", "rope_push",
     "rope_push_glm", "rebuild_k", "rebuild_k_rope", "score_logits_softmax", "score_gqa_max", "topk_total_order",
     "topk_gather", "sparse_attention", "build_cos_sin_cache", "build_glm_cos_sin_cache", "encode_layer",
-    "decode_layer_step", "LayerState", "pool_assign", "pool_from_layer", "decode_layer_step_pooled",
+    "decode_layer_step", "LayerState", "prefill_geometry", "pool_assign", "pool_from_layer", "decode_layer_step_pooled",
 ]
 
 
@@ -246,6 +246,22 @@ def build_glm_cos_sin_cache(max_length: int, base: float) -> torch.Tensor:
 # encode_layer follows models/kvcache/shadow.py:411-544 (get_svd, prefill_kv_cache) and
 # models/attention/shadow.py:8-13 (SVD of pre-RoPE K, then RoPE).
 
+def prefill_geometry(ctx: int, budget: int, chunk: int) -> dict:
+    """Prompt geometry of the offload cache: outlier chunks (budget/1024)*24 (shadow.py:329), 4 local
+    chunks and the aligned chunk count, a multiple of 8 (:477-482), the local rows left over, the
+    sparse region after the outliers (:500-501), the reference's buffer length (:346), the landmark
+    count n = aligned chunks - outliers and S = budget/chunk.
+    Pinned by: the derived-size table of the hot-path survey (tests/test_geometry_tables.py)."""
+    local_chunk, outlier_chunk = 4, (budget // 1024) * 24
+    chunks = ctx // chunk - local_chunk
+    chunks -= chunks % 8
+    prefill_local = ctx - chunks * chunk
+    sparse_start = prefill_local + outlier_chunk * chunk
+    return dict(S=budget // chunk, outlier_chunk=outlier_chunk, chunks=chunks, prefill_local=prefill_local,
+                n=chunks - outlier_chunk, sparse_start=sparse_start, sparse_end=sparse_start + budget,
+                buf_len=budget + 128 + (outlier_chunk + local_chunk) * chunk)
+
+
 class LayerState:
     """Decode state of one layer as the offload cache holds it (CPU tensors)."""
 
@@ -281,7 +297,7 @@ def encode_layer(k_pre: torch.Tensor, v: torch.Tensor, q_pre_last: torch.Tensor,
     B, H, ctx, D = k_pre.shape
     Hq = q_pre_last.shape[1]
     G = Hq // H
-    local_chunk, outlier_chunk = 4, (budget // 1024) * 24
+    outlier_chunk = (budget // 1024) * 24
     S = budget // chunk
     # get_svd (shadow.py:411-444): SVD of [B, ctx, H*D] in fp32, keep rank R.
     kflat = k_pre.transpose(1, 2).reshape(B, ctx, H * D)
@@ -295,12 +311,10 @@ def encode_layer(k_pre: torch.Tensor, v: torch.Tensor, q_pre_last: torch.Tensor,
     # prefill_kv_cache (shadow.py:463-544)
     max_ctx_chunks = ctx // chunk
     host_v = v[:, :, :max_ctx_chunks * chunk].reshape(B, H, max_ctx_chunks, chunk * D).clone()
-    chunks = ctx // chunk - local_chunk
-    chunks -= chunks % 8
-    prefill_local = ctx - chunks * chunk
-    sparse_start = prefill_local + outlier_chunk * chunk
-    sparse_end = sparse_start + budget
-    buf_len = buf_len or (budget + 128 + (outlier_chunk + local_chunk) * chunk)
+    geo = prefill_geometry(ctx, budget, chunk)
+    chunks, prefill_local = geo["chunks"], geo["prefill_local"]
+    sparse_start, sparse_end = geo["sparse_start"], geo["sparse_end"]
+    buf_len = buf_len or geo["buf_len"]
     kbuf = torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16)
     vbuf = torch.zeros(B, H, buf_len, D, dtype=torch.bfloat16)
     kbuf[:, :, :prefill_local] = k[:, :, -prefill_local:]

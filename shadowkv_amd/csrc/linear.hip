@@ -1,7 +1,7 @@
 // Skinny bf16 linear layer of the decode step: y[m, n] = bf16(sum_k x[m, k] * w[n, k]) for the
 // few token rows m of one decode step (M <= 16) against a row-major weight [N, K] — the
 // decoding model's projections (F.linear on wqkv, wo, gate_up_proj, down_proj and the lm head,
-// models/llama.py:192,203,208,214 and models/llama.py:159 with its use in the model's forward).
+// models/llama.py:192,203,208,214 and the lm head at models/base.py:98).
 //
 // At M <= 16 the call is bound by reading the weight once from HBM (2*N*K bytes), so the kernel
 // is laid out for the load path, not for the matrix cores: every wave load reads 1 KB of ONE
@@ -40,7 +40,7 @@ __device__ __forceinline__ void fold(float* v, bool upper) {
 }
 
 // bf16 pair of silu(g) * u from the bf16 pairs g2, u2 (element 0 in the low half), with the
-// arithmetic and single rounding of the SiLU-and-mul kernel (skv::silu_mul).
+// arithmetic and roundings of the SiLU-and-mul kernel (skv::silu_mul, then one bf16 rounding).
 __device__ __forceinline__ uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
   return skv::f2bf2(skv::silu_mul(skv::bf_lo(g2), skv::bf_lo(u2)), skv::silu_mul(skv::bf_hi(g2), skv::bf_hi(u2)));
 }
@@ -180,8 +180,11 @@ int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uin
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
   }
-  if (m < 1 || m > 16 || n < 1 || k < 8 || k % 8) {
-    skv_set_error("%s: m=%d n=%d k=%d (1 <= m <= 16, k a multiple of 8)", what, m, n, k);
+  // The gated form recomputes the activations of its rows in every workgroup, and its 8- and
+  // 16-row variants would hold two more sets of x registers: it is offered up to 4 rows only.
+  constexpr int kMaxRows = kGated ? 4 : 16;
+  if (m < 1 || m > kMaxRows || n < 1 || k < 8 || k % 8) {
+    skv_set_error("%s: m=%d n=%d k=%d (1 <= m <= %d, k a multiple of 8)", what, m, n, k, kMaxRows);
     return SKV_EUNSUPPORTED;
   }
   const int64_t x_need = kGated ? 2 * static_cast<int64_t>(k) : k;
@@ -203,10 +206,12 @@ int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uin
     launch<8, 2, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if (m <= 4)
     launch<8, 4, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
-  else if (m <= 8)
-    launch<8, 8, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
-  else
-    launch<2, 16, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  else if constexpr (!kGated) {
+    if (m <= 8)
+      launch<8, 8, false>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    else
+      launch<2, 16, false>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+  }
   return skv_check_launch(what);
 }
 

@@ -1,12 +1,14 @@
 // The new-token operations around the sparse path, fused (next to the path: the decode step's
 // QKV RoPE + KV append and the layer's norm / activation):
 //   skv_rmsnorm        residual add + RMSNorm: h = bf16(x + r) (the reference's bf16 residual add,
-//                      models/llama.py:110,121) and y = bf16(h * rsqrt(mean(h^2) + eps) * w) in fp32
-//                      with one rounding (flashinfer rmsnorm, models/tensor_op.py:39-44);
-//   skv_silu_and_mul   y = bf16(silu(g) * u) for the fused gate/up rows (vLLM silu_and_mul,
-//                      models/llama.py:114-118);
+//                      models/llama.py:204,215) and y = bf16(h * rsqrt(mean(h^2) + eps) * w) in fp32
+//                      with one rounding (flashinfer rmsnorm through layer_norm, models/llama.py:191,206,
+//                      models/base.py:94, models/tensor_op.py:39-44);
+//   skv_silu_and_mul   y = bf16(bf16(silu(g)) * u) for the fused gate/up rows (vLLM silu_and_mul,
+//                      models/llama.py:208-214, models/glm.py:193);
 //   skv_rope_qk_append the new token's q and k rotated with the bf16 per-op rounding of the
-//                      reference's rotary kernels (models/llama.py:55-56), q written contiguous
+//                      reference's rotary kernels (vLLM rotary_embedding, models/llama.py:149-150,
+//                      models/glm.py:200-201), q written contiguous
 //                      for the scoring kernel, rotated k and raw v appended to the key/value
 //                      buffers at a device-resident row (models/kvcache/shadow.py:621-633).
 #include "rope_math.h"

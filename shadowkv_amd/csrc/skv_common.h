@@ -40,11 +40,15 @@ __device__ __forceinline__ uint32_t f2bf2(float a, float b) {
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// silu(g) * u in fp32 with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32): a few ulp of
-// fp32, far below the one bf16 rounding applied to the result. Shared by the SiLU-and-mul kernel
-// and the down projection that forms the product while reading the gate/up rows, so both agree.
-__device__ __forceinline__ float silu_mul(float g, float u) { return __fdividef(g, 1.f + __expf(-g)) * u; }
 __device__ __forceinline__ uint16_t bmul(uint16_t a, uint16_t b) { return f2bf(bf2f(a) * bf2f(b)); }
+// x rounded to bf16 and widened back (exact).
+__device__ __forceinline__ float bround(float x) { return bf2f(f2bf(x)); }
+// silu(g) * u with vLLM silu_and_mul's roundings (the reference's activation, models/llama.py:212,
+// models/glm.py:193): silu(g) = g / (1 + exp(-g)) in fp32 (hardware exp and reciprocal, a few ulp
+// of fp32) rounded to bf16, then the bf16 x bf16 product, exact in fp32; the caller rounds the
+// result to bf16 once more. Shared by the SiLU-and-mul kernel and the down projection that forms
+// the product while reading the gate/up rows, so both agree bit for bit.
+__device__ __forceinline__ float silu_mul(float g, float u) { return bround(__fdividef(g, 1.f + __expf(-g))) * u; }
 __device__ __forceinline__ uint16_t badd(uint16_t a, uint16_t b) { return f2bf(bf2f(a) + bf2f(b)); }
 __device__ __forceinline__ uint16_t bneg(uint16_t a) { return a ^ 0x8000u; }
 

@@ -27,6 +27,7 @@ from .kernels import shadowkv
 from .models.attention import ShadowAttention
 from .models.kvcache import ShadowKVCache_CPU
 from .models.tensor_op import build_cos_sin_cache, build_glm_cos_sin_cache
+from .streams import side_stream
 
 
 @dataclass(frozen=True)
@@ -71,16 +72,7 @@ def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin:
     L, B, H, D, c, R = cache.num_layers, cache.batch_size, cache.num_key_value_heads, cache.head_dim, \
         cache.chunk_size, cache.rank
     S = cache.select_sets
-    cache.prefill = ctx
-    max_ctx_chunks = ctx // c
-    cache.max_ctx_chunks_len = max_ctx_chunks * c
-    chunks = ctx // c - cache.local_chunk
-    cache.chunks = chunks - chunks % 8
-    cache.prefill_local = ctx - cache.chunks * c
-    cache.sparse_start = cache.prefill_local + cache.outlier_chunk * c
-    cache.sparse_end = cache.sparse_start + cache.sparse_budget
-    cache.kernel_offset = cache.sparse_start * D
-    cache.kernel_stride = cache.buf_len * D
+    cache._set_geometry(ctx)
     n = cache.chunks - cache.outlier_chunk
     G = cache.num_key_value_groups
     tiles = (n + 255) // 256
@@ -193,10 +185,12 @@ class SyntheticDecoder:
                                     hidden_size=s.heads * D, num_hidden_layers=s.layers)
         lb = batch // lanes
         self.lanes = []
+        shared = None
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
                                       chunk_size=chunk_size, rank=rank, max_decode_len=decode_len,
-                                      zero_host_store=False, chunk_cache=chunk_cache)
+                                      zero_host_store=False, chunk_cache=chunk_cache,
+                                      copy_stream=shared[0] if shared else None)
             synthesize_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin)
             lane = _Lane(slice(i * lb, (i + 1) * lb), cache)
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
@@ -206,8 +200,10 @@ class SyntheticDecoder:
                 # All lanes share one value-fetch stream and one key-rebuild stream (their fetches
                 # follow one another on the host link anyway); taking the key rebuild off the
                 # compute stream keeps it out of the stretch between two lanes' fetches.
+                # Three streams in all (compute, fetch, rebuild): within the 4 hardware queues of a
+                # process, so no two of them share a queue (side_stream enforces the limit).
                 if i == 0:
-                    shared = (cache.copy_stream, torch.cuda.Stream(device=device))
+                    shared = (cache.copy_stream, side_stream(device))
                 cache.copy_stream, cache.key_stream = shared
             self.lanes.append(lane)
         self.cache = self.lanes[0].cache  # lane 0's cache (shapes are identical across lanes)
@@ -287,7 +283,7 @@ class SyntheticDecoder:
             h2, x2 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(o, lw.post_norm, s.eps, x2, residual=h, residual_out=h2)
             gate_up = self._linear(x2, lw.gate_up)
-            if self.gated_down and b <= shadowkv.LINEAR_MAX_ROWS:  # SiLU-and-mul formed by the down projection
+            if self.gated_down and b <= shadowkv.LINEAR_SILU_MUL_MAX_ROWS:  # SiLU-and-mul formed by the down projection
                 down = torch.empty(b, 1, s.hidden, dtype=self.dtype, device=self.device)
                 shadowkv.linear_silu_mul(gate_up, lw.down, down)
             else:

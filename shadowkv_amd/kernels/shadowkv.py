@@ -575,7 +575,8 @@ def rmsnorm(x, weight, eps, out, residual=None, residual_out=None):
 
 
 def silu_and_mul(x, out):
-    """out[..., j] = bf16(silu(x[..., j]) * x[..., d + j]), d = out.shape[-1] = x.shape[-1] / 2."""
+    """out[..., j] = bf16(bf16(silu(x[..., j])) * x[..., d + j]), d = out.shape[-1] = x.shape[-1] / 2
+    (vLLM silu_and_mul's two roundings)."""
     _dev(x, "x", torch.bfloat16)
     _dev(out, "out", torch.bfloat16)
     rows, xs = _rows2d(x, "x")
@@ -606,10 +607,14 @@ def linear(x, weight, out):
               _stream())
 
 
+LINEAR_SILU_MUL_MAX_ROWS = 4
+
+
 def linear_silu_mul(gate_up, weight, out):
-    """out = bf16(bf16(silu(g) * u) @ weight.T) for gate_up rows [g (k) | u (k)]: the SiLU-and-mul
-    of the gate/up projection formed while the down projection reads it (bit-identical to
-    silu_and_mul followed by linear). At most 16 rows; weight [n, k] with contiguous rows."""
+    """out = bf16(act @ weight.T), act = bf16(bf16(silu(g)) * u), for gate_up rows [g (k) | u (k)]:
+    the SiLU-and-mul of the gate/up projection formed while the down projection reads it
+    (bit-identical to silu_and_mul followed by linear). At most 4 rows (every workgroup recomputes
+    its rows' activations); weight [n, k] with contiguous rows."""
     _dev(gate_up, "gate_up", torch.bfloat16)
     _dev(weight, "weight", torch.bfloat16)
     _dev(out, "out", torch.bfloat16)
@@ -621,6 +626,8 @@ def linear_silu_mul(gate_up, weight, out):
     if gate_up.shape[-1] != 2 * k or out.shape[-1] != n or orows != rows:
         raise ValueError(f"linear_silu_mul: shape mismatch gate_up {tuple(gate_up.shape)} weight "
                          f"{tuple(weight.shape)} out {tuple(out.shape)}")
+    if rows > LINEAR_SILU_MUL_MAX_ROWS:
+        raise ValueError(f"linear_silu_mul: {rows} rows (at most {LINEAR_SILU_MUL_MAX_ROWS})")
     _lib.call("skv_linear_silu_mul", gate_up.data_ptr(), xs, weight.data_ptr(), weight.stride(0), out.data_ptr(), os_,
               rows, n, k, _stream())
 

@@ -32,6 +32,7 @@ import math
 import torch
 
 from ...kernels import shadowkv
+from ...streams import side_stream
 from ..tensor_op import batch_gather_gemm_rotary_pos_emb_cuda
 from .base import KVCacheBase
 
@@ -52,13 +53,18 @@ def low_rank_factors(k: torch.Tensor, rank: int):
     return u, s.unsqueeze(-1) * v.transpose(1, 2)
 
 
+def outlier_chunks(sparse_budget: int) -> int:
+    """Outlier chunks kept exactly per (b, h): 24 per 1024 tokens of budget (shadow.py:329)."""
+    return int((int(sparse_budget) // 1024) * 24)
+
+
 class ShadowKVCache_CPU(KVCacheBase):
     """ShadowKV with values offloaded to pinned host memory and low-rank keys rebuilt on the GPU."""
 
     def __init__(self, config, batch_size: int = 1, max_length: int = 32 * 1024, device: str = "cuda:0",
                  dtype=torch.bfloat16, sparse_budget: int = 2048, chunk_size: int = 8, rank: int = 160,
                  max_decode_len: int | None = None, zero_host_store: bool = True,
-                 chunk_cache: int | None = None) -> None:
+                 chunk_cache: int | None = None, copy_stream: torch.cuda.Stream | None = None) -> None:
         self.config = config
         self.batch_size = batch_size
         self.max_length = max_length
@@ -74,7 +80,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.chunk_size = chunk_size
         self.rank = rank
         self.local_chunk = 4
-        self.outlier_chunk = int((self.sparse_budget // 1024) * 24)
+        self.outlier_chunk = outlier_chunks(self.sparse_budget)
         self.select_sets = self.sparse_budget // self.chunk_size
         if self.select_sets * self.chunk_size != self.sparse_budget:
             raise ValueError(f"sparse_budget {self.sparse_budget} is not a multiple of chunk_size {chunk_size}")
@@ -131,7 +137,8 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.selected_chunks = torch.zeros(B, H, self.select_sets, device=device, dtype=torch.int64)
         self.keep_selected = False  # also emit the selected ids in top-k order into selected_chunks
 
-        self.copy_stream = torch.cuda.Stream(device=device)
+        # value-fetch stream: given (shared with other caches) or a new side stream
+        self.copy_stream = copy_stream if copy_stream is not None else side_stream(device)
         self.key_stream = None  # optional: run the key rebuild on this stream (joined before attention)
         self.attn_workspace = None
         self.attn_out = None

@@ -58,7 +58,8 @@ def test_silu_and_mul(gpu, rows, d):
     shadowkv.silu_and_mul(x.to(gpu), out)
     torch.cuda.synchronize()
     gt, up = x.float()[..., :d], x.float()[..., d:]
-    want = (gt / (1 + torch.exp(-gt)) * up).to(torch.bfloat16)
+    # vLLM silu_and_mul (the reference's activation): silu in fp32 rounded to bf16, then the bf16 product
+    want = ((gt / (1 + torch.exp(-gt))).to(torch.bfloat16).float() * up).to(torch.bfloat16)
     assert_bf16_close(out.cpu(), want, what="silu_and_mul")
 
 

@@ -35,3 +35,26 @@ def test_auto_lanes_follows_the_measured_choices():
     assert dm.auto_lanes(dm.GLM4_9B, 4, 2048) == 1      # 393 vs 261
     assert dm.auto_lanes(dm.LLAMA3_8B_1M, 1, 16384) == 1  # one sequence: nothing to pipeline
     assert dm.auto_lanes(dm.LLAMA31_8B, 7, 2048) == 1   # odd batch
+
+
+def test_side_streams_are_limited_to_the_hardware_queues(monkeypatch):
+    """At most 3 side streams live beside the compute stream (4 hardware queues per process):
+    a fourth raises, and a released one frees its place (a stand-in stream class, no device)."""
+    from shadowkv_amd import streams
+
+    class FakeStream:
+        n = 0
+
+        def __init__(self, device=None):
+            FakeStream.n += 1
+            self.cuda_stream = 0x1000 + FakeStream.n
+
+    monkeypatch.setattr(streams.torch.cuda, "Stream", FakeStream)
+    monkeypatch.setattr(streams, "_live", streams.weakref.WeakSet())
+    held = [streams.side_stream("cuda:0") for _ in range(streams.MAX_STREAMS - 1)]
+    assert streams.live_side_streams() == 3
+    with pytest.raises(RuntimeError, match="more than 4 streams"):
+        streams.side_stream("cuda:0")
+    held.pop()
+    held.append(streams.side_stream("cuda:0"))
+    assert streams.live_side_streams() == 3
