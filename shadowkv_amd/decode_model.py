@@ -185,12 +185,10 @@ class SyntheticDecoder:
                                     hidden_size=s.heads * D, num_hidden_layers=s.layers)
         lb = batch // lanes
         self.lanes = []
-        shared = None
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
                                       chunk_size=chunk_size, rank=rank, max_decode_len=decode_len,
-                                      zero_host_store=False, chunk_cache=chunk_cache,
-                                      copy_stream=shared[0] if shared else None)
+                                      zero_host_store=False, chunk_cache=chunk_cache)
             synthesize_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin)
             lane = _Lane(slice(i * lb, (i + 1) * lb), cache)
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
@@ -201,10 +199,8 @@ class SyntheticDecoder:
                 # follow one another on the host link anyway); taking the key rebuild off the
                 # compute stream keeps it out of the stretch between two lanes' fetches.
                 # Three streams in all (compute, fetch, rebuild): within the 4 hardware queues of a
-                # process, so no two of them share a queue (side_stream enforces the limit).
-                if i == 0:
-                    shared = (cache.copy_stream, side_stream(device))
-                cache.copy_stream, cache.key_stream = shared
+                # process, so no two of them share a queue.
+                cache.key_stream = side_stream(device, "rebuild")
             self.lanes.append(lane)
         self.cache = self.lanes[0].cache  # lane 0's cache (shapes are identical across lanes)
         # The down projection forming SiLU-and-mul from the gate/up rows (one launch instead of two).

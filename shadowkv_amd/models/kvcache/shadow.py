@@ -137,8 +137,8 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.selected_chunks = torch.zeros(B, H, self.select_sets, device=device, dtype=torch.int64)
         self.keep_selected = False  # also emit the selected ids in top-k order into selected_chunks
 
-        # value-fetch stream: given (shared with other caches) or a new side stream
-        self.copy_stream = copy_stream if copy_stream is not None else side_stream(device)
+        # value-fetch stream: the given one, else the process's shared fetch side stream
+        self.copy_stream = copy_stream if copy_stream is not None else side_stream(device, "fetch")
         self.key_stream = None  # optional: run the key rebuild on this stream (joined before attention)
         self.attn_workspace = None
         self.attn_out = None

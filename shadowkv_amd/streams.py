@@ -1,37 +1,41 @@
 """Side streams of the decode path, limited to what the hardware queues of a process hold.
 
 HIP maps a process's streams onto at most GPU_MAX_HW_QUEUES hardware queues (4 by default, the
-setting of the MI355X hosts this runs on). With more live streams than queues, two streams share
-one queue; a cross-stream wait queued in that shared queue ahead of the work it waits for can then
+setting of the MI355X hosts this runs on). With more streams than queues, two streams share one
+queue; a cross-stream wait queued in that shared queue ahead of the work it waits for can then
 block the queue for good. The decode path therefore uses at most 4 streams: the caller's compute
-stream and up to 3 side streams (the value fetch, the key rebuild, and one spare), and every side
-stream the package creates goes through side_stream(), which refuses a fourth live one.
+stream and three side streams per device, one per role (the value fetch, the key rebuild, a
+spare), created once and shared by every cache and decoder of the process. Work of different
+caches on one side stream runs in issue order, as the host link serialises the fetches anyway.
 """
 from __future__ import annotations
 
-import weakref
+import threading
 
 import torch
 
 MAX_STREAMS = 4  # compute stream + side streams, per process
-_live: "weakref.WeakSet[torch.cuda.Stream]" = weakref.WeakSet()
+ROLES = ("fetch", "rebuild", "spare")
+assert len(ROLES) + 1 <= MAX_STREAMS
+
+_lock = threading.Lock()
+_streams: dict = {}  # (device index, role) -> torch.cuda.Stream
 
 
-def live_side_streams() -> int:
-    """Distinct side streams created by side_stream() that are still referenced."""
-    return len({s.cuda_stream for s in list(_live)})
-
-
-def side_stream(device) -> torch.cuda.Stream:
-    """A new side stream at the default priority; raises RuntimeError when the process would hold
-    more than MAX_STREAMS streams with the compute stream counted."""
-    if live_side_streams() + 1 >= MAX_STREAMS:
-        import gc
-        gc.collect()  # streams of dropped caches may still sit in reference cycles
-        if live_side_streams() + 1 >= MAX_STREAMS:
-            raise RuntimeError(f"the decode path would use more than {MAX_STREAMS} streams (the hardware queues "
-                               f"of a process): {live_side_streams()} side streams are live; release caches or "
-                               f"share their streams")
-    s = torch.cuda.Stream(device=device)
-    _live.add(s)
+def side_stream(device, role: str = "fetch") -> torch.cuda.Stream:
+    """The process's side stream of `role` on `device` (created on first use, default priority)."""
+    if role not in ROLES:
+        raise ValueError(f"side stream role {role!r} is not one of {ROLES}")
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), role)
+    with _lock:
+        s = _streams.get(key)
+        if s is None:
+            s = torch.cuda.Stream(device=dev)
+            _streams[key] = s
     return s
+
+
+def side_streams_created() -> int:
+    """Side streams created so far on all devices."""
+    return len(_streams)

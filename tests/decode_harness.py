@@ -99,3 +99,95 @@ def fresh_oracle_state(case):
     return oracle.LayerState(**kw, prefill_local=st.prefill_local, sparse_start=st.sparse_start,
                              sparse_end=st.sparse_end, chunk=d["chunk"], budget=d["budget"], ctx=d["ctx"],
                              buf_len=st.buf_len, chunks=st.chunks)
+
+
+class LayerProbe:
+    """Records, for chosen layers of every lane of a SyntheticDecoder, what one eager decode step
+    did to the layer: the cache state just before the layer's selection (after the new token's
+    RoPE and append), the selection's outputs, and the buffers and attention output after the
+    layer. It wraps the lanes' ShadowAttention.decode_begin_appended / decode_end and
+    synchronises the device around the recorded calls (the step's results do not change)."""
+
+    def __init__(self, dec, layers):
+        self.records = {}
+        self._open = {}
+        for i, lane in enumerate(dec.lanes):
+            self._wrap(i, lane, set(layers))
+
+    def _wrap(self, i, lane, layers):
+        begin, end = lane.attn.decode_begin_appended, lane.attn.decode_end
+        c = lane.cache
+
+        def probe_begin(q, idx):
+            if idx not in layers:
+                return begin(q, idx)
+            torch.cuda.synchronize()
+            rec = dict(q=q.reshape(q.shape[0], q.shape[1], -1).cpu(), kbuf=c.k_cache_buffer[idx].cpu(),
+                       vbuf=c.v_cache_buffer[idx].cpu(), pos_before=c.position_ids[idx].cpu(),
+                       kv_len=int(c.kv_len_dev.item()))
+            pending = begin(q, idx)
+            torch.cuda.synchronize()
+            rows = c.batch_size * c.num_key_value_heads
+            rec.update(gemm_o=c.gemm_o.cpu(), scores=c.chunk_attn.cpu(), offsets=c.offsets.view(rows, -1).cpu(),
+                       cnts=c.cnts.cpu(), pos_after=c.position_ids[idx].cpu())
+            self.records[(i, idx)] = rec
+            self._open[id(pending)] = (i, idx)
+            return pending
+
+        def probe_end(pending):
+            key = self._open.pop(id(pending), None)
+            out = end(pending)
+            if key is not None:
+                torch.cuda.synchronize()
+                rec = self.records[key]
+                L = rec["kv_len"]
+                rec.update(out=out.reshape(out.shape[0], out.shape[2], -1).cpu(),
+                           kbuf_after=c.k_cache_buffer[key[1]][:, :, :L].cpu(),
+                           vbuf_after=c.v_cache_buffer[key[1]][:, :, :L].cpu())
+            return out
+
+        lane.attn.decode_begin_appended = probe_begin
+        lane.attn.decode_end = probe_end
+
+
+def check_layer_record(rec, cache, layer, cos_sin_cpu, what=""):
+    """One recorded layer step of one lane against the oracle: the scoring within one bf16
+    rounding step; from the device's own GQA-max scores, the selection, offsets, hit counts, slot
+    ids and the value buffer bit-exact, hit and untouched key rows bit-exact, rebuilt key rows
+    and the attention output within rtol 2e-2 / atol 2e-2."""
+    import oracle
+    B, H = cache.batch_size, cache.num_key_value_heads
+    S, c, sp0, sp1 = cache.select_sets, cache.chunk_size, cache.sparse_start, cache.sparse_end
+    landmarks = cache.k_landmark[layer].cpu()
+    n, D = landmarks.shape[-2], landmarks.shape[-1]
+    q = rec["q"]
+    G = q.shape[1] // H
+    # scoring: logits within one rounding step; probabilities from the device's own logits
+    logits_dev = rec["gemm_o"].view(B * H, G, n)
+    logits_ref, _ = oracle.score_logits_softmax(q.reshape(B * H, G, D), landmarks.reshape(B * H, n, D),
+                                                1.0 / 128 ** 0.5)
+    assert_bf16_close(logits_dev, logits_ref, what=f"{what} logits")
+    probs = torch.softmax(logits_dev.float(), dim=-1).to(torch.bfloat16).max(dim=1).values
+    assert_bf16_close(rec["scores"].view(B * H, n), probs, what=f"{what} gqa-max probabilities")
+    st = oracle.LayerState(U=cache.U[layer].cpu(), SV=cache.SV[layer].cpu(), landmarks=landmarks,
+                           landmark_idx=cache.k_landmark_idx[layer].cpu(), host_v=cache.v_cache_cpu[layer],
+                           kbuf=rec["kbuf"].clone(), vbuf=rec["vbuf"].clone(), position_ids=rec["pos_before"].clone(),
+                           prefill_local=cache.prefill_local, sparse_start=sp0, sparse_end=sp1, chunk=c,
+                           budget=cache.sparse_budget, ctx=cache.prefill, buf_len=cache.buf_len, chunks=cache.chunks)
+    L = rec["kv_len"]
+    k_new, v_new = rec["kbuf"][:, :, L - 1], rec["vbuf"][:, :, L - 1]
+    res = oracle.decode_layer_step(st, q, k_new, v_new, cos_sin_cpu, gen_offset=L - 1 - sp1, scores=rec["scores"])
+    assert res["L"] == L
+    assert torch.equal(rec["cnts"], torch.from_numpy(res["cnts"])), f"{what}: hit counts"
+    assert torch.equal(rec["offsets"], torch.from_numpy(res["offsets"])), f"{what}: offsets"
+    assert torch.equal(rec["pos_after"], st.position_ids), f"{what}: slot ids"
+    assert torch.equal(rec["vbuf_after"], st.vbuf[:, :, :L]), f"{what}: value buffer"
+    kdev, kref = rec["kbuf_after"], st.kbuf[:, :, :L]
+    for r in range(B * H):
+        b, h = divmod(r, H)
+        miss = sp0 + int(res["cnts"][r]) * c
+        assert torch.equal(kdev[b, h, :miss], kref[b, h, :miss]), f"{what}: key rows before the misses, row {r}"
+        assert torch.equal(kdev[b, h, sp1:], kref[b, h, sp1:]), f"{what}: generated key rows, row {r}"
+    torch.testing.assert_close(kdev.float(), kref.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(rec["out"].float(), res["out"].float(), rtol=2e-2, atol=2e-2)
+    return res

@@ -38,23 +38,19 @@ def test_auto_lanes_follows_the_measured_choices():
 
 
 def test_side_streams_are_limited_to_the_hardware_queues(monkeypatch):
-    """At most 3 side streams live beside the compute stream (4 hardware queues per process):
-    a fourth raises, and a released one frees its place (a stand-in stream class, no device)."""
+    """Three side streams per device at most, one per role, reused by every caller (a stand-in
+    stream class, no device): with the compute stream, 4 streams = the hardware queues."""
     from shadowkv_amd import streams
 
     class FakeStream:
-        n = 0
-
         def __init__(self, device=None):
-            FakeStream.n += 1
-            self.cuda_stream = 0x1000 + FakeStream.n
+            self.device = device
 
     monkeypatch.setattr(streams.torch.cuda, "Stream", FakeStream)
-    monkeypatch.setattr(streams, "_live", streams.weakref.WeakSet())
-    held = [streams.side_stream("cuda:0") for _ in range(streams.MAX_STREAMS - 1)]
-    assert streams.live_side_streams() == 3
-    with pytest.raises(RuntimeError, match="more than 4 streams"):
-        streams.side_stream("cuda:0")
-    held.pop()
-    held.append(streams.side_stream("cuda:0"))
-    assert streams.live_side_streams() == 3
+    monkeypatch.setattr(streams, "_streams", {})
+    got = [streams.side_stream("cuda:0", r) for r in streams.ROLES for _ in range(3)]
+    assert streams.side_streams_created() == 3 and len({id(s) for s in got}) == 3
+    assert streams.side_stream("cuda:0") is streams.side_stream("cuda:0", "fetch")
+    assert streams.side_streams_created() + 1 <= streams.MAX_STREAMS
+    with pytest.raises(ValueError):
+        streams.side_stream("cuda:0", "lane2")
