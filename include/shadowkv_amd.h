@@ -245,6 +245,21 @@ int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stri
                            int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
                            void* stream);
 
+/* Allocation-free form of skv_sparse_attn_decode. No reference counterpart: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops). The split
+ * partials live in a device array inside the library, one per GPU, of
+ * skv_sparse_attn_noalloc_max_bytes() bytes (32 MiB), held until the process ends; calls needing more
+ * (skv_sparse_attn_workspace_bytes above it, e.g. batch 8 x 32 query heads beyond 16128 keys) return
+ * SKV_EUNSUPPORTED. The call allocates nothing. All calls on one GPU share that array: calls that
+ * overlap on one GPU (on different streams, or from several threads) race; `stream` must belong to
+ * the current device. Arguments and results as skv_sparse_attn_decode. */
+int64_t skv_sparse_attn_noalloc_max_bytes(void);
+int skv_sparse_attn_decode_noalloc(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
+                                   const uint16_t* k_cache, const uint16_t* v_cache, int64_t kv_stride_b,
+                                   int64_t kv_stride_h, int64_t kv_stride_s, int batch_size, int q_heads,
+                                   int kv_heads, int head_dim, int kv_len, const int32_t* kv_len_dev, float scale,
+                                   uint16_t* out, int64_t o_stride_b, int64_t o_stride_h, void* stream);
+
 /* ---- new-token operations around the path (fused) ------------------------------------
  * skv_rmsnorm replaces the residual add + flashinfer rmsnorm pair of the reference model
  * (models/llama.py:191, :204-206, :215 and models/base.py:94, through layer_norm of

@@ -13,6 +13,7 @@
 //   attn_combine_kernel: log-sum-exp merge of the splits in one pass (running maximum), every
 //     load of a 32-split chunk issued before the first is used; bf16 output.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "wave_reduce.h"
@@ -525,4 +526,71 @@ extern "C" int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_
                      kv_stride_h, kv_stride_s, batch_size, q_heads, kv_heads, head_dim, kv_len, kv_len_dev, scale,
                      workspace, workspace_bytes, out, o_stride_b, o_stride_h, slot_list, sparse_start, select_sets,
                      chunk_size, pool_slots, stream);
+}
+
+// ---- allocation-free variant ---------------------------------------------------------------
+// The split partials of skv_sparse_attn_decode_noalloc live in this file-scope device array, one
+// copy per GPU, held until the process ends. Its device address is looked up once per device
+// (hipGetSymbolAddress with that device current) and only that address is handed to kernels;
+// the array's name is a host-side stand-in in host code. The partials need no clearing: every
+// live split writes its own before the merge reads them, and the merge reads live splits only.
+namespace {
+
+constexpr int64_t kNoallocScratchBytes = 32ll << 20;  // 32 MiB per GPU
+constexpr int kMaxDevices = 64;
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+
+// Device address of this GPU's `scratch` (the current device's), looked up on first use.
+int noalloc_scratch(const char* what, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    skv_set_error("%s: no usable current device (%s)", what, hipGetErrorString(e));
+    return SKV_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      skv_set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev, hipGetErrorString(e));
+      return SKV_ELAUNCH;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return SKV_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t skv_sparse_attn_noalloc_max_bytes(void) { return kNoallocScratchBytes; }
+
+extern "C" int skv_sparse_attn_decode_noalloc(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
+                                              const uint16_t* k_cache, const uint16_t* v_cache, int64_t kv_stride_b,
+                                              int64_t kv_stride_h, int64_t kv_stride_s, int batch_size, int q_heads,
+                                              int kv_heads, int head_dim, int kv_len, const int32_t* kv_len_dev,
+                                              float scale, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+                                              void* stream) {
+  const char* what = "sparse_attn_decode_noalloc";
+  const int64_t need = skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len);
+  if (need > kNoallocScratchBytes) {
+    skv_set_error("%s: batch %d x %d query heads x %d keys need %lld bytes of split partials, more than the %lld "
+                  "of the library's scratch; use skv_sparse_attn_decode with a workspace", what, batch_size, q_heads,
+                  kv_len, (long long)need, (long long)kNoallocScratchBytes);
+    return SKV_EUNSUPPORTED;
+  }
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch(what, &ws)) return rc;
+  return attn_decode(what, q, q_stride_b, q_stride_h, k_cache, v_cache, kv_stride_b, kv_stride_h, kv_stride_s,
+                     batch_size, q_heads, kv_heads, head_dim, kv_len, kv_len_dev, scale, ws, kNoallocScratchBytes,
+                     out, o_stride_b, o_stride_h, nullptr, 0, 0, 0, 0, stream);
 }
