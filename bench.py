@@ -362,8 +362,9 @@ def attention_microbench(args) -> int:
     cal = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
     torch.neg(cal, out=cal)
     del cal
-    for name, B, Hq, Hk, L in (("Llama-3-8B", 8, 32, 8, 2600), ("Llama-3-8B", 24, 32, 8, 2600),
-                               ("GLM-4-9B", 4, 32, 2, 2600), ("Llama-3-8B-1M", 1, 32, 8, 19616)):
+    for name, B, Hq, Hk, L in (("Llama-3-8B", 4, 32, 8, 2600), ("Llama-3-8B", 8, 32, 8, 2600),
+                               ("Llama-3-8B", 24, 32, 8, 2600), ("GLM-4-9B", 4, 32, 2, 2600),
+                               ("Llama-3-8B-1M", 1, 32, 8, 19616)):
         g = torch.Generator(device="cuda").manual_seed(L + B)
         buf = L + 32
         G = Hq // Hk

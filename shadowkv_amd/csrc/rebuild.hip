@@ -9,7 +9,9 @@
 // bf16 k(r) itself is written (reference batch_gather_gemm output).
 //
 // Work decomposition (gfx950, wave64):
-//   * workgroup = 4 waves, owns kTileRows = 256 consecutive rows of one head. At entry it stages
+//   * workgroup = kNW waves, owns kTileRows = kNW x kIters x 32 consecutive rows of one head
+//     (256 = 4 waves x 2 iterations when the grid has enough workgroups to fill the GPU, else
+//     128 = 4 x 1 or 64 = 2 x 1, so that few rows still spread over the CUs). At entry it stages
 //     SV of that head (128 x rank bf16, 40 KB at rank 160) and the U row of each of its rows
 //     (chunk id * chunk + r % chunk) into LDS;
 //   * a wave computes 32 rows x 128 columns per iteration, two iterations, with
@@ -34,14 +36,12 @@ using skv::u32x4;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kTileRows = 256;  // rows per workgroup: 4 waves x 2 iterations x 32 rows
+constexpr int kMaxWaves = 4;
+constexpr int kMaxTileRows = 256;  // rows per workgroup: at most 4 waves x 2 iterations x 32 rows
 constexpr int kHeadDim = 128;
 constexpr int kMaxRank = 192;
 constexpr int kXcds = 8;
 constexpr int kStLd = kHeadDim + 8;  // staging row (elements), padded against bank conflicts
-static_assert(kThreads == kTileRows, "the position staging gives each thread one row");
 
 enum Mode { kPlain = 0, kRopeHalf = 1, kRopeGlm = 2 };
 
@@ -97,15 +97,18 @@ struct Units {
   static constexpr int kPerLane = 16 * kPerRow / 64;
 };
 
-template <int kMode, int KS, typename IdxT>
-__global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
+template <int kMode, int KS, typename IdxT, int kNW, int kIters>
+__global__ void __launch_bounds__(kNW * 64, 2) rebuild_kernel(RebuildArgs a) {
   using U = Units<kMode>;
+  constexpr int kThreads = kNW * 64;
+  constexpr int kTileRows = kNW * kIters * 32;
+  static_assert(kTileRows <= kThreads, "the position staging gives each thread at most one row");
   extern __shared__ __align__(16) unsigned char smem[];
   const int ldr = a.rank + 8;  // padded SV row (elements)
   uint16_t* sv_lds = reinterpret_cast<uint16_t*>(smem);                         // [128][ldr]
   int32_t* pos_lds = reinterpret_cast<int32_t*>(sv_lds + kHeadDim * ldr);      // [kTileRows]
   int32_t* orow_lds = pos_lds + kTileRows;                                      // [kTileRows]
-  uint16_t* kst = reinterpret_cast<uint16_t*>(orow_lds + kTileRows);           // [kWaves][16][kStLd]
+  uint16_t* kst = reinterpret_cast<uint16_t*>(orow_lds + kTileRows);           // [kNW][16][kStLd]
 
   const int bid = blockIdx.x;
   const int xcd = bid % kXcds;
@@ -130,7 +133,7 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   const IdxT* ids = static_cast<const IdxT*>(a.ids) + b * a.id_sb + h * a.id_sh;
   int64_t my_id = 0;
   {
-    const int row = row_begin + static_cast<int>(threadIdx.x);  // kThreads == kTileRows: one row per thread
+    const int row = row_begin + min(static_cast<int>(threadIdx.x), kTileRows - 1);  // at most one row per thread
     my_id = ids[min(row, total_rows - 1) / a.chunk];
   }
   const int k8 = a.rank / 8;
@@ -144,7 +147,7 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
     const int n = ic / k8, kk = (ic - n * k8) * 8;
     svv[i] = *reinterpret_cast<const u32x4*>(&svp[n * a.sv_sn + kk]);
   }
-  {
+  if (static_cast<int>(threadIdx.x) < kTileRows) {
     const int row = row_begin + static_cast<int>(threadIdx.x);
     int32_t p = -1, orow = row;
     if (row < row_end) {
@@ -169,17 +172,17 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   uint16_t* st = kst + wave * 16 * kStLd;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  const int lr0 = wave * 64;
-  bool active[2];
+  const int lr0 = wave * kIters * 32;
+  bool active[kIters];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
+  for (int it = 0; it < kIters; ++it) {
     const int rb = row_begin + lr0 + it * 32;
     active[it] = rb < row_end && rb + 32 > miss_begin;  // wave-uniform
   }
   // U fragments (B operand) of both 32-row blocks.
-  bf16x8_t uf[2][2][KS];
+  bf16x8_t uf[kIters][2][KS];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
+  for (int it = 0; it < kIters; ++it) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int r = lr0 + it * 32 + m * 16 + li;
@@ -195,9 +198,9 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
     }
   }
   // cos/sin of both blocks' epilogue units.
-  u32x4 cs_c[2][2][U::kPerLane], cs_s[2][2][U::kPerLane];
+  u32x4 cs_c[kIters][2][U::kPerLane], cs_s[kIters][2][U::kPerLane];
 #pragma unroll
-  for (int it = 0; it < 2; ++it)
+  for (int it = 0; it < kIters; ++it)
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -231,7 +234,7 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
   __syncthreads();
 
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
+  for (int it = 0; it < kIters; ++it) {
     if (!active[it]) continue;
     const int lr = lr0 + it * 32;
 
@@ -303,31 +306,53 @@ __global__ void __launch_bounds__(kThreads, 2) rebuild_kernel(RebuildArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int kMode, int KS, typename IdxT>
+template <int kMode, int KS, typename IdxT, int kNW, int kIters>
 void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
   // Ranks above 176 need more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU): raise the
   // kernel's limit once.
   if (lds > 65536) {
-    static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(&rebuild_kernel<kMode, KS, IdxT>),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                         static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) +
-                                                                          2 * kTileRows * sizeof(int32_t) +
-                                                                          kWaves * 16 * kStLd * sizeof(uint16_t)));
+    static const hipError_t raised = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&rebuild_kernel<kMode, KS, IdxT, kNW, kIters>),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) + 2 * kMaxTileRows * sizeof(int32_t) +
+                         kMaxWaves * 16 * kStLd * sizeof(uint16_t)));
     (void)raised;
   }
-  hipLaunchKernelGGL((rebuild_kernel<kMode, KS, IdxT>), grid, dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), grid, dim3(kNW * 64), lds, stream, a);
 }
 
-template <int kMode, typename IdxT>
-void launch_mode(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
+template <int kMode, typename IdxT, int kNW, int kIters>
+void launch_tile(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
   switch (ks) {
-    case 1: launch_ks<kMode, 1, IdxT>(grid, lds, stream, a); break;
-    case 2: launch_ks<kMode, 2, IdxT>(grid, lds, stream, a); break;
-    case 3: launch_ks<kMode, 3, IdxT>(grid, lds, stream, a); break;
-    case 4: launch_ks<kMode, 4, IdxT>(grid, lds, stream, a); break;
-    case 5: launch_ks<kMode, 5, IdxT>(grid, lds, stream, a); break;
-    default: launch_ks<kMode, 6, IdxT>(grid, lds, stream, a); break;
+    case 1: launch_ks<kMode, 1, IdxT, kNW, kIters>(grid, lds, stream, a); break;
+    case 2: launch_ks<kMode, 2, IdxT, kNW, kIters>(grid, lds, stream, a); break;
+    case 3: launch_ks<kMode, 3, IdxT, kNW, kIters>(grid, lds, stream, a); break;
+    case 4: launch_ks<kMode, 4, IdxT, kNW, kIters>(grid, lds, stream, a); break;
+    case 5: launch_ks<kMode, 5, IdxT, kNW, kIters>(grid, lds, stream, a); break;
+    default: launch_ks<kMode, 6, IdxT, kNW, kIters>(grid, lds, stream, a); break;
   }
+}
+
+// tile_rows: 256 (4 waves x 2 iterations), 128 (4 x 1) or 64 (2 x 1).
+template <int kMode, typename IdxT>
+void launch_mode(int tile_rows, int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
+  if (tile_rows == 256) launch_tile<kMode, IdxT, 4, 2>(ks, grid, lds, stream, a);
+  else if (tile_rows == 128) launch_tile<kMode, IdxT, 4, 1>(ks, grid, lds, stream, a);
+  else launch_tile<kMode, IdxT, 2, 1>(ks, grid, lds, stream, a);
+}
+
+// Rows per workgroup: the largest tile that still gives the grid about 1.5 workgroups per CU
+// (256 CUs), so few (b, h) rows - GLM's 2 kv heads, a batch lane of 4 sequences - spread over
+// the GPU instead of leaving most CUs idle. SKV_REBUILD_TILE=64/128/256 forces one.
+int choose_tile_rows(int BH, int rows) {
+  const char* e = getenv("SKV_REBUILD_TILE");
+  const int forced = e ? atoi(e) : 0;
+  if (forced == 64 || forced == 128 || forced == 256) return forced;
+  constexpr int kFill = 384;
+  for (int t : {256, 128}) {
+    if (static_cast<int64_t>(BH) * ((rows + t - 1) / t) >= kFill) return t;
+  }
+  return 64;
 }
 
 int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStream_t stream) {
@@ -362,21 +387,23 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
     skv_set_error("%s: %d chunks of %d rows is too many", what, a.S, a.chunk);
     return SKV_EUNSUPPORTED;
   }
-  a.tiles = (a.S * a.chunk + kTileRows - 1) / kTileRows;
   const int BH = a.B * a.H;
+  const int tile_rows = choose_tile_rows(BH, a.S * a.chunk);
+  const int waves = tile_rows == 64 ? 2 : 4;
+  a.tiles = (a.S * a.chunk + tile_rows - 1) / tile_rows;
   const int heads_padded = (BH + kXcds - 1) / kXcds * kXcds;
   const dim3 grid(static_cast<unsigned>(heads_padded * a.tiles));
-  const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * kTileRows * sizeof(int32_t) +
-                     static_cast<size_t>(kWaves) * 16 * kStLd * sizeof(uint16_t);
+  const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * tile_rows * sizeof(int32_t) +
+                     static_cast<size_t>(waves) * 16 * kStLd * sizeof(uint16_t);
   const int ks = (a.rank + 31) / 32;
   if (ids64) {
-    if (mode == kPlain) launch_mode<kPlain, int64_t>(ks, grid, lds, stream, a);
-    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t>(ks, grid, lds, stream, a);
-    else launch_mode<kRopeGlm, int64_t>(ks, grid, lds, stream, a);
+    if (mode == kPlain) launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a);
+    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a);
+    else launch_mode<kRopeGlm, int64_t>(tile_rows, ks, grid, lds, stream, a);
   } else {
-    if (mode == kPlain) launch_mode<kPlain, int32_t>(ks, grid, lds, stream, a);
-    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int32_t>(ks, grid, lds, stream, a);
-    else launch_mode<kRopeGlm, int32_t>(ks, grid, lds, stream, a);
+    if (mode == kPlain) launch_mode<kPlain, int32_t>(tile_rows, ks, grid, lds, stream, a);
+    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int32_t>(tile_rows, ks, grid, lds, stream, a);
+    else launch_mode<kRopeGlm, int32_t>(tile_rows, ks, grid, lds, stream, a);
   }
   return skv_check_launch(what);
 }

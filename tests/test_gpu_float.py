@@ -298,3 +298,25 @@ def test_attention_device_length_long_rows(gpu):
         assert torch.equal(got.cpu(), want.cpu()), L
         ref = oracle.sparse_attention(q.cpu(), K.cpu(), V.cpu(), L)
         torch.testing.assert_close(got.cpu().float(), ref.float(), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("glm", [False, True])
+def test_rebuild_tile_shapes_agree(gpu, glm, monkeypatch):
+    """Workgroups of 256, 128 and 64 rows (chosen by the grid size, forced here) run the same
+    per-row MFMA sequence: bit-identical keys, and within tolerance of the oracle."""
+    B, H, ctx, R, S, c = 2, 8, 4096, 160, 256, 8
+    _say(f"rebuild tile shapes glm={glm}")
+    U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 21, True, False)
+    cs = oracle.build_glm_cos_sin_cache(ctx, 5e6) if glm else oracle.build_cos_sin_cache(ctx, 5e5)
+    start = 448
+    cache = torch.randn(B, H, start + S * c + 32, 128).to(torch.bfloat16)
+    outs = []
+    for tile in (256, 128, 64):
+        monkeypatch.setenv("SKV_REBUILD_TILE", str(tile))
+        cg = cache.to(gpu)
+        shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
+        torch.cuda.synchronize()
+        outs.append(cg.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    want = oracle.rebuild_k_rope(U, SV, ids, cnts, cs, c, cache.clone(), start, glm=glm)
+    torch.testing.assert_close(outs[0].float(), want.float(), rtol=RTOL, atol=ATOL)
