@@ -59,13 +59,15 @@ def parse() -> argparse.Namespace:
     p.add_argument("--graph-steps", type=int, default=8,
                    help="decode steps per captured graph (one continuous lane pipeline across steps); "
                         "reduced to a divisor of --steps")
-    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode", "pool"],
+    p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode", "pool",
+                                          "hostlink"],
                    default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
                         "attention: the sparse decode attention alone; select: the fused chunk selection alone; "
                         "linear: the skinny decode projections alone (next to torch's GEMM); encode: the prefill "
                         "encoder (low-rank factors, chunk statistics, outliers, landmarks, initial selection); "
-                        "pool: one layer's sparse step on drifting queries with and without a device chunk pool")
+                        "pool: one layer's sparse step on drifting queries with and without a device chunk pool; "
+                        "hostlink: pinned-host read rate of SDMA copies and of the value-fetch gather")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -74,7 +76,12 @@ def parse() -> argparse.Namespace:
 
 
 class KernelTimer:
-    """Brackets every call of one shim function with HIP events on the current stream."""
+    """Brackets every call of one shim function with HIP events on the current stream. The host
+    first waits for that stream's earlier work (only that stream: the other streams' work keeps
+    running beside the timed call), because a start event queued behind a cross-stream wait can be
+    timestamped before the wait resolves and would then count the wait as the call's time; then a
+    short device spin holds the stream while the start event and the call are queued, so the host's
+    launch latency does not count either."""
 
     def __init__(self, module, name: str):
         import torch
@@ -87,6 +94,8 @@ class KernelTimer:
             if not self.active:
                 return self.orig(*a, **kw)
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.current_stream().synchronize()
+            torch.cuda._sleep(100000)  # ~40 us of device spin: the call is queued before the stream resumes
             s.record()
             out = self.orig(*a, **kw)
             e.record()
@@ -135,12 +144,30 @@ def scoring_launch_ms(model, rounds: int = 8, sweeps: int = 4):
             f"sweeps over the layers, each launch on its layer's live landmarks), after the timed steps")
 
 
+def host_cpu() -> tuple[int, str]:
+    """(threads usable by this process, CPU model name from /proc/cpuinfo)."""
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except AttributeError:
+        threads = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return max(1, threads), model
+
+
 def cpu_baseline(model, runs: int) -> dict:
-    """The CPU oracle on one layer's hot-path ops at the workload's shapes (layer 0 state)."""
+    """The CPU oracle on one layer's hot-path ops at the workload's shapes (layer 0 state), on every
+    CPU this process may use."""
     import torch
     import oracle
 
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    threads, cpu_model = host_cpu()
     torch.set_num_threads(threads)
     states = []
     for lane in model.lanes:  # layer-0 state of every batch slice: the whole batch
@@ -170,16 +197,109 @@ def cpu_baseline(model, runs: int) -> dict:
             times.append(dt)
     layer_s = statistics.median(times)
     return {"value": round(B / (layer_s * cache.num_layers), 3), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
+            "kind": "port", "cpu_model": cpu_model, "os_cpu_count": os.cpu_count(),
             "sample": (f"oracle (CPU torch/numpy) restatement of one layer's hot-path ops (scoring, GQA max, top-k, "
                        f"reorder, value fetch, key compaction, rebuild+RoPE, attention) at batch {B}, ctx "
-                       f"{cache.prefill}, layer-0 state; median of {runs} runs after 3 warmups = "
-                       f"{layer_s * 1e3:.1f} ms/layer, scaled to {cache.num_layers} layers; dense layers excluded; "
-                       f"reported baseline only")}
+                       f"{cache.prefill}, layer-0 state, torch threads {threads}; median of {runs} runs after 3 "
+                       f"warmups = {layer_s * 1e3:.1f} ms/layer, scaled to {cache.num_layers} layers; dense layers "
+                       f"excluded; reported baseline only")}
+
+
+def single_layer_inputs(seed: int = 8192):
+    """Seeded inputs of the single-layer decode workload: batch 1, 8 kv heads x 4 query heads,
+    head_dim 128, ctx 8192; pre-RoPE keys A(8192 x 160).B(160 x 1024) + 0.05 N(0,1) with A, B of
+    standard deviation 1/sqrt(160); values, the last prompt query and the decode token's q, k, v
+    ~ N(0,1); bf16 CPU tensors."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    B, H, G, D, ctx, rank = 1, 8, 4, 128, 8192, 160
+    A = torch.randn(ctx, rank, generator=g) / rank ** 0.5
+    Bm = torch.randn(rank, H * D, generator=g) / rank ** 0.5
+    k_pre = (A @ Bm + 0.05 * torch.randn(ctx, H * D, generator=g)).view(1, ctx, H, D).transpose(1, 2)
+    k_pre = k_pre.to(torch.bfloat16).contiguous()
+    v = torch.randn(B, H, ctx, D, generator=g).to(torch.bfloat16)
+    q_last = torch.randn(B, H * G, 1, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, H * G, D, generator=g).to(torch.bfloat16)
+    k_new = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    return dict(k_pre=k_pre, v=v, q_last=q_last, q=q, k_new=k_new, v_new=v_new, H=H, G=G, D=D, ctx=ctx, rank=rank)
+
+
+def single_layer_gpu_ms(runs: int = 20) -> dict:
+    """The single-layer workload on the product path: the device encoder builds the layer's state
+    (get_svd + prefill_kv_cache), then one decode step of the layer through ShadowAttention.decode
+    (scoring, selection, value fetch from pinned host memory, key rebuild, attention) is timed with
+    HIP events, median over `runs` steps."""
+    import types
+    import torch
+    from shadowkv_amd.models.attention import ShadowAttention
+    from shadowkv_amd.models.kvcache import ShadowKVCache_CPU
+    from shadowkv_amd.models.tensor_op import build_cos_sin_cache
+
+    x = single_layer_inputs()
+    H, G, D, ctx = x["H"], x["G"], x["D"], x["ctx"]
+    dev = torch.device("cuda")
+    cfg = types.SimpleNamespace(num_attention_heads=H * G, num_key_value_heads=H, hidden_size=H * G * D,
+                                num_hidden_layers=1)
+    cache = ShadowKVCache_CPU(cfg, batch_size=1, max_length=ctx, device="cuda", sparse_budget=2048, chunk_size=8,
+                              rank=x["rank"], max_decode_len=runs + 8)
+    cos_sin = build_cos_sin_cache(ctx + 64, 500000.0, D, device=dev)
+
+    # the new token arrives rotated (the model's RoPE runs before the attention handler)
+    attn = ShadowAttention(cache, G, D, H * G * D,
+                           lambda q, k, p: (q.view(1, -1, H * G, D).transpose(1, 2), k.view(1, -1, H, D).transpose(1, 2)),
+                           None, cos_sin)
+    from shadowkv_amd.models.tensor_op import apply_rotary_pos_emb_cuda
+    k_pre, v = x["k_pre"].to(dev), x["v"].to(dev)
+    pos = torch.arange(ctx, device=dev).view(1, 1, ctx).expand(1, H, ctx)
+    q_pos = torch.full((1, H * G, 1), ctx - 1, dtype=torch.int64, device=dev)
+    q_last = apply_rotary_pos_emb_cuda(x["q_last"].to(dev), cos_sin, q_pos)
+    cache.get_svd(k_pre, 0)
+    cache.prefill_kv_cache(v, 0, apply_rotary_pos_emb_cuda(k_pre, cos_sin, pos), q_last)
+    cache.H2D()
+    q = x["q"].to(dev).reshape(1, 1, -1)
+    k = x["k_new"].to(dev).reshape(1, 1, -1)
+    vv = x["v_new"].to(dev).reshape(1, H, 1, D)
+    ms = []
+    for i in range(runs + 2):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        attn.decode(q, k, vv, None, 0)
+        e.record()
+        e.synchronize()
+        if i >= 2:
+            ms.append(s.elapsed_time(e))
+    return {"gpu_ms_per_step": round(statistics.median(ms), 4), "n_landmarks": int(cache.k_landmark.shape[-2]),
+            "hits_last_step": int(cache.cnts.sum())}
+
+
+def single_layer_cpu_ms(runs: int) -> dict:
+    """The CPU oracle's single-layer decode step at the single-layer workload's shape (state encoded
+    by the oracle: full SVD, bf16 cosine outliers), median of `runs` steps after 3 warmups."""
+    import copy
+    import torch
+    import oracle
+
+    threads, _ = host_cpu()
+    torch.set_num_threads(threads)
+    x = single_layer_inputs()
+    cs = oracle.build_cos_sin_cache(x["ctx"] + 64, 500000.0)
+    st0 = oracle.encode_layer(x["k_pre"], x["v"], x["q_last"], cs, rank=x["rank"], chunk=8, budget=2048)
+    times = []
+    for i in range(3 + runs):
+        st = copy.deepcopy(st0)
+        t0 = time.perf_counter()
+        oracle.decode_layer_step(st, x["q"], x["k_new"], x["v_new"], cs)
+        if i >= 3:
+            times.append(time.perf_counter() - t0)
+    return {"cpu_ms_per_step": round(statistics.median(times) * 1e3, 3), "cores": threads, "kind": "port",
+            "n_landmarks": int(st0.landmarks.shape[-2])}
 
 
 def breakdown(model, tok) -> dict:
-    """One instrumented step: per-op device time of the sparse path and the host-link rate."""
+    """One instrumented step: per-op device time of the sparse path (HIP events on the stream each
+    op runs on, in the pipelined eager step), the host-link rate, and each selection's offsets and
+    hit counts (for replaying the layer's kernels alone)."""
     import torch
     from shadowkv_amd.kernels import shadowkv
 
@@ -188,7 +308,7 @@ def breakdown(model, tok) -> dict:
              "gather_copy_d2d_with_offsets", "rebuild_k_rope", "sparse_attn_decode"]
     timers = {n: KernelTimer(shadowkv, n) for n in names}
     cache = model.cache
-    snaps = []  # (selected chunks, device copy of the hit counts) per call; no host sync in the step
+    snaps = []  # (selected chunks, device copies of offsets and hit counts) per call, in call order
     pooled = cache.pooled
     sel_name = "pool_assign" if pooled else "select_chunks"
     orig_select = timers[sel_name].orig
@@ -196,9 +316,9 @@ def breakdown(model, tok) -> dict:
     def select_and_snapshot(*a, **kw):
         out = orig_select(*a, **kw)
         if pooled:  # pool_assign(selected [rows, S], ..., cnts)
-            snaps.append((a[0].numel(), a[9].clone()))
-        else:  # select_chunks(..., rows, ..., select_sets, ..., cnts)
-            snaps.append((a[3] * a[7], a[11].clone()))
+            snaps.append((a[0].numel(), None, a[9].clone()))
+        else:  # select_chunks(..., rows, ..., select_sets, ..., position_ids, offsets, cnts)
+            snaps.append((a[3] * a[7], a[10].clone(), a[11].clone()))
         return out
 
     timers[sel_name].orig = select_and_snapshot
@@ -214,12 +334,129 @@ def breakdown(model, tok) -> dict:
     ops = {n: round(t.mean_ms() * 1e3, 2) for n, t in timers.items() if t.pairs}
     chunk_bytes = cache.chunk_size * cache.head_dim * 2
     fetch_ms = timers["gather_copy_misses_to_slots" if pooled else "gather_copy_with_offsets"].mean_ms()
-    total_sel = statistics.fmean(t for t, _ in snaps)
-    miss_mean = statistics.fmean(t - int(c.sum()) for t, c in snaps)
+    total_sel = statistics.fmean(t for t, _, _ in snaps)
+    miss_mean = statistics.fmean(t - int(c.sum()) for t, _, c in snaps)
+    # calls run layer by layer, the lanes in order within a layer: call k = (layer k // lanes, lane k % lanes)
+    nl = len(model.lanes)
+    per_layer = {(k // nl, k % nl): (o, c) for k, (_, o, c) in enumerate(snaps)}
     return {"op_us_per_layer": ops, "hit_rate": round(1 - miss_mean / total_sel, 4),
             "host_link": {"bytes_per_layer": int(miss_mean * chunk_bytes),
                           "GBps": round(miss_mean * chunk_bytes / (fetch_ms * 1e-3) / 1e9, 2),
-                          "note": "value fetch (hit compaction + zero-copy miss gather) per layer"}}
+                          "note": "value fetch (zero-copy miss gather from pinned host memory) per lane-layer, "
+                                  "HIP events on the fetch stream in one eager pipelined step"}}, per_layer
+
+
+def host_link_peak_gbps(nbytes: int = 256 << 20, reps: int = 5) -> float:
+    """Host-to-device rate of an SDMA copy (hipMemcpyAsync) of `nbytes` of pinned host memory."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        dst.copy_(src, non_blocking=True)
+    e.record()
+    e.synchronize()
+    gbps = nbytes * reps / (s.elapsed_time(e) * 1e-3) / 1e9
+    del src, dst
+    return gbps
+
+
+def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> list:
+    """Every kernel of the sparse step at the workload's shapes, each alone: `sweeps` passes over
+    the layers of lane 0 with that layer's live state (landmarks, U/SV, buffers, host store) and the
+    offsets / hit counts its selection produced in the instrumented step, captured in a HIP graph
+    and replayed between HIP events. Beside each, the in-step time (HIP events in the pipelined
+    eager step), the algorithmic bytes of one launch and the fraction of the bounding roofline."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    lane = model.lanes[0]
+    c = lane.cache
+    L = c.num_layers
+    B, H, G, D = c.batch_size, c.num_key_value_heads, c.num_key_value_groups, c.head_dim
+    BH, S, ch, R = B * H, c.select_sets, c.chunk_size, c.rank
+    n = c.k_landmark.shape[-2]
+    chunk_bytes = ch * D * 2
+    offs = [per_layer[(l, 0)][0].clone() for l in range(L)]
+    cnts = [per_layer[(l, 0)][1].clone() for l in range(L)]
+    hits = [int(x.sum()) for x in cnts]
+    mean_hits = statistics.fmean(hits)
+    mean_miss = BH * S - mean_hits
+    kv_len = c.sparse_end + c.gen_offset
+    q = torch.randn(B, H * G, 1, D, device=c.device).to(torch.bfloat16)
+    qa = q.view(B, H * G, D)
+    out = torch.empty(B, H * G, D, dtype=torch.bfloat16, device=c.device)
+    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, H * G, c.buf_len), dtype=torch.uint8, device=c.device)
+    reps = sweeps * L
+
+    def t_us(fn):
+        return gpu_time_per_call(fn, reps, rounds=4) * 1e6
+
+    res = []
+
+    def add(kernel, bound, nbytes, iso_us, step_us, peak, unit="GB/s", extra=None):
+        e = {"kernel": kernel, "bound": bound, "algorithmic_bytes": int(nbytes), "isolated_us": round(iso_us, 2),
+             "in_step_us": round(step_us, 2) if step_us else None,
+             "isolated_GBps": round(nbytes / iso_us / 1e3, 1), "peak": round(peak, 1), "unit": unit,
+             "isolated_frac": round(nbytes / iso_us / 1e3 / peak, 4),
+             "in_step_frac": round(nbytes / step_us / 1e3 / peak, 4) if step_us else None}
+        if extra:
+            e.update(extra)
+        res.append(e)
+
+    # a1: landmark scoring
+    score_us = t_us(lambda i: shadowkv.score_logits(q, c.k_landmark[i % L], c.gemm_o, c.norm, c.sum, BH, G, n, D,
+                                                    1.0 / math.sqrt(128)))
+    lb = logits_bytes(BH, G, n)
+    add("score_logits (a1 logits + per-tile softmax partials)", "hbm", lb, score_us, ops_in_step.get("score_logits"),
+        HBM_PEAK_GBS)
+    # a1 tail + a2 + a3: softmax normalisation, GQA max, top-k, id gather, reorder (the selection chain)
+    sel_us = t_us(lambda i: shadowkv.select_chunks(
+        c.gemm_o, c.norm, c.sum, BH, G, n, c.k_landmark_idx[i % L].view(BH, n), S, c.chunks,
+        c.position_ids[i % L].view(BH, -1), c.offsets, c.cnts, out_scores=c.chunk_attn, workspace=c.select_workspace))
+    sel_bytes = BH * (G * n * 2 + G * ((n + 255) // 256) * 8 + n * 8 + n * 2 + S * 8 * 2 + S * 4)
+    add("select_chunks (softmax tail + GQA max + top-k + id gather + reorder)", "latency", sel_bytes, sel_us,
+        ops_in_step.get("select_chunks"), HBM_PEAK_GBS)
+    # the survey's a1+a2 unit: landmarks + q read, scores and ids written, over scoring + selection
+    unit_bytes = BH * (n * D * 2 + G * D * 2 + n * 2 + S * 8)
+    step_unit = (ops_in_step.get("score_logits", 0) + ops_in_step.get("select_chunks", 0)) or None
+    add("a1+a2 unit (scoring + selection chain)", "hbm", unit_bytes, score_us + sel_us, step_unit, HBM_PEAK_GBS)
+    # a4/a5: in-buffer hit compaction (K and V: two launches of this per layer)
+    comp_bytes = 2 * mean_hits * chunk_bytes
+    comp_us = t_us(lambda i: shadowkv.gather_copy_d2d_with_offsets(
+        c.v_cache_buffer[i % L], offs[i % L], cnts[i % L], B, H, int(c.sparse_budget * D), c.kernel_offset,
+        c.kernel_stride, S))
+    add("gather_copy_d2d_with_offsets (hit compaction, per buffer)", "hbm", comp_bytes, comp_us,
+        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS, extra={"mean_hits": round(mean_hits, 1)})
+    # a4: value fetch of the misses from pinned host memory
+    fetch_bytes = mean_miss * chunk_bytes
+    fetch_us = t_us(lambda i: shadowkv.gather_copy_with_offsets(
+        c.v_cache_cpu[i % L], c.v_cache_buffer[i % L], None, offs[i % L], cnts[i % L], None, B, H,
+        int(c.max_ctx_chunks_len * D), int(c.sparse_budget * D), c.kernel_offset, c.kernel_stride, S,
+        misses_only=True))
+    add("gather_copy_with_offsets (value fetch of the misses, host link)", "host link", fetch_bytes, fetch_us,
+        ops_in_step.get("gather_copy_with_offsets"), link_peak,
+        extra={"peak_source": "SDMA copy (hipMemcpyAsync) of 256 MiB pinned host memory, measured in this run",
+               "nominal_link_GBps": 64.0})
+    # a5-a7: low-rank key rebuild + RoPE of the miss rows
+    rows = mean_miss * ch
+    rb_bytes = rows * (R * 2 + D * 2 + D * 2) + BH * (R * D * 2 + S * 8)
+    rb_us = t_us(lambda i: shadowkv.rebuild_k_rope(c.U[i % L], c.SV[i % L], c.position_ids[i % L], cnts[i % L],
+                                                   model.cos_sin, c.k_cache_buffer[i % L], c.sparse_start, ch))
+    flops = 2 * rows * R * D
+    add("rebuild_k_rope (gather-GEMM on MFMA + RoPE epilogue)", "hbm", rb_bytes, rb_us,
+        ops_in_step.get("rebuild_k_rope"), HBM_PEAK_GBS,
+        extra={"mfma_flops": int(flops), "isolated_mfma_util": round(flops / (rb_us * 1e-6) / MFMA_BF16_PEAK, 4)})
+    # a8: sparse attention (split + merge launches)
+    at_bytes = BH * 2 * kv_len * D * 2 + 2 * B * H * G * D * 2
+    at_us = t_us(lambda i: shadowkv.sparse_attn_decode(qa, c.k_cache_buffer[i % L][:, :, :kv_len],
+                                                       c.v_cache_buffer[i % L][:, :, :kv_len], kv_len, out, ws))
+    add("sparse_attn_decode (split + merge)", "hbm", at_bytes, at_us, ops_in_step.get("sparse_attn_decode"),
+        HBM_PEAK_GBS, extra={"kv_len": kv_len})
+    return res
 
 
 # Footprint that the input sets of one timed loop must exceed, so that back-to-back launches read
@@ -652,6 +889,48 @@ def encode_microbench(args) -> int:
     return 0
 
 
+def hostlink_microbench(args) -> int:
+    """Host-link read rate from pinned host memory: SDMA copies (hipMemcpyAsync host-to-device) of
+    16 MiB to 1 GiB, and the value-fetch kernel's zero-copy gather at the decode shape (one batch
+    lane of the Llama-3-8B workload: 4 sequences x 8 kv heads, 256 random missing 2 KB chunks per
+    (b, h) out of a 1 GiB store of 15360 chunks per row) and at 8x that many chunks. The gather's
+    workgroup count follows SKV_FETCH_WGS (read once per process). One JSON line per case."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    dev = torch.device("cuda")
+    rounds = max(args.steps, 4)
+    for mib in (16, 256, 1024):
+        nbytes = mib << 20
+        t = host_link_peak_gbps(nbytes, reps=rounds)
+        print(json.dumps({"metric": "host-to-device GB/s", "value": round(t, 2), "unit": "GB/s", "n_gpus": 1,
+                          "higher_is_better": True, "dtype": "u8", "data": "pinned host memory",
+                          "config": {"workload": f"SDMA copy (hipMemcpyAsync) of {mib} MiB pinned -> device"}}),
+              flush=True)
+    B, H, S, chunks, E = 4, 8, 256, 15360, 8 * 128
+    store = torch.empty(B, H, chunks, E, dtype=torch.bfloat16, pin_memory=True)
+    store.view(torch.int16).copy_(torch.randint(-30000, 30000, (B, H, chunks, E), dtype=torch.int16))
+    g = torch.Generator(device=dev).manual_seed(3)
+    wgs = os.environ.get("SKV_FETCH_WGS", "default (48)")
+    for mult in (1, 8):
+        s_sets = S * mult
+        buf = torch.empty(B, H, s_sets * 8, 128, dtype=torch.bfloat16, device=dev)
+        sets = [torch.rand(B * H, chunks, generator=g, device=dev).argsort(dim=-1)[:, :s_sets].sort(dim=-1)
+                .values.to(torch.int32).reshape(-1).contiguous() for _ in range(8)]
+        cnts = torch.zeros(B * H, dtype=torch.int32, device=dev)
+        t = gpu_time_per_call(lambda i: shadowkv.gather_copy_with_offsets(
+            store, buf, None, sets[i % 8], cnts, None, B, H, chunks * E, s_sets * E, 0, s_sets * E, s_sets,
+            misses_only=True), 16, rounds=rounds)
+        nbytes = B * H * s_sets * E * 2
+        print(json.dumps({"metric": "zero-copy gather GB/s", "value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                          "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
+                          "data": "pinned host store of 1 GiB, random sorted chunk ids",
+                          "config": {"workload": f"value-fetch kernel, {B * H} rows x {s_sets} chunks of 2 KB "
+                                                 f"({nbytes / 2 ** 20:.0f} MiB per launch)", "fetch_wgs": wgs,
+                                     "us_per_launch": round(t * 1e6, 2)}}), flush=True)
+    return 0
+
+
 def encode_cpu_baseline(k_pre, v, q, R, c, budget, sample_ctx: int = 16384) -> dict:
     """The CPU oracle's encode_layer on the first sample_ctx tokens of batch row 0 (a reported
     baseline only), scaled linearly to the full prompt."""
@@ -689,6 +968,8 @@ def main() -> int:
         return encode_microbench(args)
     if args.workload == "pool":
         return pool_microbench(args)
+    if args.workload == "hostlink":
+        return hostlink_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv
@@ -747,21 +1028,43 @@ def main() -> int:
     lb = logits_bytes(BH, G, n)
     k_ms, timing = scoring_launch_ms(model)
     achieved = lb / (k_ms * 1e-3) / 1e9
-    traffic = None
-    # HBM traffic per launch from FETCH_SIZE / WRITE_SIZE counter runs of this launch shape
+    traffic, traffic_source = None, None
+    # HBM traffic per launch of this launch shape, from the committed FETCH_SIZE / WRITE_SIZE
+    # counter runs (rocprofv3 --pmc cannot run inside this process)
     for tfile in sorted((ROOT / "profiles").glob("score_logits_*_traffic.json")):
         rec = json.loads(tfile.read_text())
         if rec.get("launch") == {"rows": BH, "m": G, "n": n, "k": 128}:
             traffic = rec.get("bytes_per_launch")
+            traffic_source = (f"{tfile.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this "
+                              f"launch shape, scaled by the counters' reading of a plain copy (not measured in this run)")
 
     detail = None
     if not args.no_breakdown:
-        detail = breakdown(model, tok)
+        detail, per_layer = breakdown(model, tok)
         log(f"breakdown {detail}")
+        link_peak = host_link_peak_gbps()
+        hl = detail["host_link"]
+        hl.update(peak_GBps=round(link_peak, 1), frac_of_peak=round(hl["GBps"] / link_peak, 4),
+                  peak_source="SDMA copy (hipMemcpyAsync) of 256 MiB of pinned host memory in this run; "
+                              "profiles/hostlink_microbench.md has the zero-copy gather beside it",
+                  nominal_GBps=64.0)
+        if not cache.pooled:
+            detail["kernels"] = kernel_table(model, per_layer, detail["op_us_per_layer"], link_peak)
+            for k in detail["kernels"]:
+                log(f"kernel {k['kernel'][:40]:40s} isolated {k['isolated_us']:8.2f} us "
+                    f"({k['isolated_frac'] * 100:5.1f}%), in step {k['in_step_us']} us")
+        detail["single_layer"] = {"workload": "single-layer decode step, batch 1, 8 kv heads x 4 query heads, ctx "
+                                              "8192, rank 160, budget 2048, 968 landmarks, V in pinned host memory",
+                                  **single_layer_gpu_ms()}
+        log(f"single layer {detail['single_layer']}")
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline")
         cpu = cpu_baseline(model, args.cpu_runs)
+        if detail is not None:
+            sl = single_layer_cpu_ms(args.cpu_runs)
+            detail["single_layer"].update(sl)
+            log(f"single layer CPU {sl}")
 
     out = {
         "metric": ("decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util"
@@ -785,8 +1088,8 @@ def main() -> int:
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": lb, "avg_launch_us": round(k_ms * 1e3, 2),
-                     "timing": timing},
+                     "traffic": traffic, "traffic_source": traffic_source, "algorithmic_bytes_per_launch": lb,
+                     "avg_launch_us": round(k_ms * 1e3, 2), "timing": timing},
         "cpu_baseline": cpu,
     }
     if detail is not None:

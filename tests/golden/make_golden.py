@@ -125,6 +125,39 @@ def decode_small_case(chunk=8, glm=False):
                 dims=dict(B=B, H=H, G=G, D=D, ctx=ctx, rank=rank, chunk=chunk, budget=budget))
 
 
+def single_layer_case(seed: int = 8192):
+    """The single-layer decode workload at its own shape: Llama-3-8B heads (8 kv heads x 4 query
+    heads, head_dim 128), batch 1, ctx 8192, rank 160, chunk 8, budget 2048 (256 chunks), 48
+    outlier chunks and 4 local chunks, hence 968 landmarks; pre-RoPE keys A(8192 x 160).B(160 x 1024)
+    + 0.05 N(0,1) with A, B ~ N(0, 1/160) (standard deviation 1/sqrt(160)), values, last prompt query
+    and the decode token's q/k/v ~ N(0,1), bf16; RoPE theta 5e5. Encoded by the oracle (full SVD,
+    bf16 cosine outliers, torch.topk initial selection); one oracle decode step on top."""
+    sys.path.insert(0, str(HERE.parents[1]))
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(seed)
+    B, H, G, D, ctx, rank, budget, chunk = 1, 8, 4, 128, 8192, 160, 2048, 8
+    A = torch.randn(ctx, rank, generator=g) / rank ** 0.5
+    Bm = torch.randn(rank, H * D, generator=g) / rank ** 0.5
+    k_pre = (A @ Bm + 0.05 * torch.randn(ctx, H * D, generator=g)).view(1, ctx, H, D).transpose(1, 2)
+    k_pre = k_pre.to(torch.bfloat16).contiguous()
+    v = torch.randn(B, H, ctx, D, generator=g).to(torch.bfloat16)
+    q_last = torch.randn(B, H * G, 1, D, generator=g).to(torch.bfloat16)
+    cos_sin = oracle.build_cos_sin_cache(ctx + 64, 500000.0)
+    st = oracle.encode_layer(k_pre, v, q_last, cos_sin, rank=rank, chunk=chunk, budget=budget)
+    q = torch.randn(B, H * G, D, generator=g).to(torch.bfloat16)
+    k_new = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    state_in = dict(U=st.U.clone(), SV=st.SV.clone(), landmarks=st.landmarks.clone(),
+                    landmark_idx=st.landmark_idx.clone(), host_v=st.host_v.clone(), kbuf=st.kbuf.clone(),
+                    vbuf=st.vbuf.clone(), position_ids=st.position_ids.clone())
+    res = oracle.decode_layer_step(st, q, k_new, v_new, cos_sin)
+    return dict(state_in=state_in, st=st, res=res, q=q, k_new=k_new, v_new=v_new, cos_sin=cos_sin,
+                k_pre=k_pre, v=v, q_last=q_last,
+                dims=dict(B=B, H=H, G=G, D=D, ctx=ctx, rank=rank, chunk=chunk, budget=budget))
+
+
 def digest(t) -> str:
     import hashlib
     import torch

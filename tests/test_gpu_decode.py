@@ -39,6 +39,30 @@ def test_single_layer_decode_step(gpu):
         assert np.array_equal(got["position_ids"], d["out_position_ids"])
 
 
+def test_single_layer_step_at_workload_shape(gpu):
+    """The composed single-layer step at the single-layer workload's own shape (8 kv heads, rank
+    160, ctx 8192, budget 2048, 968 landmarks) through the drop-in classes, against the oracle."""
+    print("single-layer workload shape: batch 1, 8 kv heads, ctx 8192, rank 160", flush=True)
+    case = make_golden.single_layer_case()
+    assert case["state_in"]["landmarks"].shape[-2] == 968 and case["st"].sparse_start == 448
+    got = run_decode_step_gpu(case, gpu)
+    B, H = case["dims"]["B"], case["dims"]["H"]
+    check_scoring(got["cache"], case["q"], case["state_in"]["landmarks"])
+    st = fresh_oracle_state(case)
+    res = oracle.decode_layer_step(st, case["q"], case["k_new"], case["v_new"], case["cos_sin"],
+                                   scores=got["scores"])
+    assert torch.equal(got["selected"], res["selected"])
+    assert np.array_equal(got["cnts"], res["cnts"])
+    assert np.array_equal(got["offsets"], res["offsets"].reshape(B * H, -1))
+    assert np.array_equal(got["position_ids"], st.position_ids.numpy())
+    L = res["L"]
+    assert L == 2497
+    assert torch.equal(got["vbuf"], st.vbuf[:, :, :L])
+    torch.testing.assert_close(got["kbuf"].float(), st.kbuf[:, :, :L].float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(got["out"].float(), res["out"].float(), rtol=2e-2, atol=2e-2)
+    print(f"hits per head {got['cnts'].tolist()}", flush=True)
+
+
 @pytest.mark.parametrize("device_lengths,chunk,split,glm", [(False, 8, None, False), (True, 8, None, False),
                                                            (True, 4, None, False), (True, 16, None, False),
                                                            (False, 16, None, False), (True, 8, "1", False),
