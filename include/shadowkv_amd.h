@@ -98,6 +98,40 @@ int skv_apply_rotary_pos_emb_new(const uint16_t* x, const uint16_t* cos_sin, con
                                  int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h,
                                  int64_t stride_pid_s, int half_dim, int64_t cos_sin_rows, void* stream);
 
+/* Replaces apply_rotary_pos_emb (kernels/functions.h:53-59, kernels/rope.cu:26-88): the rotation
+ * with separate cos and sin tables (rows of stride_cos / stride_sin, table_rows rows, indexed by
+ * position_ids[b,h,s], int64): output[b,h,s,d] = bf16(bf16(x1*cos[d]) + bf16(-x2*sin[d])),
+ * output[b,h,s,d+half] = bf16(bf16(x2*cos[d+half]) + bf16(x1*sin[d+half])), output addressed with
+ * x's strides; rows whose position is outside [0, table_rows) are left unwritten. Bound by the
+ * reference's module but not called by its Python. */
+int skv_apply_rotary_pos_emb(const uint16_t* x, const uint16_t* cos, const uint16_t* sin, const int64_t* position_ids,
+                             uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
+                             int64_t stride_xb, int64_t stride_xh, int64_t stride_xs, int64_t stride_xe,
+                             int64_t stride_cos, int64_t stride_sin, int64_t stride_pid_b, int64_t stride_pid_h,
+                             int64_t stride_pid_s, int half_dim, int64_t table_rows, void* stream);
+
+/* Replaces apply_rotary_pos_emb_new_v2 (kernels/functions.h:69-75, kernels/rope_new.cu:86-144): every
+ * row s rotated at table row position_ids[b,h,s/chunk_size]*chunk_size + s%chunk_size (int32 chunk
+ * ids) with the half-split [cos|sin] table, written to output at x's strides (stride_xe must be 1).
+ * Bound by the reference's module but not called by its Python. */
+int skv_apply_rotary_pos_emb_new_v2(const uint16_t* x, const uint16_t* cos_sin, const int32_t* position_ids,
+                                    uint16_t* output, int batch_size, int heads, int seq_len, int embed_dim,
+                                    int64_t stride_xb, int64_t stride_xh, int64_t stride_xs, int64_t stride_xe,
+                                    int64_t stride_cos_sin, int64_t stride_pid_b, int64_t stride_pid_h,
+                                    int64_t stride_pid_s, int half_dim, int chunk_size, int64_t cos_sin_rows,
+                                    void* stream);
+
+/* Replaces apply_rotary_pos_emb_push_cache (kernels/functions.h:77-86, kernels/rope_new.cu:146-222):
+ * the same contract as skv_apply_rotary_pos_emb_push_cache_opt below (the reference's "_opt" form is
+ * a faster launch of the same rows). Bound by the reference's module but not called by its Python. */
+int skv_apply_rotary_pos_emb_push_cache(
+    const uint16_t* x, const uint16_t* cos_sin, const int32_t* position_ids, uint16_t* output,
+    const int32_t* cnts, int batch_size, int heads, int seq_len, int embed_dim, int64_t stride_xb,
+    int64_t stride_xh, int64_t stride_xs, int64_t stride_xe, int64_t stride_cos_sin, int64_t stride_pid_b,
+    int64_t stride_pid_h, int64_t stride_pid_s, int64_t stride_output_b, int64_t stride_output_h,
+    int64_t stride_output_s, int offset_output_s_start, int offset_output_s_end, int half_dim,
+    int chunk_size, int64_t cos_sin_rows, void* stream);
+
 /* Replaces apply_rotary_pos_emb_push_cache_opt (kernels/functions.h:88-97, kernels/rope_new.cu:224-302):
  * for rows s with s/chunk_size >= cnts[b*heads+h] and start+s < end, writes
  * rope(x[b,h,s], cos_sin[position_ids[b,h,s/chunk]*chunk + s%chunk]) to output[b,h,start+s];

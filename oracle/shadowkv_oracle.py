@@ -15,7 +15,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "reorder", "cached_gather_copy", "compact_hits", "gather_copy_plain", "rope_half_split", "rope_push",
-    "rope_push_glm", "rebuild_k", "rebuild_k_rope", "score_logits_softmax", "score_gqa_max", "topk_total_order",
+    "rope_push_glm", "rope_two_tables", "rebuild_k", "rebuild_k_rope", "score_logits_softmax", "score_gqa_max", "topk_total_order",
     "topk_gather", "sparse_attention", "build_cos_sin_cache", "build_glm_cos_sin_cache", "encode_layer",
     "decode_layer_step", "LayerState", "prefill_geometry", "pool_assign", "pool_from_layer", "decode_layer_step_pooled",
 ]
@@ -96,6 +96,17 @@ def rope_half_split(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> to
     s = torch.cat((sin, sin), dim=-1)
     rot = torch.cat((-x[..., h:], x[..., :h]), dim=-1)
     return (x * c) + (rot * s)
+
+
+def rope_two_tables(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Reference apply_rotary_pos_emb (kernels/rope.cu:26-62): x [..., D] bf16 with full-width cos
+    and sin rows [..., D] bf16; the first half rotated with cos[:D/2], sin[:D/2], the second with
+    cos[D/2:], sin[D/2:], every product and sum rounded to bf16.
+    Pinned by: numpy float32 with explicit round-to-nearest-even (tests/test_oracle_float.py) and,
+    for tables with equal halves, equality with rope_half_split."""
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h], x[..., h:]
+    return torch.cat(((x1 * cos[..., :h]) + ((-x2) * sin[..., :h]), (x2 * cos[..., h:]) + (x1 * sin[..., h:])), dim=-1)
 
 
 def rope_push(x: torch.Tensor, cos_sin: torch.Tensor, chunk_ids: torch.Tensor, cnts: torch.Tensor, chunk: int,

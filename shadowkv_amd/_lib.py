@@ -39,6 +39,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_apply_rotary_pos_emb_push_cache_opt_glm": (
         _i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _p]),
+    "skv_apply_rotary_pos_emb": (
+        _i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+               _i64, _p]),
+    "skv_apply_rotary_pos_emb_new_v2": (
+        _i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64,
+               _p]),
+    "skv_apply_rotary_pos_emb_push_cache": (
+        _i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+               _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _p]),
     "skv_batch_gather_gemm": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
     "skv_rebuild_k_rope": (
         _i32, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i32,

@@ -202,6 +202,60 @@ def apply_rotary_pos_emb_new(x, cos_sin, position_ids, output, batch_size, heads
               stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, cos_sin.shape[0], _stream())
 
 
+def apply_rotary_pos_emb(x, cos, sin, position_ids, output, batch_size, heads, seq_len, embed_dim, stride_xb,
+                         stride_xh, stride_xs, stride_xe, stride_cos, stride_sin, stride_pid_b, stride_pid_h,
+                         stride_pid_s, half_dim):
+    """RoPE with separate cos and sin tables (kernels/functions.h:53-59): output at x's strides."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(cos, "cos", torch.bfloat16)
+    _dev(sin, "sin", torch.bfloat16)
+    _dev(position_ids, "position_ids", torch.int64)
+    _dev(output, "output", torch.bfloat16)
+    xs = (batch_size, heads, seq_len, embed_dim)
+    xst = (stride_xb, stride_xh, stride_xs, stride_xe)
+    _need_offsets(x, xs, xst, "x")
+    _need_offsets(output, xs, xst, "output")
+    _need_offsets(position_ids, (batch_size, heads, seq_len), (stride_pid_b, stride_pid_h, stride_pid_s), "position_ids")
+    rows = min(cos.numel() // max(1, stride_cos), sin.numel() // max(1, stride_sin))
+    if rows < 1 or cos.shape[-1] < embed_dim or sin.shape[-1] < embed_dim:
+        raise ValueError("apply_rotary_pos_emb: cos/sin tables need rows of embed_dim entries")
+    _lib.call("skv_apply_rotary_pos_emb", x.data_ptr(), cos.data_ptr(), sin.data_ptr(), position_ids.data_ptr(),
+              output.data_ptr(), batch_size, heads, seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe,
+              stride_cos, stride_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, rows, _stream())
+
+
+def apply_rotary_pos_emb_new_v2(x, cos_sin, position_ids, output, batch_size, heads, seq_len, embed_dim, stride_xb,
+                                stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h,
+                                stride_pid_s, half_dim, chunk_size):
+    """RoPE of every row at the position of its chunk id (kernels/functions.h:69-75): row s of (b, h)
+    at table row position_ids[b, h, s // chunk_size] * chunk_size + s % chunk_size (int32 ids)."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(cos_sin, "cos_sin", torch.bfloat16)
+    _dev(position_ids, "position_ids", torch.int32)
+    _dev(output, "output", torch.bfloat16)
+    xs = (batch_size, heads, seq_len, embed_dim)
+    xst = (stride_xb, stride_xh, stride_xs, stride_xe)
+    _need_offsets(x, xs, xst, "x")
+    _need_offsets(output, xs, xst, "output")
+    _need_offsets(position_ids, (batch_size, heads, (seq_len + chunk_size - 1) // chunk_size),
+                  (stride_pid_b, stride_pid_h, stride_pid_s), "position_ids")
+    _lib.call("skv_apply_rotary_pos_emb_new_v2", x.data_ptr(), cos_sin.data_ptr(), position_ids.data_ptr(),
+              output.data_ptr(), batch_size, heads, seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe,
+              stride_cos_sin, stride_pid_b, stride_pid_h, stride_pid_s, half_dim, chunk_size, cos_sin.shape[0],
+              _stream())
+
+
+def apply_rotary_pos_emb_push_cache(x, cos_sin, position_ids, output, cnts, batch_size, heads, seq_len, embed_dim,
+                                    stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b,
+                                    stride_pid_h, stride_pid_s, stride_output_b, stride_output_h, stride_output_s,
+                                    offset_output_s_start, offset_output_s_end, half_dim, chunk_size):
+    """kernels/functions.h:77-86: the contract of apply_rotary_pos_emb_push_cache_opt."""
+    _push("skv_apply_rotary_pos_emb_push_cache", x, cos_sin, position_ids, output, cnts, batch_size, heads,
+          seq_len, embed_dim, stride_xb, stride_xh, stride_xs, stride_xe, stride_cos_sin, stride_pid_b, stride_pid_h,
+          stride_pid_s, stride_output_b, stride_output_h, stride_output_s, offset_output_s_start, offset_output_s_end,
+          half_dim, chunk_size)
+
+
 def _push(name, x, cos_sin, position_ids, output, cnts, *ints):
     _dev(x, "x", torch.bfloat16)
     _dev(cos_sin, "cos_sin", torch.bfloat16)

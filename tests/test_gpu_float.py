@@ -320,3 +320,49 @@ def test_rebuild_tile_shapes_agree(gpu, glm, monkeypatch):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     want = oracle.rebuild_k_rope(U, SV, ids, cnts, cs, c, cache.clone(), start, glm=glm)
     torch.testing.assert_close(outs[0].float(), want.float(), rtol=RTOL, atol=ATOL)
+
+
+def test_rope_two_tables_and_chunk_positions(gpu):
+    """The reference's remaining rotary bindings: separate cos/sin tables (apply_rotary_pos_emb),
+    chunk-id positions without hit rows (apply_rotary_pos_emb_new_v2), and push_cache (the _opt
+    contract), bit-exact against the oracle."""
+    _say("rope two tables / new_v2 / push_cache")
+    g = torch.Generator().manual_seed(77)
+    B, H, Ls, D, rows = 2, 4, 40, 128, 600
+    x = torch.randn(B, H, Ls, D, generator=g).to(torch.bfloat16)
+    cos = torch.randn(rows, D, generator=g).to(torch.bfloat16)
+    sin = torch.randn(rows, D, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, rows, (B, H, Ls), generator=g)
+    pos[0, 1, 3] = rows + 7  # outside the tables: row left unwritten
+    out = torch.full_like(x, 5.0).to(gpu)
+    xs = x.stride()
+    shadowkv.apply_rotary_pos_emb(x.to(gpu), cos.to(gpu), sin.to(gpu), pos.to(gpu), out, B, H, Ls, D, *xs,
+                                  cos.stride(0), sin.stride(0), *pos.stride(), D // 2)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    want = oracle.rope_two_tables(x, cos[pos.clamp_max(rows - 1)], sin[pos.clamp_max(rows - 1)])
+    want[0, 1, 3] = 5.0
+    assert torch.equal(got, want)
+    # new_v2: every row at its chunk id's position
+    c, S = 8, Ls // 8
+    cs = oracle.build_cos_sin_cache(4096, 5e5)
+    ids = torch.randint(0, 4000 // c, (B, H, S), generator=g, dtype=torch.int32)
+    out2 = torch.zeros_like(x).to(gpu)
+    shadowkv.apply_rotary_pos_emb_new_v2(x.to(gpu), cs.to(gpu), ids.to(gpu), out2, B, H, Ls, D, *xs, cs.stride(0),
+                                         *ids.stride(), D // 2, c)
+    torch.cuda.synchronize()
+    want2 = oracle.rope_push(x, cs, ids, torch.zeros(B * H, dtype=torch.int32), c, torch.zeros_like(x), 0, Ls)
+    assert torch.equal(out2.cpu(), want2)
+    # push_cache == push_cache_opt
+    cnts = torch.tensor([0, 1, 5, 2, 3, 0, 4, 1], dtype=torch.int32)
+    buf = torch.randn(B, H, Ls + 20, D, generator=g).to(torch.bfloat16)
+    outs = []
+    for fn in (shadowkv.apply_rotary_pos_emb_push_cache, shadowkv.apply_rotary_pos_emb_push_cache_opt):
+        o = buf.to(gpu)
+        fn(x.to(gpu), cs.to(gpu), ids.to(gpu), o, cnts.to(gpu), B, H, Ls, D, *xs, cs.stride(0), *ids.stride(),
+           *o.stride()[:3], 10, 10 + Ls - 4, D // 2, c)
+        torch.cuda.synchronize()
+        outs.append(o.cpu())
+    assert torch.equal(outs[0], outs[1])
+    want3 = oracle.rope_push(x, cs, ids, cnts, c, buf.clone(), 10, 10 + Ls - 4)
+    assert torch.equal(outs[0], want3)

@@ -240,3 +240,20 @@ def test_glm_token_rope_matches_glm_push():
     assert torch.equal(got, cache)
     assert torch.equal(got[:, :, 0], x[:, :, 0])
     assert torch.equal(got[..., 64:], x[..., 64:])
+
+
+def test_rope_two_tables_bit_exact_vs_numpy():
+    """The separate-table rotation: numpy float32 with explicit rounding, second half with the
+    tables' second halves; with equal halves it is the half-split rotation."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(200, 128, generator=g).to(torch.bfloat16)
+    c = torch.randn(200, 128, generator=g).to(torch.bfloat16)
+    s = torch.randn(200, 128, generator=g).to(torch.bfloat16)
+    got = to_np(oracle.rope_two_tables(x, c, s))
+    xn, cn, sn = to_np(x), to_np(c), to_np(s)
+    y1 = bf16_round_np(bf16_round_np(xn[:, :64] * cn[:, :64]) + bf16_round_np(-xn[:, 64:] * sn[:, :64]))
+    y2 = bf16_round_np(bf16_round_np(xn[:, 64:] * cn[:, 64:]) + bf16_round_np(xn[:, :64] * sn[:, 64:]))
+    assert np.array_equal(got, np.concatenate([y1, y2], axis=1))
+    ch = torch.cat((c[:, :64], c[:, :64]), dim=-1)
+    sh = torch.cat((s[:, :64], s[:, :64]), dim=-1)
+    assert torch.equal(oracle.rope_two_tables(x, ch, sh), oracle.rope_half_split(x, c[:, :64], s[:, :64]))
