@@ -336,17 +336,40 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const uint32_t T = (b1 << 8) | static_cast<uint32_t>(sh.found[0]);
   const int need_eq = S - above1 - sh.found[1];
 
-  // Rank the ties in index order (blocked ownership makes the scan order the index order).
-  int my_eq = 0;
-  for_keys([&](int, uint32_t kj) { my_eq += kj == T; });
-  int total_eq = 0;
-  int eq_rank = scan_excl(my_eq, sh.scan, &total_eq);
+  // Winners at their positions without atomics: one pass counts each thread's keys above T and
+  // equal to T, one scan gives every thread its first slot for each (blocked ownership makes the
+  // scan order the index order, so ties are ranked by index), a second pass writes them:
+  // keys > T at [0, c_gt), the first need_eq ties at [c_gt, S). The keys > T number fewer than S
+  // (T is the S-th largest), so their prefix fits 12 bits; ties take the upper 20 bits when n
+  // allows, else a scan of their own.
+  int my_gt = 0, my_eq = 0;
+  for_keys([&](int, uint32_t kj) {
+    my_gt += kj > T;
+    my_eq += kj == T;
+  });
+  int gt_pos, eq_rank, c_gt;
+  if (n < (1 << 19)) {
+    int total = 0;
+    const int excl = scan_excl(my_gt | (my_eq << 12), sh.scan, &total);
+    gt_pos = excl & 0xfff;
+    eq_rank = excl >> 12;
+    c_gt = total & 0xfff;
+  } else {
+    gt_pos = scan_excl(my_gt, sh.scan, &c_gt);
+    int total_eq = 0;
+    eq_rank = scan_excl(my_eq, sh.scan, &total_eq);
+  }
   const int64_t* lrow = a.lidx + static_cast<int64_t>(row) * a.lstride;
   for_keys([&](int j, uint32_t kj) {
-    bool win = kj > T;
-    if (kj == T) win = eq_rank++ < need_eq;
-    if (win) sorted[atomicAdd(&sel_count, 1)] = (static_cast<uint64_t>(0xffffu - kj) << 32) | static_cast<uint32_t>(j);
+    const uint64_t comp = (static_cast<uint64_t>(0xffffu - kj) << 32) | static_cast<uint32_t>(j);
+    if (kj > T) {
+      sorted[gt_pos++] = comp;
+    } else if (kj == T) {
+      if (eq_rank < need_eq) sorted[c_gt + eq_rank] = comp;
+      ++eq_rank;
+    }
   });
+  if (tid == 0) sel_count = S;
   __syncthreads();
   if (a.pos) {
     // The winners' chunk ids into the selection bitmap: every id load of the workgroup in flight

@@ -366,3 +366,4 @@ def test_rope_two_tables_and_chunk_positions(gpu):
     assert torch.equal(outs[0], outs[1])
     want3 = oracle.rope_push(x, cs, ids, cnts, c, buf.clone(), 10, 10 + Ls - 4)
     assert torch.equal(outs[0], want3)
+
