@@ -55,6 +55,9 @@ def parse() -> argparse.Namespace:
                         "GLM-4-9B (2 kv heads of 16 query heads, GLM RoPE), Llama-3-8B-1M (RoPE theta 3.58e6)")
     p.add_argument("--lanes", type=int, default=None,
                    help="independent batch slices pipelined per layer (default: 2 where the value fetch outweighs the dense layers, see decode_model.auto_lanes)")
+    p.add_argument("--separate-hit-moves", action="store_true",
+                   help="move the hits of the key and value buffers in their own launches instead of in the "
+                        "selection's last launch (the same work, for comparison)")
     p.add_argument("--no-graph", action="store_true", help="time eager steps instead of HIP graph replays")
     p.add_argument("--graph-steps", type=int, default=8,
                    help="decode steps per captured graph (one continuous lane pipeline across steps); "
@@ -429,8 +432,12 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
     comp_us = t_us(lambda i: shadowkv.gather_copy_d2d_with_offsets(
         c.v_cache_buffer[i % L], offs[i % L], cnts[i % L], B, H, int(c.sparse_budget * D), c.kernel_offset,
         c.kernel_stride, S))
+    folded = getattr(c, "fold_hit_moves", False) and not c.pooled
     add("gather_copy_d2d_with_offsets (hit compaction, per buffer)", "hbm", comp_bytes, comp_us,
-        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS, extra={"mean_hits": round(mean_hits, 1)})
+        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS,
+        extra={"mean_hits": round(mean_hits, 1),
+               "in_step": ("key buffer only: the value buffer's hits move inside the select_chunks launch"
+                           if folded else "both buffers")})
     # a4: value fetch of the misses from pinned host memory
     fetch_bytes = mean_miss * chunk_bytes
     fetch_us = t_us(lambda i: shadowkv.gather_copy_with_offsets(
@@ -986,6 +993,9 @@ def main() -> int:
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes,
                                           chunk_cache=args.chunk_cache)
+    if args.separate_hit_moves:
+        for lane in model.lanes:
+            lane.cache.fold_hit_moves = False
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")
@@ -1084,6 +1094,8 @@ def main() -> int:
                                f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, V in pinned host memory, "
                                + (f"device chunk pool of {args.chunk_cache} slots, " if args.chunk_cache else "")
                                + f"{lanes} interleaved batch lane(s), "
+                               + ("hit moves in their own launches, " if args.separate_hit_moves else
+                                  "hit moves in the selection launch, ")
                                + (f"HIP graphs of {per_call} step(s)" if graph else "eager steps"),
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),

@@ -260,6 +260,25 @@ int skv_select_chunks_ws(const uint16_t* D, const float* norm, const float* sum,
                          int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
                          int64_t* out_selected, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* skv_select_chunks_ws (workspace may be null, as for skv_select_chunks) with the hit moves folded
+ * into its last launch: after the reorder, the workgroup that owns row r compacts the row's hits
+ * in place in each non-null buffer, exactly as skv_gather_copy_d2d_with_offsets would with the
+ * offsets and cnts just written: slot(i) <- slot(offsets[r,i]) for i < cnts[r], where
+ *   slot(i) = buffer + r*buf_stride + buf_offset + i*chunk_elems   (bf16 elements).
+ * Requires position_ids/offsets/cnts (the reorder), chunk_elems a positive multiple of 8,
+ * buf_offset and buf_stride multiples of 8, buf_stride >= buf_offset + select_sets*chunk_elems and
+ * 16-byte aligned buffers. With it the value buffer needs only the host-link half of the fetch
+ * (skv_gather_copy_misses_with_offsets) and the key buffer no compaction before the rebuild.
+ * Variant of skv_select_chunks_ws (same reference lines, models/kvcache/shadow.py:553-574, plus
+ * the hit moves of gather_copy_with_offsets / gather_copy_d2d_with_offsets,
+ * models/kvcache/shadow.py:578-590). */
+int skv_select_chunks_compact(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                              const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks,
+                              int64_t* position_ids, int32_t* offsets, int32_t* cnts, uint16_t* out_scores,
+                              int64_t* out_selected, void* workspace, int64_t workspace_bytes, void* v_buffer,
+                              void* k_buffer, int64_t buf_offset, int64_t buf_stride, int chunk_elems,
+                              void* stream);
+
 /* ---- a8: sparse decode attention ----------------------------------------------------------------
  * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, causal=True) for one query token
  * (models/attention/shadow.py:48): for b, query head hq, kv head h = hq / (q_heads/kv_heads):

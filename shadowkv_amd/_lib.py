@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_select_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "skv_select_chunks_ws": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p,
                                     _i64, _p]),
+    "skv_select_chunks_compact": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _i32, _i32, _p, _p, _p, _p, _p,
+                                         _p, _i64, _p, _p, _i64, _i64, _i32, _p]),
     "skv_topk_gather": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p]),
     "skv_sparse_attn_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "skv_rmsnorm": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p]),

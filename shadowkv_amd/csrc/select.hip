@@ -55,6 +55,13 @@ struct SelectArgs {
   uint16_t* out_scores;  // [rows][n], required when n_lds == 0
   int pre;               // out_scores already holds the GQA-max probabilities (split path)
   int64_t* out_sel;      // [rows][S] ids in top-k order, optional
+  // Hit moves folded into the selection (optional): after the reorder, row r's hit chunks of each
+  // non-null buffer are compacted in place, slot i <- slot offsets[i] for i < cnt, where slot i of
+  // row r is at mv_buf[k] + r * mv_stride + mv_offset + i * mv_chunk (bf16 elements).
+  uint16_t* mv_buf[2];
+  int64_t mv_stride, mv_offset;
+  int mv_chunk;
+  int hit_src_off;  // byte offset of the LDS list of the hits' old slots (S int32), when moving
 };
 
 __device__ __forceinline__ int scan_excl(int v, int* scratch, int* total) {
@@ -71,7 +78,8 @@ __device__ __forceinline__ uint16_t half_of(const u32x4& v, int e) {
 // prow[0, S) and offs[0, S) rewritten in place, *cnt = number of hits (the reorder of
 // kernels/map.cuh:475-516). Called by every thread of a kThreads workgroup.
 __device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* oldmap, int words, int64_t* prow,
-                                     int32_t* offs, int32_t* cnt, int S, int* scan) {
+                                     int32_t* offs, int32_t* cnt, int S, int* scan, int32_t* hit_src = nullptr,
+                                     int* hits_out = nullptr) {
   const int tid = threadIdx.x;
   const int Es = (S + kThreads - 1) / kThreads;
   const int slo = min(tid * Es, S), shi = min(slo + Es, S);
@@ -100,6 +108,7 @@ __device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* old
     const int j = static_cast<int>(hit_ids[h] >> 40);
     prow[hrank] = id;
     offs[hrank] = j;
+    if (hit_src) hit_src[hrank] = j;
     ++hrank;
   }
   for (int w = wlo; w < whi; ++w) {
@@ -114,6 +123,67 @@ __device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* old
     }
   }
   if (tid == 0) *cnt = total_hits;
+  if (hits_out) *hits_out = total_hits;  // the same value in every thread
+}
+
+// The folded hit moves of one row: in each buffer the call names, in-place forward compaction
+// of the row's hit chunks, slot i <- slot src[i] for i < hits (src = the reorder's hit offsets, in
+// LDS, strictly ascending with src[i] >= i). src[i] - i never decreases, so the moves with
+// src[i] == i form a prefix [0, p), found by a binary search every thread makes alike, and are
+// skipped; every later move has src[i] > i. The rest go in ascending batches of kPer 16-byte
+// vectors per thread and buffer, every load of a batch completing (barrier) before any of its
+// stores. A batch never reads what an earlier batch wrote (it reads slots src[i] > i >= every
+// slot written before), and a slot a batch writes was read, if at all, by an earlier move: in an
+// earlier batch, whose loads every thread consumed (stored) before reaching this batch's barrier,
+// or in this batch, before the barrier. Called by every thread of the workgroup.
+__device__ void move_row_hits(const SelectArgs& a, int row, const int32_t* src, int hits) {
+  constexpr int kPer = 4;
+  __syncthreads();  // src complete
+  int lo = 0, hi = hits;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (src[mid] == mid) lo = mid + 1;
+    else hi = mid;
+  }
+  const int p = lo;
+  if (p == hits) return;  // nothing to move (uniform)
+  const int tid = threadIdx.x;
+  const int vecs = a.mv_chunk / 8;
+  const int64_t total = static_cast<int64_t>(hits - p) * vecs;
+  uint16_t* base[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+    base[b] = a.mv_buf[b] ? a.mv_buf[b] + static_cast<int64_t>(row) * a.mv_stride + a.mv_offset : nullptr;
+  for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(kThreads) * kPer) {
+    u32x4 d[2][kPer];
+    int64_t from[kPer], to[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int64_t v = v0 + static_cast<int64_t>(k) * kThreads + tid;
+      to[k] = -1;
+      if (v < total) {
+        const int i = p + static_cast<int>(v / vecs);
+        const int e = static_cast<int>(v - static_cast<int64_t>(i - p) * vecs) * 8;
+        from[k] = static_cast<int64_t>(src[i]) * a.mv_chunk + e;
+        to[k] = static_cast<int64_t>(i) * a.mv_chunk + e;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (!base[b]) continue;  // uniform
+#pragma unroll
+      for (int k = 0; k < kPer; ++k)
+        if (to[k] >= 0) d[b][k] = *reinterpret_cast<const u32x4*>(base[b] + from[k]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (!base[b]) continue;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k)
+        if (to[k] >= 0) *reinterpret_cast<u32x4*>(base[b] + to[k]) = d[b][k];
+    }
+  }
 }
 
 template <int MP>
@@ -379,7 +449,10 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
       if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
     }
     __syncthreads();
-    reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan);
+    int32_t* hit_src = a.hit_src_off ? reinterpret_cast<int32_t*>(smem + a.hit_src_off) : nullptr;
+    int hits = 0;
+    reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan, hit_src, &hits);
+    if (hit_src) move_row_hits(a, row, hit_src, hits);
   }
 
   if (a.out_sel) {
@@ -647,7 +720,12 @@ __global__ void __launch_bounds__(kThreads) select_finish_kernel(SelectArgs a, P
     if (id >= 0 && id < 32ll * a.words) atomicOr(&selmap[id >> 5], 1u << (id & 31));
   }
   __syncthreads();
-  if (reorder) reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan);
+  if (reorder) {
+    int32_t* hit_src = a.hit_src_off ? reinterpret_cast<int32_t*>(smem + a.hit_src_off) : nullptr;
+    int hits = 0;
+    reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan, hit_src, &hits);
+    if (hit_src) move_row_hits(a, row, hit_src, hits);
+  }
   if (a.out_sel) {
     for (int i = S + tid; i < a.P; i += kThreads) sorted[i] = ~0ull;
     __syncthreads();
@@ -717,9 +795,19 @@ SelectPath select_path(int rows, int m, int n, bool has_scores, bool has_ws) {
 int select_impl(const char* what, const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
                 const int64_t* landmark_idx, int64_t idx_stride, int select_sets, int num_chunks, int64_t* position_ids,
                 int32_t* offsets, int32_t* cnts, uint16_t* out_scores, int64_t* out_selected, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+                int64_t workspace_bytes, void* stream, uint16_t* mv_v = nullptr, uint16_t* mv_k = nullptr,
+                int64_t mv_offset = 0, int64_t mv_stride = 0, int mv_chunk = 0) {
   // No previous slots: selection only, the ids in top-k order into out_selected.
   const bool reorder = position_ids != nullptr;
+  const bool move = mv_v || mv_k;
+  if (move && (!reorder || mv_chunk < 8 || mv_chunk % 8 || mv_offset < 0 || mv_offset % 8 ||
+               mv_stride < mv_offset + static_cast<int64_t>(select_sets) * mv_chunk || mv_stride % 8 ||
+               (reinterpret_cast<uintptr_t>(mv_v) & 15u) || (reinterpret_cast<uintptr_t>(mv_k) & 15u))) {
+    skv_set_error("%s: hit moves need previous slots, a chunk of a multiple of 8 elements, 16-byte aligned "
+                  "buffers and a row stride holding the selected region (chunk=%d offset=%lld stride=%lld)",
+                  what, mv_chunk, (long long)mv_offset, (long long)mv_stride);
+    return SKV_EINVAL;
+  }
   if (!D || !norm || !sum || !landmark_idx || (reorder && (!offsets || !cnts)) || (!reorder && !out_selected)) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -737,7 +825,9 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
   int P = 64;
   while (P < select_sets) P <<= 1;
   const int words = reorder ? (num_chunks + 31) / 32 : 0;
-  const size_t fixed = (static_cast<size_t>(words) * 8 + static_cast<size_t>(P) * 8 + 15) / 16 * 16;
+  const size_t base_lds = (static_cast<size_t>(words) * 8 + static_cast<size_t>(P) * 8 + 15) / 16 * 16;
+  // the hits' old slots, for the folded hit moves
+  const size_t fixed = base_lds + (move ? (static_cast<size_t>(select_sets) * 4 + 15) / 16 * 16 : 0);
   if (fixed > kLdsBudget) {
     skv_set_error("%s: %d chunks need %zu bytes of bitmap, above the LDS budget", what, num_chunks, fixed);
     return SKV_EUNSUPPORTED;
@@ -764,6 +854,12 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
   a.vec = (n % 8 == 0 && (reinterpret_cast<uintptr_t>(D) & 15u) == 0 &&
            (!out_scores || (reinterpret_cast<uintptr_t>(out_scores) & 15u) == 0));
   a.keys_off = static_cast<int>(fixed);
+  a.hit_src_off = move ? static_cast<int>(base_lds) : 0;
+  a.mv_buf[0] = mv_v;
+  a.mv_buf[1] = mv_k;
+  a.mv_offset = mv_offset;
+  a.mv_stride = mv_stride;
+  a.mv_chunk = mv_chunk;
   a.D = D;
   a.norm = norm;
   a.sum = sum;
@@ -835,4 +931,20 @@ extern "C" int skv_select_chunks_ws(const uint16_t* D, const float* norm, const 
   }
   return select_impl("select_chunks_ws", D, norm, sum, rows, m, n, landmark_idx, idx_stride, select_sets, num_chunks,
                      position_ids, offsets, cnts, out_scores, out_selected, workspace, workspace_bytes, stream);
+}
+
+extern "C" int skv_select_chunks_compact(const uint16_t* D, const float* norm, const float* sum, int rows, int m, int n,
+                                         const int64_t* landmark_idx, int64_t idx_stride, int select_sets,
+                                         int num_chunks, int64_t* position_ids, int32_t* offsets, int32_t* cnts,
+                                         uint16_t* out_scores, int64_t* out_selected, void* workspace,
+                                         int64_t workspace_bytes, void* v_buffer, void* k_buffer, int64_t buf_offset,
+                                         int64_t buf_stride, int chunk_elems, void* stream) {
+  if (!v_buffer && !k_buffer) {
+    skv_set_error("select_chunks_compact: no buffer to compact (use skv_select_chunks_ws)");
+    return SKV_EINVAL;
+  }
+  return select_impl("select_chunks_compact", D, norm, sum, rows, m, n, landmark_idx, idx_stride, select_sets,
+                     num_chunks, position_ids, offsets, cnts, out_scores, out_selected, workspace, workspace_bytes,
+                     stream, static_cast<uint16_t*>(v_buffer), static_cast<uint16_t*>(k_buffer), buf_offset,
+                     buf_stride, chunk_elems);
 }

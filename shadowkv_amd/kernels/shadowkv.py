@@ -450,7 +450,7 @@ def select_workspace_bytes(rows: int, n: int, select_sets: int) -> int:
 
 
 def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunks, position_ids, offsets, cnts,
-                  out_scores=None, out_selected=None, workspace=None):
+                  out_scores=None, out_selected=None, workspace=None, move=None):
     """Fused softmax + GQA max + top-k + id gather + reorder (one workgroup per row; for few rows
     the softmax + GQA max runs first on many workgroups into out_scores, a second launch).
 
@@ -462,7 +462,11 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
     workspace: optional device buffer of select_workspace_bytes(rows, n, select_sets) bytes, with
     which few rows (<= 32) are each selected by many workgroups. position_ids, offsets and cnts
     None: selection only (no previous slots, no reorder), the ids in top-k order into the then
-    required out_selected (what a chunk pool selects before its own hit lookup)."""
+    required out_selected (what a chunk pool selects before its own hit lookup).
+    move: optional (v_buffer, k_buffer, buf_offset, buf_stride, chunk_elems): the hit moves folded
+    into the selection's last launch, i.e. gather_copy_d2d_with_offsets(buffer, offsets, cnts, ...)
+    on each buffer given (either may be None; buffer rows of buf_stride elements, the selected
+    region at buf_offset, chunks of chunk_elems) done by the selection itself."""
     _dev(D, "D", torch.bfloat16)
     _dev(Norm, "Norm", torch.float32)
     _dev(Sum, "Sum", torch.float32)
@@ -504,14 +508,35 @@ def select_chunks(D, Norm, Sum, rows, m, n, landmark_idx, select_sets, num_chunk
     args = (D.data_ptr(), Norm.data_ptr(), Sum.data_ptr(), rows, m, n, landmark_idx.data_ptr(),
             landmark_idx.stride(0), select_sets, num_chunks, position_ids.data_ptr() if reorder else None,
             offsets.data_ptr() if reorder else None, cnts.data_ptr() if reorder else None, sp, op)
-    if workspace is None:
-        _lib.call("skv_select_chunks", *args, _stream())
-    else:
+    wp, nbytes = None, 0
+    if workspace is not None:
         _dev(workspace, "workspace")
         nbytes = workspace.numel() * workspace.element_size()
         if nbytes < select_workspace_bytes(rows, n, select_sets):
             raise ValueError(f"workspace of {nbytes} bytes, {select_workspace_bytes(rows, n, select_sets)} needed")
-        _lib.call("skv_select_chunks_ws", *args, workspace.data_ptr(), nbytes, _stream())
+        wp = workspace.data_ptr()
+    if move is not None:
+        if not reorder:
+            raise ValueError("the folded hit moves need position_ids, offsets and cnts")
+        v_buf, k_buf, buf_offset, buf_stride, chunk_elems = move
+        if v_buf is None and k_buf is None:
+            raise ValueError("move names no buffer")
+        ptrs = []
+        for t, nm in ((v_buf, "v_buffer"), (k_buf, "k_buffer")):
+            if t is None:
+                ptrs.append(None)
+                continue
+            _dev(t, nm, torch.bfloat16)
+            if not t.is_contiguous():
+                raise ValueError(f"{nm} must be contiguous")
+            _need(t, (rows - 1) * buf_stride + buf_offset + select_sets * chunk_elems, nm)
+            ptrs.append(t.data_ptr())
+        _lib.call("skv_select_chunks_compact", *args, wp, nbytes, ptrs[0], ptrs[1], int(buf_offset), int(buf_stride),
+                  int(chunk_elems), _stream())
+    elif workspace is None:
+        _lib.call("skv_select_chunks", *args, _stream())
+    else:
+        _lib.call("skv_select_chunks_ws", *args, wp, nbytes, _stream())
 
 
 def topk_gather(scores, landmark_idx, k, out_ids):

@@ -136,6 +136,12 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.position_ids = torch.full((L, B, H, self.select_sets), -1, device=device, dtype=torch.int64)
         self.selected_chunks = torch.zeros(B, H, self.select_sets, device=device, dtype=torch.int64)
         self.keep_selected = False  # also emit the selected ids in top-k order into selected_chunks
+        # Fold the value buffer's hit moves into the selection's last launch, so that the value fetch
+        # follows the selection directly (the key buffer's moves stay a launch of the key path,
+        # which overlaps the fetch); _folded[l] names the buffers whose hits the last selection of
+        # layer l already moved, consumed by get_value_cache / get_key_cache.
+        self.fold_hit_moves = True
+        self._folded = [set() for _ in range(L)]
 
         # value-fetch stream: the given one, else the process's shared fetch side stream
         self.copy_stream = copy_stream if copy_stream is not None else side_stream(device, "fetch")
@@ -384,12 +390,18 @@ class ShadowKVCache_CPU(KVCacheBase):
                 self.selected_chunks.copy_(self.position_ids[layer_idx])
             return self.position_ids[layer_idx]
         # softmax + GQA max + top-k + landmark-id gather + reorder in one launch. The GQA-max scores are kept in
-        # chunk_attn; the selected ids in top-k order (selected_chunks) only when keep_selected is set.
+        # chunk_attn; the selected ids in top-k order (selected_chunks) only when keep_selected is set. With
+        # fold_hit_moves the same launch also moves the value buffer's hits to their new slots.
+        move = None
+        if self.fold_hit_moves:
+            move = (self.v_cache_buffer[layer_idx], None, self.kernel_offset, self.kernel_stride,
+                    self.chunk_size * D)
         shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, B * H, G, n, self.k_landmark_idx[layer_idx].view(B * H, n),
                                self.select_sets, self.chunks, self.position_ids[layer_idx].view(B * H, -1), self.offsets,
                                self.cnts, out_scores=self.chunk_attn,
                                out_selected=self.selected_chunks if self.keep_selected else None,
-                               workspace=self.select_workspace)
+                               workspace=self.select_workspace, move=move)
+        self._folded[layer_idx] = {"v"} if move is not None else set()
         return self.position_ids[layer_idx]
 
     def _gen_len(self, layer_idx: int) -> int:
@@ -421,6 +433,9 @@ class ShadowKVCache_CPU(KVCacheBase):
                                                  self.buf_len * D, self.select_sets, self.pool_slots,
                                                  self.chunk_size * D)
             return self._live_view(self.v_cache_buffer[layer_idx], layer_idx)
+        if "v" in self._folded[layer_idx]:  # the selection moved the hits
+            self._folded[layer_idx].discard("v")
+            hits_moved = True
         shadowkv.gather_copy_with_offsets(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.temp,
                                           self.offsets, self.cnts, self.signals, self.batch_size,
                                           self.num_key_value_heads, int(self.max_ctx_chunks_len * self.head_dim),
@@ -431,8 +446,8 @@ class ShadowKVCache_CPU(KVCacheBase):
     def move_value_hits(self, layer_idx: int):
         """The in-buffer half of the value fetch alone (hit rows to their new slots), so that a
         later get_value_cache(..., hits_moved=True) on the copy stream is host-link work only.
-        Nothing to move with a chunk pool."""
-        if self.pooled:
+        Nothing to move with a chunk pool, nor when the selection already moved them."""
+        if self.pooled or "v" in self._folded[layer_idx]:
             return
         shadowkv.gather_copy_d2d_with_offsets(self.v_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
                                               self.num_key_value_heads, int(self.sparse_budget * self.head_dim),
@@ -445,9 +460,13 @@ class ShadowKVCache_CPU(KVCacheBase):
                                     cos_sin_cache, self.k_cache_buffer[layer_idx], self.sparse_start, self.chunk_size,
                                     miss_slot=self.miss_slot.view(B, H, S), pool_slots=self.pool_slots)
             return self._live_view(self.k_cache_buffer[layer_idx], layer_idx)
-        shadowkv.gather_copy_d2d_with_offsets(self.k_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
-                                              self.num_key_value_heads, int(self.sparse_budget * self.head_dim),
-                                              self.kernel_offset, self.kernel_stride, self.select_sets)
+        if "k" in self._folded[layer_idx]:  # the selection moved the hits
+            self._folded[layer_idx].discard("k")
+        else:
+            shadowkv.gather_copy_d2d_with_offsets(self.k_cache_buffer[layer_idx], self.offsets, self.cnts,
+                                                  self.batch_size, self.num_key_value_heads,
+                                                  int(self.sparse_budget * self.head_dim), self.kernel_offset,
+                                                  self.kernel_stride, self.select_sets)
         batch_gather_gemm_rotary_pos_emb_cuda(self.U[layer_idx], self.SV[layer_idx], cos_sin_cache, position_ids,
                                               self.output, self.chunk_size, self.k_cache_buffer[layer_idx],
                                               self.sparse_start, self.sparse_end, self.cnts)

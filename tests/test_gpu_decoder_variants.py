@@ -2,6 +2,8 @@
 * the down projection forming SiLU-and-mul from the gate/up rows (two lanes of 4 sequences, the
   batch-8 decode's setting) gives the same tokens and cache state, bit for bit, as the
   SiLU-and-mul kernel followed by the linear kernel;
+* the hit moves folded into the selection launch give the same tokens and cache state, bit for
+  bit, as the separate in-buffer compaction launches (one lane and two lanes);
 * the fused new-token step (residual + RMSNorm, skinny linear, SiLU-and-mul, RoPE + append
   kernels) agrees with the reference call sequence on torch operations (F.rms_norm, F.linear,
   F.silu, apply_rotary_pos_emb_new + update_kv_cache) within bf16 tolerance."""
@@ -40,6 +42,29 @@ def test_gated_down_projection_matches_two_kernels(gpu):
         assert torch.equal(tg, tp), t
         for a, b in zip(_state(gated), _state(plain)):
             assert torch.equal(a, b), t
+
+
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_folded_hit_moves_match_separate_compaction(gpu, lanes):
+    print(f"folded hit moves vs separate compaction, batch 8 in {lanes} lane(s)", flush=True)
+    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    kw = dict(sparse_budget=2048, decode_len=8, lanes=lanes, seed=15)
+    folded = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    separate = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    for lane in separate.lanes:
+        lane.cache.fold_hit_moves = False
+    assert all(lane.cache.fold_hit_moves for lane in folded.lanes)
+    tf = ts = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(5))
+    hits = 0
+    for t in range(4):
+        tf = folded.decode_step(tf)
+        ts = separate.decode_step(ts)
+        torch.cuda.synchronize()
+        assert torch.equal(tf, ts), t
+        for a, b in zip(_state(folded), _state(separate)):
+            assert torch.equal(a, b), t
+        hits += sum(int(lane.cache.cnts.sum()) for lane in folded.lanes)
+    assert hits > 0, "the steps moved no hit"
 
 
 def _hidden_after_layers(dec, tok):

@@ -323,3 +323,108 @@ def test_select_chunks_selects_every_landmark(gpu, monkeypatch, rows, m, n, spli
     assert (cnt.cpu() == 0).all()
     assert torch.equal(off.view(rows, S).cpu(), lidx.cpu().to(torch.int32))
     assert torch.equal(sel.cpu(), oracle.topk_gather(scores.cpu(), lidx.cpu(), S))
+
+
+def _old_slots(sel, lidx, S, mode, g):
+    """Previous slots for a folded-move test, per row: "half" about half of this step's selection
+    among other ids, shuffled; "shift" the first quarter of the selection in place, one other id,
+    then the next quarter (every later hit moves one slot down: each move reads the chunk the next
+    move writes); "all" the selection reversed (every slot a hit, no move); "none" no hit."""
+    old = []
+    for r in range(sel.shape[0]):
+        s = sel[r].cpu()
+        pool = lidx[r].cpu()
+        others = pool[~torch.isin(pool, s)]
+        others = others[torch.randperm(len(others), generator=g)]
+        if mode == "half":
+            keep = s[:S // 2]
+            row = torch.cat([keep, others[:S - len(keep)]])[torch.randperm(S, generator=g)]
+        elif mode == "shift":
+            q = max(S // 4, 1)
+            row = torch.cat([s[:q], others[:1], s[q:2 * q]])
+            row = torch.cat([row, others[1:1 + S - len(row)]])[:S]
+        elif mode == "all":
+            row = s.flip(0)
+        else:
+            row = others[:S]
+        old.append(row)
+    return torch.stack(old)
+
+
+@pytest.mark.parametrize("mode", ["half", "shift", "all", "none"])
+@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("rows,m,n,S,chunk_elems", [(64, 4, 15304, 256, 1024), (8, 4, 130680, 2048, 1024),
+                                                    (8, 4, 968, 256, 1024), (2, 1, 300, 7, 16)])
+def test_select_chunks_folded_hit_moves(gpu, monkeypatch, rows, m, n, S, chunk_elems, split, mode):
+    """skv_select_chunks_compact: the selection that also moves each row's hits in both buffers
+    (in place, slot i <- slot offsets[i] for i < cnts) leaves the same selection, offsets, counts
+    and slot ids as the plain selection, and buffers bit-identical to the plain selection followed
+    by the separate compaction kernel on each buffer and to a slot-by-slot compaction on the host;
+    also with the value buffer alone."""
+    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    _say(f"select_chunks folded moves rows={rows} m={m} n={n} S={S} split={split} mode={mode}")
+    g = torch.Generator().manual_seed(rows * n + S + len(mode))
+    q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
+    L = torch.randn(rows, n, 128, generator=g).to(torch.bfloat16).to(gpu)
+    lidx = torch.stack([torch.randperm(n + n // 10, generator=g)[:n].sort().values for _ in range(rows)]).to(gpu)
+    tiles = (n + 255) // 256
+    D = torch.empty(rows, m, n, dtype=torch.bfloat16, device=gpu)
+    norm = torch.empty(rows, m, tiles, device=gpu)
+    ssum = torch.empty_like(norm)
+    shadowkv.score_logits(q, L, D, norm, ssum, rows, m, n, 128)
+    nchunks = n + n // 10
+    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split == "ws" else None
+    sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
+    shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, None, None, None,
+                           out_scores=torch.empty(rows, n, dtype=torch.bfloat16, device=gpu), out_selected=sel,
+                           workspace=ws)
+    torch.cuda.synchronize()
+    old = _old_slots(sel, lidx, S, mode, g).to(gpu)
+    prefix, tail = 40, 24  # elements before and after the selected region of each buffer row
+    stride = prefix + S * chunk_elems + tail
+    bufs = [torch.randint(-32768, 32768, (rows, stride), generator=g, dtype=torch.int32).to(torch.int16)
+            .view(torch.bfloat16).to(gpu) for _ in range(2)]
+
+    def plain():
+        pos, off, cnt = old.clone(), torch.empty(rows * S, dtype=torch.int32, device=gpu), \
+            torch.empty(rows, dtype=torch.int32, device=gpu)
+        sc = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+        shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos, off, cnt, out_scores=sc,
+                               workspace=ws)
+        return pos, off, cnt, sc
+
+    pos1, off1, cnt1, sc1 = plain()
+    want = [b.clone() for b in bufs]
+    for b in want:
+        shadowkv.gather_copy_d2d_with_offsets(b, off1, cnt1, 1, rows, S * chunk_elems, prefix, stride, S)
+    for which in ("both", "v"):
+        got = [b.clone() for b in bufs]
+        pos2, off2, cnt2 = old.clone(), torch.empty_like(off1), torch.empty_like(cnt1)
+        sc2 = torch.empty_like(sc1)
+        sel2 = torch.empty_like(sel)
+        shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos2, off2, cnt2, out_scores=sc2,
+                               out_selected=sel2, workspace=ws,
+                               move=(got[0], got[1] if which == "both" else None, prefix, stride, chunk_elems))
+        torch.cuda.synchronize()
+        assert torch.equal(sel2, sel) and torch.equal(sc2, sc1)
+        assert torch.equal(pos2, pos1) and torch.equal(off2, off1) and torch.equal(cnt2, cnt1)
+        # bit patterns compared (random bits include NaNs)
+        assert torch.equal(got[0].view(torch.int16), want[0].view(torch.int16)), f"{which}: value buffer"
+        assert torch.equal(got[1].view(torch.int16), (want[1] if which == "both" else bufs[1]).view(torch.int16)), \
+            f"{which}: key buffer"
+    # the host restatement: hits in previous-slot order, slot i <- old slot offsets[i]
+    ids, offs, cnts = oracle.reorder(old.cpu().numpy(), sel.cpu().numpy())
+    assert np.array_equal(cnt1.cpu().numpy(), cnts) and np.array_equal(off1.view(rows, S).cpu().numpy(), offs)
+    host = bufs[0].cpu().view(torch.int16).numpy()
+    ref = host.copy()
+    for r in range(rows):
+        for i in range(int(cnts[r])):
+            j = int(offs[r, i])
+            ref[r, prefix + i * chunk_elems:prefix + (i + 1) * chunk_elems] = \
+                host[r, prefix + j * chunk_elems:prefix + (j + 1) * chunk_elems]
+    assert np.array_equal(want[0].cpu().view(torch.int16).numpy(), ref)
+    expect = {"all": S, "none": 0}.get(mode)
+    if expect is not None:
+        assert (cnts == expect).all()
+    if mode == "shift" and S >= 4:
+        assert (cnts >= 2 * (S // 4)).all() and (offs[:, S // 4] == S // 4 + 1).all()

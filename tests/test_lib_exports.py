@@ -10,6 +10,39 @@ def test_header_and_binding_agree():
     assert sorted(declared) == sorted(_lib.SIGNATURES), "ctypes signatures must cover the header exactly"
 
 
+def _header_argument_kinds():
+    """{name: (return kind, [argument kinds])} parsed from the header's declarations, a kind being
+    "p" (any pointer), "i64", "i32" or "f32"."""
+    import re
+    text = re.sub(r"/\*.*?\*/", "", _lib.HEADER_PATH.read_text(), flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(r"^\s*(const\s+char\s*\*|int64_t|int)\s+(skv_\w+)\s*\(([^;]*?)\)\s*;",
+                                        text, flags=re.M):
+        kinds = []
+        for prm in params.split(","):
+            prm = " ".join(prm.split())
+            if not prm or prm == "void":
+                continue
+            kinds.append("p" if "*" in prm else "i64" if prm.startswith("int64_t") else
+                         "f32" if prm.startswith("float") else "i32" if prm.startswith("int ") else prm)
+        out[name] = ("p" if "*" in ret else "i64" if ret == "int64_t" else "i32", kinds)
+    return out
+
+
+def test_header_argument_types_match_bindings():
+    """Every ctypes signature has the header's arity and argument kinds (a missing or extra
+    argument would shift every later one at the call)."""
+    import ctypes as C
+    kind = {C.c_void_p: "p", C.c_char_p: "p", C.c_int64: "i64", C.c_int32: "i32", C.c_float: "f32"}
+    decl = _header_argument_kinds()
+    assert sorted(decl) == sorted(_lib.SIGNATURES)
+    for name, (ret, args) in _lib.SIGNATURES.items():
+        want_ret, want_args = decl[name]
+        got = ["p" if isinstance(a, type) and issubclass(a, C._Pointer) else kind.get(a, str(a)) for a in args]
+        assert got == want_args, f"{name}: binding {got} vs header {want_args}"
+        assert kind.get(ret, str(ret)) == want_ret, f"{name}: return type"
+
+
 def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     for name in _lib.header_functions():
