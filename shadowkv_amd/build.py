@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -43,12 +44,33 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+def scratch_kernels(remarks: str) -> list[tuple[str, int]]:
+    """(kernel, bytes per lane) for every kernel whose resource-usage remark reports scratch."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) and name:
+            out.append((name, int(m.group(1))))
+    return out
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+           str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    # No kernel may touch scratch memory: a register spill or a stack object (a device function
+    # left as a call, an array indexed at run time) in a hot loop costs more than any kernel here
+    # saves, and nothing else reports it.
+    bad = scratch_kernels(proc.stderr)
+    if bad:
+        raise RuntimeError(f"{src.name}: kernels using scratch memory (bytes per lane): {bad}")
     return obj
 
 

@@ -75,11 +75,12 @@ __device__ __forceinline__ uint16_t half_of(const u32x4& v, int e) {
 
 // Hits in previous-slot order, then misses in ascending id order, from the selection bitmap
 // `selmap` (every winner's chunk id) and `oldmap` (the previous slots' ids), both in LDS:
-// prow[0, S) and offs[0, S) rewritten in place, *cnt = number of hits (the reorder of
-// kernels/map.cuh:475-516). Called by every thread of a kThreads workgroup.
-__device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* oldmap, int words, int64_t* prow,
-                                     int32_t* offs, int32_t* cnt, int S, int* scan, int32_t* hit_src = nullptr,
-                                     int* hits_out = nullptr) {
+// prow[0, S) and offs[0, S) rewritten in place, *cnt = number of hits, also returned (the reorder of
+// kernels/map.cuh:475-516); hit_src, when given, receives the hits' old slots. Called by every
+// thread of a kThreads workgroup.
+__device__ __forceinline__ int reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* oldmap, int words,
+                                                    int64_t* prow, int32_t* offs, int32_t* cnt, int S, int* scan,
+                                                    int32_t* hit_src = nullptr) {
   const int tid = threadIdx.x;
   const int Es = (S + kThreads - 1) / kThreads;
   const int slo = min(tid * Es, S), shi = min(slo + Es, S);
@@ -123,7 +124,7 @@ __device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* old
     }
   }
   if (tid == 0) *cnt = total_hits;
-  if (hits_out) *hits_out = total_hits;  // the same value in every thread
+  return total_hits;  // the same value in every thread
 }
 
 // The folded hit moves of one row: in each buffer the call names, in-place forward compaction
@@ -136,7 +137,7 @@ __device__ void reorder_from_bitmaps(const uint32_t* selmap, const uint32_t* old
 // slot written before), and a slot a batch writes was read, if at all, by an earlier move: in an
 // earlier batch, whose loads every thread consumed (stored) before reaching this batch's barrier,
 // or in this batch, before the barrier. Called by every thread of the workgroup.
-__device__ void move_row_hits(const SelectArgs& a, int row, const int32_t* src, int hits) {
+__device__ __forceinline__ void move_row_hits(const SelectArgs& a, int row, const int32_t* src, int hits) {
   constexpr int kPer = 4;
   __syncthreads();  // src complete
   int lo = 0, hi = hits;
@@ -150,17 +151,17 @@ __device__ void move_row_hits(const SelectArgs& a, int row, const int32_t* src, 
   const int tid = threadIdx.x;
   const int vecs = a.mv_chunk / 8;
   const int64_t total = static_cast<int64_t>(hits - p) * vecs;
-  uint16_t* base[2];
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-    base[b] = a.mv_buf[b] ? a.mv_buf[b] + static_cast<int64_t>(row) * a.mv_stride + a.mv_offset : nullptr;
+  const int64_t roff = static_cast<int64_t>(row) * a.mv_stride + a.mv_offset;
+  uint16_t* const bv = a.mv_buf[0] ? a.mv_buf[0] + roff : nullptr;
+  uint16_t* const bk = a.mv_buf[1] ? a.mv_buf[1] + roff : nullptr;
   for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(kThreads) * kPer) {
-    u32x4 d[2][kPer];
+    u32x4 dv[kPer], dk[kPer];
     int64_t from[kPer], to[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int64_t v = v0 + static_cast<int64_t>(k) * kThreads + tid;
       to[k] = -1;
+      from[k] = 0;
       if (v < total) {
         const int i = p + static_cast<int>(v / vecs);
         const int e = static_cast<int>(v - static_cast<int64_t>(i - p) * vecs) * 8;
@@ -169,19 +170,17 @@ __device__ void move_row_hits(const SelectArgs& a, int row, const int32_t* src, 
       }
     }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      if (!base[b]) continue;  // uniform
-#pragma unroll
-      for (int k = 0; k < kPer; ++k)
-        if (to[k] >= 0) d[b][k] = *reinterpret_cast<const u32x4*>(base[b] + from[k]);
+    for (int k = 0; k < kPer; ++k) {
+      if (to[k] < 0) continue;
+      if (bv) dv[k] = *reinterpret_cast<const u32x4*>(bv + from[k]);
+      if (bk) dk[k] = *reinterpret_cast<const u32x4*>(bk + from[k]);
     }
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      if (!base[b]) continue;
-#pragma unroll
-      for (int k = 0; k < kPer; ++k)
-        if (to[k] >= 0) *reinterpret_cast<u32x4*>(base[b] + to[k]) = d[b][k];
+    for (int k = 0; k < kPer; ++k) {
+      if (to[k] < 0) continue;
+      if (bv) *reinterpret_cast<u32x4*>(bv + to[k]) = dv[k];
+      if (bk) *reinterpret_cast<u32x4*>(bk + to[k]) = dk[k];
     }
   }
 }
@@ -450,8 +449,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
     }
     __syncthreads();
     int32_t* hit_src = a.hit_src_off ? reinterpret_cast<int32_t*>(smem + a.hit_src_off) : nullptr;
-    int hits = 0;
-    reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan, hit_src, &hits);
+    const int hits = reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, sh.scan, hit_src);
     if (hit_src) move_row_hits(a, row, hit_src, hits);
   }
 
@@ -722,8 +720,7 @@ __global__ void __launch_bounds__(kThreads) select_finish_kernel(SelectArgs a, P
   __syncthreads();
   if (reorder) {
     int32_t* hit_src = a.hit_src_off ? reinterpret_cast<int32_t*>(smem + a.hit_src_off) : nullptr;
-    int hits = 0;
-    reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan, hit_src, &hits);
+    const int hits = reorder_from_bitmaps(selmap, oldmap, a.words, prow, a.offsets + base, a.cnts + row, S, scan, hit_src);
     if (hit_src) move_row_hits(a, row, hit_src, hits);
   }
   if (a.out_sel) {

@@ -95,3 +95,16 @@ def test_selection_only_needs_an_output():
     assert rc == 1 and "null pointer" in _lib.last_error()
     rc = lib.skv_select_chunks(p, p, p, 8, 4, 1000, p, 1000, 256, 1100, p, None, p, p, None, None)
     assert rc == 1 and "null pointer" in _lib.last_error()
+
+
+def test_build_rejects_kernels_that_use_scratch():
+    """The build's scan of hipcc's resource-usage remarks names every kernel with scratch."""
+    from shadowkv_amd import build
+    remarks = "\n".join([
+        "x.hip:1:1: remark: Function Name: k_ok [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: k_spills [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     VGPRs: 128 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 320 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build.scratch_kernels(remarks) == [("k_spills", 320)]
