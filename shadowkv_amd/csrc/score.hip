@@ -16,6 +16,9 @@
 //     reference's 256-column partial layout).
 //   softmax_kernel: each workgroup merges the partials of its z, then normalises its 256
 //     columns for every query row and keeps the running max over rows.
+#include <type_traits>
+
+#include "softmax_keys.h"
 #include "wave_reduce.h"
 
 namespace {
@@ -125,22 +128,7 @@ __global__ void __launch_bounds__(kThreads) softmax_kernel(const uint16_t* __res
   __shared__ float gmax[kMaxM], ginv[kMaxM];
   const int z = blockIdx.y;
   const int tile = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int i = wave; i < m; i += 4) {
-    const float* nr = norm + (static_cast<int64_t>(z) * m + i) * tiles;
-    const float* sr = sum + (static_cast<int64_t>(z) * m + i) * tiles;
-    float mx = -INFINITY;
-    for (int t = lane; t < tiles; t += 64) mx = fmaxf(mx, nr[t]);
-    mx = skv::wave_max_dpp(mx);
-    float s = 0.f;
-    for (int t = lane; t < tiles; t += 64) s += sr[t] * expf(nr[t] - mx);
-    s = skv::wave_sum_dpp(s);
-    if (lane == 0) {
-      gmax[i] = mx;
-      ginv[i] = 1.f / s;
-    }
-  }
+  skv::merge_softmax_partials<kThreads / 64>(norm, sum, z, m, tiles, gmax, ginv);
   __syncthreads();
   const int j = tile * kTile + threadIdx.x;
   if (j >= n) return;
@@ -152,6 +140,99 @@ __global__ void __launch_bounds__(kThreads) softmax_kernel(const uint16_t* __res
     best = fmaxf(best, skv::bf2f(p));
   }
   if (kWriteMax) out_max[static_cast<int64_t>(z) * n + j] = skv::f2bf(best);
+}
+
+// The same results for rows of n % 8 == 0 columns, each thread taking kCpt consecutive columns
+// (8, 4 or 2: 16-, 8- or 4-byte vectors), chosen so that few rows still spread over many
+// workgroups. Every D vector of the thread is requested at entry, before the partials merge, so
+// their latencies overlap.
+template <int kCpt>
+struct ColVec;
+template <>
+struct ColVec<8> {
+  using T = u32x4;
+};
+template <>
+struct ColVec<4> {
+  using T = uint32_t __attribute__((ext_vector_type(2)));
+};
+template <>
+struct ColVec<2> {
+  using T = uint32_t __attribute__((ext_vector_type(1)));
+};
+
+template <bool kWriteSoftmax, bool kWriteMax, int MP, int kCpt>
+__global__ void __launch_bounds__(kThreads) softmax_vec_kernel(const uint16_t* __restrict__ D,
+                                                               const float* __restrict__ norm,
+                                                               const float* __restrict__ sum, uint16_t* __restrict__ P,
+                                                               uint16_t* __restrict__ out_max, uint32_t* __restrict__ hist,
+                                                               int m, int n, int tiles) {
+  using V = typename ColVec<kCpt>::T;
+  constexpr int kW = kCpt / 2;  // 32-bit words per vector
+  __shared__ float gmax[kMaxM], ginv[kMaxM];
+  __shared__ uint32_t lh[256];
+  const int z = blockIdx.y;
+  const int c0 = (blockIdx.x * kThreads + threadIdx.x) * kCpt;
+  if (kWriteMax && hist) lh[threadIdx.x] = 0;  // kThreads == 256 bins; the merge's barrier orders it
+  const bool live = c0 < n;  // n % 8 == 0: all kCpt columns live
+  V dv[MP];
+#pragma unroll
+  for (int i = 0; i < MP; ++i) {
+    dv[i] = V{};
+    if (i < m && live) dv[i] = *reinterpret_cast<const V*>(D + (static_cast<int64_t>(z) * m + i) * n + c0);
+  }
+  skv::merge_softmax_partials<kThreads / 64>(norm, sum, z, m, tiles, gmax, ginv);
+  __syncthreads();
+  if (!live && !(kWriteMax && hist)) return;  // (with a histogram every thread reaches its barrier)
+  float best[kCpt];
+#pragma unroll
+  for (int e = 0; e < kCpt; ++e) best[e] = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MP; ++i) {
+    if (i >= m) continue;  // (not break: the loop must unroll fully so dv stays in registers)
+    const float gm = gmax[i], gi = ginv[i];
+    V pv;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      uint32_t pw = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint16_t x = static_cast<uint16_t>(h ? (dv[i][w] >> 16) : (dv[i][w] & 0xffffu));
+        const uint16_t p = skv::f2bf(expf(skv::bf2f(x) - gm) * gi);
+        best[2 * w + h] = fmaxf(best[2 * w + h], skv::bf2f(p));
+        pw |= static_cast<uint32_t>(p) << (16 * h);
+      }
+      pv[w] = pw;
+    }
+    if (kWriteSoftmax && live) *reinterpret_cast<V*>(P + (static_cast<int64_t>(z) * m + i) * n + c0) = pv;
+  }
+  if (kWriteMax) {
+    V mv;
+#pragma unroll
+    for (int w = 0; w < kW; ++w)
+      mv[w] = static_cast<uint32_t>(skv::f2bf(best[2 * w])) | (static_cast<uint32_t>(skv::f2bf(best[2 * w + 1])) << 16);
+    if (live) *reinterpret_cast<V*>(out_max + static_cast<int64_t>(z) * n + c0) = mv;
+    if (hist) {
+      // this workgroup's keys by high order-key byte; a thread's adjacent columns often share a
+      // bin, so equal bins are added together
+      if (live) {
+        uint32_t run_bin = 0xffffffffu, run = 0;
+#pragma unroll
+        for (int e = 0; e < kCpt; ++e) {
+          const uint32_t bin = skv::bf16_order_key(skv::f2bf(best[e])) >> 8;
+          if (bin != run_bin) {
+            if (run) atomicAdd(&lh[run_bin], run);
+            run_bin = bin;
+            run = 0;
+          }
+          ++run;
+        }
+        atomicAdd(&lh[run_bin], run);
+      }
+      __syncthreads();
+      hist[(static_cast<int64_t>(z) * gridDim.x + blockIdx.x) * 256 + threadIdx.x] = lh[threadIdx.x];
+    }
+  }
 }
 
 int check_scoring_shape(const char* what, int batch_count, int m, int n, int k) {
@@ -185,8 +266,16 @@ int launch_logits(const char* what, const uint16_t* A, const uint16_t* B, uint16
   return skv_check_launch(what);
 }
 
+// Columns per thread of the vector softmax: the widest vector that still gives >= 512 workgroups
+// (2 per CU).
+int softmax_cols_per_thread(int batch_count, int n) {
+  int cpt = 8;
+  while (cpt > 2 && static_cast<int64_t>(batch_count) * ((n + kThreads * cpt - 1) / (kThreads * cpt)) < 512) cpt /= 2;
+  return cpt;
+}
+
 int launch_softmax(const char* what, const uint16_t* D, const float* norm, const float* sum, uint16_t* softmax,
-                   uint16_t* out_max, int batch_count, int m, int n, hipStream_t stream) {
+                   uint16_t* out_max, int batch_count, int m, int n, hipStream_t stream, uint32_t* hist = nullptr) {
   if (!D || !norm || !sum || (!softmax && !out_max)) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -194,6 +283,38 @@ int launch_softmax(const char* what, const uint16_t* D, const float* norm, const
   int rc = check_scoring_shape(what, batch_count, m, n, kHeadDim);
   if (rc) return rc;
   const int tiles = (n + kTile - 1) / kTile;
+  const bool vec = n % 8 == 0 && ((reinterpret_cast<uintptr_t>(D) | reinterpret_cast<uintptr_t>(softmax) |
+                                   reinterpret_cast<uintptr_t>(out_max)) & 15u) == 0;
+  if (vec) {
+    const int cpt = softmax_cols_per_thread(batch_count, n);
+    auto go = [&](auto mp, auto cp) {
+      constexpr int MP = decltype(mp)::value;
+      constexpr int C = decltype(cp)::value;
+      const dim3 vgrid((n + kThreads * C - 1) / (kThreads * C), batch_count);
+      if (softmax && out_max)
+        hipLaunchKernelGGL((softmax_vec_kernel<true, true, MP, C>), vgrid, dim3(kThreads), 0, stream, D, norm, sum,
+                           softmax, out_max, nullptr, m, n, tiles);
+      else if (softmax)
+        hipLaunchKernelGGL((softmax_vec_kernel<true, false, MP, C>), vgrid, dim3(kThreads), 0, stream, D, norm, sum,
+                           softmax, out_max, nullptr, m, n, tiles);
+      else
+        hipLaunchKernelGGL((softmax_vec_kernel<false, true, MP, C>), vgrid, dim3(kThreads), 0, stream, D, norm, sum,
+                           softmax, out_max, hist, m, n, tiles);
+    };
+    auto by_cols = [&](auto mp) {
+      if (cpt == 8) go(mp, std::integral_constant<int, 8>{});
+      else if (cpt == 4) go(mp, std::integral_constant<int, 4>{});
+      else go(mp, std::integral_constant<int, 2>{});
+    };
+    if (m <= 4) by_cols(std::integral_constant<int, 4>{});
+    else if (m <= 8) by_cols(std::integral_constant<int, 8>{});
+    else by_cols(std::integral_constant<int, 16>{});
+    return skv_check_launch(what);
+  }
+  if (hist) {
+    skv_set_error("%s: key histograms need n %% 8 == 0 and 16-byte aligned buffers", what);
+    return SKV_EINVAL;
+  }
   const dim3 grid(tiles, batch_count);
   if (softmax && out_max)
     hipLaunchKernelGGL((softmax_kernel<true, true>), grid, dim3(kThreads), 0, stream, D, norm, sum, softmax, out_max, m, n, tiles);
@@ -245,3 +366,18 @@ extern "C" int skv_score_gqa_max(const uint16_t* A, const uint16_t* B, uint16_t*
   if (rc) return rc;
   return launch_softmax("score_gqa_max", D, norm, sum, nullptr, out, batch_count, m, n, s);
 }
+
+namespace skv {
+
+int softmax_hist_parts(int rows, int n) {
+  if (rows < 1 || n < 8 || n % 8) return 0;
+  const int cpt = softmax_cols_per_thread(rows, n);
+  return (n + kThreads * cpt - 1) / (kThreads * cpt);
+}
+
+int softmax_keys_hist(const uint16_t* D, const float* norm, const float* sum, uint16_t* out_max, uint32_t* hist,
+                      int rows, int m, int n, hipStream_t stream) {
+  return launch_softmax("softmax_keys_hist", D, norm, sum, nullptr, out_max, rows, m, n, stream, hist);
+}
+
+}  // namespace skv

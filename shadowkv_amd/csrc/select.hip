@@ -29,6 +29,7 @@
 #include <cstdlib>
 
 #include "select_core.h"
+#include "softmax_keys.h"
 
 namespace {
 
@@ -62,6 +63,10 @@ struct SelectArgs {
   int64_t mv_stride, mv_offset;
   int mv_chunk;
   int hit_src_off;  // byte offset of the LDS list of the hits' old slots (S int32), when moving
+  // Split path: the softmax kernel's per-workgroup histograms of the keys' high bytes
+  // ([rows][h1_parts][256]), summed here instead of counting the keys again; null: count them.
+  const uint32_t* h1;
+  int h1_parts;
 };
 
 __device__ __forceinline__ int scan_excl(int v, int* scratch, int* total) {
@@ -204,20 +209,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const int64_t base = static_cast<int64_t>(row) * S;
   int64_t* prow = a.pos ? a.pos + base : nullptr;
 
-  for (int i = wave; i < (a.pre ? 0 : m); i += kThreads / 64) {
-    const float* nr = a.norm + (static_cast<int64_t>(row) * m + i) * a.tiles;
-    const float* sr = a.sum + (static_cast<int64_t>(row) * m + i) * a.tiles;
-    float mx = -INFINITY;
-    for (int t = lane; t < a.tiles; t += 64) mx = fmaxf(mx, nr[t]);
-    mx = skv::wave_max_dpp(mx);
-    float s = 0.f;
-    for (int t = lane; t < a.tiles; t += 64) s += sr[t] * expf(nr[t] - mx);
-    s = skv::wave_sum_dpp(s);
-    if (lane == 0) {
-      gmax[i] = mx;
-      ginv[i] = 1.f / s;
-    }
-  }
+  if (!a.pre) skv::merge_softmax_partials<kThreads / 64>(a.norm, a.sum, row, m, a.tiles, gmax, ginv);
   for (int i = tid; i < 256; i += kThreads) sh.hist[i] = 0;
   for (int w = tid; w < 2 * a.words; w += kThreads) selmap[w] = 0;  // selmap and oldmap
   if (tid == 0) sel_count = 0;
@@ -320,21 +312,22 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
         atomicAdd(&sh.hist[bin], 1u);
       }
     };
+    const bool counted = a.h1 != nullptr;  // the softmax kernel counted the keys (uniform)
     if (a.pre && a.n_lds) {  // the keys staged in LDS on the way, for the later passes
       if (a.vec) {
         for_keys_global_any([&](int j, uint32_t kj) {
           keys[j] = static_cast<uint16_t>(kj);
-          count_win(kj >> 8);
+          if (!counted) count_win(kj >> 8);
         });
       } else {
         for (int j = lo; j < hi; ++j) {
           const uint32_t kj = skv::bf16_order_key(srow[j]);
           keys[j] = static_cast<uint16_t>(kj);
-          count_win(kj >> 8);
+          if (!counted) count_win(kj >> 8);
         }
       }
     } else if (a.pre) {
-      for_keys_any([&](int, uint32_t kj) { count_win(kj >> 8); });
+      if (!counted) for_keys_any([&](int, uint32_t kj) { count_win(kj >> 8); });
     } else if (a.vec) {
       for (int u = ulo; u < uhi; ++u) {
         u32x4 dv[MP];
@@ -379,6 +372,26 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (wc[k]) atomicAdd(&sh.hist[wbase + k], wc[k]);
+    if (counted) {
+      // the row's partial histograms: thread t adds bin t % 256 of parts t / 256, t / 256 + 4, ...
+      // (16 loads requested before the first is used), the 4 part groups meeting in sh.hist
+      static_assert(kThreads % 256 == 0, "whole bins per thread group");
+      constexpr int kG = kThreads / 256;
+      const uint32_t* hr = a.h1 + static_cast<int64_t>(row) * a.h1_parts * 256;
+      const int b = tid & 255;
+      uint32_t acc = 0;
+      for (int q0 = tid >> 8; q0 < a.h1_parts; q0 += kG * 16) {
+        uint32_t v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int q = q0 + kG * u;
+          v[u] = q < a.h1_parts ? hr[static_cast<int64_t>(q) * 256 + b] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc += v[u];
+      }
+      if (acc) atomicAdd(&sh.hist[b], acc);
+    }
   }
   __syncthreads();
   skv::select_bin(sh.hist, S, sh.found);
@@ -490,6 +503,7 @@ struct PartArgs {
   int32_t* cnt;   // [rows][parts][2]: keys > T, keys == T
   int32_t* thr;   // [rows][4]: T, keys > T over the row, ties that win
   uint64_t* win;  // [rows][S]: (0xffff - key) << 32 | landmark index
+  int h1_parts;   // partial histograms per row in h1 (parts, or the softmax kernel's workgroups)
 };
 
 // Sums the rows' partial histograms h[parts][256] into tot and finds the bin of the want-th
@@ -551,7 +565,7 @@ __global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
   for (int b = tid; b < 256; b += kPartThreads) hist[b] = 0;
   uint32_t b1 = 0;
   if (kPass == 2) {
-    sum_select(a.h1 + static_cast<int64_t>(row) * a.parts * 256, a.parts, a.S, tot, part_tot, found);
+    sum_select(a.h1 + static_cast<int64_t>(row) * a.h1_parts * 256, a.h1_parts, a.S, tot, part_tot, found);
     b1 = static_cast<uint32_t>(found[0]);
   } else {
     __syncthreads();
@@ -594,7 +608,7 @@ __global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
 // T, keys > T over the row (c_gt) and the ties that win (need_eq), from the summed histograms.
 __device__ void row_threshold(const PartArgs& a, int row, uint32_t* tot, uint32_t (*part_tot)[256], int* found,
                               uint32_t* T, int* c_gt, int* need_eq) {
-  sum_select(a.h1 + static_cast<int64_t>(row) * a.parts * 256, a.parts, a.S, tot, part_tot, found);
+  sum_select(a.h1 + static_cast<int64_t>(row) * a.h1_parts * 256, a.h1_parts, a.S, tot, part_tot, found);
   const uint32_t b1 = static_cast<uint32_t>(found[0]);
   const int above1 = found[1];
   __syncthreads();  // tot and found are rewritten below
@@ -745,25 +759,29 @@ void part_plan(int rows, int n, int* parts, int* part_len) {
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
-// Workspace layout of skv_select_chunks_ws: h1, h2, cnt, thr, win.
-size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws) {
+// Workspace layout of skv_select_chunks_ws: h1, h2, cnt, thr, win, then the softmax kernel's
+// per-workgroup key histograms (hs: [rows][softmax_hist_parts][256]; *hs_out when asked).
+size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws, uint32_t** hs_out = nullptr) {
   int parts, len;
   part_plan(rows, n, &parts, &len);
   const size_t h = align256(static_cast<size_t>(rows) * parts * 256 * 4);
   const size_t c = align256(static_cast<size_t>(rows) * parts * 2 * 4);
   const size_t t = align256(static_cast<size_t>(rows) * 4 * 4);
   const size_t wn = align256(static_cast<size_t>(rows) * S * 8);
+  const size_t hs = align256(static_cast<size_t>(rows) * skv::softmax_hist_parts(rows, n) * 256 * 4);
+  unsigned char* p = static_cast<unsigned char*>(ws);
   if (pa) {
-    unsigned char* p = static_cast<unsigned char*>(ws);
     pa->parts = parts;
     pa->part_len = len;
     pa->h1 = reinterpret_cast<uint32_t*>(p);
+    pa->h1_parts = parts;
     pa->h2 = reinterpret_cast<uint32_t*>(p + h);
     pa->cnt = reinterpret_cast<int32_t*>(p + 2 * h);
     pa->thr = reinterpret_cast<int32_t*>(p + 2 * h + c);
     pa->win = reinterpret_cast<uint64_t*>(p + 2 * h + c + t);
   }
-  return 2 * h + c + t + wn;
+  if (hs_out) *hs_out = hs ? reinterpret_cast<uint32_t*>(p + 2 * h + c + t + wn) : nullptr;
+  return 2 * h + c + t + wn + hs;
 }
 
 // Path of a selection call. kFused: the selection kernel computes the keys itself (one workgroup
@@ -878,8 +896,17 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
   const size_t lds = fixed + static_cast<size_t>(n_lds) * 2;
   const size_t ldsb = (lds + 15) / 16 * 16;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  // With the full workspace the softmax kernel also counts the keys' high bytes per workgroup,
+  // and the selection sums those counts instead of counting every key again.
+  uint32_t* hs = nullptr;
+  if (split && workspace && n % 8 == 0 && ((reinterpret_cast<uintptr_t>(D) | reinterpret_cast<uintptr_t>(out_scores)) & 15u) == 0 &&
+      workspace_bytes >= static_cast<int64_t>(part_workspace(rows, n, select_sets, nullptr, nullptr)))
+    part_workspace(rows, n, select_sets, nullptr, workspace, &hs);
+  a.h1 = hs;
+  a.h1_parts = hs ? skv::softmax_hist_parts(rows, n) : 0;
   if (split) {
-    const int rc = skv_softmax_gqa_max(D, norm, sum, nullptr, out_scores, rows, m, n, stream);
+    const int rc = hs ? skv::softmax_keys_hist(D, norm, sum, out_scores, hs, rows, m, n, st)
+                      : skv_softmax_gqa_max(D, norm, sum, nullptr, out_scores, rows, m, n, stream);
     if (rc) return rc;
   }
   if (parts) {
@@ -889,7 +916,12 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
     pa.S = select_sets;
     part_workspace(rows, n, select_sets, &pa, workspace);
     const dim3 pg(pa.parts, rows);
-    hipLaunchKernelGGL(part_hist_kernel<1>, pg, dim3(kPartThreads), 0, st, pa);
+    if (hs) {  // the high-byte histograms are the softmax kernel's
+      pa.h1 = hs;
+      pa.h1_parts = a.h1_parts;
+    } else {
+      hipLaunchKernelGGL(part_hist_kernel<1>, pg, dim3(kPartThreads), 0, st, pa);
+    }
     hipLaunchKernelGGL(part_hist_kernel<2>, pg, dim3(kPartThreads), 0, st, pa);
     hipLaunchKernelGGL(part_count_kernel, pg, dim3(kPartThreads), 0, st, pa);
     hipLaunchKernelGGL(part_emit_kernel, pg, dim3(kPartThreads), 0, st, pa);

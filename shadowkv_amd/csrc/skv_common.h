@@ -88,6 +88,71 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// Softmax normalisers of the m query rows of batch entry z from their per-tile partials (norm:
+// tile maximum, sum: tile sum of exp(x - tile maximum); [z][i][tile] arrays of `tiles` entries):
+//   gmax[i] = max_t norm[t],   ginv[i] = 1 / sum_t sum[t] * exp(norm[t] - gmax[i]).
+// Wave w of the kWaves-wave workgroup takes rows w, w + kWaves, ..., lane l the tiles l, l + 64,
+// ... in increasing order, the lanes' sums added by wave_sum_dpp: that assignment alone fixes
+// the arithmetic, so every kernel calling this gets bit-identical normalisers. With at most 512
+// tiles every row's partials are requested before the first is used (one memory latency for
+// the whole merge instead of two per row). gmax/ginv are LDS arrays; the caller synchronises.
+template <int kWaves>
+__device__ __forceinline__ void merge_softmax_partials(const float* __restrict__ norm, const float* __restrict__ sum,
+                                                       int z, int m, int tiles, float* gmax, float* ginv) {
+  constexpr int kPL = 8;                 // tiles per lane held in registers
+  constexpr int kR = 16 / kWaves;        // rows per wave (m <= 16)
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (tiles <= 64 * kPL) {
+    float nv[kR][kPL], sv[kR][kPL];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int i = wave + r * kWaves;
+      const int64_t base = (static_cast<int64_t>(z) * m + min(i, m - 1)) * tiles;
+#pragma unroll
+      for (int u = 0; u < kPL; ++u) {
+        const int t = lane + 64 * u;
+        const bool ok = i < m && t < tiles;
+        nv[r][u] = ok ? norm[base + t] : -INFINITY;
+        sv[r][u] = ok ? sum[base + t] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int i = wave + r * kWaves;
+      if (i >= m) continue;  // wave-uniform (continue, not break: the loop unrolls fully)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kPL; ++u) mx = fmaxf(mx, nv[r][u]);
+      mx = wave_max_dpp(mx);
+      float s = 0.f;
+#pragma unroll
+      for (int u = 0; u < kPL; ++u)
+        if (lane + 64 * u < tiles) s += sv[r][u] * expf(nv[r][u] - mx);
+      s = wave_sum_dpp(s);
+      if (lane == 0) {
+        gmax[i] = mx;
+        ginv[i] = 1.f / s;
+      }
+    }
+    return;
+  }
+  for (int i = wave; i < m; i += kWaves) {
+    const float* nr = norm + (static_cast<int64_t>(z) * m + i) * tiles;
+    const float* sr = sum + (static_cast<int64_t>(z) * m + i) * tiles;
+    float mx = -INFINITY;
+    for (int t = lane; t < tiles; t += 64) mx = fmaxf(mx, nr[t]);
+    mx = wave_max_dpp(mx);
+    float s = 0.f;
+    for (int t = lane; t < tiles; t += 64) s += sr[t] * expf(nr[t] - mx);
+    s = wave_sum_dpp(s);
+    if (lane == 0) {
+      gmax[i] = mx;
+      ginv[i] = 1.f / s;
+    }
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

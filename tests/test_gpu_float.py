@@ -217,6 +217,39 @@ def test_scoring(gpu, Z, m, n):
     assert torch.equal(out.cpu(), Pg.cpu().max(dim=1).values)  # GQA max of the kernel's own probabilities
 
 
+@pytest.mark.parametrize("Z,m,n", [(8, 16, 32712), (32, 4, 15304), (2, 4, 140000), (3, 8, 2048), (1, 1, 8),
+                                   (256, 4, 4096), (128, 16, 4096)])
+def test_softmax_vector_and_scalar_paths_agree(gpu, Z, m, n):
+    """The softmax + GQA-max kernel's vector path (rows of n % 8 == 0 columns, aligned buffers;
+    8, 4 or 2 columns per thread, by the workgroup count: 8 for 256 x 4096, 4 for 128 x 4096, 2
+    for the few-row shapes) and its one-column-per-thread path (taken here by handing it outputs 2 bytes off alignment)
+    give bit-identical probabilities and maxima, also past 512 partial tiles per row (140000
+    columns), where the partials merge no longer holds a row's partials in registers; the
+    probabilities agree with the oracle's softmax of the same logits within one rounding step."""
+    _say(f"softmax paths Z={Z} m={m} n={n}")
+    g = torch.Generator().manual_seed(n + m)
+    q = torch.randn(Z, m, 128, generator=g).to(torch.bfloat16).to(gpu)
+    L = torch.randn(Z, n, 128, generator=g).to(torch.bfloat16).to(gpu)
+    tiles = (n + 255) // 256
+    D = torch.empty(Z, m, n, dtype=torch.bfloat16, device=gpu)
+    norm = torch.empty(Z, m, tiles, device=gpu)
+    ssum = torch.empty_like(norm)
+    shadowkv.score_logits(q, L, D, norm, ssum, Z, m, n, 128, 1.0 / math.sqrt(128))
+    outs = {}
+    for name, off in (("vector", 0), ("scalar", 1)):
+        sm_buf = torch.empty(Z * m * n + 8, dtype=torch.bfloat16, device=gpu)
+        mx_buf = torch.empty(Z * n + 8, dtype=torch.bfloat16, device=gpu)
+        sm, mx = sm_buf[off:off + Z * m * n], mx_buf[off:off + Z * n]
+        shadowkv.softmax_gqa_max(D, norm, ssum, mx, Z, m, n, softmax=sm)
+        torch.cuda.synchronize()
+        outs[name] = (sm.view(Z, m, n).cpu(), mx.view(Z, n).cpu())
+    assert torch.equal(outs["vector"][0], outs["scalar"][0])
+    assert torch.equal(outs["vector"][1], outs["scalar"][1])
+    assert torch.equal(outs["vector"][1], outs["vector"][0].max(dim=1).values)
+    logits = D.cpu().float()
+    _assert_rounding_close(outs["vector"][0], torch.softmax(logits, dim=-1).to(torch.bfloat16), floor=1e-9)
+
+
 @pytest.mark.parametrize("B,Hq,Hk,L,strided", [(1, 32, 8, 2497, True), (8, 32, 8, 2600, True), (2, 32, 2, 2497, True),
                                                (1, 8, 8, 1, False), (3, 16, 4, 300, False), (1, 32, 8, 19521, True),
                                                (1, 32, 8, 8193, False), (2, 24, 2, 700, True), (1, 16, 1, 129, False),

@@ -192,14 +192,14 @@ def test_topk_gather_bit_exact(gpu, n, k, ties):
     assert torch.equal(out.cpu(), want)
 
 
-@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("split", ["0", "1", "1ws", "ws"])
 @pytest.mark.parametrize("rows,m,n,S", [(64, 4, 15304, 256), (8, 16, 32712, 256), (8, 4, 130680, 2048),
                                         (8, 4, 968, 256), (2, 1, 300, 7)])
 def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, split):
     """The fused selection (keys computed per row in the selection kernel; on the split path by
     the many-workgroup softmax + GQA-max kernel first; on the parts path ("ws") also the radix
     passes over many workgroups per row, with a caller workspace) equals the unfused sequence."""
-    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    monkeypatch.setenv("SKV_SELECT_SPLIT", {"ws": "2", "1ws": "1"}.get(split, split))
     _say(f"select_chunks rows={rows} m={m} n={n} S={S} split={split}")
     g = torch.Generator().manual_seed(rows * n + S)
     q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
@@ -231,13 +231,14 @@ def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, spl
     sel2 = torch.empty_like(sel)
     nchunks = n + n // 10
     ws = None
-    if split == "ws":  # each row's selection over many workgroups (scratch from the caller)
+    if split in ("ws", "1ws"):  # with the caller's workspace: the key histograms counted by the
+        # softmax kernel ("1ws"), or each row's selection over many workgroups ("ws")
         ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu)
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos2, off2, cnt2, out_scores=scores2,
                            out_selected=sel2, workspace=ws)
     pos3, off3, cnt3 = old.clone(), torch.empty_like(off1), torch.empty_like(cnt1)
     staging = torch.empty_like(scores) if n > 16384 else None  # scores beyond LDS need global staging
-    if split == "ws" and staging is None:
+    if split in ("ws", "1ws") and staging is None:
         staging = torch.empty_like(scores)  # the many-workgroup path needs the keys in global memory
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos3, off3, cnt3, out_scores=staging,
                            workspace=ws)
@@ -259,12 +260,12 @@ def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, spl
     assert (cnts >= S // 2).all()
 
 
-@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("split", ["0", "1", "1ws", "ws"])
 @pytest.mark.parametrize("rows,m,n,S", [(8, 4, 130680, 2048), (8, 16, 32712, 256), (4, 4, 15304, 256)])
 def test_select_chunks_all_ties(gpu, monkeypatch, rows, m, n, S, split):
     """Zero queries: every logit 0, every probability 1/n, so all keys tie and the selection is
     the S lowest landmark indices (ties broken by index across every slice of a row)."""
-    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    monkeypatch.setenv("SKV_SELECT_SPLIT", {"ws": "2", "1ws": "1"}.get(split, split))
     _say(f"select_chunks all ties rows={rows} m={m} n={n} S={S} split={split}")
     g = torch.Generator().manual_seed(n + S)
     q = torch.zeros(rows, m, 128, dtype=torch.bfloat16, device=gpu)
@@ -281,7 +282,7 @@ def test_select_chunks_all_ties(gpu, monkeypatch, rows, m, n, S, split):
     cnt = torch.empty(rows, dtype=torch.int32, device=gpu)
     scores = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
     sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
-    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split == "ws" else None
+    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split in ("ws", "1ws") else None
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, pos, off, cnt, out_scores=scores,
                            out_selected=sel, workspace=ws)
     torch.cuda.synchronize()
@@ -293,13 +294,13 @@ def test_select_chunks_all_ties(gpu, monkeypatch, rows, m, n, S, split):
     assert torch.equal(off.view(rows, S).cpu(), want.to(torch.int32))
 
 
-@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("split", ["0", "1", "1ws", "ws"])
 @pytest.mark.parametrize("rows,m,n", [(4, 4, 256), (2, 16, 1000), (1, 8, 2048)])
 def test_select_chunks_selects_every_landmark(gpu, monkeypatch, rows, m, n, split):
     """select_sets = n: every landmark is selected; with empty previous slots all are misses, so
     the slots hold the landmark ids ascending and the top-k order is the scores' total order."""
     S = n
-    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    monkeypatch.setenv("SKV_SELECT_SPLIT", {"ws": "2", "1ws": "1"}.get(split, split))
     _say(f"select every landmark rows={rows} m={m} n={n} split={split}")
     g = torch.Generator().manual_seed(n + m)
     q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
@@ -315,7 +316,7 @@ def test_select_chunks_selects_every_landmark(gpu, monkeypatch, rows, m, n, spli
     cnt = torch.empty(rows, dtype=torch.int32, device=gpu)
     scores = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
     sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
-    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split == "ws" else None
+    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split in ("ws", "1ws") else None
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, 2 * n, pos, off, cnt, out_scores=scores,
                            out_selected=sel, workspace=ws)
     torch.cuda.synchronize()
@@ -352,7 +353,7 @@ def _old_slots(sel, lidx, S, mode, g):
 
 
 @pytest.mark.parametrize("mode", ["half", "shift", "all", "none"])
-@pytest.mark.parametrize("split", ["0", "1", "ws"])
+@pytest.mark.parametrize("split", ["0", "1", "1ws", "ws"])
 @pytest.mark.parametrize("rows,m,n,S,chunk_elems", [(64, 4, 15304, 256, 1024), (8, 4, 130680, 2048, 1024),
                                                     (8, 4, 968, 256, 1024), (2, 1, 300, 7, 16)])
 def test_select_chunks_folded_hit_moves(gpu, monkeypatch, rows, m, n, S, chunk_elems, split, mode):
@@ -361,7 +362,7 @@ def test_select_chunks_folded_hit_moves(gpu, monkeypatch, rows, m, n, S, chunk_e
     and slot ids as the plain selection, and buffers bit-identical to the plain selection followed
     by the separate compaction kernel on each buffer and to a slot-by-slot compaction on the host;
     also with the value buffer alone."""
-    monkeypatch.setenv("SKV_SELECT_SPLIT", "2" if split == "ws" else split)
+    monkeypatch.setenv("SKV_SELECT_SPLIT", {"ws": "2", "1ws": "1"}.get(split, split))
     _say(f"select_chunks folded moves rows={rows} m={m} n={n} S={S} split={split} mode={mode}")
     g = torch.Generator().manual_seed(rows * n + S + len(mode))
     q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
@@ -373,7 +374,7 @@ def test_select_chunks_folded_hit_moves(gpu, monkeypatch, rows, m, n, S, chunk_e
     ssum = torch.empty_like(norm)
     shadowkv.score_logits(q, L, D, norm, ssum, rows, m, n, 128)
     nchunks = n + n // 10
-    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split == "ws" else None
+    ws = torch.empty(shadowkv.select_workspace_bytes(rows, n, S), dtype=torch.uint8, device=gpu) if split in ("ws", "1ws") else None
     sel = torch.empty(rows, S, dtype=torch.int64, device=gpu)
     shadowkv.select_chunks(D, norm, ssum, rows, m, n, lidx, S, nchunks, None, None, None,
                            out_scores=torch.empty(rows, n, dtype=torch.bfloat16, device=gpu), out_selected=sel,

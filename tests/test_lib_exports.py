@@ -67,16 +67,24 @@ def test_argument_errors_are_reported_without_a_gpu():
 
 def test_selection_workspace_plan():
     """The selection workspace covers the slice histograms, counts and winners of the plan the
-    library uses (about 256 / rows slices of at most 4096 keys per row), and bad sizes give 0."""
+    library uses (about 256 / rows slices of at most 4096 keys per row) and the softmax kernel's
+    per-workgroup key histograms, and bad sizes give 0."""
     lib = _lib.lib()
     assert lib.skv_select_workspace_bytes(0, 100, 10) == 0
     assert lib.skv_select_workspace_bytes(8, 0, 10) == 0
-    for rows, n, S in ((8, 130680, 2048), (8, 32712, 256), (32, 15304, 256), (1, 1000, 7)):
+    for rows, n, S in ((8, 130680, 2048), (8, 32712, 256), (32, 15304, 256), (1, 1000, 7), (4, 1001, 7)):
         target = max(1, min(64, 256 // rows))
         part_len = max(256, min(4096, -(-(-(-n // target)) // 256) * 256))
         parts = -(-n // part_len)
         align = lambda b: -(-b // 256) * 256
         want = 2 * align(rows * parts * 256 * 4) + align(rows * parts * 8) + align(rows * 16) + align(rows * S * 8)
+        # the softmax kernel's per-workgroup key histograms: 8, 4 or 2 columns per thread of 256,
+        # the widest giving >= 512 workgroups (n % 8 == 0 rows only)
+        cpt = 8
+        while cpt > 2 and rows * -(-n // (256 * cpt)) < 512:
+            cpt //= 2
+        sparts = -(-n // (256 * cpt)) if n % 8 == 0 else 0
+        want += align(rows * sparts * 256 * 4)
         assert lib.skv_select_workspace_bytes(rows, n, S) == want, (rows, n, S)
     # select_chunks_ws rejects a null workspace and a short one on the host
     p = ctypes.c_void_p(16)
