@@ -67,10 +67,23 @@ struct SelectArgs {
   // ([rows][h1_parts][256]), summed here instead of counting the keys again; null: count them.
   const uint32_t* h1;
   int h1_parts;
+  // With h1, the keys whose high byte is at least the threshold bin's are first compacted (index
+  // order) into an LDS candidate list of at most cand_cap entries at byte offset cand_off (keys,
+  // then 16-byte aligned indices), and every later pass runs over the list; more candidates than
+  // that (e.g. all keys tied) fall back to the passes over all keys. cand_cap 0: no list.
+  int cand_off, cand_cap;
 };
 
 __device__ __forceinline__ int scan_excl(int v, int* scratch, int* total) {
   return skv::block_exclusive_scan(v, scratch, total);
+}
+
+// Largest of the 8 raw 16-bit halves of v (written on 32-bit operations: this compiler reduced a
+// max over ext_vector_type(2) unsigned shorts of the four words to one word's halves).
+__device__ __forceinline__ uint32_t unit_max_raw(const u32x4& v) {
+  const uint32_t a = max(v.x & 0xffffu, v.x >> 16), b = max(v.y & 0xffffu, v.y >> 16);
+  const uint32_t c = max(v.z & 0xffffu, v.z >> 16), d = max(v.w & 0xffffu, v.w >> 16);
+  return max(max(a, b), max(c, d));
 }
 
 __device__ __forceinline__ uint16_t half_of(const u32x4& v, int e) {
@@ -208,6 +221,22 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const int m = a.m, n = a.n, S = a.S;
   const int64_t base = static_cast<int64_t>(row) * S;
   int64_t* prow = a.pos ? a.pos + base : nullptr;
+  // Candidate-list path with at most kRegU 8-key units per thread (the MP = 4 instance, which the
+  // launcher uses for every split-path call): the thread's keys are requested here, at entry, and
+  // tested from registers once the threshold bin is known.
+  constexpr int kRegU = MP == 4 ? 8 : 1;
+  const int reg_eu = (n / 8 + kThreads - 1) / kThreads;
+  const bool regs = MP == 4 && a.h1 != nullptr && a.pre && a.vec && a.cand_cap > 0 && reg_eu <= kRegU;  // uniform
+  u32x4 kr[kRegU];
+  if (regs) {
+    const int u0 = min(tid * reg_eu, n / 8), u1 = min(u0 + reg_eu, n / 8);
+    const u32x4* sv = reinterpret_cast<const u32x4*>(a.out_scores + static_cast<int64_t>(row) * n);
+#pragma unroll
+    for (int u = 0; u < kRegU; ++u) {
+      kr[u] = u32x4{0u, 0u, 0u, 0u};
+      if (u0 + u < u1) kr[u] = sv[u0 + u];
+    }
+  }
 
   if (!a.pre) skv::merge_softmax_partials<kThreads / 64>(a.norm, a.sum, row, m, a.tiles, gmax, ginv);
   for (int i = tid; i < 256; i += kThreads) sh.hist[i] = 0;
@@ -228,6 +257,12 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const int lo = ulo * kU, hi = min(uhi * kU, n);
   const uint16_t* Drow = a.D + static_cast<int64_t>(row) * m * n;
   uint16_t* srow = a.out_scores ? a.out_scores + static_cast<int64_t>(row) * n : nullptr;
+  // candidate list (see SelectArgs::cand_cap): set once the threshold bin is known
+  const bool cand_try = a.h1 != nullptr && a.pre && a.vec && a.cand_cap > 0;  // uniform
+  uint16_t* ck = reinterpret_cast<uint16_t*>(smem + a.cand_off);
+  int32_t* ci = reinterpret_cast<int32_t*>(smem + a.cand_off + (static_cast<size_t>(a.cand_cap) * 2 + 15) / 16 * 16);
+  bool cand = false;
+  int nc = 0, clo = 0, chi = 0;
   auto prob_max = [&](float (&dv)[MP]) -> uint16_t {  // bf16 of max_i bf16(softmax_i)
     float best = -INFINITY;
 #pragma unroll
@@ -241,6 +276,10 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   };
   // The keys of this thread's block, 8 at a time where the unit allows: f(j, key) for j in [lo, hi).
   auto for_keys = [&](auto&& f) {
+    if (cand) {  // this thread's block of the candidate list (index order)
+      for (int c = clo; c < chi; ++c) f(ci[c], static_cast<uint32_t>(ck[c]));
+      return;
+    }
     if (a.vec) {
       for (int u = ulo; u < uhi; ++u) {
         uint32_t k8[8];
@@ -280,7 +319,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
     }
   };
   auto for_keys_any = [&](auto&& f) {
-    if (a.n_lds || !a.vec) {
+    if (cand || a.n_lds || !a.vec) {
       for_keys(f);
       return;
     }
@@ -313,7 +352,7 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
       }
     };
     const bool counted = a.h1 != nullptr;  // the softmax kernel counted the keys (uniform)
-    if (a.pre && a.n_lds) {  // the keys staged in LDS on the way, for the later passes
+    if (a.pre && a.n_lds && !cand_try) {  // the keys staged in LDS on the way, for the later passes
       if (a.vec) {
         for_keys_global_any([&](int j, uint32_t kj) {
           keys[j] = static_cast<uint16_t>(kj);
@@ -399,6 +438,72 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
   const int above1 = sh.found[1];
   __syncthreads();
   for (int i = tid; i < 256; i += kThreads) sh.hist[i] = 0;
+  if (cand_try) {
+    // Keys with high byte >= b1 (every winner among them): count this thread's, scan, and, if
+    // they fit, write them in index order to the candidate list (the row is read twice from
+    // global memory, the second time from the L2); else stage all keys as the passes expect.
+    const u32x4* sv = reinterpret_cast<const u32x4*>(srow);
+    int my_c = 0;
+    uint64_t hitmask = 0;  // regs: bit 8u + e marks key e of unit u as a candidate
+    if (regs) {  // (ulo, uhi) are the units loaded into kr at entry
+      // A unit whose 8 raw bf16 values are all below kraw (with the threshold bin non-negative,
+      // raw order is value order for non-negative values) holds no candidate: one packed maximum
+      // over the unit instead of 8 key tests (about 1 unit in 10 holds a candidate). A negative
+      // value (sign bit set) fails the test and takes the per-key path.
+      const uint32_t kraw = b1 >= 0x80u ? (b1 << 8) - 0x8000u : 0u;
+#pragma unroll
+      for (int u = 0; u < kRegU; ++u) {
+        if (ulo + u < uhi) {
+          if (b1 >= 0x80u && unit_max_raw(kr[u]) < kraw) continue;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            hitmask |= static_cast<uint64_t>((skv::bf16_order_key(half_of(kr[u], e)) >> 8) >= b1) << (8 * u + e);
+        }
+      }
+      my_c = __popcll(hitmask);
+    } else {
+      for (int u = ulo; u < uhi; ++u) {
+        const u32x4 v = sv[u];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) my_c += (skv::bf16_order_key(half_of(v, e)) >> 8) >= b1;
+      }
+    }
+    int pos = scan_excl(my_c, sh.scan, &nc);
+    if (nc <= a.cand_cap) {
+      if (regs) {
+#pragma unroll
+        for (int u = 0; u < kRegU; ++u) {
+          uint32_t bits = static_cast<uint32_t>(hitmask >> (8 * u)) & 0xffu;
+          while (bits) {
+            const int e = __ffs(bits) - 1;
+            bits &= bits - 1;
+            ck[pos] = static_cast<uint16_t>(skv::bf16_order_key(half_of(kr[u], e)));
+            ci[pos] = 8 * (ulo + u) + e;
+            ++pos;
+          }
+        }
+      } else {
+        for (int u = ulo; u < uhi; ++u) {
+          const u32x4 v = sv[u];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t kj = skv::bf16_order_key(half_of(v, e));
+            if ((kj >> 8) >= b1) {
+              ck[pos] = static_cast<uint16_t>(kj);
+              ci[pos] = 8 * u + e;
+              ++pos;
+            }
+          }
+        }
+      }
+      cand = true;
+      const int Ec = (nc + kThreads - 1) / kThreads;
+      clo = min(tid * Ec, nc);
+      chi = min(clo + Ec, nc);
+    } else if (a.n_lds) {
+      for_keys_global_any([&](int j, uint32_t kj) { keys[j] = static_cast<uint16_t>(kj); });
+    }
+  }
   __syncthreads();
   {
     uint32_t run_bin = 0xffffffffu, run = 0;
@@ -785,8 +890,8 @@ size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws, uint32_t**
 }
 
 // Path of a selection call. kFused: the selection kernel computes the keys itself (one workgroup
-// per row). kSplit: few rows (rows * 8 <= 256 CUs) and m*n >= 2^15, so the keys come from the
-// many-workgroup softmax kernel first. kParts: as kSplit, and long rows (n >= kPartsMinKeys) with a
+// per row). kSplit: few rows (at most 32, or 64 with a workspace) and m*n >= 2^15, so the keys
+// come from the many-workgroup softmax kernel first. kParts: as kSplit, and long rows (n >= kPartsMinKeys) with a
 // workspace, so the selection passes also run over many workgroups per row. Environment
 // SKV_SELECT_SPLIT=0/1/2 forces fused / split / parts (parts only with a workspace), read per call.
 enum SelectPath { kFused = 0, kSplitPath = 1, kParts = 2 };
@@ -803,7 +908,9 @@ SelectPath select_path(int rows, int m, int n, bool has_scores, bool has_ws) {
     const int v = e[0] - '0';
     return v == 2 ? (has_ws ? kParts : kSplitPath) : static_cast<SelectPath>(v);
   }
-  if (rows > 32 || static_cast<int64_t>(m) * n < (int64_t{1} << 15)) return kFused;
+  // With a workspace the keys-first selection works on a candidate list and stays ahead of the
+  // fused kernel up to 64 rows (measured at 64 x 4 x 15304: 16.9 vs 21.2 µs; 192 rows: 29.6 vs 23.3).
+  if (rows > (has_ws ? 64 : 32) || static_cast<int64_t>(m) * n < (int64_t{1} << 15)) return kFused;
   return (has_ws && n >= kPartsMinKeys) ? kParts : kSplitPath;
 }
 
@@ -893,8 +1000,7 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
   a.out_scores = out_scores;
   a.out_sel = out_selected;
   a.pre = split ? 1 : 0;
-  const size_t lds = fixed + static_cast<size_t>(n_lds) * 2;
-  const size_t ldsb = (lds + 15) / 16 * 16;
+  size_t lds = fixed + static_cast<size_t>(n_lds) * 2;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   // With the full workspace the softmax kernel also counts the keys' high bytes per workgroup,
   // and the selection sums those counts instead of counting every key again.
@@ -904,6 +1010,20 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
     part_workspace(rows, n, select_sets, nullptr, workspace, &hs);
   a.h1 = hs;
   a.h1_parts = hs ? skv::softmax_hist_parts(rows, n) : 0;
+  // The candidate list: in the keys' LDS region when the row fits LDS (free until the keys would
+  // be staged, which only the fallback does), else in what the budget leaves after the fixed part.
+  a.cand_off = 0;
+  a.cand_cap = 0;
+  if (hs && !parts && a.vec) {
+    const size_t room = n_lds ? static_cast<size_t>(n_lds) * 2 : std::min<size_t>(kLdsBudget - fixed, 96 * 1024);
+    const size_t cap = room >= 32 ? (room - 16) / 6 : 0;
+    if (cap >= static_cast<size_t>(select_sets)) {
+      a.cand_off = static_cast<int>(fixed);
+      a.cand_cap = static_cast<int>(cap);
+      if (!n_lds) lds = fixed + room;
+    }
+  }
+  const size_t ldsb = (lds + 15) / 16 * 16;
   if (split) {
     const int rc = hs ? skv::softmax_keys_hist(D, norm, sum, out_scores, hs, rows, m, n, st)
                       : skv_softmax_gqa_max(D, norm, sum, nullptr, out_scores, rows, m, n, stream);
@@ -929,7 +1049,8 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
     hipLaunchKernelGGL(select_finish_kernel, dim3(rows), dim3(kThreads), fb, st, a, pa);
     return skv_check_launch(what);
   }
-  if (m <= 4) hipLaunchKernelGGL(select_kernel<4>, dim3(rows), dim3(kThreads), ldsb, st, a);
+  // (keys precomputed: the query count plays no part, and the MP = 4 instance keeps them in registers)
+  if (m <= 4 || split) hipLaunchKernelGGL(select_kernel<4>, dim3(rows), dim3(kThreads), ldsb, st, a);
   else if (m <= 8) hipLaunchKernelGGL(select_kernel<8>, dim3(rows), dim3(kThreads), ldsb, st, a);
   else hipLaunchKernelGGL(select_kernel<16>, dim3(rows), dim3(kThreads), ldsb, st, a);
   return skv_check_launch(what);
