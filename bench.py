@@ -63,14 +63,15 @@ def parse() -> argparse.Namespace:
                    help="decode steps per captured graph (one continuous lane pipeline across steps); "
                         "reduced to a divisor of --steps")
     p.add_argument("--workload", choices=["decode", "rebuild", "attention", "select", "linear", "encode", "pool",
-                                          "hostlink"],
+                                          "hostlink", "envelope"],
                    default="decode",
                    help="decode: the 32-layer decode step; rebuild: the low-rank key rebuild + RoPE kernel alone; "
                         "attention: the sparse decode attention alone; select: the fused chunk selection alone; "
                         "linear: the skinny decode projections alone (next to torch's GEMM); encode: the prefill "
                         "encoder (low-rank factors, chunk statistics, outliers, landmarks, initial selection); "
                         "pool: one layer's sparse step on drifting queries with and without a device chunk pool; "
-                        "hostlink: pinned-host read rate of SDMA copies and of the value-fetch gather")
+                        "hostlink: pinned-host read rate of SDMA copies and of the value-fetch gather; "
+                        "envelope: HBM streaming rate of the scoring kernel and of a device copy by transfer size")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -497,6 +498,59 @@ def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
     e.record()
     e.synchronize()
     return s.elapsed_time(e) * 1e-3 / (rounds * reps)
+
+
+def envelope_microbench(args) -> int:
+    """HBM streaming envelope of this GPU at decode-kernel sizes: the landmark scoring kernel (a
+    pure stream of landmark rows with a little MFMA work, the bench line's roofline kernel) and
+    torch's device copy, each over a range of transfer sizes, cold (every launch reads buffers
+    that the previous ones did not touch, > 1 GiB in rotation). A least-squares fit time = t0 +
+    bytes / rate over the sizes gives the marginal streaming rate and the fixed per-launch cost,
+    which together bound the HBM fraction a kernel of a given size can reach."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    n, m = 15304, 4
+    row_bytes = n * 128 * 2 + m * 128 * 2 + m * n * 2 + m * ((n + 255) // 256) * 8
+    sets = 8
+    res = {"scoring": [], "copy": []}
+    for rows in (8, 16, 32, 48, 64, 96, 128):
+        g = torch.Generator(device="cuda").manual_seed(rows)
+        Ls = [torch.randn(rows, n, 128, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
+        q = torch.randn(rows, m, 128, generator=g, device="cuda").to(torch.bfloat16)
+        tiles = (n + 255) // 256
+        D = torch.empty(rows, m, n, dtype=torch.bfloat16, device="cuda")
+        nm = torch.empty(rows, m, tiles, device="cuda")
+        sm = torch.empty_like(nm)
+        t = gpu_time_per_call(lambda i: shadowkv.score_logits(q, Ls[i % sets], D, nm, sm, rows, m, n, 128,
+                                                              1.0 / math.sqrt(128)), 4 * sets)
+        res["scoring"].append((rows * row_bytes, t))
+        del Ls, D, nm, sm
+        # a device copy moving the same bytes (half read, half written)
+        half = rows * row_bytes // 2 // 2  # bf16 elements per side
+        src = [torch.empty(half, dtype=torch.bfloat16, device="cuda") for _ in range(sets)]
+        dst = [torch.empty(half, dtype=torch.bfloat16, device="cuda") for _ in range(sets)]
+        t = gpu_time_per_call(lambda i: dst[i % sets].copy_(src[i % sets]), 4 * sets)
+        res["copy"].append((4 * half, t))
+        del src, dst
+        torch.cuda.empty_cache()
+    for kind, pts in res.items():
+        xs = [b for b, _ in pts]
+        ys = [t for _, t in pts]
+        k = len(xs)
+        mx, my = sum(xs) / k, sum(ys) / k
+        slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        t0 = my - slope * mx
+        rate = 1.0 / slope / 1e9
+        for b, t in pts:
+            print(json.dumps({"metric": f"{kind} streaming rate", "value": round(b / t / 1e9, 1), "unit": "GB/s",
+                              "bytes": int(b), "us": round(t * 1e6, 2), "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                              "config": {"workload": f"{kind}: {b / 1e6:.1f} MB per launch, cold buffers"}}), flush=True)
+        print(json.dumps({"metric": f"{kind} fit time = t0 + bytes / rate", "rate_GBps": round(rate, 1),
+                          "rate_frac": round(rate / HBM_PEAK_GBS, 4), "t0_us": round(t0 * 1e6, 2),
+                          "frac_at_100MB": round(100e6 / (t0 + 100e6 / (rate * 1e9)) / 1e9 / HBM_PEAK_GBS, 4)}),
+              flush=True)
+    return 0
 
 
 def rebuild_bytes(rows_per_head: int, BH: int, S: int, R: int = 160, D: int = 128) -> int:
@@ -977,6 +1031,8 @@ def main() -> int:
         return pool_microbench(args)
     if args.workload == "hostlink":
         return hostlink_microbench(args)
+    if args.workload == "envelope":
+        return envelope_microbench(args)
     import torch
     from shadowkv_amd import decode_model
     from shadowkv_amd.kernels import shadowkv
