@@ -730,7 +730,7 @@ def select_microbench(args) -> int:
         t_all = gpu_time_per_call(run, reps)
         t_copy = gpu_time_per_call(lambda _: pos.copy_(pos0), reps)
         env = os.environ.get("SKV_SELECT_SPLIT")
-        few = rows <= 32 and G * n >= 1 << 15
+        few = rows <= (64 if ws is not None else 32) and G * n >= 1 << 15  # the library's path rule
         path = {"0": "fused", "1": "split", "2": "parts"}.get(env, ("parts" if n >= 65536 else "split") if few else "fused")
         t = t_all - t_copy
         out_line = {"metric": "fused chunk selection latency", "value": round(t * 1e6, 2), "unit": "us",
@@ -741,7 +741,8 @@ def select_microbench(args) -> int:
                     "config": {"workload": f"{name} selection: {rows} rows x {G} queries x {n} landmarks, top {S}",
                                "rows": rows, "m": G, "n": n, "select_sets": S},
                     "roofline": {"kernel": {"fused": "select_kernel",
-                                            "split": "softmax_kernel + select_kernel (keys on many workgroups)",
+                                            "split": "softmax_vec_kernel + select_kernel (keys and key histograms on "
+                                                     "many workgroups, selection on a candidate list)",
                                             "parts": "softmax_kernel + part_*_kernel + select_finish_kernel "
                                                      "(many workgroups per row)"}[path],
                                  "bound": "latency", "achieved": None, "peak": None,
