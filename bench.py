@@ -55,6 +55,10 @@ def parse() -> argparse.Namespace:
                         "GLM-4-9B (2 kv heads of 16 query heads, GLM RoPE), Llama-3-8B-1M (RoPE theta 3.58e6)")
     p.add_argument("--lanes", type=int, default=None,
                    help="independent batch slices pipelined per layer (default: 2 where the value fetch outweighs the dense layers, see decode_model.auto_lanes)")
+    p.add_argument("--pool-variant", type=int, default=2048,
+                   help="after the main (reference-mode) measurement, time the same decode with a device chunk "
+                        "pool of this many slots per (b, h) and layer and report it in detail.chunk_pool "
+                        "(0: skip; only with the breakdown)")
     p.add_argument("--separate-hit-moves", action="store_true",
                    help="move the hits of the key and value buffers in their own launches instead of in the "
                         "selection's last launch (the same work, for comparison)")
@@ -498,6 +502,55 @@ def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
     e.record()
     e.synchronize()
     return s.elapsed_time(e) * 1e-3 / (rounds * reps)
+
+
+def pool_variant(args, shape, lanes) -> dict:
+    """The same decode workload with a device chunk pool (f3: P >= S chunk slots per (b, h) and
+    layer kept across steps, least recently used replaced; the same chunks are selected and the
+    attention outputs equal the reference mode's to bf16 summation order), timed as the main
+    measurement. The reference-mode
+    decoder is released first (its pinned host store is 64 GiB at batch 8)."""
+    import gc
+    import torch
+    from shadowkv_amd import decode_model
+
+    P = args.pool_variant
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+    log(f"chunk pool variant: {P} slots per (b, h) and layer")
+    pm = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
+                                       decode_len=args.warmup + args.steps + 8, lanes=lanes, chunk_cache=P)
+    tok = torch.randint(0, shape.vocab, (args.batch, 1), device="cuda")
+    for _ in range(args.warmup):
+        tok = pm.decode_step(tok)
+    per_call = math.gcd(args.steps, max(1, args.graph_steps))
+    pm.capture(tok, steps=per_call)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps // per_call):
+        tok = pm.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    hits = [float(lane.cache.cnts.float().mean()) for lane in pm.lanes]  # last layer of the last step
+    c = pm.cache
+    extra = (P - c.select_sets) * c.chunk_size * c.head_dim * 2 * 2 * args.batch * shape.kv_heads * shape.layers
+    res = {"slots": P, "tokens_per_s": round(args.batch * args.steps / elapsed, 3),
+           "ms_per_step": round(elapsed * 1e3 / args.steps, 3),
+           "hit_rate_last_layer": round(statistics.fmean(hits) / c.select_sets, 4),
+           "extra_device_GB": round(extra / 1e9, 2),
+           "note": "same workload with a device chunk pool (f3): the same chunks selected and attention outputs "
+                   "equal to the reference mode's within bf16 summation order (tests/test_gpu_pool.py); hits are "
+                   "chunks still resident from earlier steps (synthetic queries are independent from step to step, "
+                   "so the hit rate is about slots / landmarks)"}
+    log(f"chunk pool variant {res}")
+    del pm
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+    return res
 
 
 def envelope_microbench(args) -> int:
@@ -1132,6 +1185,10 @@ def main() -> int:
             sl = single_layer_cpu_ms(args.cpu_runs)
             detail["single_layer"].update(sl)
             log(f"single layer CPU {sl}")
+
+    if detail is not None and args.chunk_cache is None and args.pool_variant > 0:
+        model = cache = step = None  # release the reference-mode decoder first
+        detail["chunk_pool"] = pool_variant(args, shape, lanes)
 
     out = {
         "metric": ("decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util"

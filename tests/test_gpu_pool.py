@@ -102,25 +102,35 @@ def test_pooled_decode_matches_oracle(gpu, P, device_lengths, drift):
     assert P == S or sum(hits[layers:]) > 0  # the drifting queries do reuse chunks
 
 
-def test_pool_equal_to_budget_matches_reference_mode(gpu):
-    """P = S: the pool holds exactly the selected chunks, like the reference's slots; hit counts and
-    attention outputs agree with a cache without a pool (slot order differs, so outputs to fp32
-    summation order)."""
-    _say("pool P = S vs reference mode")
+@pytest.mark.parametrize("mult", [1, 2, 4])
+def test_pool_matches_reference_mode(gpu, mult):
+    """A pool of P = mult * S slots selects the same chunks as a cache without a pool and gives the
+    same attention outputs (to fp32 summation order: the slots are read in another order). P = S
+    holds exactly the selected chunks, like the reference's slots, so the hit counts agree too;
+    larger pools keep chunks across steps and hit at least as often."""
+    _say(f"pool P = {mult} S vs reference mode")
     case = make_golden.decode_small_case()
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
     steps, layers = 4, 2
+    S = case["dims"]["budget"] // case["dims"]["chunk"]
     caches = [build_cache(case, gpu, max_decode_len=steps, num_layers=layers, chunk_cache=P)
-              for P in (None, case["dims"]["budget"] // case["dims"]["chunk"])]
+              for P in (None, mult * S)]
+    for cch in caches:
+        cch.keep_selected = True
     attns = [ShadowAttention(cch, G, D, H * G * D, identity_rope(B, H * G, H, D), None, case["cos_sin"].to(gpu))
              for cch in caches]
     for t, row in enumerate(_queries(B, H, G, D, steps, layers, 9, 0.3)):
         for layer, (q, k, v) in enumerate(row):
-            outs, cnts = [], []
+            outs, cnts, sels = [], [], []
             for cch, attn in zip(caches, attns):
                 outs.append(attn.decode(q.to(gpu).reshape(B, 1, -1), k.to(gpu).reshape(B, 1, -1),
                                         v.to(gpu).reshape(B, H, 1, D), None, layer).cpu())
                 cnts.append(cch.cnts.cpu().numpy().copy())
-            assert np.array_equal(cnts[0], cnts[1]), (t, layer)
+                sels.append(cch.selected_chunks.cpu().clone())
+            assert torch.equal(sels[0], sels[1]), (t, layer)  # the same chunks, in top-k order
+            if mult == 1:
+                assert np.array_equal(cnts[0], cnts[1]), (t, layer)
+            else:
+                assert (cnts[1] >= cnts[0]).all(), (t, layer)
             torch.testing.assert_close(outs[0].float(), outs[1].float(), rtol=1e-2, atol=1e-2)
