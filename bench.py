@@ -59,6 +59,9 @@ def parse() -> argparse.Namespace:
                    help="after the main (reference-mode) measurement, time the same decode with a device chunk "
                         "pool of this many slots per (b, h) and layer and report it in detail.chunk_pool "
                         "(0: skip; only with the breakdown)")
+    p.add_argument("--no-act-epilogue", action="store_true",
+                   help="form SiLU-and-mul outside the gate/up projection (the down projection reading "
+                        "[gate | up], or the SiLU-and-mul kernel) instead of in its epilogue, for comparison")
     p.add_argument("--separate-hit-moves", action="store_true",
                    help="move the hits of the key and value buffers in their own launches instead of in the "
                         "selection's last launch (the same work, for comparison)")
@@ -1106,6 +1109,8 @@ def main() -> int:
     if args.separate_hit_moves:
         for lane in model.lanes:
             lane.cache.fold_hit_moves = False
+    if args.no_act_epilogue:
+        model.act_epilogue = False
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")

@@ -347,6 +347,16 @@ int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int6
 int skv_linear_silu_mul(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
                         uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream);
 
+/* The gate/up projection with the SiLU-and-mul in its epilogue: weight rows are (gate, up) pairs,
+ * row 2j the gate and row 2j + 1 the up projection of output j (the reference's gate_up_proj
+ * [gate (n/2 rows) | up (n/2 rows)] with its halves interleaved row by row), and
+ *   y[i, j] = bf16(bf16(silu(g)) * u),  g = bf16(x[i] . w[2j]),  u = bf16(x[i] . w[2j + 1]),
+ * exactly skv_linear on the reference layout followed by skv_silu_and_mul (models/llama.py:208-212,
+ * models/glm.py:190-193), without writing the [gate | up] rows. n even; y rows hold n/2 elements;
+ * m <= 16. */
+int skv_linear_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                            uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream);
+
 /* ---- f1: prefill encoder ----------------------------------------------------------------
  * Replace the chunk statistics, outlier selection and landmark compaction of prefill_kv_cache
  * (models/kvcache/shadow.py:486-519). skv_chunk_stats: for each (b, h, chunk i < chunks) of the

@@ -47,14 +47,19 @@ __device__ __forceinline__ uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
 
 // kGated: x rows hold [gate (K) | up (K)] and the multiplied row is silu(gate) * up, formed from
 // the two halves as they are loaded (the down projection reading the gate/up projection's output).
-template <int R, int MP, bool kGated>
+// kAct: the weight rows are (gate, up) pairs, row 2j the gate and row 2j + 1 the up projection of
+// output j, and the workgroup writes y[:, j] = bf16(silu(bf16(g)) * bf16(u)) for its R / 2 pairs
+// (the gate/up projection with the SiLU-and-mul in its epilogue: no [gate | up] round trip).
+template <int R, int MP, bool kGated, bool kAct = false>
 __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* __restrict__ x, int64_t xs,
                                                                const uint16_t* __restrict__ w, int64_t ws,
                                                                uint16_t* __restrict__ y, int64_t ys, int M, int N,
                                                                int K) {
   constexpr int V = R * MP;  // partial sums per lane
   static_assert(V >= 16 && V <= 64 && (V & (V - 1)) == 0, "R * MP must be 16, 32 or 64");
+  static_assert(!(kGated && kAct) && (!kAct || R % 2 == 0), "gate/up pairs need an even row count");
   __shared__ float red[kMaxWaves * 4 * V];
+  __shared__ float fin[kAct ? V : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loop control
   const int nw = blockDim.x >> 6;
@@ -150,7 +155,19 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
     float s = 0.f;
     for (int i = 0; i < nw * 4; ++i) s += red[i * V + t];
     const int r = t / MP, m = t % MP;
-    if (m < M && n0 + r < N) y[static_cast<int64_t>(m) * ys + n0 + r] = skv::f2bf(s);
+    if (kAct) fin[t] = s;
+    else if (m < M && n0 + r < N) y[static_cast<int64_t>(m) * ys + n0 + r] = skv::f2bf(s);
+  }
+  if (kAct) {
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < V / 2) {
+      const int t = threadIdx.x;
+      const int r = 2 * (t / MP), m = t % MP;  // gate row r, up row r + 1 of this workgroup
+      if (m < M && n0 + r + 1 < N) {
+        const float g = skv::bround(fin[r * MP + m]), u = skv::bround(fin[(r + 1) * MP + m]);
+        y[static_cast<int64_t>(m) * ys + (n0 + r) / 2] = skv::f2bf(skv::silu_mul(g, u));
+      }
+    }
   }
 }
 
@@ -158,7 +175,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int g_waves_override = -1;  // SKV_LINEAR_WAVES, read once
 
-template <int R, int MP, bool kGated>
+template <int R, int MP, bool kGated, bool kAct = false>
 void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16_t* y, int64_t ys, int M, int N, int K,
             hipStream_t s) {
   const int groups = (N + R - 1) / R;
@@ -170,10 +187,11 @@ void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16
   int nw = MP <= 4 ? 4 : groups <= 512 ? 4 : groups >= 8192 ? 2 : 1;
   if (g_waves_override > 0) nw = g_waves_override;
   while (nw > 1 && nw > nblk) nw /= 2;
-  hipLaunchKernelGGL((linear_kernel<R, MP, kGated>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y, ys, M, N, K);
+  hipLaunchKernelGGL((linear_kernel<R, MP, kGated, kAct>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y, ys, M,
+                     N, K);
 }
 
-template <bool kGated>
+template <bool kGated, bool kAct = false>
 int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
                 uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
   if (!x || !weight || !y) {
@@ -187,9 +205,13 @@ int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uin
     skv_set_error("%s: m=%d n=%d k=%d (1 <= m <= %d, k a multiple of 8)", what, m, n, k, kMaxRows);
     return SKV_EUNSUPPORTED;
   }
+  if (kAct && n % 2) {
+    skv_set_error("%s: n=%d weight rows do not form (gate, up) pairs", what, n);
+    return SKV_EINVAL;
+  }
   const int64_t x_need = kGated ? 2 * static_cast<int64_t>(k) : k;
   if (!aligned16(x) || !aligned16(weight) || x_stride % 8 || weight_stride % 8 || x_stride < x_need ||
-      weight_stride < k || y_stride < n) {
+      weight_stride < k || y_stride < (kAct ? n / 2 : n)) {
     skv_set_error("%s: x and weight rows must be 16-byte aligned and hold %lld and k elements", what,
                   (long long)x_need);
     return SKV_EINVAL;
@@ -201,16 +223,16 @@ int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uin
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (m == 1)
-    launch<16, 1, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<16, 1, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if (m == 2)
-    launch<8, 2, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 2, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if (m <= 4)
-    launch<8, 4, kGated>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 4, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   else if constexpr (!kGated) {
     if (m <= 8)
-      launch<8, 8, false>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+      launch<8, 8, false, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
     else
-      launch<2, 16, false>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+      launch<2, 16, false, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
   }
   return skv_check_launch(what);
 }
@@ -226,4 +248,11 @@ extern "C" int skv_linear_silu_mul(const uint16_t* x, int64_t x_stride, const ui
                                    int64_t weight_stride, uint16_t* y, int64_t y_stride, int m, int n, int k,
                                    void* stream) {
   return linear_impl<true>("linear_silu_mul", x, x_stride, weight, weight_stride, y, y_stride, m, n, k, stream);
+}
+
+extern "C" int skv_linear_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint16_t* weight,
+                                       int64_t weight_stride, uint16_t* y, int64_t y_stride, int m, int n, int k,
+                                       void* stream) {
+  return linear_impl<false, true>("linear_gate_up_silu", x, x_stride, weight, weight_stride, y, y_stride, m, n, k,
+                                  stream);
 }

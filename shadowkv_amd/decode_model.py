@@ -209,6 +209,16 @@ class SyntheticDecoder:
         # the step gains from the launch it saves (Llama-3.1-8B batch 8: 384.9 vs 381.7 tokens/s);
         # the one-lane compute chain loses (GLM-4-9B batch 4: 385.4 vs 396.5 tokens/s).
         self.gated_down = lanes > 1 and lb <= 4
+        # The gate/up projection with the SiLU-and-mul in its epilogue (interleaved gate/up weight
+        # rows; bit-identical to the two kernels, one launch and no [gate | up] round trip). Taken
+        # on one-lane chains, where the saved launch is on the critical path (GLM-4-9B batch 4:
+        # 418.5 vs 413.5 tokens/s; Llama-3-8B-1M 37.8 vs 37.7); two lanes keep the gated down
+        # projection above (Llama-3.1-8B batch 8: 383.5 vs 380.3 tokens/s, with a 2048-slot chunk
+        # pool 423.9 vs 415.7: the epilogue's extra barrier in each of the 3584 gate/up workgroups).
+        self.act_epilogue = fused and lanes == 1
+        if fused:
+            for lw in self.layers:
+                lw.gate_up_il = shadowkv.interleave_gate_up(lw.gate_up)
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
         self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
         self.graph = None
@@ -278,14 +288,19 @@ class SyntheticDecoder:
             o = self._linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
             h2, x2 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(o, lw.post_norm, s.eps, x2, residual=h, residual_out=h2)
-            gate_up = self._linear(x2, lw.gate_up)
-            if self.gated_down and b <= shadowkv.LINEAR_SILU_MUL_MAX_ROWS:  # SiLU-and-mul formed by the down projection
-                down = torch.empty(b, 1, s.hidden, dtype=self.dtype, device=self.device)
-                shadowkv.linear_silu_mul(gate_up, lw.down, down)
-            else:
+            if self.act_epilogue and b <= shadowkv.LINEAR_MAX_ROWS:  # SiLU-and-mul in the gate/up epilogue
                 act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
-                shadowkv.silu_and_mul(gate_up, act)
+                shadowkv.linear_gate_up_silu(x2, lw.gate_up_il, act)
                 down = self._linear(act, lw.down)
+            else:
+                gate_up = self._linear(x2, lw.gate_up)
+                if self.gated_down and b <= shadowkv.LINEAR_SILU_MUL_MAX_ROWS:  # SiLU-and-mul formed by the down projection
+                    down = torch.empty(b, 1, s.hidden, dtype=self.dtype, device=self.device)
+                    shadowkv.linear_silu_mul(gate_up, lw.down, down)
+                else:
+                    act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
+                    shadowkv.silu_and_mul(gate_up, act)
+                    down = self._linear(act, lw.down)
             w_next = self.layers[idx + 1].in_norm if idx + 1 < s.layers else self.norm_w
             h3, x3 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(down, w_next, s.eps, x3, residual=h2, residual_out=h3)

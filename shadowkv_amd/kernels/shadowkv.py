@@ -711,6 +711,32 @@ def linear_silu_mul(gate_up, weight, out):
               rows, n, k, _stream())
 
 
+def interleave_gate_up(weight):
+    """The reference's gate_up_proj weight [gate (f rows) | up (f rows)] with its halves interleaved
+    row by row (row 2j = gate row j, row 2j + 1 = up row j), the layout linear_gate_up_silu reads."""
+    f = weight.shape[0] // 2
+    return weight.view(2, f, weight.shape[1]).transpose(0, 1).reshape(2 * f, weight.shape[1]).contiguous()
+
+
+def linear_gate_up_silu(x, weight_il, out):
+    """out = bf16(bf16(silu(g)) * u) with g, u the bf16 gate and up projections of x, from the
+    interleaved gate/up weight (interleave_gate_up): silu_and_mul(linear(x, gate_up)) in one
+    launch, bit-identical. x [..., k] (at most 16 rows), weight_il [2f, k], out [..., f]."""
+    _dev(x, "x", torch.bfloat16)
+    _dev(weight_il, "weight", torch.bfloat16)
+    _dev(out, "out", torch.bfloat16)
+    rows, xs = _rows2d(x, "x")
+    orows, os_ = _rows2d(out, "out")
+    if weight_il.dim() != 2 or weight_il.stride(-1) != 1:
+        raise ValueError("linear_gate_up_silu: weight must be [n, k] with contiguous rows")
+    n, k = weight_il.shape
+    if n % 2 or x.shape[-1] != k or out.shape[-1] != n // 2 or orows != rows:
+        raise ValueError(f"linear_gate_up_silu: shape mismatch x {tuple(x.shape)} weight {tuple(weight_il.shape)} "
+                         f"out {tuple(out.shape)}")
+    _lib.call("skv_linear_gate_up_silu", x.data_ptr(), xs, weight_il.data_ptr(), weight_il.stride(0), out.data_ptr(),
+              os_, rows, n, k, _stream())
+
+
 def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache, append_row):
     """The new token's q and k rotated at positions[b] (bf16 per-op rounding; half-split for a
     [rows, 128] cos_sin, GLM-interleaved for [rows, 64]) and the KV append in one launch:

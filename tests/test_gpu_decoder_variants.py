@@ -33,6 +33,7 @@ def test_gated_down_projection_matches_two_kernels(gpu):
     gated = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
     plain = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
     assert gated.gated_down, "two lanes of 4 rows take the gated down projection"
+    gated.act_epilogue = plain.act_epilogue = False  # (the epilogue form comes first where it runs)
     plain.gated_down = False
     tg = tp = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(3))
     for t in range(3):
@@ -65,6 +66,29 @@ def test_folded_hit_moves_match_separate_compaction(gpu, lanes):
             assert torch.equal(a, b), t
         hits += sum(int(lane.cache.cnts.sum()) for lane in folded.lanes)
     assert hits > 0, "the steps moved no hit"
+
+
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_silu_epilogue_matches_two_kernels(gpu, lanes):
+    """The gate/up projection with SiLU-and-mul in its epilogue (interleaved weight) gives the same
+    tokens and cache state, bit for bit, as the projection followed by the SiLU-and-mul kernel."""
+    print(f"SiLU epilogue vs two kernels, batch 8 in {lanes} lane(s)", flush=True)
+    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    kw = dict(sparse_budget=2048, decode_len=8, lanes=lanes, seed=16)
+    epi = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    two = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    assert epi.act_epilogue == (lanes == 1)  # the decoder's own choice
+    epi.act_epilogue = True  # (compared at both lane counts)
+    two.act_epilogue = False
+    two.gated_down = False
+    te = tt = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(6))
+    for t in range(3):
+        te = epi.decode_step(te)
+        tt = two.decode_step(tt)
+        torch.cuda.synchronize()
+        assert torch.equal(te, tt), t
+        for a, b in zip(_state(epi), _state(two)):
+            assert torch.equal(a, b), t
 
 
 def _hidden_after_layers(dec, tok):

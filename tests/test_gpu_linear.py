@@ -95,3 +95,47 @@ def test_linear_silu_mul_rejects_more_than_four_rows(gpu):
         shadowkv.linear_silu_mul(gu, w, out)
     rc = _lib.lib().skv_linear_silu_mul(gu.data_ptr(), 2 * k, w.data_ptr(), k, out.data_ptr(), n, 5, n, k, None)
     assert rc == 2  # SKV_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("rows,f,k", [(4, 14336, 4096), (4, 13696, 4096), (1, 14336, 4096), (8, 13696, 4096),
+                                      (3, 65, 1032), (13, 100, 2048), (16, 7, 8)])
+def test_linear_gate_up_silu_equals_the_two_kernels(gpu, rows, f, k):
+    """The gate/up projection on the interleaved weight with the SiLU-and-mul in its epilogue gives,
+    bit for bit, linear on the reference's [gate | up] weight followed by silu_and_mul, at the
+    Llama-3-8B and GLM-4-9B MLP shapes and every row count the kernel takes (1, 3, 4, 8, 13, 16);
+    output counts that leave a last workgroup part-full (65, 7 gate/up pairs, which the
+    SiLU-and-mul kernel does not take) are checked against torch's SiLU of the projections."""
+    _say(f"linear_gate_up_silu rows={rows} f={f} k={k}")
+    g = torch.Generator().manual_seed(rows * 977 + f + k)
+    x = torch.randn(rows, 1, k, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(2 * f, k, generator=g) / k ** 0.5 * 3).to(torch.bfloat16).to(gpu)
+    gu = torch.empty(rows, 1, 2 * f, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear(x, w, gu)
+    w_il = shadowkv.interleave_gate_up(w)
+    assert torch.equal(w_il[0::2], w[:f]) and torch.equal(w_il[1::2], w[f:])
+    got = torch.full((rows, 1, f), 7.0, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear_gate_up_silu(x, w_il, got)
+    if f % 8 == 0:  # the SiLU-and-mul kernel takes rows of multiples of 8
+        want = torch.empty(rows, 1, f, dtype=torch.bfloat16, device=gpu)
+        shadowkv.silu_and_mul(gu, want)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), want.cpu())
+    torch.cuda.synchronize()
+    # the projections pinned against fp32 torch (one rounding step), the activation against
+    # torch's SiLU of the same bf16 projections
+    assert_bf16_close(gu.cpu(), _ref(x.cpu(), w.cpu()), floor=1e-4, what=f"gate/up projection {rows}x{f}x{k}")
+    gf, uf = gu.cpu().float()[..., :f], gu.cpu().float()[..., f:]
+    ref = (torch.nn.functional.silu(gf).to(torch.bfloat16).float() * uf).to(torch.bfloat16)
+    assert_bf16_close(got.cpu(), ref, floor=1e-3, what=f"linear_gate_up_silu {rows}x{f}x{k}")
+
+
+def test_linear_gate_up_silu_rejects_odd_rows(gpu):
+    from shadowkv_amd import _lib
+    k, n = 64, 9
+    x = torch.zeros(2, k, dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros(n, k, dtype=torch.bfloat16, device=gpu)
+    out = torch.empty(2, 8, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        shadowkv.linear_gate_up_silu(x, w, out)
+    rc = _lib.lib().skv_linear_gate_up_silu(x.data_ptr(), k, w.data_ptr(), k, out.data_ptr(), 8, 2, n, k, None)
+    assert rc == 1  # SKV_EINVAL
