@@ -78,7 +78,8 @@ def parse() -> argparse.Namespace:
                         "encoder (low-rank factors, chunk statistics, outliers, landmarks, initial selection); "
                         "pool: one layer's sparse step on drifting queries with and without a device chunk pool; "
                         "hostlink: pinned-host read rate of SDMA copies and of the value-fetch gather; "
-                        "envelope: HBM streaming rate of the scoring kernel and of a device copy by transfer size")
+                        "envelope: HBM streaming rate of the scoring kernel, a device copy and the read-only probe by "
+                             "transfer size")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -558,9 +559,11 @@ def pool_variant(args, shape, lanes) -> dict:
 
 def envelope_microbench(args) -> int:
     """HBM streaming envelope of this GPU at decode-kernel sizes: the landmark scoring kernel (a
-    pure stream of landmark rows with a little MFMA work, the bench line's roofline kernel) and
-    torch's device copy, each over a range of transfer sizes, cold (every launch reads buffers
-    that the previous ones did not touch, > 1 GiB in rotation). A least-squares fit time = t0 +
+    pure stream of landmark rows with a little MFMA work, the bench line's roofline kernel),
+    torch's device copy and the library's read-only probe (1 KB contiguous wave loads, or the
+    MFMA-operand order of the scoring and attention loads; plain or non-temporal; one or four 64 KB
+    tiles per workgroup), each over a range of transfer sizes, cold (every launch reads buffers that the
+    previous ones did not touch, > 1 GiB in rotation). A least-squares fit time = t0 +
     bytes / rate over the sizes gives the marginal streaming rate and the fixed per-launch cost,
     which together bound the HBM fraction a kernel of a given size can reach."""
     import torch
@@ -569,7 +572,11 @@ def envelope_microbench(args) -> int:
     n, m = 15304, 4
     row_bytes = n * 128 * 2 + m * 128 * 2 + m * n * 2 + m * ((n + 255) // 256) * 8
     sets = 8
-    res = {"scoring": [], "copy": []}
+    probes = (("read contiguous", "contiguous", 1, False), ("read contiguous nt", "contiguous", 1, True),
+              ("read contiguous nt, 4 tiles per workgroup", "contiguous", 4, True),
+              ("read operand order", "operand", 1, False), ("read operand order nt", "operand", 1, True),
+              ("read operand order, 4 tiles per workgroup", "operand", 4, False))
+    res = {"scoring": [], "copy": [], **{name: [] for name, *_ in probes}}
     for rows in (8, 16, 32, 48, 64, 96, 128):
         g = torch.Generator(device="cuda").manual_seed(rows)
         Ls = [torch.randn(rows, n, 128, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
@@ -589,6 +596,16 @@ def envelope_microbench(args) -> int:
         t = gpu_time_per_call(lambda i: dst[i % sets].copy_(src[i % sets]), 4 * sets)
         res["copy"].append((4 * half, t))
         del src, dst
+        # read-only probe over the same bytes (rounded down to 64 KB tiles)
+        tiles = rows * row_bytes // shadowkv.HBM_PROBE_TILE_BYTES
+        src = [torch.empty(tiles * shadowkv.HBM_PROBE_TILE_BYTES, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+        for x in src:
+            x.random_(0, 256, generator=g)
+        sink = torch.empty(tiles * 4096, dtype=torch.uint8, device="cuda")
+        for name, pattern, per_wg, nt in probes:
+            t = gpu_time_per_call(lambda i: shadowkv.hbm_read_probe(src[i % sets], per_wg, pattern, sink, nt), 4 * sets)
+            res[name].append((tiles * shadowkv.HBM_PROBE_TILE_BYTES, t))
+        del src, sink
         torch.cuda.empty_cache()
     for kind, pts in res.items():
         xs = [b for b, _ in pts]

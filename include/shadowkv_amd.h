@@ -443,6 +443,19 @@ int skv_rope_qk_append(const uint16_t* qkv, int64_t qkv_stride_b, int batch_size
                        uint16_t* k_cache, uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
                        int64_t kv_stride_s, const int64_t* append_row, int64_t buf_len, void* stream);
 
+/* ---- measurement -------------------------------------------------------------------------
+ * HBM read envelope probe. No reference counterpart: it measures what a read-only launch of a
+ * given size reaches, the ceiling the streaming kernels are read against. Reads `tiles` tiles of
+ * 64 KB from src, tiles_per_workgroup (1..64) consecutive tiles per workgroup of 256 threads, each
+ * tile's 16 loads per thread in flight together, in one of two orders: pattern 0, every wave
+ * instruction reads 1 KB of consecutive bytes; pattern 1, the tile as 256 rows of 256 bytes read
+ * 64 bytes from each of 16 rows per instruction (the order of the scoring and attention kernels'
+ * MFMA operand loads); pattern + 2, the same with non-temporal loads (global_load ... nt).
+ * Thread t of workgroup g writes the XOR of the 16-byte vectors it read to
+ * sink[g*256 + t] (16 bytes each; sink_bytes >= ceil(tiles / tiles_per_workgroup) * 4096). */
+int skv_hbm_read_probe(const void* src, int64_t tiles, int tiles_per_workgroup, int pattern, void* sink,
+                       int64_t sink_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -224,8 +224,10 @@ __device__ __forceinline__ u32x4 load16_or_zero(const void* p, bool ok) {
 }
 
 // 16-byte load with the non-temporal (streaming) hint: global_load_dwordx4 ... nt. Used for reads
-// of pinned host memory over the host link, which are read once; it keeps those long-latency
-// requests from holding cache resources that concurrent kernels' HBM traffic needs.
+// of pinned host memory over the host link, which are read once (it keeps those long-latency
+// requests from holding cache resources that concurrent kernels' HBM traffic needs), and for HBM
+// streams read whole lines per wave load (attention's V rows), which it speeds up. Reads that
+// split each 128-byte line over two loads (the MFMA operand order) stream slower with it.
 __device__ __forceinline__ u32x4 load_nt(const u32x4* p) {
   typedef uint32_t v4u __attribute__((ext_vector_type(4)));
   const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));

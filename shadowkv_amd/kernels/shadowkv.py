@@ -871,3 +871,28 @@ def gather_copy_misses_to_slots(values, v_cache_buffer, miss_ids, cnts, miss_slo
     _lib.call("skv_gather_copy_misses_to_slots", device_address(values), v_cache_buffer.data_ptr(), miss_ids.data_ptr(),
               cnts.data_ptr(), miss_slot.data_ptr(), batch_size, heads, row_stride, pool_offset, gpu_v_stride,
               map_size, pool_slots, chunk_elems, _stream())
+
+
+HBM_PROBE_TILE_BYTES = 65536
+HBM_PROBE_PATTERNS = {"contiguous": 0, "operand": 1}
+
+
+def hbm_read_probe(src, tiles_per_workgroup, pattern, sink, nontemporal=False):
+    """Read-only HBM envelope probe (no reference counterpart): reads src (a multiple of 64 KB) in
+    64 KB tiles, tiles_per_workgroup per workgroup of 256 threads, in the "contiguous" order (1 KB
+    of consecutive bytes per wave instruction) or the "operand" order (64 bytes from each of 16
+    rows of 256 bytes per instruction, as the scoring and attention kernels load MFMA operands),
+    with plain or non-temporal loads. Thread t of workgroup g writes the XOR of the 16-byte vectors
+    it read to sink[g*256 + t]."""
+    _dev(src, "src")
+    _dev(sink, "sink")
+    if not src.is_contiguous() or not sink.is_contiguous():
+        raise ValueError("hbm_read_probe: src and sink must be contiguous")
+    nbytes = src.numel() * src.element_size()
+    if nbytes % HBM_PROBE_TILE_BYTES:
+        raise ValueError(f"hbm_read_probe: src holds {nbytes} bytes, not a multiple of {HBM_PROBE_TILE_BYTES}")
+    if pattern not in HBM_PROBE_PATTERNS:
+        raise ValueError(f"hbm_read_probe: pattern must be one of {sorted(HBM_PROBE_PATTERNS)}")
+    _lib.call("skv_hbm_read_probe", src.data_ptr(), nbytes // HBM_PROBE_TILE_BYTES, tiles_per_workgroup,
+              HBM_PROBE_PATTERNS[pattern] + (2 if nontemporal else 0), sink.data_ptr(),
+              sink.numel() * sink.element_size(), _stream())
