@@ -376,6 +376,36 @@ def host_link_peak_gbps(nbytes: int = 256 << 20, reps: int = 5) -> float:
     return gbps
 
 
+def measured_peaks() -> dict:
+    """The nominal peaks (8 TB/s HBM, 2.5 PFLOP/s dense bf16 MFMA) checked on this GPU with the
+    library's probes: a read-only stream of 1 GiB (contiguous non-temporal wave loads, four 64 KB
+    tiles per workgroup, buffers rotated so reads come from HBM) and back-to-back bf16 MFMAs on
+    register operands (2048 workgroups of 4 waves, 32x32x16 instructions). Reported beside the
+    rooflines, which keep the published peaks."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    nbytes = 1 << 30
+    src = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    for x in src:
+        x.fill_(0x5a)
+    sink = torch.empty(nbytes // shadowkv.HBM_PROBE_TILE_BYTES // 4 * 4096, dtype=torch.uint8, device="cuda")
+    t = gpu_time_per_call(lambda i: shadowkv.hbm_read_probe(src[i % 2], 4, "contiguous", sink, True), 8)
+    hbm = nbytes / t / 1e9
+    del src, sink
+    wgs, iters = 2048, 1024
+    msink = torch.empty(wgs * 256, dtype=torch.float32, device="cuda")
+    flops = shadowkv.mfma_peak_probe(wgs, iters, msink)
+    t = gpu_time_per_call(lambda i: shadowkv.mfma_peak_probe(wgs, iters, msink), 8)
+    mfma = flops / t / 1e12
+    torch.cuda.empty_cache()
+    return {"hbm_read_GBps": round(hbm, 1), "hbm_frac_of_nominal": round(hbm / HBM_PEAK_GBS, 4),
+            "hbm_probe": "read-only stream of 1 GiB, contiguous non-temporal wave loads, 4 x 64 KB tiles per workgroup",
+            "mfma_bf16_TFLOPs": round(mfma, 1), "mfma_frac_of_nominal": round(mfma * 1e12 / MFMA_BF16_PEAK, 4),
+            "mfma_probe": "v_mfma_f32_32x32x16_bf16 back to back on register operands, 4 chains per wave, "
+                          "2048 workgroups of 4 waves"}
+
+
 def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> list:
     """Every kernel of the sparse step at the workload's shapes, each alone: `sweeps` passes over
     the layers of lane 0 with that layer's live state (landmarks, U/SV, buffers, host store) and the
@@ -607,6 +637,8 @@ def envelope_microbench(args) -> int:
             res[name].append((tiles * shadowkv.HBM_PROBE_TILE_BYTES, t))
         del src, sink
         torch.cuda.empty_cache()
+    peaks = measured_peaks()
+    print(json.dumps({"metric": "measured peaks", **peaks}), flush=True)
     for kind, pts in res.items():
         xs = [b for b, _ in pts]
         ys = [t for _, t in pts]
@@ -1195,6 +1227,8 @@ def main() -> int:
             for k in detail["kernels"]:
                 log(f"kernel {k['kernel'][:40]:40s} isolated {k['isolated_us']:8.2f} us "
                     f"({k['isolated_frac'] * 100:5.1f}%), in step {k['in_step_us']} us")
+        detail["measured_peaks"] = measured_peaks()
+        log(f"measured peaks {detail['measured_peaks']}")
         detail["single_layer"] = {"workload": "single-layer decode step, batch 1, 8 kv heads x 4 query heads, ctx "
                                               "8192, rank 160, budget 2048, 968 landmarks, V in pinned host memory",
                                   **single_layer_gpu_ms()}

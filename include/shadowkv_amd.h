@@ -456,6 +456,14 @@ int skv_rope_qk_append(const uint16_t* qkv, int64_t qkv_stride_b, int batch_size
 int skv_hbm_read_probe(const void* src, int64_t tiles, int tiles_per_workgroup, int pattern, void* sink,
                        int64_t sink_bytes, void* stream);
 
+/* MFMA peak probe. No reference counterpart: it measures the bf16 matrix rate the rebuild's MFMA
+ * utilisation is read against. Every wave of `workgroups` workgroups of 256 threads issues
+ * iters x 4 independent v_mfma_f32_32x32x16_bf16 on register operands (no memory traffic) and
+ * thread t of workgroup g writes one float to sink[g*256 + t] (sink_bytes >= workgroups * 1024).
+ * skv_mfma_peak_probe_flops gives the flops of one call (0 for bad arguments). */
+int skv_mfma_peak_probe(int workgroups, int iters, float* sink, int64_t sink_bytes, void* stream);
+int64_t skv_mfma_peak_probe_flops(int workgroups, int iters);
+
 #ifdef __cplusplus
 }
 #endif

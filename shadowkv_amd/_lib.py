@@ -84,6 +84,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
                _i64, _p]),
     "skv_hbm_read_probe": (_i32, [_p, _i64, _i32, _i32, _p, _i64, _p]),
+    "skv_mfma_peak_probe": (_i32, [_i32, _i32, _p, _i64, _p]),
+    "skv_mfma_peak_probe_flops": (_i64, [_i32, _i32]),
     "skv_sparse_attn_noalloc_max_bytes": (_i64, []),
     "skv_sparse_attn_decode_noalloc": (
         _i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p, _f32, _p, _i64, _i64, _p]),

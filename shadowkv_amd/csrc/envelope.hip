@@ -1,7 +1,9 @@
-// HBM read envelope probe: the read rate a launch of a given size reaches on this GPU, by access
-// order. No counterpart in the reference; it measures the ceiling the streaming kernels
-// (landmark scoring, attention, rebuild) are read against.
+// Measurement probes (no counterpart in the reference): the HBM read rate a launch of a given
+// size reaches on this GPU, by access order, the ceiling the streaming kernels (landmark scoring,
+// attention, rebuild) are read against; and the bf16 MFMA rate of back-to-back matrix
+// instructions on register operands, the ceiling of the rebuild's MFMA utilisation.
 //
+// HBM read probe:
 // Each workgroup of 256 threads (4 waves) reads `tiles_per_wg` consecutive tiles of 64 KB
 // (4096 16-byte vectors), tile after tile, with all 16 of a thread's loads of a tile issued before
 // any is used, and XORs what it read into one vector per thread, written to sink (so no load is
@@ -48,7 +50,62 @@ __global__ void __launch_bounds__(kThreads) read_probe_kernel(const u32x4* __res
   sink[static_cast<int64_t>(blockIdx.x) * kThreads + tid] = acc;
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kMfmaChains = 4;  // independent accumulators per wave (cover the instruction's latency)
+constexpr int64_t kMfmaFlops = 32 * 32 * 16 * 2;  // one v_mfma_f32_32x32x16_bf16
+
+// Every wave issues iters x kMfmaChains v_mfma_f32_32x32x16_bf16 on operands built from its lane
+// id and `seed` (no memory traffic), then writes one float per thread so that no product is dead.
+// (The 32x32 form: four named 16-float accumulators stay in place across the loop, where eight
+// 16x16x32 chains are shuffled between register tuples by the compiler; measured 2.05 vs 1.95
+// PFLOP/s on MI355X.)
+__global__ void __launch_bounds__(kThreads) mfma_probe_kernel(int iters, uint32_t seed, float* __restrict__ sink) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t wa = 0x3f803f80u ^ ((t * 2654435761u + seed) & 0x007f007fu);  // bf16 pairs near 1
+  const uint32_t wb = 0x3f803f80u ^ ((t * 2246822519u + seed) & 0x007f007fu);
+  const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4{wa, wa ^ 1u, wa ^ 2u, wa ^ 3u});
+  const bf16x8_t b = __builtin_bit_cast(bf16x8_t, u32x4{wb, wb ^ 4u, wb ^ 8u, wb ^ 12u});
+  f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int i = 0; i < iters; ++i) {
+    c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c1, 0, 0, 0);
+    c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c2, 0, 0, 0);
+    c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c3, 0, 0, 0);
+  }
+  const f32x16_t q = (c0 + c1) + (c2 + c3);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s += q[e];
+  sink[static_cast<int64_t>(blockIdx.x) * kThreads + t] = s;
+}
+
 }  // namespace
+
+extern "C" int skv_mfma_peak_probe(int workgroups, int iters, float* sink, int64_t sink_bytes, void* stream) {
+  const char* what = "mfma_peak_probe";
+  if (!sink || (reinterpret_cast<uintptr_t>(sink) & 3u)) {
+    skv_set_error("%s: null or misaligned sink", what);
+    return SKV_EINVAL;
+  }
+  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 20)) {
+    skv_set_error("%s: workgroups=%d (1..2^20) iters=%d (1..2^20)", what, workgroups, iters);
+    return SKV_EINVAL;
+  }
+  if (sink_bytes < static_cast<int64_t>(workgroups) * kThreads * 4) {
+    skv_set_error("%s: sink of %lld bytes, %lld needed", what, (long long)sink_bytes,
+                  (long long)workgroups * kThreads * 4);
+    return SKV_EINVAL;
+  }
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(workgroups), dim3(kThreads), 0, static_cast<hipStream_t>(stream), iters,
+                     static_cast<uint32_t>(iters * 31 + workgroups), sink);
+  return skv_check_launch(what);
+}
+
+extern "C" int64_t skv_mfma_peak_probe_flops(int workgroups, int iters) {
+  if (workgroups < 1 || iters < 1) return 0;
+  return static_cast<int64_t>(workgroups) * (kThreads / 64) * iters * kMfmaChains * kMfmaFlops;
+}
 
 extern "C" int skv_hbm_read_probe(const void* src, int64_t tiles, int tiles_per_workgroup, int pattern, void* sink,
                                   int64_t sink_bytes, void* stream) {

@@ -896,3 +896,13 @@ def hbm_read_probe(src, tiles_per_workgroup, pattern, sink, nontemporal=False):
     _lib.call("skv_hbm_read_probe", src.data_ptr(), nbytes // HBM_PROBE_TILE_BYTES, tiles_per_workgroup,
               HBM_PROBE_PATTERNS[pattern] + (2 if nontemporal else 0), sink.data_ptr(),
               sink.numel() * sink.element_size(), _stream())
+
+
+def mfma_peak_probe(workgroups, iters, sink):
+    """MFMA peak probe (no reference counterpart): every wave of `workgroups` 256-thread workgroups
+    issues iters x 4 independent bf16 32x32x16 MFMAs on register operands; one float per thread is
+    written to sink (float32, at least workgroups * 256). Returns the flops of the call."""
+    _dev(sink, "sink", torch.float32)
+    _need(sink, workgroups * 256, "sink")
+    _lib.call("skv_mfma_peak_probe", workgroups, iters, sink.data_ptr(), sink.numel() * 4, _stream())
+    return int(_lib.lib().skv_mfma_peak_probe_flops(workgroups, iters))

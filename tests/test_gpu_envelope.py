@@ -65,3 +65,22 @@ def test_read_probe_rejects_bad_arguments(gpu):
         shadowkv.hbm_read_probe(src, 0, "contiguous", sink)
     with pytest.raises(RuntimeError, match="sink of"):
         shadowkv.hbm_read_probe(src, 1, "contiguous", sink[:4096])
+
+
+def test_mfma_probe_flops_and_output(gpu):
+    """The MFMA peak probe writes one finite, nonzero float per thread and reports the flops of
+    its bf16 32x32x16 instructions (4 chains per wave, 4 waves per workgroup)."""
+    sink = torch.full((3 * 256 + 16,), 123.0, dtype=torch.float32, device=gpu)
+    flops = shadowkv.mfma_peak_probe(3, 5, sink)
+    torch.cuda.synchronize()
+    assert flops == 3 * 4 * 5 * 4 * 32 * 32 * 16 * 2
+    out = sink.cpu()
+    assert torch.isfinite(out[:768]).all() and (out[:768] != 0).all()
+    assert (out[768:] == 123.0).all()  # nothing past the workgroups' threads
+    with pytest.raises(RuntimeError, match="workgroups"):
+        shadowkv.mfma_peak_probe(0, 5, sink)
+    with pytest.raises(ValueError, match="are addressed"):  # the shim's bound check
+        shadowkv.mfma_peak_probe(4, 5, sink)
+    from shadowkv_amd import _lib
+    with pytest.raises(RuntimeError, match="sink of"):  # and the library's own
+        _lib.call("skv_mfma_peak_probe", 4, 5, sink.data_ptr(), sink.numel() * 4, 0)
