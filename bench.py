@@ -84,6 +84,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-breakdown", action="store_true")
+    p.add_argument("--two-stream-fetch", action="store_true",
+                   help="one-lane decoders: value fetch on the copy stream and key rebuild on the compute stream "
+                        "(the reference's arrangement) instead of one fused launch on the compute stream")
     return p.parse_args()
 
 
@@ -336,9 +339,16 @@ def breakdown(model, tok) -> dict:
     timers[sel_name].orig = select_and_snapshot
     for t in timers.values():
         t.active = True
+    # (the instrumented step times the value fetch and the key rebuild as separate calls, so
+    # one-lane decoders take the two-stream arrangement for it)
+    one_stream = [lane.cache.one_stream_fetch for lane in model.lanes]
+    for lane in model.lanes:
+        lane.cache.one_stream_fetch = False
     torch.cuda.synchronize()
     model.decode_step(tok)
     torch.cuda.synchronize()
+    for lane, v in zip(model.lanes, one_stream):
+        lane.cache.one_stream_fetch = v
     timers[sel_name].orig = orig_select
     for t in timers.values():
         t.active = False
@@ -1160,6 +1170,10 @@ def main() -> int:
             lane.cache.fold_hit_moves = False
     if args.no_act_epilogue:
         model.act_epilogue = False
+    if args.two_stream_fetch:
+        for lane in model.lanes:
+            lane.cache.one_stream_fetch = False
+    cache_one_stream = all(lane.cache.one_stream_active() for lane in model.lanes)
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")
@@ -1266,6 +1280,8 @@ def main() -> int:
                                + f"{lanes} interleaved batch lane(s), "
                                + ("hit moves in their own launches, " if args.separate_hit_moves else
                                   "hit moves in the selection launch, ")
+                               + ("value fetch and key rebuild in one launch on the compute stream, "
+                                  if cache_one_stream else "")
                                + (f"HIP graphs of {per_call} step(s)" if graph else "eager steps"),
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),

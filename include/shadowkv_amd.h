@@ -379,6 +379,27 @@ int skv_select_outliers(const float* min_cos, int rows, int chunks, int outliers
 int skv_gather_rows(const uint16_t* src, int rows, int src_rows, const int64_t* idx, int dst_rows, uint16_t* dst,
                     void* stream);
 
+/* The value fetch of the misses and the key rebuild in one launch: the work of
+ * skv_gather_copy_misses_with_offsets(values, v_cache_buffer, offsets, cnts, batch_size, heads,
+ * cpu_v_length, num_chunks*chunk_size*head_dim, gpu_v_offset, gpu_v_stride, num_chunks,
+ * chunk_size*head_dim) and of skv_rebuild_k_rope(u, ..., cache, ...) with the same cnts, whose
+ * workgroups run side by side (the first ones gather from the host link, the rest rebuild keys).
+ * Both buffers' hits must already be in place (the selection's folded hit moves,
+ * skv_select_chunks_compact with both buffers). No reference counterpart as one call: it replaces
+ * the pair at models/kvcache/shadow.py:578-593 (value fetch on copy_stream, key rebuild on the
+ * current stream) for callers that run the step on one stream, saving the two cross-stream waits
+ * around the fetch. Results are those of the two calls. */
+int skv_fetch_misses_rebuild_k_rope(const void* values, void* v_cache_buffer, const int32_t* offsets,
+                                    int64_t cpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
+                                    const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
+                                    int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b, int64_t sv_stride_h,
+                                    int64_t sv_stride_n, const int64_t* position_ids, int64_t pid_stride_b,
+                                    int64_t pid_stride_h, const int32_t* cnts, const uint16_t* cos_sin,
+                                    int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode, uint16_t* cache,
+                                    int64_t stride_cache_b, int64_t stride_cache_h, int64_t stride_cache_s,
+                                    int sparse_start, int batch_size, int heads, int num_chunks, int chunk_size,
+                                    int rank, int head_dim, void* stream);
+
 /* ---- f3: device chunk pool (a GPU cache of P >= S chunk slots per (b, h) and layer) ------
  * No reference counterpart: extends the slot reuse of reorder_keys_and_compute_offsets
  * (kernels/map.cuh:475-516, models/kvcache/shadow.py:574-593) to a cache larger than the

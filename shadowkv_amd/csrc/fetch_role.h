@@ -1,0 +1,103 @@
+// The value-fetch role: miss chunks gathered from the pinned host store (zero-copy 16-byte
+// non-temporal loads over the host link) into the GPU value buffer. Shared by gather_chunks_kernel
+// (gather_copy.hip) and by the one-launch value fetch + key rebuild (rebuild.hip), where the first
+// workgroups of the grid take this role.
+#pragma once
+
+#include <cstdlib>
+
+#include "skv_common.h"
+
+namespace skv {
+
+constexpr int kFetchUnroll = 8;        // 16-byte vectors in flight per lane
+constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch tile
+// Upper bound on fetch workgroups (environment SKV_FETCH_WGS overrides it, read once). The
+// fetch is host-link bound, and every host read in flight also slows the HBM traffic of kernels
+// running concurrently (measured: a 4096x28672 GEMM 1.9x slower beside 32 workgroups, 2.7x
+// beside 256; landmark scoring 1.1x vs 3.1x). 48 workgroups of 256 threads (1.5 MiB of
+// non-temporal loads in flight) give the fastest pipelined Llama-3-8B decode step on MI355X
+// (tokens/s at 32/40/44/48/52/56/64/96 workgroups: 354/368/375/381/376/365/344/305), and the
+// fastest GLM-4-9B one (418.5 vs 414.0 / 415.3 / 407.4 at 32 / 96 / 160).
+constexpr int kDefaultFetchWGs = 48;
+
+inline int fetch_workgroups() {
+  static const int wgs = [] {
+    const char* e = getenv("SKV_FETCH_WGS");
+    const int v = e ? atoi(e) : 0;
+    return (v >= 1 && v <= 65536) ? v : kDefaultFetchWGs;
+  }();
+  return wgs;
+}
+
+// dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where start =
+// cnts[row] (or 0 without cnts). With dst_slot, entry i goes to destination slot
+// dst_slot[row*S + i] (skipped outside [0, pool_slots)). Ids outside [0, src_chunks) are
+// skipped, so a bad id can never read past the source row.
+template <typename IdxT>
+struct FetchArgs {
+  const u32x4* src;
+  int64_t src_row_vec;
+  u32x4* dst;
+  int64_t dst_row_vec, dst_offset_vec;
+  const IdxT* ids;
+  const int32_t* cnts;
+  const int32_t* dst_slot;
+  int pool_slots;
+  int S, chunk_vec;
+  int64_t src_chunks;
+  int rows, tiles;  // tiles of kChunksPerFetchWG slots per row
+  int workgroups;   // workgroups taking this role
+};
+
+// Copies slots [i0, i1) of one row, 16-byte vectors, kFetchUnroll loads in flight per lane.
+template <typename IdxT>
+__device__ __forceinline__ void fetch_tile(const FetchArgs<IdxT>& f, int row, int i0, int i1) {
+  const int64_t total = static_cast<int64_t>(i1 - i0) * f.chunk_vec;
+  const u32x4* s = f.src + static_cast<int64_t>(row) * f.src_row_vec;
+  u32x4* d = f.dst + static_cast<int64_t>(row) * f.dst_row_vec + f.dst_offset_vec;
+  const IdxT* id = f.ids + static_cast<int64_t>(row) * f.S;
+  const int32_t* ds = f.dst_slot ? f.dst_slot + static_cast<int64_t>(row) * f.S : nullptr;
+  for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(blockDim.x) * kFetchUnroll) {
+    u32x4 r[kFetchUnroll];
+#pragma unroll
+    for (int u = 0; u < kFetchUnroll; ++u) {
+      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      if (v < total) {
+        int i = i0 + static_cast<int>(v / f.chunk_vec);
+        int e = static_cast<int>(v % f.chunk_vec);
+        int64_t c = static_cast<int64_t>(id[i]);
+        if (c >= 0 && c < f.src_chunks) r[u] = load_nt(s + c * f.chunk_vec + e);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kFetchUnroll; ++u) {
+      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
+      if (v < total) {
+        int i = i0 + static_cast<int>(v / f.chunk_vec);
+        int e = static_cast<int>(v % f.chunk_vec);
+        int64_t c = static_cast<int64_t>(id[i]);
+        const int slot = ds ? ds[i] : i;
+        if (c >= 0 && c < f.src_chunks && (!ds || (slot >= 0 && slot < f.pool_slots)))
+          d[static_cast<int64_t>(slot) * f.chunk_vec + e] = r[u];
+      }
+    }
+  }
+}
+
+// Workgroup wg of nwg: tile t of a row covers kChunksPerFetchWG consecutive slots starting at
+// start + t*kChunksPerFetchWG; the rows * tiles tiles are walked with a stride of nwg.
+template <typename IdxT>
+__device__ void fetch_role(const FetchArgs<IdxT>& f, int wg, int nwg) {
+  const int total_tiles = f.rows * f.tiles;
+  for (int tile = wg; tile < total_tiles; tile += nwg) {
+    const int row = tile / f.tiles;
+    const int t = tile - row * f.tiles;
+    const int start = f.cnts ? max(0, f.cnts[row]) : 0;
+    const int i0 = start + t * kChunksPerFetchWG;
+    if (i0 >= f.S) continue;
+    fetch_tile(f, row, i0, min(i0 + kChunksPerFetchWG, f.S));
+  }
+}
+
+}  // namespace skv

@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include "fetch_role.h"
 #include "skv_common.h"
 
 namespace {
@@ -19,24 +20,9 @@ namespace {
 using skv::u32x4;
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 8;             // 16-byte vectors in flight per lane
-constexpr int kChunksPerFetchWG = 16;  // miss chunks per fetch tile
-// Upper bound on fetch workgroups (environment SKV_FETCH_WGS overrides it, read once). The
-// fetch is host-link bound, and every host read in flight also slows the HBM traffic of kernels
-// running concurrently (measured: a 4096x28672 GEMM 1.9x slower beside 32 workgroups, 2.7x
-// beside 256; landmark scoring 1.1x vs 3.1x). 48 workgroups (1.5 MiB of non-temporal loads in
-// flight) give the fastest pipelined Llama-3-8B decode step on MI355X (tokens/s at 32/40/44/48/
-// 52/56/64/96 workgroups: 354/368/375/381/376/365/344/305).
-constexpr int kDefaultFetchWGs = 48;
-
-int fetch_workgroups() {
-  static const int wgs = [] {
-    const char* e = getenv("SKV_FETCH_WGS");
-    const int v = e ? atoi(e) : 0;
-    return (v >= 1 && v <= 65536) ? v : kDefaultFetchWGs;
-  }();
-  return wgs;
-}
+constexpr int kUnroll = 8;  // 16-byte vectors in flight per lane (hit compaction)
+using skv::fetch_workgroups;
+using skv::kChunksPerFetchWG;
 
 // In-place forward compaction of the hit chunks of one row. Offsets are strictly ascending
 // with offsets[i] >= i, so the hits whose offset equals their index form a prefix that is
@@ -114,68 +100,10 @@ void launch_compact_hits(u32x4* buf, const int32_t* offsets, const int32_t* cnts
                        row_stride_vec, row_offset_vec, S, chunk_vec);
 }
 
-// Copies slots [i0, i1) of one row, 16-byte vectors, kUnroll loads in flight per lane. With
-// dst_slot, entry i goes to destination slot dst_slot[row*S + i] (skipped outside [0, pool_slots)).
+// The miss gather over a grid of fetch workgroups (skv::fetch_role).
 template <typename IdxT>
-__device__ __forceinline__ void gather_tile(const u32x4* __restrict__ src, int64_t src_row_vec, u32x4* __restrict__ dst,
-                                            int64_t dst_row_vec, int64_t dst_offset_vec, const IdxT* __restrict__ ids,
-                                            const int32_t* __restrict__ dst_slot, int pool_slots, int row, int i0,
-                                            int i1, int S, int chunk_vec, int64_t src_chunks) {
-  const int64_t total = static_cast<int64_t>(i1 - i0) * chunk_vec;
-  const u32x4* s = src + static_cast<int64_t>(row) * src_row_vec;
-  u32x4* d = dst + static_cast<int64_t>(row) * dst_row_vec + dst_offset_vec;
-  const IdxT* id = ids + static_cast<int64_t>(row) * S;
-  const int32_t* ds = dst_slot ? dst_slot + static_cast<int64_t>(row) * S : nullptr;
-  for (int64_t v0 = 0; v0 < total; v0 += static_cast<int64_t>(blockDim.x) * kUnroll) {
-    u32x4 r[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
-      if (v < total) {
-        int i = i0 + static_cast<int>(v / chunk_vec);
-        int e = static_cast<int>(v % chunk_vec);
-        int64_t c = static_cast<int64_t>(id[i]);
-        if (c >= 0 && c < src_chunks) r[u] = skv::load_nt(s + c * chunk_vec + e);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t v = v0 + static_cast<int64_t>(u) * blockDim.x + threadIdx.x;
-      if (v < total) {
-        int i = i0 + static_cast<int>(v / chunk_vec);
-        int e = static_cast<int>(v % chunk_vec);
-        int64_t c = static_cast<int64_t>(id[i]);
-        const int slot = ds ? ds[i] : i;
-        if (c >= 0 && c < src_chunks && (!ds || (slot >= 0 && slot < pool_slots)))
-          d[static_cast<int64_t>(slot) * chunk_vec + e] = r[u];
-      }
-    }
-  }
-}
-
-// dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where
-// start = cnts[row] (or 0 without cnts). The work is rows * tiles tiles; tile t of a row covers
-// kChunksPerFetchWG consecutive slots starting at start + t*kChunksPerFetchWG; workgroups walk
-// the tiles with a grid stride. Ids outside [0, src_chunks) are skipped, so a bad id can never
-// read past the source row.
-template <typename IdxT>
-__global__ void __launch_bounds__(kThreads) gather_chunks_kernel(const u32x4* __restrict__ src, int64_t src_row_vec,
-                                                                  u32x4* __restrict__ dst, int64_t dst_row_vec,
-                                                                  int64_t dst_offset_vec, const IdxT* __restrict__ ids,
-                                                                  const int32_t* __restrict__ cnts,
-                                                                  const int32_t* __restrict__ dst_slot, int pool_slots,
-                                                                  int S, int chunk_vec, int64_t src_chunks, int rows,
-                                                                  int tiles) {
-  const int total_tiles = rows * tiles;
-  for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
-    const int row = tile / tiles;
-    const int t = tile - row * tiles;
-    const int start = cnts ? max(0, cnts[row]) : 0;
-    const int i0 = start + t * kChunksPerFetchWG;
-    if (i0 >= S) continue;
-    gather_tile(src, src_row_vec, dst, dst_row_vec, dst_offset_vec, ids, dst_slot, pool_slots, row, i0,
-                min(i0 + kChunksPerFetchWG, S), S, chunk_vec, src_chunks);
-  }
+__global__ void __launch_bounds__(kThreads) gather_chunks_kernel(skv::FetchArgs<IdxT> f) {
+  skv::fetch_role(f, blockIdx.x, gridDim.x);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -226,6 +154,27 @@ extern "C" int skv_gather_copy_d2d_with_offsets(void* keys, const int32_t* offse
 
 namespace {
 
+// The fetch role's arguments for rows of map_size slots (int32 chunk ids at `offsets`).
+void fetch_args(const void* values, void* v_cache_buffer, const int32_t* offsets, const int32_t* cnts, int rows,
+               int64_t cpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride, int map_size, int chunk_elems,
+               const int32_t* dst_slot, int pool_slots, skv::FetchArgs<int32_t>* f) {
+  f->src = static_cast<const u32x4*>(values);
+  f->src_row_vec = cpu_v_length / 8;
+  f->dst = static_cast<u32x4*>(v_cache_buffer);
+  f->dst_row_vec = gpu_v_stride / 8;
+  f->dst_offset_vec = gpu_v_offset / 8;
+  f->ids = offsets;
+  f->cnts = cnts;
+  f->dst_slot = dst_slot;
+  f->pool_slots = pool_slots;
+  f->S = map_size;
+  f->chunk_vec = chunk_elems / 8;
+  f->src_chunks = cpu_v_length / chunk_elems;
+  f->rows = rows;
+  f->tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
+  f->workgroups = std::min(rows * f->tiles, fetch_workgroups());
+}
+
 // Shared by the two value-fetch entry points: argument checks, then (compact) the in-buffer hit
 // move and the host-link gather of the misses, in that order on one stream.
 int value_fetch(const char* what, bool compact, const void* values, void* v_cache_buffer, const int32_t* offsets,
@@ -253,11 +202,10 @@ int value_fetch(const char* what, bool compact, const void* values, void* v_cach
     rc = skv_check_launch(what);
     if (rc) return rc;
   }
-  const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
-  hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0, s,
-                     static_cast<const u32x4*>(values), cpu_v_length / 8, static_cast<u32x4*>(v_cache_buffer),
-                     gpu_v_stride / 8, gpu_v_offset / 8, offsets, cnts, dst_slot, pool_slots, map_size,
-                     chunk_elems / 8, cpu_v_length / chunk_elems, rows, tiles);
+  skv::FetchArgs<int32_t> f{};
+  fetch_args(values, v_cache_buffer, offsets, cnts, rows, cpu_v_length, gpu_v_offset, gpu_v_stride, map_size,
+             chunk_elems, dst_slot, pool_slots, &f);
+  hipLaunchKernelGGL(gather_chunks_kernel<int32_t>, dim3(f.workgroups), dim3(kThreads), 0, s, f);
   return skv_check_launch(what);
 }
 
@@ -310,11 +258,20 @@ extern "C" int skv_gather_copy(const void* values, void* v_cache_buffer, const i
     return SKV_EINVAL;
   }
   const int rows = batch_size * heads;
-  const int tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
-  hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(std::min(rows * tiles, fetch_workgroups())), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(values), cpu_v_length / 8,
-                     static_cast<u32x4*>(v_cache_buffer), gpu_v_length / 8, int64_t(0), position_ids,
-                     static_cast<const int32_t*>(nullptr), static_cast<const int32_t*>(nullptr), 0, map_size,
-                     chunk_elems / 8, cpu_v_length / chunk_elems, rows, tiles);
+  skv::FetchArgs<int64_t> f{};
+  f.src = static_cast<const u32x4*>(values);
+  f.src_row_vec = cpu_v_length / 8;
+  f.dst = static_cast<u32x4*>(v_cache_buffer);
+  f.dst_row_vec = gpu_v_length / 8;
+  f.dst_offset_vec = 0;
+  f.ids = position_ids;
+  f.S = map_size;
+  f.chunk_vec = chunk_elems / 8;
+  f.src_chunks = cpu_v_length / chunk_elems;
+  f.rows = rows;
+  f.tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
+  f.workgroups = std::min(rows * f.tiles, fetch_workgroups());
+  hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(f.workgroups), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), f);
   return skv_check_launch(what);
 }

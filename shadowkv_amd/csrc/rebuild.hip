@@ -27,6 +27,9 @@
 //   * blockIdx -> (head, tile) is XCD-aware: all tiles of a head land on the same XCD
 //     (workgroups are dealt round-robin over the 8 XCDs), so SV is fetched from HBM once per
 //     head and re-read from that XCD's L2.
+#include <algorithm>
+
+#include "fetch_role.h"
 #include "rope_math.h"
 
 namespace {
@@ -97,8 +100,10 @@ struct Units {
   static constexpr int kPerLane = 16 * kPerRow / 64;
 };
 
+// The rebuild of tile workgroup `bid` (blockIdx.x of rebuild_kernel; offset by the fetch
+// workgroups in fetch_rebuild_kernel).
 template <int kMode, int KS, typename IdxT, int kNW, int kIters>
-__global__ void __launch_bounds__(kNW * 64, 2) rebuild_kernel(RebuildArgs a) {
+__device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
   using U = Units<kMode>;
   constexpr int kThreads = kNW * 64;
   constexpr int kTileRows = kNW * kIters * 32;
@@ -110,7 +115,6 @@ __global__ void __launch_bounds__(kNW * 64, 2) rebuild_kernel(RebuildArgs a) {
   int32_t* orow_lds = pos_lds + kTileRows;                                      // [kTileRows]
   uint16_t* kst = reinterpret_cast<uint16_t*>(orow_lds + kTileRows);           // [kNW][16][kStLd]
 
-  const int bid = blockIdx.x;
   const int xcd = bid % kXcds;
   const int local = bid / kXcds;
   const int head = xcd + kXcds * (local / a.tiles);
@@ -304,41 +308,90 @@ __global__ void __launch_bounds__(kNW * 64, 2) rebuild_kernel(RebuildArgs a) {
   }
 }
 
+template <int kMode, int KS, typename IdxT, int kNW, int kIters>
+__global__ void __launch_bounds__(kNW * 64, 2) rebuild_kernel(RebuildArgs a) {
+  rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, blockIdx.x);
+}
+
+// The value fetch of the misses and the key rebuild in one launch: workgroups [0, f.workgroups)
+// gather the miss chunks from the pinned host store (skv::fetch_role, host-link bound), the rest
+// rebuild the key rows (HBM bound), side by side. Both need only the selection's offsets and
+// counts, with the hits already moved in both buffers; one launch on one stream then replaces a
+// fetch on a second stream and the two cross-stream waits around it (~5 us each on MI355X).
+// f.workgroups is a multiple of 8, so rebuild tile `bid` keeps the XCD of blockIdx bid.
+template <int kMode, int KS, typename IdxT, int kNW, int kIters>
+__global__ void __launch_bounds__(kNW * 64, 2) fetch_rebuild_kernel(RebuildArgs a, skv::FetchArgs<int32_t> f) {
+  const int wg = blockIdx.x;
+  if (wg < f.workgroups) {
+    skv::fetch_role(f, wg, f.workgroups);
+    return;
+  }
+  rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, wg - f.workgroups);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int kMode, int KS, typename IdxT, int kNW, int kIters>
-void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
+// Fetch workgroups of a fused launch with kNW-wave workgroups: the in-flight loads of the
+// stand-alone fetch grid (its workgroups are 4 waves), rounded up to a multiple of 8.
+int fused_fetch_workgroups(const skv::FetchArgs<int32_t>& f, int waves) {
+  const int want = std::min(f.rows * f.tiles, skv::fetch_workgroups() * 4 / waves);
+  return (std::max(want, 1) + kXcds - 1) / kXcds * kXcds;
+}
+
+template <int kMode, int KS, typename IdxT, int kNW, int kIters, bool kFused>
+void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, const skv::FetchArgs<int32_t>* f) {
   // Ranks above 176 need more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU): raise the
   // kernel's limit once.
-  if (lds > 65536) {
-    static const hipError_t raised = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&rebuild_kernel<kMode, KS, IdxT, kNW, kIters>),
-        hipFuncAttributeMaxDynamicSharedMemorySize,
-        static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) + 2 * kMaxTileRows * sizeof(int32_t) +
-                         kMaxWaves * 16 * kStLd * sizeof(uint16_t)));
-    (void)raised;
+  const int max_lds = static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) + 2 * kMaxTileRows * sizeof(int32_t) +
+                                       kMaxWaves * 16 * kStLd * sizeof(uint16_t));
+  if constexpr (kFused && KS == 6 && kIters == 2) {
+    // Not instantiated: ranks above 160 with 256-row tiles spill beside the fetch role's
+    // registers, so launch_rebuild gives fused launches of that rank 128-row tiles.
+    (void)grid, (void)lds, (void)stream, (void)a, (void)f;
+  } else if constexpr (kFused) {
+    if (lds > 65536) {
+      static const hipError_t raised = hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&fetch_rebuild_kernel<kMode, KS, IdxT, kNW, kIters>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+      (void)raised;
+    }
+    skv::FetchArgs<int32_t> ff = *f;
+    ff.workgroups = fused_fetch_workgroups(ff, kNW);
+    hipLaunchKernelGGL((fetch_rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), dim3(grid.x + ff.workgroups),
+                       dim3(kNW * 64), lds, stream, a, ff);
+  } else {
+    (void)f;
+    if (lds > 65536) {
+      static const hipError_t raised = hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&rebuild_kernel<kMode, KS, IdxT, kNW, kIters>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+      (void)raised;
+    }
+    hipLaunchKernelGGL((rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), grid, dim3(kNW * 64), lds, stream, a);
   }
-  hipLaunchKernelGGL((rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), grid, dim3(kNW * 64), lds, stream, a);
 }
 
-template <int kMode, typename IdxT, int kNW, int kIters>
-void launch_tile(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
+template <int kMode, typename IdxT, int kNW, int kIters, bool kFused>
+void launch_tile(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
+                 const skv::FetchArgs<int32_t>* f) {
   switch (ks) {
-    case 1: launch_ks<kMode, 1, IdxT, kNW, kIters>(grid, lds, stream, a); break;
-    case 2: launch_ks<kMode, 2, IdxT, kNW, kIters>(grid, lds, stream, a); break;
-    case 3: launch_ks<kMode, 3, IdxT, kNW, kIters>(grid, lds, stream, a); break;
-    case 4: launch_ks<kMode, 4, IdxT, kNW, kIters>(grid, lds, stream, a); break;
-    case 5: launch_ks<kMode, 5, IdxT, kNW, kIters>(grid, lds, stream, a); break;
-    default: launch_ks<kMode, 6, IdxT, kNW, kIters>(grid, lds, stream, a); break;
+    case 1: launch_ks<kMode, 1, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
+    case 2: launch_ks<kMode, 2, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
+    case 3: launch_ks<kMode, 3, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
+    case 4: launch_ks<kMode, 4, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
+    case 5: launch_ks<kMode, 5, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
+    default: launch_ks<kMode, 6, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
   }
 }
 
-// tile_rows: 256 (4 waves x 2 iterations), 128 (4 x 1) or 64 (2 x 1).
-template <int kMode, typename IdxT>
-void launch_mode(int tile_rows, int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a) {
-  if (tile_rows == 256) launch_tile<kMode, IdxT, 4, 2>(ks, grid, lds, stream, a);
-  else if (tile_rows == 128) launch_tile<kMode, IdxT, 4, 1>(ks, grid, lds, stream, a);
-  else launch_tile<kMode, IdxT, 2, 1>(ks, grid, lds, stream, a);
+// tile_rows: 256 (4 waves x 2 iterations), 128 (4 x 1) or 64 (2 x 1). kFused: the launch also
+// takes the value fetch's workgroups (fetch_rebuild_kernel).
+template <int kMode, typename IdxT, bool kFused = false>
+void launch_mode(int tile_rows, int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
+                 const skv::FetchArgs<int32_t>* f = nullptr) {
+  if (tile_rows == 256) launch_tile<kMode, IdxT, 4, 2, kFused>(ks, grid, lds, stream, a, f);
+  else if (tile_rows == 128) launch_tile<kMode, IdxT, 4, 1, kFused>(ks, grid, lds, stream, a, f);
+  else launch_tile<kMode, IdxT, 2, 1, kFused>(ks, grid, lds, stream, a, f);
 }
 
 // Rows per workgroup: the largest tile that still gives the grid about 1.5 workgroups per CU
@@ -355,7 +408,8 @@ int choose_tile_rows(int BH, int rows) {
   return 64;
 }
 
-int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStream_t stream) {
+int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStream_t stream,
+                   const skv::FetchArgs<int32_t>* fetch = nullptr) {
   if (!a.u || !a.sv || !a.ids || !a.cnts || !a.out || (mode != kPlain && !a.cs)) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -388,7 +442,8 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
     return SKV_EUNSUPPORTED;
   }
   const int BH = a.B * a.H;
-  const int tile_rows = choose_tile_rows(BH, a.S * a.chunk);
+  int tile_rows = choose_tile_rows(BH, a.S * a.chunk);
+  if (fetch && tile_rows == 256 && a.rank > 160) tile_rows = 128;  // (no spill-free fused 256-row kernel there)
   const int waves = tile_rows == 64 ? 2 : 4;
   a.tiles = (a.S * a.chunk + tile_rows - 1) / tile_rows;
   const int heads_padded = (BH + kXcds - 1) / kXcds * kXcds;
@@ -396,7 +451,10 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
   const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * tile_rows * sizeof(int32_t) +
                      static_cast<size_t>(waves) * 16 * kStLd * sizeof(uint16_t);
   const int ks = (a.rank + 31) / 32;
-  if (ids64) {
+  if (fetch) {  // (the fused launch: the RoPE modes with int64 chunk ids of skv_rebuild_k_rope)
+    if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+    else launch_mode<kRopeGlm, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+  } else if (ids64) {
     if (mode == kPlain) launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a);
     else if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a);
     else launch_mode<kRopeGlm, int64_t>(tile_rows, ks, grid, lds, stream, a);
@@ -489,6 +547,83 @@ extern "C" int skv_rebuild_k_rope(const uint16_t* u, int64_t u_stride_b, int64_t
   r.chunk = chunk_size;
   r.rank = rank;
   return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, true, r, static_cast<hipStream_t>(stream));
+}
+
+// The value fetch of the misses (skv_gather_copy_misses_with_offsets) and the key rebuild
+// (skv_rebuild_k_rope) in one launch, for a selection that already moved the hits of both buffers.
+extern "C" int skv_fetch_misses_rebuild_k_rope(
+    const void* values, void* v_cache_buffer, const int32_t* offsets, int64_t cpu_v_length, int64_t gpu_v_offset,
+    int64_t gpu_v_stride, const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
+    int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b, int64_t sv_stride_h, int64_t sv_stride_n,
+    const int64_t* position_ids, int64_t pid_stride_b, int64_t pid_stride_h, const int32_t* cnts,
+    const uint16_t* cos_sin, int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode, uint16_t* cache,
+    int64_t stride_cache_b, int64_t stride_cache_h, int64_t stride_cache_s, int sparse_start, int batch_size,
+    int heads, int num_chunks, int chunk_size, int rank, int head_dim, void* stream) {
+  const char* what = "fetch_misses_rebuild_k_rope";
+  if (head_dim != kHeadDim || (rope_mode != 0 && rope_mode != 1)) {
+    skv_set_error("%s: head_dim=%d (must be 128), rope_mode=%d (0 half-split, 1 GLM)", what, head_dim, rope_mode);
+    return SKV_EUNSUPPORTED;
+  }
+  if (!values || !v_cache_buffer || !offsets || !cnts) {
+    skv_set_error("%s: null value-fetch pointer", what);
+    return SKV_EINVAL;
+  }
+  const int64_t chunk_elems = static_cast<int64_t>(chunk_size) * head_dim;
+  if (!aligned16(values) || !aligned16(v_cache_buffer) || cpu_v_length % 8 || gpu_v_offset % 8 || gpu_v_stride % 8 ||
+      cpu_v_length < chunk_elems || gpu_v_offset < 0 ||
+      gpu_v_stride < gpu_v_offset + static_cast<int64_t>(num_chunks) * chunk_elems) {
+    skv_set_error("%s: value rows must be 16-byte aligned and hold the selected region (cpu_v_length=%lld "
+                  "offset=%lld stride=%lld)", what, (long long)cpu_v_length, (long long)gpu_v_offset,
+                  (long long)gpu_v_stride);
+    return SKV_EINVAL;
+  }
+  if (batch_size <= 0 || heads <= 0 || num_chunks <= 0 || chunk_size <= 0 ||
+      static_cast<int64_t>(num_chunks) * chunk_elems > (int64_t{1} << 31)) {
+    skv_set_error("%s: invalid shape batch=%d heads=%d chunks=%d chunk=%d", what, batch_size, heads, num_chunks,
+                  chunk_size);
+    return SKV_EINVAL;
+  }
+  skv::FetchArgs<int32_t> f{};
+  f.src = static_cast<const u32x4*>(values);
+  f.src_row_vec = cpu_v_length / 8;
+  f.dst = static_cast<u32x4*>(v_cache_buffer);
+  f.dst_row_vec = gpu_v_stride / 8;
+  f.dst_offset_vec = gpu_v_offset / 8;
+  f.ids = offsets;
+  f.cnts = cnts;
+  f.S = num_chunks;
+  f.chunk_vec = static_cast<int>(chunk_elems / 8);
+  f.src_chunks = cpu_v_length / chunk_elems;
+  f.rows = batch_size * heads;
+  f.tiles = (num_chunks + skv::kChunksPerFetchWG - 1) / skv::kChunksPerFetchWG;
+  RebuildArgs r{};
+  r.u = u;
+  r.u_sb = u_stride_b;
+  r.u_sh = u_stride_h;
+  r.u_sr = u_stride_row;
+  r.u_rows = u_rows;
+  r.sv = sv;
+  r.sv_sb = sv_stride_b;
+  r.sv_sh = sv_stride_h;
+  r.sv_sn = sv_stride_n;
+  r.ids = position_ids;
+  r.id_sb = pid_stride_b;
+  r.id_sh = pid_stride_h;
+  r.cnts = cnts;
+  r.cs = cos_sin;
+  r.cs_stride = stride_cos_sin;
+  r.cs_rows = cos_sin_rows;
+  r.out = cache;
+  r.o_sb = stride_cache_b;
+  r.o_sh = stride_cache_h;
+  r.o_ss = stride_cache_s;
+  r.o_start = sparse_start;
+  r.B = batch_size;
+  r.H = heads;
+  r.S = num_chunks;
+  r.chunk = chunk_size;
+  r.rank = rank;
+  return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, true, r, static_cast<hipStream_t>(stream), &f);
 }
 
 extern "C" int skv_rebuild_k_rope_slots(const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h,

@@ -151,7 +151,8 @@ class SyntheticDecoder:
 
     def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
-                 dtype=torch.bfloat16, lanes: int = 1, fused: bool = True, chunk_cache: int | None = None):
+                 dtype=torch.bfloat16, lanes: int = 1, fused: bool = True, chunk_cache: int | None = None,
+                 one_stream_fetch: bool | None = None):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
         # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels and
         # the projections on the skinny linear kernel (libshadowkv_amd), instead of torch operations
@@ -194,6 +195,11 @@ class SyntheticDecoder:
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
                                         self.cos_sin)
             cache.use_device_lengths()
+            # One lane: the step runs on the compute stream alone, the value fetch and key rebuild
+            # as one launch after a selection that moved both buffers' hits (no cross-stream wait
+            # before or after the fetch: GLM-4-9B batch 4 and Llama-3-8B-1M, measured in DESIGN).
+            cache.one_stream_fetch = (lanes == 1 and chunk_cache is None) if one_stream_fetch is None \
+                else bool(one_stream_fetch)
             if lanes > 1:
                 # All lanes share one value-fetch stream and one key-rebuild stream (their fetches
                 # follow one another on the host link anyway); taking the key rebuild off the

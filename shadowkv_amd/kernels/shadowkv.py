@@ -327,9 +327,31 @@ def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chun
     [B, H, S] int32 their slots; entry i goes to rows sparse_start + miss_slot[i]*chunk_size + j.
     """
     B, H, S = position_ids.shape
+    _dev(position_ids, "position_ids", torch.int32 if miss_slot is not None else torch.int64)
+    slots = S if miss_slot is None else pool_slots
+    geo = _rebuild_geometry(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chunk_size, slots)
+    (u_sb, u_sh, u_sr, u_rows, sv_sb, sv_sh, sv_sn, mode, rank) = geo
+    if miss_slot is not None:
+        _dev(miss_slot, "miss_slot", torch.int32)
+        if not (position_ids.is_contiguous() and miss_slot.is_contiguous()) or miss_slot.numel() != B * H * S:
+            raise ValueError("pool miss lists must be contiguous [B, H, S]")
+        _lib.call("skv_rebuild_k_rope_slots", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh,
+                  sv_sn, position_ids.data_ptr(), miss_slot.data_ptr(), cnts.data_ptr(), cos_sin.data_ptr(),
+                  cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0), cache.stride(1),
+                  cache.stride(2), sparse_start, pool_slots, B, H, S, chunk_size, rank, 128, _stream())
+        return
+    _lib.call("skv_rebuild_k_rope", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh, sv_sn,
+              position_ids.data_ptr(), position_ids.stride(0), position_ids.stride(1), cnts.data_ptr(),
+              cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0),
+              cache.stride(1), cache.stride(2), sparse_start, B, H, S, chunk_size, rank, 128, _stream())
+
+
+def _rebuild_geometry(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chunk_size, slots):
+    """Checks of the rebuild operands and their strides: (u_sb, u_sh, u_sr, u_rows, sv_sb, sv_sh,
+    sv_sn, rope mode, rank)."""
+    B, H, S = position_ids.shape
     _dev(u, "u", torch.bfloat16)
     _dev(sv, "sv", torch.bfloat16)
-    _dev(position_ids, "position_ids", torch.int32 if miss_slot is not None else torch.int64)
     _dev(cnts, "cnts", torch.int32)
     _dev(cos_sin, "cos_sin", torch.bfloat16)
     _dev(cache, "cache", torch.bfloat16)
@@ -362,23 +384,37 @@ def rebuild_k_rope(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chun
         raise ValueError(f"Invalid cos_sin shape {tuple(cos_sin.shape)}")
     if cache.dim() != 4 or cache.shape[-1] != 128 or cache.stride(-1) != 1:
         raise ValueError("cache must be [B, H, buf_len, 128]")
-    slots = S if miss_slot is None else pool_slots
     if sparse_start + slots * chunk_size > cache.shape[2]:
         raise ValueError("sparse region exceeds the cache buffer")
     if position_ids.stride(2) != 1:
         raise ValueError("position_ids must be contiguous along the chunk axis")
     _need(cnts, B * H, "cnts")
-    if miss_slot is not None:
-        _dev(miss_slot, "miss_slot", torch.int32)
-        if not (position_ids.is_contiguous() and miss_slot.is_contiguous()) or miss_slot.numel() != B * H * S:
-            raise ValueError("pool miss lists must be contiguous [B, H, S]")
-        _lib.call("skv_rebuild_k_rope_slots", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh,
-                  sv_sn, position_ids.data_ptr(), miss_slot.data_ptr(), cnts.data_ptr(), cos_sin.data_ptr(),
-                  cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0), cache.stride(1),
-                  cache.stride(2), sparse_start, pool_slots, B, H, S, chunk_size, rank, 128, _stream())
-        return
-    _lib.call("skv_rebuild_k_rope", u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh, sv_sn,
-              position_ids.data_ptr(), position_ids.stride(0), position_ids.stride(1), cnts.data_ptr(),
+    return u_sb, u_sh, u_sr, u_rows, sv_sb, sv_sh, sv_sn, mode, rank
+
+
+def fetch_misses_rebuild_k_rope(values, v_cache_buffer, offsets, cnts, cpu_v_length, gpu_v_offset, gpu_v_stride,
+                                u, sv, position_ids, cos_sin, cache, sparse_start, chunk_size):
+    """The value fetch of the misses (gather_copy_with_offsets(..., misses_only=True)) and the key
+    rebuild (rebuild_k_rope) in one launch on the current stream, their workgroups side by side.
+    Both buffers' hits must already be in place (select_chunks with move=(v_buffer, k_buffer, ...)).
+    Same arguments and results as the two calls; the value chunk is chunk_size * 128 elements."""
+    B, H, S = position_ids.shape
+    _dev(position_ids, "position_ids", torch.int64)
+    u_sb, u_sh, u_sr, u_rows, sv_sb, sv_sh, sv_sn, mode, rank = _rebuild_geometry(
+        u, sv, position_ids, cnts, cos_sin, cache, sparse_start, chunk_size, S)
+    rows = B * H
+    chunk_elems = chunk_size * 128
+    row_stride = _host_row_stride(values, rows, cpu_v_length)
+    _need(values, (rows - 1) * row_stride + row_stride, "values")
+    if values.dtype != torch.bfloat16:
+        raise ValueError("values must be bf16")
+    _dev(v_cache_buffer, "v_cache_buffer", torch.bfloat16)
+    _need(v_cache_buffer, (rows - 1) * gpu_v_stride + gpu_v_offset + S * chunk_elems, "v_cache_buffer")
+    _dev(offsets, "offsets", torch.int32)
+    _need(offsets, rows * S, "offsets")
+    _lib.call("skv_fetch_misses_rebuild_k_rope", device_address(values), v_cache_buffer.data_ptr(), offsets.data_ptr(),
+              row_stride, gpu_v_offset, gpu_v_stride, u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb,
+              sv_sh, sv_sn, position_ids.data_ptr(), position_ids.stride(0), position_ids.stride(1), cnts.data_ptr(),
               cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0),
               cache.stride(1), cache.stride(2), sparse_start, B, H, S, chunk_size, rank, 128, _stream())
 

@@ -142,6 +142,10 @@ class ShadowKVCache_CPU(KVCacheBase):
         # layer l already moved, consumed by get_value_cache / get_key_cache.
         self.fold_hit_moves = True
         self._folded = [set() for _ in range(L)]
+        # One-stream fetch (callers that run the whole step on one stream): the selection moves
+        # both buffers' hits, and fetch_and_rebuild() issues the value fetch and the key rebuild
+        # as one launch on the current stream (no copy-stream hop before or after the fetch).
+        self.one_stream_fetch = False
 
         # value-fetch stream: the given one, else the process's shared fetch side stream
         self.copy_stream = copy_stream if copy_stream is not None else side_stream(device, "fetch")
@@ -394,14 +398,14 @@ class ShadowKVCache_CPU(KVCacheBase):
         # fold_hit_moves the same launch also moves the value buffer's hits to their new slots.
         move = None
         if self.fold_hit_moves:
-            move = (self.v_cache_buffer[layer_idx], None, self.kernel_offset, self.kernel_stride,
-                    self.chunk_size * D)
+            move = (self.v_cache_buffer[layer_idx], self.k_cache_buffer[layer_idx] if self.one_stream_active() else None,
+                    self.kernel_offset, self.kernel_stride, self.chunk_size * D)
         shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, B * H, G, n, self.k_landmark_idx[layer_idx].view(B * H, n),
                                self.select_sets, self.chunks, self.position_ids[layer_idx].view(B * H, -1), self.offsets,
                                self.cnts, out_scores=self.chunk_attn,
                                out_selected=self.selected_chunks if self.keep_selected else None,
                                workspace=self.select_workspace, move=move)
-        self._folded[layer_idx] = {"v"} if move is not None else set()
+        self._folded[layer_idx] = set() if move is None else {"v", "k"} if move[1] is not None else {"v"}
         return self.position_ids[layer_idx]
 
     def _gen_len(self, layer_idx: int) -> int:
@@ -471,6 +475,30 @@ class ShadowKVCache_CPU(KVCacheBase):
                                               self.output, self.chunk_size, self.k_cache_buffer[layer_idx],
                                               self.sparse_start, self.sparse_end, self.cnts)
         return self._live_view(self.k_cache_buffer[layer_idx], layer_idx)
+
+    def one_stream_active(self) -> bool:
+        """The decode step's value fetch and key rebuild run as one launch on the current stream
+        (one_stream_fetch, with the selection moving both buffers' hits; no chunk pool)."""
+        return self.one_stream_fetch and self.fold_hit_moves and not self.pooled
+
+    def fetch_and_rebuild(self, layer_idx: int, position_ids: torch.Tensor, cos_sin_cache: torch.Tensor):
+        """get_value_cache and get_key_cache as one launch on the current stream: the misses'
+        value chunks gathered from the host store beside the misses' key rebuild + RoPE, after a
+        selection that moved both buffers' hits (one_stream_fetch). Returns (keys, values), the
+        live views of the two buffers."""
+        if self.pooled or self._folded[layer_idx] != {"v", "k"}:
+            raise RuntimeError("fetch_and_rebuild needs a selection that moved both buffers' hits "
+                               "(one_stream_fetch, no chunk pool)")
+        self._folded[layer_idx].clear()
+        if position_ids.dtype != torch.int64:
+            position_ids = position_ids.to(torch.int64)
+        shadowkv.fetch_misses_rebuild_k_rope(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.offsets,
+                                             self.cnts, int(self.max_ctx_chunks_len * self.head_dim),
+                                             self.kernel_offset, self.kernel_stride, self.U[layer_idx],
+                                             self.SV[layer_idx], position_ids, cos_sin_cache,
+                                             self.k_cache_buffer[layer_idx], self.sparse_start, self.chunk_size)
+        return (self._live_view(self.k_cache_buffer[layer_idx], layer_idx),
+                self._live_view(self.v_cache_buffer[layer_idx], layer_idx))
 
     def H2D(self):
         gc.collect()
