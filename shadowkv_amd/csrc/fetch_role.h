@@ -30,6 +30,23 @@ inline int fetch_workgroups() {
   return wgs;
 }
 
+// Fetch workgroups (of 4 waves' worth) of a launch that also rebuilds keys (fetch_rebuild_kernel,
+// one-lane decoders, where nothing else runs beside the fetch); environment SKV_FUSED_FETCH_WGS
+// overrides it, read once. Measured on MI355X, GLM-4-9B batch 4 (128 tiles of 16 chunks, 2-wave
+// workgroups): 443 tokens/s with 128 workgroups (one tile each), 441 with 64, 428 with 96 and 414
+// with 112 (a second round of tiles for some of them); Llama-3-8B-1M (1024 tiles): 38.0-38.5 from
+// 32 to 64 four-wave workgroups, 35.3 with 24.
+constexpr int kDefaultFusedFetchWGs = 64;
+
+inline int fused_fetch_workgroups_target() {
+  static const int wgs = [] {
+    const char* e = getenv("SKV_FUSED_FETCH_WGS");
+    const int v = e ? atoi(e) : 0;
+    return (v >= 1 && v <= 65536) ? v : kDefaultFusedFetchWGs;
+  }();
+  return wgs;
+}
+
 // dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where start =
 // cnts[row] (or 0 without cnts). With dst_slot, entry i goes to destination slot
 // dst_slot[row*S + i] (skipped outside [0, pool_slots)). Ids outside [0, src_chunks) are

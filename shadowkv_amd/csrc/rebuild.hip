@@ -331,11 +331,16 @@ __global__ void __launch_bounds__(kNW * 64, 2) fetch_rebuild_kernel(RebuildArgs 
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Fetch workgroups of a fused launch with kNW-wave workgroups: the in-flight loads of the
-// stand-alone fetch grid (its workgroups are 4 waves), rounded up to a multiple of 8.
+// Fetch workgroups of a fused launch with `waves`-wave workgroups: the target in 4-wave
+// workgroups (skv::fused_fetch_workgroups_target) scaled to the workgroup size, then as few as give
+// every workgroup the same number of tiles (the launch lasts as long as its busiest fetch
+// workgroup), rounded up to a multiple of 8 for the rebuild tiles' XCD map.
 int fused_fetch_workgroups(const skv::FetchArgs<int32_t>& f, int waves) {
-  const int want = std::min(f.rows * f.tiles, skv::fetch_workgroups() * 4 / waves);
-  return (std::max(want, 1) + kXcds - 1) / kXcds * kXcds;
+  const int tiles = std::max(f.rows * f.tiles, 1);
+  const int target = std::max(1, skv::fused_fetch_workgroups_target() * 4 / waves);
+  const int per = (tiles + target - 1) / target;  // tiles per workgroup
+  const int want = (tiles + per - 1) / per;
+  return (want + kXcds - 1) / kXcds * kXcds;
 }
 
 template <int kMode, int KS, typename IdxT, int kNW, int kIters, bool kFused>
