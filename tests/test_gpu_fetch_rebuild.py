@@ -15,11 +15,13 @@ from shadowkv_amd.models.tensor_op import build_cos_sin_cache, build_glm_cos_sin
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("B,H,S,glm", [(1, 8, 256, False), (4, 8, 256, False), (8, 8, 256, False),
-                                       (4, 2, 256, True), (1, 8, 2048, False), (3, 2, 40, True)])
-def test_one_launch_equals_fetch_then_rebuild(gpu, B, H, S, glm):
-    print(f"fetch+rebuild one launch B={B} H={H} S={S} glm={glm}", flush=True)
-    c, D, R = 8, 128, 160
+@pytest.mark.parametrize("B,H,S,glm,R", [(1, 8, 256, False, 160), (4, 8, 256, False, 160), (8, 8, 256, False, 160),
+                                         (4, 2, 256, True, 160), (1, 8, 2048, False, 160), (3, 2, 40, True, 160),
+                                         (8, 8, 256, False, 192), (2, 2, 64, True, 96)])
+def test_one_launch_equals_fetch_then_rebuild(gpu, B, H, S, glm, R):
+    """(rank 192 at batch 8: the fused launch takes 128-row tiles where the rebuild alone takes 256)"""
+    print(f"fetch+rebuild one launch B={B} H={H} S={S} glm={glm} rank={R}", flush=True)
+    c, D = 8, 128
     chunks = max(4 * S, 2048)
     ctx = chunks * c
     sparse_start, buf_len = 64, 64 + S * c + 32
