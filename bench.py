@@ -1174,6 +1174,7 @@ def main() -> int:
         for lane in model.lanes:
             lane.cache.one_stream_fetch = False
     cache_one_stream = all(lane.cache.one_stream_active() for lane in model.lanes)
+    qkv_rope_epi = model.qkv_rope_epilogue
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
         f"landmarks {cache.k_landmark.shape[-2]}")
@@ -1282,6 +1283,8 @@ def main() -> int:
                                   "hit moves in the selection launch, ")
                                + ("value fetch and key rebuild in one launch on the compute stream, "
                                   if cache_one_stream else "")
+                               + ("RoPE + KV append in the QKV projection's epilogue, "
+                                  if qkv_rope_epi else "")
                                + (f"HIP graphs of {per_call} step(s)" if graph else "eager steps"),
                    "global_batch": args.batch, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "score_logits (landmark scoring)", "bound": "hbm", "achieved": round(achieved, 1),

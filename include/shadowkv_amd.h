@@ -464,6 +464,21 @@ int skv_rope_qk_append(const uint16_t* qkv, int64_t qkv_stride_b, int batch_size
                        uint16_t* k_cache, uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
                        int64_t kv_stride_s, const int64_t* append_row, int64_t buf_len, void* stream);
 
+/* The fused QKV projection (models/llama.py:192, models/glm.py:186) with skv_rope_qk_append in its
+ * epilogue: the [q | k | v] row of each of the m (<= 4) token rows x[b] (k elements) is formed
+ * against the weight and rounded to bf16, then rotated and appended exactly as skv_rope_qk_append
+ * does it (same arguments and results; the fused row itself is not written). For rope_mode 0 the
+ * weight is the projection's with each q and k head's rows interleaved as (0, 64, 1, 65, ...,
+ * 63, 127), so that both rows of a rotation pair fall in one workgroup (v rows unchanged); for
+ * rope_mode 1 (GLM: pairs (2i, 2i+1)) it is the projection's weight as is. Weight rows:
+ * (q_heads + 2*kv_heads) * 128. Bit-identical to skv_linear followed by skv_rope_qk_append. */
+int skv_linear_qkv_rope_append(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                               int m, int k, int q_heads, int kv_heads, const int64_t* positions,
+                               const uint16_t* cos_sin, int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode,
+                               uint16_t* q_out, int64_t q_out_stride_b, uint16_t* k_cache, uint16_t* v_cache,
+                               int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s,
+                               const int64_t* append_row, int64_t buf_len, void* stream);
+
 /* ---- measurement -------------------------------------------------------------------------
  * HBM read envelope probe. No reference counterpart: it measures what a read-only launch of a
  * given size reaches, the ceiling the streaming kernels are read against. Reads `tiles` tiles of

@@ -83,6 +83,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_rope_qk_append": (
         _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
                _i64, _p]),
+    "skv_linear_qkv_rope_append": (
+        _i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64,
+               _p, _i64, _p]),
     "skv_fetch_misses_rebuild_k_rope": (
         _i32, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
                _i64, _i64, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),

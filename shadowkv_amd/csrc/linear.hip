@@ -11,6 +11,16 @@
 // the next block's loads in flight while the current one is multiplied. The per-lane partial
 // sums are folded within 16-lane rows by a DPP transpose-reduce (each step halves the values a
 // lane holds), then summed across rows and waves in LDS; one rounding to bf16 at the end.
+//
+// The QKV projection with the new token's RoPE and KV append in its epilogue
+// (skv_linear_qkv_rope_append): a workgroup's 8 output rows lie in one head, and with the
+// half-split heads' q/k weight rows interleaved (dims d and d + 64 adjacent; GLM's rotation pairs
+// are adjacent already) every rotation pair of the workgroup is in it. The workgroup rounds its
+// sums to bf16, rotates them with the bf16 per-op rounding of skv_rope_qk_append and writes q to
+// q_out and k, v to the append row of the key/value buffers: bit-identical to skv_linear followed
+// by skv_rope_qk_append, one launch and the fused row's round trip fewer. The position and
+// cos/sin loads are issued before the weight stream starts.
+#include "rope_math.h"
 #include "skv_common.h"
 
 namespace {
@@ -19,6 +29,45 @@ using skv::u32x4;
 
 constexpr int kBlockK = 512;     // k elements per wave load (64 lanes x 8)
 constexpr int kMaxWaves = 8;     // workgroup size limit (2 waves per SIMD at 256 VGPRs)
+constexpr int kHeadDim = 128;
+
+enum RopeMode { kNoRope = 0, kRopeHalf = 1, kRopeGlm = 2 };
+
+// The RoPE + append epilogue's operands (skv_rope_qk_append's, for the fused row of Hq q heads,
+// Hkv k heads and Hkv v heads).
+struct RopeEpi {
+  int Hq, Hkv;
+  const int64_t* pos;  // [M] positions
+  const uint16_t* cs;
+  int64_t cs_stride, cs_rows;
+  uint16_t* q_out;
+  int64_t qo_sb;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t kv_sb, kv_sh, kv_ss;
+  const int64_t* row_dev;  // the append row
+  int64_t buf_len;
+};
+
+// Output dims of rotation pair `p` (rows 2p, 2p + 1 of a workgroup starting at row n0) and whether
+// it is rotated: half-split q/k heads hold dims (j/2, 64 + j/2) in row order j (interleaved
+// weight), v heads and GLM heads dims (j, j + 1); GLM rotates only dims below 64.
+template <int kRope>
+__device__ __forceinline__ void rope_pair_dims(const RopeEpi& re, int n1, int& head, int& d1, int& d2, int& kind,
+                                               int& ci) {
+  head = n1 / kHeadDim;
+  const int j = n1 - head * kHeadDim;  // even
+  kind = head < re.Hq ? 0 : head < re.Hq + re.Hkv ? 1 : 2;  // q, k, v
+  if (kRope == kRopeHalf && kind < 2) {
+    d1 = j / 2;
+    d2 = 64 + j / 2;
+    ci = kind < 2 ? d1 : -1;  // cos at [d1], sin at [d1 + 64]
+  } else {
+    d1 = j;
+    d2 = j + 1;
+    ci = (kRope == kRopeGlm && kind < 2 && j < 64) ? j / 2 : -1;  // cos at [j/2], sin at [j/2 + 32]
+  }
+}
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -50,16 +99,20 @@ __device__ __forceinline__ uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
 // kAct: the weight rows are (gate, up) pairs, row 2j the gate and row 2j + 1 the up projection of
 // output j, and the workgroup writes y[:, j] = bf16(silu(bf16(g)) * bf16(u)) for its R / 2 pairs
 // (the gate/up projection with the SiLU-and-mul in its epilogue: no [gate | up] round trip).
-template <int R, int MP, bool kGated, bool kAct = false>
+// kRope (kRopeHalf / kRopeGlm): the RoPE + append epilogue; y is not written.
+template <int R, int MP, bool kGated, bool kAct = false, int kRope = kNoRope>
 __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* __restrict__ x, int64_t xs,
                                                                const uint16_t* __restrict__ w, int64_t ws,
                                                                uint16_t* __restrict__ y, int64_t ys, int M, int N,
-                                                               int K) {
+                                                               int K, RopeEpi re) {
   constexpr int V = R * MP;  // partial sums per lane
   static_assert(V >= 16 && V <= 64 && (V & (V - 1)) == 0, "R * MP must be 16, 32 or 64");
   static_assert(!(kGated && kAct) && (!kAct || R % 2 == 0), "gate/up pairs need an even row count");
+  static_assert(kRope == kNoRope || (!kGated && !kAct && R % 2 == 0 && kHeadDim % R == 0),
+                "the RoPE epilogue takes whole rotation pairs of one head per workgroup");
+  constexpr bool kFin = kAct || kRope != kNoRope;
   __shared__ float red[kMaxWaves * 4 * V];
-  __shared__ float fin[kAct ? V : 1];
+  __shared__ float fin[kFin ? V : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loop control
   const int nw = blockDim.x >> 6;
@@ -113,9 +166,32 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
   // loop every prefetch is unconditional, so the compiler's wait before each multiply covers only
   // that block's loads (a conditional prefetch would make it wait for both sets).
   const int nb = wave < nblk ? (nblk - 1 - wave) / nw + 1 : 0;  // wave-uniform
+  u32x4 wa[R], xa[MP], ua[MP], wb[R], xb[MP], ub[MP];
+  // RoPE epilogue thread t < (R/2)*MP takes pair p = t / MP of token row m = t % MP: its position
+  // and append row are requested first, its cos/sin after the first weight block (so the wait for
+  // the position leaves the weight loads in flight).
+  int64_t rp_pos = -1, rp_row = -1;
+  uint16_t rp_c = 0, rp_s = 0;
+  const int et = threadIdx.x;
+  if constexpr (kRope != kNoRope) {
+    if (et < (R / 2) * MP && et % MP < M) {
+      rp_pos = re.pos[et % MP];
+      rp_row = *re.row_dev;
+    }
+  }
+  if (nb > 0) load(wave, wa, xa, ua);
+  if constexpr (kRope != kNoRope) {
+    if (et < (R / 2) * MP && et % MP < M) {
+      int head, d1, d2, kind, ci;
+      rope_pair_dims<kRope>(re, n0 + 2 * (et / MP), head, d1, d2, kind, ci);
+      if (ci >= 0 && rp_pos >= 0 && rp_pos < re.cs_rows) {
+        const uint16_t* c = re.cs + rp_pos * re.cs_stride;
+        rp_c = c[ci];
+        rp_s = c[ci + (kRope == kRopeHalf ? 64 : 32)];
+      }
+    }
+  }
   if (nb > 0) {
-    u32x4 wa[R], xa[MP], ua[MP], wb[R], xb[MP], ub[MP];
-    load(wave, wa, xa, ua);
     int b = wave, i = 1;  // set a holds block b = b_{i-1}; b_i is the next block to load
     for (; i + 1 < nb; i += 2, b += 2 * nw) {
       load(b + nw, wb, xb, ub);
@@ -155,8 +231,30 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
     float s = 0.f;
     for (int i = 0; i < nw * 4; ++i) s += red[i * V + t];
     const int r = t / MP, m = t % MP;
-    if (kAct) fin[t] = s;
+    if (kFin) fin[t] = s;
     else if (m < M && n0 + r < N) y[static_cast<int64_t>(m) * ys + n0 + r] = skv::f2bf(s);
+  }
+  if constexpr (kRope != kNoRope) {
+    __syncthreads();
+    if (et < (R / 2) * MP && et % MP < M) {
+      const int p = et / MP, m = et % MP;
+      int head, d1, d2, kind, ci;
+      rope_pair_dims<kRope>(re, n0 + 2 * p, head, d1, d2, kind, ci);
+      const uint16_t x1 = skv::f2bf(fin[(2 * p) * MP + m]), x2 = skv::f2bf(fin[(2 * p + 1) * MP + m]);
+      uint16_t y1 = x1, y2 = x2;
+      if (ci >= 0 && rp_pos >= 0 && rp_pos < re.cs_rows) skv::rope_half_split(x1, x2, rp_c, rp_s, y1, y2);
+      uint16_t* dst = nullptr;
+      if (kind == 0) {
+        dst = re.q_out + m * re.qo_sb + static_cast<int64_t>(head) * kHeadDim;
+      } else if (rp_row >= 0 && rp_row < re.buf_len) {  // beyond the buffer: nothing appended
+        const int h = kind == 1 ? head - re.Hq : head - re.Hq - re.Hkv;
+        dst = (kind == 1 ? re.k_cache : re.v_cache) + m * re.kv_sb + h * re.kv_sh + rp_row * re.kv_ss;
+      }
+      if (dst) {
+        dst[d1] = y1;
+        dst[d2] = y2;
+      }
+    }
   }
   if (kAct) {
     __syncthreads();
@@ -175,9 +273,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int g_waves_override = -1;  // SKV_LINEAR_WAVES, read once
 
-template <int R, int MP, bool kGated, bool kAct = false>
+template <int R, int MP, bool kGated, bool kAct = false, int kRope = kNoRope>
 void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16_t* y, int64_t ys, int M, int N, int K,
-            hipStream_t s) {
+            hipStream_t s, const RopeEpi& re = RopeEpi{}) {
   const int groups = (N + R - 1) / R;
   const int nblk = (K + kBlockK - 1) / kBlockK;
   // Waves per workgroup, from sweeps of the Llama-3-8B projections and lm head on MI355X with
@@ -187,8 +285,8 @@ void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16
   int nw = MP <= 4 ? 4 : groups <= 512 ? 4 : groups >= 8192 ? 2 : 1;
   if (g_waves_override > 0) nw = g_waves_override;
   while (nw > 1 && nw > nblk) nw /= 2;
-  hipLaunchKernelGGL((linear_kernel<R, MP, kGated, kAct>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y, ys, M,
-                     N, K);
+  hipLaunchKernelGGL((linear_kernel<R, MP, kGated, kAct, kRope>), dim3(groups), dim3(64 * nw), 0, s, x, xs, w, ws, y,
+                     ys, M, N, K, re);
 }
 
 template <bool kGated, bool kAct = false>
@@ -255,4 +353,51 @@ extern "C" int skv_linear_gate_up_silu(const uint16_t* x, int64_t x_stride, cons
                                        void* stream) {
   return linear_impl<false, true>("linear_gate_up_silu", x, x_stride, weight, weight_stride, y, y_stride, m, n, k,
                                   stream);
+}
+
+namespace {
+
+template <int kRope>
+void launch_qkv_rope(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, int m, int n, int k, hipStream_t s,
+                     const RopeEpi& re) {
+  if (m == 1) launch<16, 1, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
+  else if (m == 2) launch<8, 2, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
+  else launch<8, 4, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
+}
+
+}  // namespace
+
+extern "C" int skv_linear_qkv_rope_append(const uint16_t* x, int64_t x_stride, const uint16_t* weight,
+                                          int64_t weight_stride, int m, int k, int q_heads, int kv_heads,
+                                          const int64_t* positions, const uint16_t* cos_sin, int64_t stride_cos_sin,
+                                          int64_t cos_sin_rows, int rope_mode, uint16_t* q_out,
+                                          int64_t q_out_stride_b, uint16_t* k_cache, uint16_t* v_cache,
+                                          int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s,
+                                          const int64_t* append_row, int64_t buf_len, void* stream) {
+  const char* what = "linear_qkv_rope_append";
+  if (!x || !weight || !positions || !cos_sin || !q_out || !k_cache || !v_cache || !append_row) {
+    skv_set_error("%s: null pointer", what);
+    return SKV_EINVAL;
+  }
+  if (m < 1 || m > 4 || k < 8 || k % 8 || q_heads < 1 || kv_heads < 1 || (rope_mode != 0 && rope_mode != 1)) {
+    skv_set_error("%s: m=%d (1..4) k=%d (a multiple of 8) q_heads=%d kv_heads=%d rope_mode=%d", what, m, k, q_heads,
+                  kv_heads, rope_mode);
+    return SKV_EUNSUPPORTED;
+  }
+  if (!aligned16(x) || !aligned16(weight) || x_stride % 8 || weight_stride % 8 || x_stride < k || weight_stride < k) {
+    skv_set_error("%s: x and weight rows must be 16-byte aligned and hold k elements", what);
+    return SKV_EINVAL;
+  }
+  if (q_out_stride_b < static_cast<int64_t>(q_heads) * kHeadDim || kv_stride_s < kHeadDim || buf_len < 0) {
+    skv_set_error("%s: q_out rows of %lld elements (%d heads of 128 needed), key/value rows of %lld", what,
+                  (long long)q_out_stride_b, q_heads, (long long)kv_stride_s);
+    return SKV_EINVAL;
+  }
+  const int n = (q_heads + 2 * kv_heads) * kHeadDim;
+  RopeEpi re{q_heads, kv_heads, positions, cos_sin, stride_cos_sin, cos_sin_rows, q_out, q_out_stride_b, k_cache,
+             v_cache, kv_stride_b, kv_stride_h, kv_stride_s, append_row, buf_len};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rope_mode == 0) launch_qkv_rope<kRopeHalf>(x, x_stride, weight, weight_stride, m, n, k, s, re);
+  else launch_qkv_rope<kRopeGlm>(x, x_stride, weight, weight_stride, m, n, k, s, re);
+  return skv_check_launch(what);
 }

@@ -222,9 +222,14 @@ class SyntheticDecoder:
         # projection above (Llama-3.1-8B batch 8: 383.5 vs 380.3 tokens/s, with a 2048-slot chunk
         # pool 423.9 vs 415.7: the epilogue's extra barrier in each of the 3584 gate/up workgroups).
         self.act_epilogue = fused and lanes == 1
+        # The QKV projection with the new token's RoPE and KV append in its epilogue (q/k weight rows
+        # of half-split heads interleaved; bit-identical to the projection followed by the RoPE +
+        # append kernel, one launch fewer per layer): lanes of at most 4 rows.
+        self.qkv_rope_epilogue = fused and lb <= shadowkv.QKV_ROPE_MAX_ROWS
         if fused:
             for lw in self.layers:
                 lw.gate_up_il = shadowkv.interleave_gate_up(lw.gate_up)
+                lw.wqkv_rope = shadowkv.qkv_rope_weight(lw.wqkv, s.heads, s.kv_heads, s.rope == "glm")
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
         self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
         self.graph = None
@@ -269,9 +274,13 @@ class SyntheticDecoder:
         if self.fused:
             h, x = state
             b = h.shape[0]
-            qkv = self._linear(x, lw.wqkv)
             q_out = torch.empty(b, s.heads, D, dtype=self.dtype, device=self.device)
-            q = lane.cache.rope_and_append(qkv.view(b, -1), self.pos[lane.rows], self.cos_sin, idx, q_out)
+            if self.qkv_rope_epilogue and b <= shadowkv.QKV_ROPE_MAX_ROWS:
+                q = lane.cache.qkv_rope_and_append(x.view(b, -1), lw.wqkv_rope, self.pos[lane.rows], self.cos_sin,
+                                                   idx, q_out)
+            else:
+                qkv = self._linear(x, lw.wqkv)
+                q = lane.cache.rope_and_append(qkv.view(b, -1), self.pos[lane.rows], self.cos_sin, idx, q_out)
             return lane.attn.decode_begin_appended(q, idx)
         h = state
         b = h.shape[0]

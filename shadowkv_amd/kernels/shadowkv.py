@@ -808,6 +808,65 @@ def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v
               k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
               append_row.data_ptr(), k_cache.shape[2], _stream())
 
+
+def qkv_rope_weight(weight, q_heads, kv_heads, glm):
+    """The fused QKV weight [(Hq + 2 Hkv) * 128, k] in the row order linear_qkv_rope_append reads:
+    for the half-split rotation each q and k head's rows interleaved as (0, 64, 1, 65, ..., 63, 127)
+    (v rows unchanged); for GLM's interleaved pairs the weight as is."""
+    D = 128
+    if weight.shape[0] != (q_heads + 2 * kv_heads) * D:
+        raise ValueError(f"qkv_rope_weight: {weight.shape[0]} rows for {q_heads} + 2 x {kv_heads} heads")
+    if glm:
+        return weight.contiguous()
+    qk = (q_heads + kv_heads) * D
+    order = torch.arange(D, device=weight.device).view(2, D // 2).t().reshape(-1)  # 0, 64, 1, 65, ...
+    idx = (torch.arange(q_heads + kv_heads, device=weight.device)[:, None] * D + order).reshape(-1)
+    idx = torch.cat([idx, torch.arange(qk, weight.shape[0], device=weight.device)])
+    return weight.index_select(0, idx).contiguous()
+
+
+QKV_ROPE_MAX_ROWS = 4
+
+
+def linear_qkv_rope_append(x, weight_rope, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache,
+                           append_row):
+    """linear(x, wqkv) followed by rope_qk_append(...) in one launch, bit-identical, on the weight in
+    qkv_rope_weight's row order (half-split for a [rows, 128] cos_sin, GLM for [rows, 64]). x:
+    [..., k] token rows (at most 4); the other arguments as rope_qk_append's."""
+    D = 128
+    _dev(x, "x", torch.bfloat16)
+    _dev(weight_rope, "weight", torch.bfloat16)
+    _dev(q_out, "q_out", torch.bfloat16)
+    _dev(positions, "positions", torch.int64)
+    _dev(cos_sin, "cos_sin", torch.bfloat16)
+    _dev(append_row, "append_row", torch.int64)
+    B, xs = _rows2d(x, "x")
+    if weight_rope.dim() != 2 or weight_rope.stride(-1) != 1:
+        raise ValueError("linear_qkv_rope_append: weight must be [n, k] with contiguous rows")
+    n, k = weight_rope.shape
+    if n != (q_heads + 2 * kv_heads) * D or x.shape[-1] != k:
+        raise ValueError(f"linear_qkv_rope_append: shape mismatch x {tuple(x.shape)} weight {tuple(weight_rope.shape)}"
+                         f" for {q_heads} + 2 x {kv_heads} heads")
+    if B > QKV_ROPE_MAX_ROWS:
+        raise ValueError(f"linear_qkv_rope_append: {B} rows (at most {QKV_ROPE_MAX_ROWS})")
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _dev(t, nm, torch.bfloat16)
+        if t.dim() != 4 or t.shape[0] != B or t.shape[1] != kv_heads or t.shape[3] != D or t.stride(3) != 1:
+            raise ValueError(f"{nm} must be [B, Hkv, buf_len, 128]")
+    if k_cache.stride() != v_cache.stride() or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must share a layout")
+    if q_out.numel() != B * q_heads * D or not q_out.is_contiguous():
+        raise ValueError("q_out must be a contiguous [B, Hq, 128]")
+    if positions.numel() < B:
+        raise ValueError("positions too short")
+    mode = 0 if cos_sin.shape[-1] == 128 else 1 if cos_sin.shape[-1] == 64 else -1
+    if mode < 0:
+        raise ValueError(f"Invalid cos_sin shape {tuple(cos_sin.shape)}")
+    _lib.call("skv_linear_qkv_rope_append", x.data_ptr(), xs, weight_rope.data_ptr(), weight_rope.stride(0), B, k,
+              q_heads, kv_heads, positions.data_ptr(), cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode,
+              q_out.data_ptr(), q_heads * D, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+              k_cache.stride(1), k_cache.stride(2), append_row.data_ptr(), k_cache.shape[2], _stream())
+
 # ---------------------------------------------------------------------------------------------
 # f1: prefill encoder (chunk statistics, outlier selection, landmark gather)
 

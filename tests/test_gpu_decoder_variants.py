@@ -4,6 +4,8 @@
   SiLU-and-mul kernel followed by the linear kernel;
 * the hit moves folded into the selection launch give the same tokens and cache state, bit for
   bit, as the separate in-buffer compaction launches (one lane and two lanes);
+* the QKV projection with RoPE + append in its epilogue gives the same tokens and cache state, bit
+  for bit, as the projection followed by the RoPE + append kernel;
 * the fused new-token step (residual + RMSNorm, skinny linear, SiLU-and-mul, RoPE + append
   kernels) agrees with the reference call sequence on torch operations (F.rms_norm, F.linear,
   F.silu, apply_rotary_pos_emb_new + update_kv_cache) within bf16 tolerance."""
@@ -89,6 +91,39 @@ def test_silu_epilogue_matches_two_kernels(gpu, lanes):
         assert torch.equal(te, tt), t
         for a, b in zip(_state(epi), _state(two)):
             assert torch.equal(a, b), t
+
+
+@pytest.mark.parametrize("model,lanes", [("llama", 1), ("llama", 2), ("glm", 1)])
+def test_qkv_rope_epilogue_matches_two_kernels(gpu, model, lanes):
+    """The QKV projection with RoPE + append in its epilogue gives the same tokens and cache state,
+    bit for bit, as the projection followed by the RoPE + append kernel (half-split and GLM
+    rotations; one and two lanes of 4 rows), eager and in captured graphs."""
+    batch = 4 * lanes
+    print(f"QKV RoPE epilogue vs two kernels, {model} batch {batch} in {lanes} lane(s)", flush=True)
+    base = decode_model.GLM4_9B if model == "glm" else decode_model.LLAMA31_8B
+    shape = replace(base, layers=2, vocab=1000)
+    kw = dict(sparse_budget=2048, decode_len=8, lanes=lanes, seed=18)
+    epi = decode_model.SyntheticDecoder(shape, batch, 16384, **kw)
+    two = decode_model.SyntheticDecoder(shape, batch, 16384, **kw)
+    assert epi.qkv_rope_epilogue  # the decoder's own choice at 4 rows per lane
+    two.qkv_rope_epilogue = False
+    te = tt = torch.randint(0, shape.vocab, (batch, 1), device=gpu,
+                            generator=torch.Generator(device=gpu).manual_seed(8))
+    for t in range(3):
+        te = epi.decode_step(te)
+        tt = two.decode_step(tt)
+        torch.cuda.synchronize()
+        assert torch.equal(te, tt), t
+        for a, b in zip(_state(epi), _state(two)):
+            assert torch.equal(a, b), t
+    epi.capture(te)
+    two.capture(tt)
+    for t in range(2):
+        te, tt = epi.replay(), two.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(te, tt), ("replay", t)
+        for a, b in zip(_state(epi), _state(two)):
+            assert torch.equal(a, b), ("replay", t)
 
 
 def _hidden_after_layers(dec, tok):

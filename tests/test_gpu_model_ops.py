@@ -108,3 +108,80 @@ def test_rope_qk_append(gpu, glm):
                             torch.tensor([buf], device=gpu))
     torch.cuda.synchronize()
     assert torch.equal(kg.cpu(), want_k) and torch.equal(vg.cpu(), want_v)
+
+
+# (rows, q heads, kv heads, k, glm): the Llama-3 (32 / 8) and GLM-4 (32 / 2) shapes at 1-4 token
+# rows, and a small shape whose k is not a multiple of the 512-element block.
+QKV_ROPE_CASES = [(4, 32, 8, 4096, False), (1, 32, 8, 4096, False), (3, 32, 8, 4096, False),
+                  (4, 32, 2, 4096, True), (2, 32, 2, 4096, True), (3, 4, 2, 1032, False), (3, 4, 2, 1032, True)]
+
+
+@pytest.mark.parametrize("B,Hq,Hk,k,glm", QKV_ROPE_CASES)
+def test_linear_qkv_rope_append_equals_linear_then_rope(gpu, B, Hq, Hk, k, glm):
+    """The QKV projection with RoPE + append in its epilogue writes, bit for bit, what the skinny
+    linear followed by rope_qk_append writes: rotated q, the appended rotated k and raw v rows;
+    positions outside the table leave q/k unrotated, an append row outside the buffer writes no
+    key/value row."""
+    D, buf = 128, 40
+    _say(f"linear_qkv_rope_append B={B} Hq={Hq} Hk={Hk} k={k} glm={glm}")
+    g = torch.Generator().manual_seed(B * 31 + Hk + k + glm)
+    cs = oracle.build_glm_cos_sin_cache(3000, 5e6) if glm else oracle.build_cos_sin_cache(3000, 5e5)
+    n = (Hq + 2 * Hk) * D
+    x = torch.randn(B, 1, k, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5 * 2).to(torch.bfloat16).to(gpu)
+    w_rope = shadowkv.qkv_rope_weight(w, Hq, Hk, glm)
+    if glm:
+        assert torch.equal(w_rope, w)
+    else:  # rows (d, d + 64) of every q/k head adjacent, v rows in place
+        qk = (Hq + Hk) * D
+        wh, rh = w[:qk].view(Hq + Hk, 2, 64, k), w_rope[:qk].view(Hq + Hk, 64, 2, k)
+        assert torch.equal(rh[:, :, 0], wh[:, 0]) and torch.equal(rh[:, :, 1], wh[:, 1])
+        assert torch.equal(w_rope[qk:], w[qk:])
+    pos = torch.tensor([1777, 0, cs.shape[0] + 5, 2999][:B], device=gpu)  # an ordinary row, identity, beyond the table
+    row = torch.tensor([17], device=gpu)
+    kc = torch.randn(B, Hk, buf, D, generator=g).to(torch.bfloat16).to(gpu)
+    vc = torch.randn(B, Hk, buf, D, generator=g).to(torch.bfloat16).to(gpu)
+    csg = cs.to(gpu)
+    qkv = torch.empty(B, 1, n, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear(x, w, qkv)
+    q_want = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=gpu)
+    k_want, v_want = kc.clone(), vc.clone()
+    shadowkv.rope_qk_append(qkv.view(B, n), Hq, Hk, pos, csg, q_want, k_want, v_want, row)
+    q_got = torch.full((B, Hq, D), 3.0, dtype=torch.bfloat16, device=gpu)
+    k_got, v_got = kc.clone(), vc.clone()
+    shadowkv.linear_qkv_rope_append(x.view(B, k), w_rope, Hq, Hk, pos, csg, q_got, k_got, v_got, row)
+    torch.cuda.synchronize()
+    assert torch.equal(q_got.cpu(), q_want.cpu())
+    assert torch.equal(k_got.cpu(), k_want.cpu())
+    assert torch.equal(v_got.cpu(), v_want.cpu())
+    assert not torch.equal(k_got.cpu(), kc.cpu())  # the row was appended
+    # an append row outside the buffer: q written, no key/value row
+    q2 = torch.zeros_like(q_got)
+    k2, v2 = kc.clone(), vc.clone()
+    shadowkv.linear_qkv_rope_append(x.view(B, k), w_rope, Hq, Hk, pos, csg, q2, k2, v2,
+                                    torch.tensor([buf], device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(q2.cpu(), q_want.cpu())
+    assert torch.equal(k2.cpu(), kc.cpu()) and torch.equal(v2.cpu(), vc.cpu())
+
+
+def test_linear_qkv_rope_append_rejects(gpu):
+    from shadowkv_amd import _lib
+    Hq, Hk, k, D = 4, 2, 64, 128
+    n = (Hq + 2 * Hk) * D
+    w = torch.zeros(n, k, dtype=torch.bfloat16, device=gpu)
+    cs = torch.zeros(10, 128, dtype=torch.bfloat16, device=gpu)
+    row = torch.zeros(1, dtype=torch.int64, device=gpu)
+    x5 = torch.zeros(5, k, dtype=torch.bfloat16, device=gpu)
+    kc = torch.zeros(5, Hk, 4, D, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="at most 4"):
+        shadowkv.linear_qkv_rope_append(x5, w, Hq, Hk, torch.zeros(5, dtype=torch.int64, device=gpu), cs,
+                                        torch.empty(5, Hq, D, dtype=torch.bfloat16, device=gpu), kc, kc.clone(), row)
+    rc = _lib.lib().skv_linear_qkv_rope_append(x5.data_ptr(), k, w.data_ptr(), k, 5, k, Hq, Hk, row.data_ptr(),
+                                               cs.data_ptr(), 128, 10, 0, kc.data_ptr(), Hq * D, kc.data_ptr(),
+                                               kc.data_ptr(), Hk * 4 * D, 4 * D, D, row.data_ptr(), 4, None)
+    assert rc == 2  # SKV_EUNSUPPORTED
+    with pytest.raises(ValueError, match="shape mismatch"):  # weight rows for other head counts
+        shadowkv.linear_qkv_rope_append(x5[:2], w[:-128], Hq, Hk, row.repeat(2), cs,
+                                        torch.empty(2, Hq, D, dtype=torch.bfloat16, device=gpu), kc[:2],
+                                        kc[:2].clone(), row)
