@@ -338,6 +338,12 @@ int skv_silu_and_mul(const uint16_t* x, int64_t x_stride, uint16_t* out, int64_t
 int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride, uint16_t* y,
                int64_t y_stride, int m, int n, int k, void* stream);
 
+/* skv_linear with a bias: y[i, j] = bf16(sum_k x[i, k] * w[j, k] + bias[j]), the bias added to the
+ * fp32 sum before the one rounding (F.linear(x, w, b) with a bias epilogue: GLM's query_key_value
+ * projection, models/glm.py:165). bias: n bf16 values. */
+int skv_linear_bias(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                    const uint16_t* bias, uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream);
+
 /* skv_linear on the SiLU-and-mul of the gate/up projection, formed as the rows are read: x rows
  * hold [gate (k) | up (k)] (x_stride >= 2k) and the multiplied row is bf16(bf16(silu(gate)) * up)
  * as skv_silu_and_mul computes it, so the result equals skv_silu_and_mul followed by skv_linear
@@ -464,16 +470,17 @@ int skv_rope_qk_append(const uint16_t* qkv, int64_t qkv_stride_b, int batch_size
                        uint16_t* k_cache, uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
                        int64_t kv_stride_s, const int64_t* append_row, int64_t buf_len, void* stream);
 
-/* The fused QKV projection (models/llama.py:192, models/glm.py:186) with skv_rope_qk_append in its
- * epilogue: the [q | k | v] row of each of the m (<= 4) token rows x[b] (k elements) is formed
- * against the weight and rounded to bf16, then rotated and appended exactly as skv_rope_qk_append
- * does it (same arguments and results; the fused row itself is not written). For rope_mode 0 the
- * weight is the projection's with each q and k head's rows interleaved as (0, 64, 1, 65, ...,
- * 63, 127), so that both rows of a rotation pair fall in one workgroup (v rows unchanged); for
- * rope_mode 1 (GLM: pairs (2i, 2i+1)) it is the projection's weight as is. Weight rows:
- * (q_heads + 2*kv_heads) * 128. Bit-identical to skv_linear followed by skv_rope_qk_append. */
+/* The fused QKV projection (models/llama.py:192, models/glm.py:165 with its bias) with
+ * skv_rope_qk_append in its epilogue: the [q | k | v] row of each of the m (<= 4) token rows x[b]
+ * (k elements) is formed against the weight (plus bias, when not NULL, in the same row order) and
+ * rounded to bf16, then rotated and appended exactly as skv_rope_qk_append does it (same arguments
+ * and results; the fused row itself is not written). For rope_mode 0 the weight (and bias) is the
+ * projection's with each q and k head's rows interleaved as (0, 64, 1, 65, ..., 63, 127), so that
+ * both rows of a rotation pair fall in one workgroup (v rows unchanged); for rope_mode 1 (GLM:
+ * pairs (2i, 2i+1)) it is the projection's weight as is. Weight rows: (q_heads + 2*kv_heads) * 128.
+ * Bit-identical to skv_linear (skv_linear_bias) followed by skv_rope_qk_append. */
 int skv_linear_qkv_rope_append(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
-                               int m, int k, int q_heads, int kv_heads, const int64_t* positions,
+                               const uint16_t* bias, int m, int k, int q_heads, int kv_heads, const int64_t* positions,
                                const uint16_t* cos_sin, int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode,
                                uint16_t* q_out, int64_t q_out_stride_b, uint16_t* k_cache, uint16_t* v_cache,
                                int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s,

@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_linear": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p]),
     "skv_linear_silu_mul": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p]),
     "skv_linear_gate_up_silu": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p]),
+    "skv_linear_bias": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p]),
     "skv_chunk_stats": (_i32, [_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "skv_select_outliers": (_i32, [_p, _i32, _i32, _i32, _p, _p, _p]),
     "skv_gather_rows": (_i32, [_p, _i32, _i32, _p, _i32, _p, _p]),
@@ -84,8 +85,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
                _i64, _p]),
     "skv_linear_qkv_rope_append": (
-        _i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64,
-               _p, _i64, _p]),
+        _i32, [_p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64,
+               _i64, _p, _i64, _p]),
     "skv_fetch_misses_rebuild_k_rope": (
         _i32, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
                _i64, _i64, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),

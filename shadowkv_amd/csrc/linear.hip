@@ -33,9 +33,11 @@ constexpr int kHeadDim = 128;
 
 enum RopeMode { kNoRope = 0, kRopeHalf = 1, kRopeGlm = 2 };
 
-// The RoPE + append epilogue's operands (skv_rope_qk_append's, for the fused row of Hq q heads,
-// Hkv k heads and Hkv v heads).
+// Epilogue operands: an optional bias added to the fp32 sums before the one bf16 rounding (the
+// reference's F.linear(x, w, b), models/glm.py:165), and the RoPE + append epilogue's operands
+// (skv_rope_qk_append's, for the fused row of Hq q heads, Hkv k heads and Hkv v heads).
 struct RopeEpi {
+  const uint16_t* bias;  // [N] or null
   int Hq, Hkv;
   const int64_t* pos;  // [M] positions
   const uint16_t* cs;
@@ -173,6 +175,9 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
   int64_t rp_pos = -1, rp_row = -1;
   uint16_t rp_c = 0, rp_s = 0;
   const int et = threadIdx.x;
+  // The bias of the sum this thread finishes (thread t < R*MP: row t / MP), requested up front.
+  float bias_v = 0.f;
+  if (re.bias && et < V && n0 + et / MP < N) bias_v = skv::bf2f(re.bias[n0 + et / MP]);
   if constexpr (kRope != kNoRope) {
     if (et < (R / 2) * MP && et % MP < M) {
       rp_pos = re.pos[et % MP];
@@ -231,6 +236,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) linear_kernel(const uint16_t* 
     float s = 0.f;
     for (int i = 0; i < nw * 4; ++i) s += red[i * V + t];
     const int r = t / MP, m = t % MP;
+    if (re.bias) s += bias_v;  // (uniform: without a bias no add, so -0 sums stay -0)
     if (kFin) fin[t] = s;
     else if (m < M && n0 + r < N) y[static_cast<int64_t>(m) * ys + n0 + r] = skv::f2bf(s);
   }
@@ -291,7 +297,7 @@ void launch(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t ws, uint16
 
 template <bool kGated, bool kAct = false>
 int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
-                uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
+                uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream, const uint16_t* bias = nullptr) {
   if (!x || !weight || !y) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -320,17 +326,19 @@ int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uin
     g_waves_override = (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  RopeEpi re{};
+  re.bias = bias;
   if (m == 1)
-    launch<16, 1, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<16, 1, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s, re);
   else if (m == 2)
-    launch<8, 2, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 2, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s, re);
   else if (m <= 4)
-    launch<8, 4, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+    launch<8, 4, kGated, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s, re);
   else if constexpr (!kGated) {
     if (m <= 8)
-      launch<8, 8, false, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+      launch<8, 8, false, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s, re);
     else
-      launch<2, 16, false, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s);
+      launch<2, 16, false, kAct>(x, x_stride, weight, weight_stride, y, y_stride, m, n, k, s, re);
   }
   return skv_check_launch(what);
 }
@@ -340,6 +348,16 @@ int linear_impl(const char* what, const uint16_t* x, int64_t x_stride, const uin
 extern "C" int skv_linear(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
                           uint16_t* y, int64_t y_stride, int m, int n, int k, void* stream) {
   return linear_impl<false>("linear", x, x_stride, weight, weight_stride, y, y_stride, m, n, k, stream);
+}
+
+extern "C" int skv_linear_bias(const uint16_t* x, int64_t x_stride, const uint16_t* weight, int64_t weight_stride,
+                               const uint16_t* bias, uint16_t* y, int64_t y_stride, int m, int n, int k,
+                               void* stream) {
+  if (!bias) {
+    skv_set_error("linear_bias: null bias");
+    return SKV_EINVAL;
+  }
+  return linear_impl<false>("linear_bias", x, x_stride, weight, weight_stride, y, y_stride, m, n, k, stream, bias);
 }
 
 extern "C" int skv_linear_silu_mul(const uint16_t* x, int64_t x_stride, const uint16_t* weight,
@@ -368,7 +386,8 @@ void launch_qkv_rope(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t w
 }  // namespace
 
 extern "C" int skv_linear_qkv_rope_append(const uint16_t* x, int64_t x_stride, const uint16_t* weight,
-                                          int64_t weight_stride, int m, int k, int q_heads, int kv_heads,
+                                          int64_t weight_stride, const uint16_t* bias, int m, int k, int q_heads,
+                                          int kv_heads,
                                           const int64_t* positions, const uint16_t* cos_sin, int64_t stride_cos_sin,
                                           int64_t cos_sin_rows, int rope_mode, uint16_t* q_out,
                                           int64_t q_out_stride_b, uint16_t* k_cache, uint16_t* v_cache,
@@ -394,8 +413,8 @@ extern "C" int skv_linear_qkv_rope_append(const uint16_t* x, int64_t x_stride, c
     return SKV_EINVAL;
   }
   const int n = (q_heads + 2 * kv_heads) * kHeadDim;
-  RopeEpi re{q_heads, kv_heads, positions, cos_sin, stride_cos_sin, cos_sin_rows, q_out, q_out_stride_b, k_cache,
-             v_cache, kv_stride_b, kv_stride_h, kv_stride_s, append_row, buf_len};
+  RopeEpi re{bias, q_heads, kv_heads, positions, cos_sin, stride_cos_sin, cos_sin_rows, q_out, q_out_stride_b,
+             k_cache, v_cache, kv_stride_b, kv_stride_h, kv_stride_s, append_row, buf_len};
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (rope_mode == 0) launch_qkv_rope<kRopeHalf>(x, x_stride, weight, weight_stride, m, n, k, s, re);
   else launch_qkv_rope<kRopeGlm>(x, x_stride, weight, weight_stride, m, n, k, s, re);

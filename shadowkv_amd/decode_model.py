@@ -43,11 +43,12 @@ class ModelShape:
     head_dim: int = 128
     eps: float = 1e-5
     rope: str = "half"  # "half": Llama half-split; "glm": interleaved pairs on the first 64 dims
+    qkv_bias: bool = False  # GLM's query_key_value projection has a bias (models/glm.py:165)
 
 
 LLAMA31_8B = ModelShape("Llama-3.1-8B", 32, 4096, 14336, 32, 8, 128256, 500000.0)
 LLAMA3_8B_1M = ModelShape("Llama-3-8B-1M", 32, 4096, 14336, 32, 8, 128256, 3580000.0)
-GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="glm")
+GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="glm", qkv_bias=True)
 
 
 
@@ -173,6 +174,7 @@ class SyntheticDecoder:
         for _ in range(s.layers):
             self.layers.append(types.SimpleNamespace(
                 wqkv=w((s.heads + 2 * s.kv_heads) * D, s.hidden), wo=w(s.hidden, s.heads * D),
+                bqkv=w((s.heads + 2 * s.kv_heads) * D, scale=0.1) if s.qkv_bias else None,
                 gate_up=w(2 * s.ffn, s.hidden), down=w(s.hidden, s.ffn),
                 in_norm=torch.ones(s.hidden, dtype=dtype, device=device),
                 post_norm=torch.ones(s.hidden, dtype=dtype, device=device)))
@@ -230,6 +232,8 @@ class SyntheticDecoder:
             for lw in self.layers:
                 lw.gate_up_il = shadowkv.interleave_gate_up(lw.gate_up)
                 lw.wqkv_rope = shadowkv.qkv_rope_weight(lw.wqkv, s.heads, s.kv_heads, s.rope == "glm")
+                lw.bqkv_rope = None if lw.bqkv is None else \
+                    shadowkv.qkv_rope_weight(lw.bqkv, s.heads, s.kv_heads, s.rope == "glm")
         # RoPE position of the token being decoded, per sequence; advanced on the device by each step.
         self.pos = torch.full((batch,), ctx, dtype=torch.int64, device=device)
         self.graph = None
@@ -257,13 +261,13 @@ class SyntheticDecoder:
     def _norm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         return F.rms_norm(x, (x.shape[-1],), w, self.shape.eps)
 
-    def _linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """x @ w.T; fused: the library's skinny linear (weights streamed once) up to its row limit."""
+    def _linear(self, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
+        """x @ w.T (+ b); fused: the library's skinny linear (weights streamed once) up to its row limit."""
         rows = x.numel() // x.shape[-1]
         if not self.fused or rows > shadowkv.LINEAR_MAX_ROWS:
-            return F.linear(x, w)
+            return F.linear(x, w, b)
         out = torch.empty(*x.shape[:-1], w.shape[0], dtype=self.dtype, device=self.device)
-        shadowkv.linear(x, w, out)
+        shadowkv.linear(x, w, out, bias=b)
         return out
 
     def _layer_begin(self, idx: int, state, lane: _Lane):
@@ -277,15 +281,15 @@ class SyntheticDecoder:
             q_out = torch.empty(b, s.heads, D, dtype=self.dtype, device=self.device)
             if self.qkv_rope_epilogue and b <= shadowkv.QKV_ROPE_MAX_ROWS:
                 q = lane.cache.qkv_rope_and_append(x.view(b, -1), lw.wqkv_rope, self.pos[lane.rows], self.cos_sin,
-                                                   idx, q_out)
+                                                   idx, q_out, bias_rope=lw.bqkv_rope)
             else:
-                qkv = self._linear(x, lw.wqkv)
+                qkv = self._linear(x, lw.wqkv, lw.bqkv)
                 q = lane.cache.rope_and_append(qkv.view(b, -1), self.pos[lane.rows], self.cos_sin, idx, q_out)
             return lane.attn.decode_begin_appended(q, idx)
         h = state
         b = h.shape[0]
         x = self._norm(h, lw.in_norm)
-        qkv = F.linear(x, lw.wqkv)
+        qkv = F.linear(x, lw.wqkv, lw.bqkv)
         q, k, v = qkv.split([s.heads * D, s.kv_heads * D, s.kv_heads * D], dim=-1)
         v = v.view(b, 1, s.kv_heads, D).transpose(1, 2)
         return lane.attn.decode_begin(q, k, v, self.pos[lane.rows], idx)

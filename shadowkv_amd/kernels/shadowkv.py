@@ -705,9 +705,10 @@ def silu_and_mul(x, out):
 LINEAR_MAX_ROWS = 16
 
 
-def linear(x, weight, out):
-    """out = bf16(x @ weight.T) in fp32 for decode-sized x (at most 16 rows of [..., k]); weight
-    [n, k] with contiguous rows. The HBM-bound skinny form of F.linear (weights read once)."""
+def linear(x, weight, out, bias=None):
+    """out = bf16(x @ weight.T [+ bias]) in fp32 (one rounding) for decode-sized x (at most 16 rows of
+    [..., k]); weight [n, k] with contiguous rows, bias [n]. The HBM-bound skinny form of F.linear
+    (weights read once)."""
     _dev(x, "x", torch.bfloat16)
     _dev(weight, "weight", torch.bfloat16)
     _dev(out, "out", torch.bfloat16)
@@ -718,8 +719,15 @@ def linear(x, weight, out):
     n, k = weight.shape
     if x.shape[-1] != k or out.shape[-1] != n or orows != rows:
         raise ValueError(f"linear: shape mismatch x {tuple(x.shape)} weight {tuple(weight.shape)} out {tuple(out.shape)}")
-    _lib.call("skv_linear", x.data_ptr(), xs, weight.data_ptr(), weight.stride(0), out.data_ptr(), os_, rows, n, k,
-              _stream())
+    if bias is None:
+        _lib.call("skv_linear", x.data_ptr(), xs, weight.data_ptr(), weight.stride(0), out.data_ptr(), os_, rows, n, k,
+                  _stream())
+        return
+    _dev(bias, "bias", torch.bfloat16)
+    if bias.numel() != n or not bias.is_contiguous():
+        raise ValueError(f"linear: bias must be a contiguous [{n}]")
+    _lib.call("skv_linear_bias", x.data_ptr(), xs, weight.data_ptr(), weight.stride(0), bias.data_ptr(), out.data_ptr(),
+              os_, rows, n, k, _stream())
 
 
 LINEAR_SILU_MUL_MAX_ROWS = 4
@@ -810,9 +818,10 @@ def rope_qk_append(qkv, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v
 
 
 def qkv_rope_weight(weight, q_heads, kv_heads, glm):
-    """The fused QKV weight [(Hq + 2 Hkv) * 128, k] in the row order linear_qkv_rope_append reads:
-    for the half-split rotation each q and k head's rows interleaved as (0, 64, 1, 65, ..., 63, 127)
-    (v rows unchanged); for GLM's interleaved pairs the weight as is."""
+    """The fused QKV weight [(Hq + 2 Hkv) * 128, k] (or its bias [(Hq + 2 Hkv) * 128]) in the row
+    order linear_qkv_rope_append reads: for the half-split rotation each q and k head's rows
+    interleaved as (0, 64, 1, 65, ..., 63, 127) (v rows unchanged); for GLM's interleaved pairs the
+    weight as is."""
     D = 128
     if weight.shape[0] != (q_heads + 2 * kv_heads) * D:
         raise ValueError(f"qkv_rope_weight: {weight.shape[0]} rows for {q_heads} + 2 x {kv_heads} heads")
@@ -829,10 +838,10 @@ QKV_ROPE_MAX_ROWS = 4
 
 
 def linear_qkv_rope_append(x, weight_rope, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache,
-                           append_row):
-    """linear(x, wqkv) followed by rope_qk_append(...) in one launch, bit-identical, on the weight in
-    qkv_rope_weight's row order (half-split for a [rows, 128] cos_sin, GLM for [rows, 64]). x:
-    [..., k] token rows (at most 4); the other arguments as rope_qk_append's."""
+                           append_row, bias_rope=None):
+    """linear(x, wqkv[, bias]) followed by rope_qk_append(...) in one launch, bit-identical, on the
+    weight (and bias) in qkv_rope_weight's row order (half-split for a [rows, 128] cos_sin, GLM for
+    [rows, 64]). x: [..., k] token rows (at most 4); the other arguments as rope_qk_append's."""
     D = 128
     _dev(x, "x", torch.bfloat16)
     _dev(weight_rope, "weight", torch.bfloat16)
@@ -862,7 +871,13 @@ def linear_qkv_rope_append(x, weight_rope, q_heads, kv_heads, positions, cos_sin
     mode = 0 if cos_sin.shape[-1] == 128 else 1 if cos_sin.shape[-1] == 64 else -1
     if mode < 0:
         raise ValueError(f"Invalid cos_sin shape {tuple(cos_sin.shape)}")
-    _lib.call("skv_linear_qkv_rope_append", x.data_ptr(), xs, weight_rope.data_ptr(), weight_rope.stride(0), B, k,
+    bp = None
+    if bias_rope is not None:
+        _dev(bias_rope, "bias", torch.bfloat16)
+        if bias_rope.numel() != n or not bias_rope.is_contiguous():
+            raise ValueError(f"linear_qkv_rope_append: bias must be a contiguous [{n}]")
+        bp = bias_rope.data_ptr()
+    _lib.call("skv_linear_qkv_rope_append", x.data_ptr(), xs, weight_rope.data_ptr(), weight_rope.stride(0), bp, B, k,
               q_heads, kv_heads, positions.data_ptr(), cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode,
               q_out.data_ptr(), q_heads * D, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
               k_cache.stride(1), k_cache.stride(2), append_row.data_ptr(), k_cache.shape[2], _stream())

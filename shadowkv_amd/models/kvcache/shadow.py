@@ -558,10 +558,11 @@ class ShadowKVCache_CPU(KVCacheBase):
         return q_out.view(q_out.shape[0], self.num_attention_heads, 1, self.head_dim)
 
     def qkv_rope_and_append(self, x: torch.Tensor, wqkv_rope: torch.Tensor, position_ids: torch.Tensor,
-                            cos_sin: torch.Tensor, layer_idx: int, q_out: torch.Tensor) -> torch.Tensor:
-        """rope_and_append() with the QKV projection of the token rows x [B, hidden] in the same
-        launch (shadowkv.linear_qkv_rope_append, the weight in qkv_rope_weight's row order): the
-        fused projection row is never written. Returns q_out viewed [B, Hq, 1, 128]."""
+                            cos_sin: torch.Tensor, layer_idx: int, q_out: torch.Tensor,
+                            bias_rope: torch.Tensor | None = None) -> torch.Tensor:
+        """rope_and_append() with the QKV projection of the token rows x [B, hidden] (and its bias) in
+        the same launch (shadowkv.linear_qkv_rope_append, weight and bias in qkv_rope_weight's row
+        order): the fused projection row is never written. Returns q_out viewed [B, Hq, 1, 128]."""
         if self.append_row_dev is None:
             raise RuntimeError("qkv_rope_and_append needs use_device_lengths()")
         self.check_capacity(1)
@@ -570,7 +571,7 @@ class ShadowKVCache_CPU(KVCacheBase):
             self.kv_len_dev.add_(1)
         shadowkv.linear_qkv_rope_append(x, wqkv_rope, self.num_attention_heads, self.num_key_value_heads,
                                         position_ids, cos_sin, q_out, self.k_cache_buffer[layer_idx],
-                                        self.v_cache_buffer[layer_idx], self.append_row_dev)
+                                        self.v_cache_buffer[layer_idx], self.append_row_dev, bias_rope)
         if layer_idx == self.num_layers - 1:
             self.advance(1)
         return q_out.view(q_out.shape[0], self.num_attention_heads, 1, self.head_dim)

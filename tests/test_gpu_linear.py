@@ -36,6 +36,30 @@ def test_linear(gpu, rows, n, k):
     assert_bf16_close(out.cpu(), _ref(x, w), floor=1e-4, what=f"linear {rows}x{n}x{k}")
 
 
+@pytest.mark.parametrize("rows,n,k", [(4, 4608, 4096), (1, 4608, 4096), (3, 77, 4096), (16, 96, 4104)])
+def test_linear_bias(gpu, rows, n, k):
+    """The projection with a bias (GLM's query_key_value, models/glm.py:165): the bias added to the
+    fp32 sum before the one rounding, against fp32 torch; without a bias the call is skv_linear's."""
+    _say(f"linear bias rows={rows} n={n} k={k}")
+    g = torch.Generator().manual_seed(rows * 17 + n + k)
+    x = torch.randn(rows, 1, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(n, generator=g) * 2).to(torch.bfloat16)
+    out = torch.full((rows, 1, n), 7.0, dtype=torch.bfloat16, device=gpu)
+    shadowkv.linear(x.to(gpu), w.to(gpu), out, bias=b.to(gpu))
+    plain = torch.empty_like(out)
+    shadowkv.linear(x.to(gpu), w.to(gpu), plain)
+    torch.cuda.synchronize()
+    want = (x.float() @ w.float().t() + b.float()).to(torch.bfloat16)
+    assert_bf16_close(out.cpu(), want, floor=1e-3, what=f"linear bias {rows}x{n}x{k}")
+    # the same sums: the biased output is the unbiased fp32 sum plus the bias, rounded once, so it
+    # is within one bf16 step of the rounded plain output plus the bias
+    near = (plain.cpu().float() + b.float()).to(torch.bfloat16)
+    assert ((out.cpu().float() - near.float()).abs() <= near.float().abs() * 2 ** -7 + 1e-2).all()
+    with pytest.raises(ValueError, match="bias"):
+        shadowkv.linear(x.to(gpu), w.to(gpu), out, bias=b[:-1].to(gpu))
+
+
 def test_linear_strided_views(gpu):
     """Rows taken from wider buffers (x a column slice, out a slice of a fused output), as the
     decode step passes views of its fused projections."""

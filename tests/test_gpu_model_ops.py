@@ -112,24 +112,31 @@ def test_rope_qk_append(gpu, glm):
 
 # (rows, q heads, kv heads, k, glm): the Llama-3 (32 / 8) and GLM-4 (32 / 2) shapes at 1-4 token
 # rows, and a small shape whose k is not a multiple of the 512-element block.
-QKV_ROPE_CASES = [(4, 32, 8, 4096, False), (1, 32, 8, 4096, False), (3, 32, 8, 4096, False),
-                  (4, 32, 2, 4096, True), (2, 32, 2, 4096, True), (3, 4, 2, 1032, False), (3, 4, 2, 1032, True)]
+# GLM's projection with its bias (models/glm.py:165), the half-split one with and without.
+QKV_ROPE_CASES = [(4, 32, 8, 4096, False, False), (1, 32, 8, 4096, False, True), (3, 32, 8, 4096, False, False),
+                  (4, 32, 2, 4096, True, True), (2, 32, 2, 4096, True, True), (3, 4, 2, 1032, False, True),
+                  (3, 4, 2, 1032, True, False)]
 
 
-@pytest.mark.parametrize("B,Hq,Hk,k,glm", QKV_ROPE_CASES)
-def test_linear_qkv_rope_append_equals_linear_then_rope(gpu, B, Hq, Hk, k, glm):
+@pytest.mark.parametrize("B,Hq,Hk,k,glm,bias", QKV_ROPE_CASES)
+def test_linear_qkv_rope_append_equals_linear_then_rope(gpu, B, Hq, Hk, k, glm, bias):
     """The QKV projection with RoPE + append in its epilogue writes, bit for bit, what the skinny
-    linear followed by rope_qk_append writes: rotated q, the appended rotated k and raw v rows;
-    positions outside the table leave q/k unrotated, an append row outside the buffer writes no
-    key/value row."""
+    linear (with the bias) followed by rope_qk_append writes: rotated q, the appended rotated k and
+    raw v rows; positions outside the table leave q/k unrotated, an append row outside the buffer
+    writes no key/value row."""
     D, buf = 128, 40
-    _say(f"linear_qkv_rope_append B={B} Hq={Hq} Hk={Hk} k={k} glm={glm}")
+    _say(f"linear_qkv_rope_append B={B} Hq={Hq} Hk={Hk} k={k} glm={glm} bias={bias}")
     g = torch.Generator().manual_seed(B * 31 + Hk + k + glm)
     cs = oracle.build_glm_cos_sin_cache(3000, 5e6) if glm else oracle.build_cos_sin_cache(3000, 5e5)
     n = (Hq + 2 * Hk) * D
     x = torch.randn(B, 1, k, generator=g).to(torch.bfloat16).to(gpu)
     w = (torch.randn(n, k, generator=g) / k ** 0.5 * 2).to(torch.bfloat16).to(gpu)
+    bq = (torch.randn(n, generator=g) * 0.5).to(torch.bfloat16).to(gpu) if bias else None
     w_rope = shadowkv.qkv_rope_weight(w, Hq, Hk, glm)
+    b_rope = shadowkv.qkv_rope_weight(bq, Hq, Hk, glm) if bias else None
+    if bias and not glm:  # the bias in the weight's row order
+        qk = (Hq + Hk) * D
+        assert torch.equal(b_rope[:qk].view(Hq + Hk, 64, 2)[:, :, 1], bq[:qk].view(Hq + Hk, 2, 64)[:, 1])
     if glm:
         assert torch.equal(w_rope, w)
     else:  # rows (d, d + 64) of every q/k head adjacent, v rows in place
@@ -143,13 +150,13 @@ def test_linear_qkv_rope_append_equals_linear_then_rope(gpu, B, Hq, Hk, k, glm):
     vc = torch.randn(B, Hk, buf, D, generator=g).to(torch.bfloat16).to(gpu)
     csg = cs.to(gpu)
     qkv = torch.empty(B, 1, n, dtype=torch.bfloat16, device=gpu)
-    shadowkv.linear(x, w, qkv)
+    shadowkv.linear(x, w, qkv, bias=bq)
     q_want = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=gpu)
     k_want, v_want = kc.clone(), vc.clone()
     shadowkv.rope_qk_append(qkv.view(B, n), Hq, Hk, pos, csg, q_want, k_want, v_want, row)
     q_got = torch.full((B, Hq, D), 3.0, dtype=torch.bfloat16, device=gpu)
     k_got, v_got = kc.clone(), vc.clone()
-    shadowkv.linear_qkv_rope_append(x.view(B, k), w_rope, Hq, Hk, pos, csg, q_got, k_got, v_got, row)
+    shadowkv.linear_qkv_rope_append(x.view(B, k), w_rope, Hq, Hk, pos, csg, q_got, k_got, v_got, row, b_rope)
     torch.cuda.synchronize()
     assert torch.equal(q_got.cpu(), q_want.cpu())
     assert torch.equal(k_got.cpu(), k_want.cpu())
@@ -159,7 +166,7 @@ def test_linear_qkv_rope_append_equals_linear_then_rope(gpu, B, Hq, Hk, k, glm):
     q2 = torch.zeros_like(q_got)
     k2, v2 = kc.clone(), vc.clone()
     shadowkv.linear_qkv_rope_append(x.view(B, k), w_rope, Hq, Hk, pos, csg, q2, k2, v2,
-                                    torch.tensor([buf], device=gpu))
+                                    torch.tensor([buf], device=gpu), b_rope)
     torch.cuda.synchronize()
     assert torch.equal(q2.cpu(), q_want.cpu())
     assert torch.equal(k2.cpu(), kc.cpu()) and torch.equal(v2.cpu(), vc.cpu())
@@ -177,7 +184,7 @@ def test_linear_qkv_rope_append_rejects(gpu):
     with pytest.raises(ValueError, match="at most 4"):
         shadowkv.linear_qkv_rope_append(x5, w, Hq, Hk, torch.zeros(5, dtype=torch.int64, device=gpu), cs,
                                         torch.empty(5, Hq, D, dtype=torch.bfloat16, device=gpu), kc, kc.clone(), row)
-    rc = _lib.lib().skv_linear_qkv_rope_append(x5.data_ptr(), k, w.data_ptr(), k, 5, k, Hq, Hk, row.data_ptr(),
+    rc = _lib.lib().skv_linear_qkv_rope_append(x5.data_ptr(), k, w.data_ptr(), k, None, 5, k, Hq, Hk, row.data_ptr(),
                                                cs.data_ptr(), 128, 10, 0, kc.data_ptr(), Hq * D, kc.data_ptr(),
                                                kc.data_ptr(), Hk * 4 * D, 4 * D, D, row.data_ptr(), 4, None)
     assert rc == 2  # SKV_EUNSUPPORTED
