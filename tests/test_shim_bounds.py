@@ -54,3 +54,24 @@ def test_side_streams_are_limited_to_the_hardware_queues(monkeypatch):
     assert streams.side_streams_created() + 1 <= streams.MAX_STREAMS
     with pytest.raises(ValueError):
         streams.side_stream("cuda:0", "lane2")
+
+
+def test_qkv_rope_weight_row_order():
+    """The QKV weight (and bias) row order of the RoPE epilogue, on the CPU: each q and k head's rows
+    interleaved as (0, 64, 1, 65, ...) so that a rotation pair (d, d + 64) sits in adjacent rows, v
+    rows in place; GLM's weight (pairs (2i, 2i + 1) already adjacent) unchanged."""
+    Hq, Hk, D = 3, 2, 128
+    n = (Hq + 2 * Hk) * D
+    w = torch.arange(n, dtype=torch.float32)[:, None].repeat(1, 5)  # row r holds r
+    got = shadowkv.qkv_rope_weight(w, Hq, Hk, glm=False)[:, 0].long()
+    for head in range(Hq + Hk):
+        for i in range(64):
+            assert got[head * D + 2 * i] == head * D + i
+            assert got[head * D + 2 * i + 1] == head * D + 64 + i
+    assert torch.equal(got[(Hq + Hk) * D:], torch.arange((Hq + Hk) * D, n))
+    assert sorted(got.tolist()) == list(range(n))  # a permutation
+    b = torch.arange(n, dtype=torch.float32)
+    assert torch.equal(shadowkv.qkv_rope_weight(b, Hq, Hk, glm=False).long(), got)  # the bias alike
+    assert torch.equal(shadowkv.qkv_rope_weight(w, Hq, Hk, glm=True), w)
+    with pytest.raises(ValueError):
+        shadowkv.qkv_rope_weight(w[:-1], Hq, Hk, glm=False)
