@@ -63,7 +63,7 @@ __device__ __forceinline__ void rope_pair_dims(const RopeEpi& re, int n1, int& h
   if (kRope == kRopeHalf && kind < 2) {
     d1 = j / 2;
     d2 = 64 + j / 2;
-    ci = kind < 2 ? d1 : -1;  // cos at [d1], sin at [d1 + 64]
+    ci = d1;  // cos at [d1], sin at [d1 + 64]
   } else {
     d1 = j;
     d2 = j + 1;
