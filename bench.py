@@ -62,6 +62,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-act-epilogue", action="store_true",
                    help="form SiLU-and-mul outside the gate/up projection (the down projection reading "
                         "[gate | up], or the SiLU-and-mul kernel) instead of in its epilogue, for comparison")
+    p.add_argument("--no-qkv-rope-epilogue", action="store_true",
+                   help="rotate q/k and append the new token's k/v in their own kernel after the QKV projection "
+                        "instead of in its epilogue, for comparison")
     p.add_argument("--separate-hit-moves", action="store_true",
                    help="move the hits of the key and value buffers in their own launches instead of in the "
                         "selection's last launch (the same work, for comparison)")
@@ -1170,6 +1173,8 @@ def main() -> int:
             lane.cache.fold_hit_moves = False
     if args.no_act_epilogue:
         model.act_epilogue = False
+    if args.no_qkv_rope_epilogue:
+        model.qkv_rope_epilogue = False
     if args.two_stream_fetch:
         for lane in model.lanes:
             lane.cache.one_stream_fetch = False
