@@ -199,9 +199,26 @@ def test_select_chunks_fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, spl
     """The fused selection (keys computed per row in the selection kernel; on the split path by
     the many-workgroup softmax + GQA-max kernel first; on the parts path ("ws") also the radix
     passes over many workgroups per row, with a caller workspace) equals the unfused sequence."""
+    _fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, split, rows * n + S)
+
+
+def test_select_chunks_random_shapes(gpu, monkeypatch):
+    """The same check on 12 seeded random shapes (rows 1-40, 1-16 queries, landmark counts that are
+    not multiples of 8 or of the 256-column tile, selections from 1 to 2048) on every path."""
+    rng = np.random.default_rng(2024)
+    for case in range(12):
+        m = int(rng.choice([1, 2, 3, 4, 5, 8, 9, 12, 16]))
+        rows = int(rng.integers(1, 41))
+        n = int(rng.integers(100, 40001))
+        S = int(min(n // 2, rng.choice([1, 2, 7, 64, 255, 256, 1000, 2048])))  # (half the ids stay unselected)
+        for split in ("0", "1", "1ws", "ws"):
+            _fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, split, 7919 * case + 11)
+
+
+def _fused_equals_unfused(gpu, monkeypatch, rows, m, n, S, split, seed):
     monkeypatch.setenv("SKV_SELECT_SPLIT", {"ws": "2", "1ws": "1"}.get(split, split))
     _say(f"select_chunks rows={rows} m={m} n={n} S={S} split={split}")
-    g = torch.Generator().manual_seed(rows * n + S)
+    g = torch.Generator().manual_seed(seed)
     q = torch.randn(rows, m, 128, generator=g).to(torch.bfloat16).to(gpu)
     L = torch.randn(rows, n, 128, generator=g).to(torch.bfloat16).to(gpu)
     lidx = torch.stack([torch.randperm(n + n // 10, generator=g)[:n].sort().values for _ in range(rows)]).to(gpu)
