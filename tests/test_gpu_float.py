@@ -400,3 +400,60 @@ def test_rope_two_tables_and_chunk_positions(gpu):
     want3 = oracle.rope_push(x, cs, ids, cnts, c, buf.clone(), 10, 10 + Ls - 4)
     assert torch.equal(outs[0], want3)
 
+
+
+def test_rebuild_k_rope_random_shapes(gpu):
+    """The rebuild + RoPE push on 10 seeded random shapes (batch 1-3, 1-8 heads, rank 8-192,
+    1-300 chunks of 4, 8 or 16 rows, random hit counts, both rotations, per-head or shared U/SV)
+    against the oracle: the rebuilt rows within tolerance, every other row untouched."""
+    rng = np.random.default_rng(77)
+    for case in range(10):
+        B, H = int(rng.integers(1, 4)), int(rng.choice([1, 2, 3, 8]))
+        R = 8 * int(rng.integers(1, 25))
+        c = int(rng.choice([4, 8, 16]))
+        S = int(rng.integers(1, 301))
+        ctx = c * max(S + 16, int(rng.integers(S + 16, 1200)))
+        glm, per_head_u, shared_sv = (bool(rng.integers(0, 2)) for _ in range(3))
+        _say(f"rebuild random case {case}: B={B} H={H} R={R} c={c} S={S} ctx={ctx} glm={glm} "
+             f"per_head_u={per_head_u} shared_sv={shared_sv}")
+        U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 1000 + case, per_head_u, shared_sv)
+        cs = oracle.build_glm_cos_sin_cache(ctx, 5e6) if glm else oracle.build_cos_sin_cache(ctx, 5e5)
+        start = int(rng.integers(0, 64)) * 8
+        buf = start + S * c + 24
+        cache = torch.randn(B, H, buf, 128).to(torch.bfloat16)
+        SVf = SV.unsqueeze(0).expand(B, -1, -1, -1) if shared_sv else SV
+        want = oracle.rebuild_k_rope(U, SVf, ids, cnts, cs, c, cache.clone(), start, glm=glm)
+        cg = cache.to(gpu)
+        shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
+        torch.cuda.synchronize()
+        got = cg.cpu()
+        assert torch.equal(got[:, :, :start], cache[:, :, :start])
+        assert torch.equal(got[:, :, start + S * c:], cache[:, :, start + S * c:])
+        for bh in range(B * H):
+            b, h = divmod(bh, H)
+            miss = start + int(cnts[bh]) * c
+            assert torch.equal(got[b, h, start:miss], cache[b, h, start:miss])
+            torch.testing.assert_close(got[b, h, miss:start + S * c].float(), want[b, h, miss:start + S * c].float(),
+                                       rtol=RTOL, atol=ATOL)
+
+
+def test_sparse_attention_random_shapes(gpu):
+    """Sparse decode attention on 10 seeded random shapes (batch 1-6, 1-8 kv heads of 1-16 query
+    heads, lengths 1-20000, buffers longer than the length) against the oracle."""
+    rng = np.random.default_rng(78)
+    for case in range(10):
+        B, Hk, G = int(rng.integers(1, 7)), int(rng.choice([1, 2, 4, 8])), int(rng.choice([1, 2, 4, 8, 16]))
+        L = int(rng.choice([1, 2, 127, 128, 129])) if case < 3 else int(rng.integers(1, 20001))
+        Hq = Hk * G
+        _say(f"attention random case {case}: B={B} Hq={Hq} Hk={Hk} L={L}")
+        g = torch.Generator().manual_seed(500 + case)
+        buf = L + int(rng.integers(0, 50))
+        K = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
+        V = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
+        q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16)
+        want = oracle.sparse_attention(q, K, V, L)
+        ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+        out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
+        shadowkv.sparse_attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), L, out, ws)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu().float(), want.float(), rtol=RTOL, atol=ATOL)
