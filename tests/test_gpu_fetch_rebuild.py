@@ -20,13 +20,29 @@ pytestmark = pytest.mark.gpu
                                          (8, 8, 256, False, 192), (2, 2, 64, True, 96)])
 def test_one_launch_equals_fetch_then_rebuild(gpu, B, H, S, glm, R):
     """(rank 192 at batch 8: the fused launch takes 128-row tiles where the rebuild alone takes 256)"""
-    print(f"fetch+rebuild one launch B={B} H={H} S={S} glm={glm} rank={R}", flush=True)
-    c, D = 8, 128
+    _one_launch_case(gpu, B, H, S, glm, R, 8, B * 100 + H * 10 + S)
+
+
+def test_one_launch_random_shapes(gpu):
+    """The same equality on 10 seeded random shapes: batch 1-4, 1-8 heads, 1-600 chunks of 4, 8 or
+    16 rows, ranks 8-192, both rotary layouts."""
+    import numpy as np
+    rng = np.random.default_rng(79)
+    for case in range(10):
+        B, H = int(rng.integers(1, 5)), int(rng.choice([1, 2, 3, 8]))
+        S, c = int(rng.integers(1, 601)), int(rng.choice([4, 8, 16]))
+        R, glm = 8 * int(rng.integers(1, 25)), bool(rng.integers(0, 2))
+        _one_launch_case(gpu, B, H, S, glm, R, c, 9000 + case)
+
+
+def _one_launch_case(gpu, B, H, S, glm, R, c, seed):
+    print(f"fetch+rebuild one launch B={B} H={H} S={S} glm={glm} rank={R} chunk={c}", flush=True)
+    D = 128
     chunks = max(4 * S, 2048)
     ctx = chunks * c
     sparse_start, buf_len = 64, 64 + S * c + 32
-    g = torch.Generator().manual_seed(B * 100 + H * 10 + S)
-    gd = torch.Generator(device=gpu).manual_seed(B * 100 + H * 10 + S)
+    g = torch.Generator().manual_seed(seed)
+    gd = torch.Generator(device=gpu).manual_seed(seed)
     values = torch.randn(B, H, chunks, c * D, generator=g).to(torch.bfloat16).pin_memory()
     U = torch.randn(B, H, ctx, R, generator=gd, device=gpu).to(torch.bfloat16)
     SV = (torch.randn(H, D, R, generator=gd, device=gpu) / R ** 0.5).to(torch.bfloat16)
