@@ -193,8 +193,22 @@ def test_rebuild_basis_rows_exact(gpu):
 
 @pytest.mark.parametrize("Z,m,n", [(8, 4, 968), (64, 4, 15304), (8, 16, 32712), (4, 1, 300), (2, 8, 257)])
 def test_scoring(gpu, Z, m, n):
+    _scoring_case(gpu, Z, m, n, n)
+
+
+def test_scoring_random_shapes(gpu):
+    """Scoring + softmax + GQA max on 10 seeded random shapes (1-40 rows, 1-16 queries, 1-40000
+    landmarks, including counts below one 256-column tile)."""
+    rng = np.random.default_rng(80)
+    for case in range(10):
+        Z, m = int(rng.integers(1, 41)), int(rng.integers(1, 17))
+        n = int(rng.integers(1, 300)) if case < 3 else int(rng.integers(300, 40001))
+        _scoring_case(gpu, Z, m, n, 3000 + case)
+
+
+def _scoring_case(gpu, Z, m, n, seed):
     _say(f"scoring Z={Z} m={m} n={n}")
-    g = torch.Generator().manual_seed(n)
+    g = torch.Generator().manual_seed(seed)
     q = torch.randn(Z, m, 128, generator=g).to(torch.bfloat16)
     L = torch.randn(Z, n, 128, generator=g).to(torch.bfloat16)
     alpha = 1.0 / math.sqrt(128)

@@ -60,6 +60,26 @@ def test_linear_bias(gpu, rows, n, k):
         shadowkv.linear(x.to(gpu), w.to(gpu), out, bias=b[:-1].to(gpu))
 
 
+def test_linear_random_shapes(gpu):
+    """The skinny linear on 12 seeded random shapes (1-16 rows, n 1-9000, k a multiple of 8 up to
+    16000, with and without a bias) against fp32 torch."""
+    import numpy as np
+    rng = np.random.default_rng(81)
+    for case in range(12):
+        rows, n, k = int(rng.integers(1, 17)), int(rng.integers(1, 9001)), 8 * int(rng.integers(1, 2001))
+        bias = bool(rng.integers(0, 2))
+        _say(f"linear random case {case}: rows={rows} n={n} k={k} bias={bias}")
+        g = torch.Generator().manual_seed(4000 + case)
+        x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+        w = (torch.randn(n, k, generator=g) / k ** 0.5).to(torch.bfloat16)
+        b = torch.randn(n, generator=g).to(torch.bfloat16) if bias else None
+        out = torch.full((rows, n), 7.0, dtype=torch.bfloat16, device=gpu)
+        shadowkv.linear(x.to(gpu), w.to(gpu), out, bias=None if b is None else b.to(gpu))
+        torch.cuda.synchronize()
+        want = x.float() @ w.float().t() + (b.float() if bias else 0)
+        assert_bf16_close(out.cpu(), want.to(torch.bfloat16), floor=1e-3, what=f"linear random case {case}")
+
+
 def test_linear_strided_views(gpu):
     """Rows taken from wider buffers (x a column slice, out a slice of a fused output), as the
     decode step passes views of its fused projections."""
