@@ -78,9 +78,49 @@ def test_multi_layer_multi_step_decode(gpu, monkeypatch, device_lengths, chunk, 
     print(f"decode small fixture, 2 layers x 4 steps, device_lengths={device_lengths}, chunk={chunk}, split={split}, "
           f"glm={glm}", flush=True)
     case = make_golden.decode_small_case(chunk, glm=glm)
+    _decode_and_check(gpu, case, device_lengths, steps=4, layers=2, seed=77)
+
+
+def _random_case(seed, B, H, G, ctx, rank, budget, chunk, glm):
+    """decode_small_case's construction (low-rank pre-RoPE keys plus noise, N(0,1) values and
+    queries, encoded by the oracle) at other dimensions."""
+    g = torch.Generator().manual_seed(seed)
+    D = 128
+    A = torch.randn(B, ctx, rank, generator=g) / rank ** 0.5
+    Bm = torch.randn(B, rank, H * D, generator=g) / rank ** 0.5
+    k_pre = (A @ Bm + 0.05 * torch.randn(B, ctx, H * D, generator=g)).view(B, ctx, H, D).transpose(1, 2)
+    k_pre = k_pre.to(torch.bfloat16).contiguous()
+    v = torch.randn(B, H, ctx, D, generator=g).to(torch.bfloat16)
+    q_last = torch.randn(B, H * G, 1, D, generator=g).to(torch.bfloat16)
+    cos_sin = oracle.build_glm_cos_sin_cache(ctx + 64, 10000.0) if glm else oracle.build_cos_sin_cache(ctx + 64, 500000.0)
+    st = oracle.encode_layer(k_pre, v, q_last, cos_sin, rank=rank, chunk=chunk, budget=budget)
+    state_in = dict(U=st.U.clone(), SV=st.SV.clone(), landmarks=st.landmarks.clone(),
+                    landmark_idx=st.landmark_idx.clone(), host_v=st.host_v.clone(), kbuf=st.kbuf.clone(),
+                    vbuf=st.vbuf.clone(), position_ids=st.position_ids.clone())
+    return dict(state_in=state_in, st=st, cos_sin=cos_sin,
+                dims=dict(B=B, H=H, G=G, D=D, ctx=ctx, rank=rank, chunk=chunk, budget=budget))
+
+
+def test_decode_random_configurations(gpu):
+    """Whole decode steps through the drop-in cache and attention classes on 6 seeded random
+    configurations (batch 1-3, 1-4 kv heads of 1-16 query heads, chunks of 4/8/16 rows, budgets
+    1024/2048, ranks 16-64, contexts 2-4x the budget, both rotary tables), 1 layer x 3 steps, checked
+    against the oracle as in the fixture test."""
+    rng = np.random.default_rng(82)
+    for case_i in range(6):
+        B, H = int(rng.integers(1, 4)), int(rng.choice([1, 2, 4]))
+        G, chunk = int(rng.choice([1, 2, 4, 8, 16])), int(rng.choice([4, 8, 16]))
+        budget, rank, glm = int(rng.choice([1024, 2048])), int(rng.choice([16, 32, 64])), bool(rng.integers(0, 2))
+        ctx = 64 * int(rng.integers(budget * 2 // 64, budget * 4 // 64 + 1))
+        print(f"decode random configuration {case_i}: B={B} H={H} G={G} chunk={chunk} budget={budget} rank={rank} "
+              f"ctx={ctx} glm={glm}", flush=True)
+        case = _random_case(600 + case_i, B, H, G, ctx, rank, budget, chunk, glm)
+        _decode_and_check(gpu, case, device_lengths=bool(case_i % 2), steps=3, layers=1, seed=900 + case_i)
+
+
+def _decode_and_check(gpu, case, device_lengths, steps, layers, seed):
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
-    steps, layers = 4, 2
     cache = build_cache(case, gpu, max_decode_len=steps, num_layers=layers)
     if device_lengths:
         cache.use_device_lengths()
@@ -90,7 +130,7 @@ def test_multi_layer_multi_step_decode(gpu, monkeypatch, device_lengths, chunk, 
     from tests.decode_harness import identity_rope
     cos_sin = case["cos_sin"]
     attn = ShadowAttention(cache, G, D, H * G * D, identity_rope(B, H * G, H, D), None, cos_sin.to(gpu))
-    g = torch.Generator().manual_seed(77)
+    g = torch.Generator().manual_seed(seed)
     for t in range(steps):
         for layer in range(layers):
             q = torch.randn(B, H * G, D, generator=g).to(torch.bfloat16)
