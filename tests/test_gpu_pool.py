@@ -66,10 +66,31 @@ def _queries(B, H, G, D, steps, layers, seed, drift):
 @pytest.mark.parametrize("P,device_lengths,drift", [(256, True, 0.3), (160, False, 1.0), (128, True, 0.3)])
 def test_pooled_decode_matches_oracle(gpu, P, device_lengths, drift):
     _say(f"pooled decode P={P} device_lengths={device_lengths} drift={drift}")
-    case = make_golden.decode_small_case()
+    _pooled_decode(gpu, make_golden.decode_small_case(), P, device_lengths, drift, steps=5, layers=2)
+
+
+def test_pooled_decode_random_configurations(gpu):
+    """Pooled decode steps on 5 seeded random configurations (batch 1-3, 1-4 kv heads of 1-16 query
+    heads, chunks of 4/8/16 rows, budget 1024, pools of S to 3S slots) against the oracle's pooled
+    step."""
+    from tests.test_gpu_decode import _random_case
+    rng = np.random.default_rng(83)
+    for i in range(5):
+        B, H = int(rng.integers(1, 4)), int(rng.choice([1, 2, 4]))
+        G, chunk = int(rng.choice([1, 4, 16])), int(rng.choice([4, 8, 16]))
+        S = 1024 // chunk
+        P = int(rng.integers(S, 3 * S + 1))
+        rank, glm, drift = int(rng.choice([16, 32])), bool(rng.integers(0, 2)), float(rng.choice([0.2, 0.5]))
+        ctx = 64 * int(rng.integers(1024 * 2 // 64, 1024 * 4 // 64 + 1))
+        _say(f"pooled random configuration {i}: B={B} H={H} G={G} chunk={chunk} P={P} rank={rank} ctx={ctx} "
+             f"glm={glm} drift={drift}")
+        case = _random_case(700 + i, B, H, G, ctx, rank, 1024, chunk, glm)
+        _pooled_decode(gpu, case, P, bool(i % 2), drift, steps=4, layers=1)
+
+
+def _pooled_decode(gpu, case, P, device_lengths, drift, steps, layers):
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
-    steps, layers = 5, 2
     cache = build_cache(case, gpu, max_decode_len=steps, num_layers=layers, chunk_cache=P)
     if device_lengths:
         cache.use_device_lengths()
