@@ -186,6 +186,27 @@ def test_prefill_batch2_llama_heads(gpu):
     _check_prefill(gpu, k_pre, v, q_last, cos_sin, 8, 1024, R)
 
 
+def test_prefill_random_configurations(gpu):
+    """The device prefill on 5 seeded random configurations (batch 1-2, 1-8 kv heads of 1-16 query
+    heads, ranks 16-160, chunks of 4/8/16 rows, budgets 1024/2048, contexts 2-4x the budget)
+    against the oracle's encode_layer, checked as in the fixed cases."""
+    rng = np.random.default_rng(84)
+    for i in range(5):
+        B, H, G = int(rng.integers(1, 3)), int(rng.choice([1, 2, 4, 8])), int(rng.choice([1, 4, 16]))
+        chunk, budget, R = int(rng.choice([4, 8, 16])), int(rng.choice([1024, 2048])), int(rng.choice([16, 32, 64, 160]))
+        ctx = 64 * int(rng.integers(budget * 2 // 64, budget * 4 // 64 + 1))
+        _say(f"prefill random configuration {i}: B={B} H={H} G={G} chunk={chunk} budget={budget} rank={R} ctx={ctx}")
+        g = torch.Generator().manual_seed(800 + i)
+        D = 128
+        a = torch.randn(B, ctx, R, generator=g) @ torch.randn(B, R, H * D, generator=g) / R ** 0.5
+        k_pre = (a + 0.1 * torch.randn(B, ctx, H * D, generator=g)).view(B, ctx, H, D).transpose(1, 2)
+        k_pre = k_pre.to(torch.bfloat16).contiguous()
+        v = torch.randn(B, H, ctx, D, generator=g).to(torch.bfloat16)
+        q_last = torch.randn(B, H * G, 1, D, generator=g).to(torch.bfloat16)
+        cos_sin = oracle.build_cos_sin_cache(ctx + 64, 500000.0)
+        _check_prefill(gpu, k_pre, v, q_last, cos_sin, chunk, budget, R)
+
+
 def test_prefill_rejects_host_tensors(gpu):
     cfg = types.SimpleNamespace(num_attention_heads=8, num_key_value_heads=2, hidden_size=1024, num_hidden_layers=1)
     cache = ShadowKVCache_CPU(cfg, batch_size=1, max_length=2048, device=str(gpu), sparse_budget=1024, chunk_size=8,
