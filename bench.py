@@ -907,7 +907,8 @@ def linear_microbench(args) -> int:
                                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(t * 1e6, 2),
                                      "torch_matmul_us": round(t_torch * 1e6, 2)},
                         "cpu_baseline": None}
-            if name == "down":  # the same weight read through SiLU-and-mul of [gate | up] rows
+            if name == "down" and rows <= shadowkv.LINEAR_SILU_MUL_MAX_ROWS:
+                # the same weight read through SiLU-and-mul of [gate | up] rows (offered up to 4 rows)
                 gu = torch.randn(rows, 2 * k, generator=g, device="cuda").to(torch.bfloat16)
                 act = torch.empty(rows, k, dtype=torch.bfloat16, device="cuda")
                 t_gated = gpu_time_per_call(lambda i: shadowkv.linear_silu_mul(gu, ws[i % sets], y), set_reps)
