@@ -444,7 +444,7 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
     q = torch.randn(B, H * G, 1, D, device=c.device).to(torch.bfloat16)
     qa = q.view(B, H * G, D)
     out = torch.empty(B, H * G, D, dtype=torch.bfloat16, device=c.device)
-    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, H * G, c.buf_len), dtype=torch.uint8, device=c.device)
+    ws = shadowkv.sparse_attn_workspace(B, H * G, c.buf_len, c.device)
     reps = sweeps * L
 
     def t_us(fn):
@@ -534,10 +534,12 @@ def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
     the call's index, so a caller can rotate through several input sets."""
     import torch
 
+    from shadowkv_amd.streams import side_stream
+
     fn(0)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=side_stream(torch.cuda.current_device(), "capture")):
         for i in range(reps):
             fn(i)
     g.replay()
@@ -791,7 +793,7 @@ def attention_microbench(args) -> int:
         V = [torch.randn(B, Hk, buf, D, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
         q = [torch.randn(B, Hq, D, generator=g, device="cuda").to(torch.bfloat16) for _ in range(sets)]
         out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device="cuda")
-        ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device="cuda")
+        ws = shadowkv.sparse_attn_workspace(B, Hq, L, "cuda")
         t = gpu_time_per_call(lambda i: shadowkv.sparse_attn_decode(q[i % sets], K[i % sets], V[i % sets], L, out, ws),
                               set_reps)
         out_line = {"metric": "sparse decode attention (b,h) rows/s", "value": round(B * Hq / t, 1), "unit": "rows/s",

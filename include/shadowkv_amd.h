@@ -285,12 +285,20 @@ int skv_select_chunks_compact(const uint16_t* D, const float* norm, const float*
  *   out[b, hq] = softmax(scale * q[b,hq] . K[b,h,:kv_len]^T) . V[b,h,:kv_len]   (fp32 math, bf16 out)
  * q row: q + b*q_stride_b + hq*q_stride_h; K/V row s of (b,h): base + b*kv_stride_b + h*kv_stride_h
  * + s*kv_stride_s; out row: out + b*o_stride_b + hq*o_stride_h. head_dim must be 128.
- * workspace: caller-provided device scratch of skv_sparse_attn_workspace_bytes(...) bytes.
- * kv_len at most 262144.
+ * workspace: caller-provided device scratch of skv_sparse_attn_workspace_bytes(...) bytes, 16-byte
+ * aligned and zero-filled before its first use: its head holds per-row arrival counters that every
+ * call leaves at zero (so a zeroed workspace stays valid across calls, shapes and graph replays);
+ * calls that overlap on one workspace race. kv_len at most 262144.
  * kv_len_dev (optional, no reference counterpart): device int32 holding the live length, read
  * when the kernel runs and clamped to [1, kv_len]; kv_len is then the maximum. This keeps the
  * call valid inside a captured HIP graph while the cache grows by one row per replay. */
 int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, int kv_len);
+/* Diagnostic of the one-launch merge (no reference counterpart): for the current device, whether
+ * the probe confirmed that workgroups sharing blockIdx mod 8 run on one XCD (*state 1; -1 not
+ * confirmed, the attention then merges in a second launch; 0 not probed yet), the XCC id seen
+ * for each class (4 bits each, *xcc_map), and whether any fused attention workgroup since the
+ * library loaded found itself on another XCC (*misplaced nonzero). Synchronous. */
+int skv_sparse_attn_xcd_check(int32_t* state, uint32_t* xcc_map, uint32_t* misplaced);
 int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
                            const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
                            int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
@@ -302,7 +310,7 @@ int skv_sparse_attn_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stri
  * cannot allocate device memory (code under HIP graph capture, tight serving loops). The split
  * partials live in a device array inside the library, one per GPU, of
  * skv_sparse_attn_noalloc_max_bytes() bytes (32 MiB), held until the process ends; calls needing more
- * (skv_sparse_attn_workspace_bytes above it, e.g. batch 8 x 32 query heads beyond 16128 keys) return
+ * (skv_sparse_attn_workspace_bytes above it, e.g. batch 8 x 32 query heads beyond 16064 keys) return
  * SKV_EUNSUPPORTED. The call allocates nothing. All calls on one GPU share that array: calls that
  * overlap on one GPU (on different streams, or from several threads) race; `stream` must belong to
  * the current device. Arguments and results as skv_sparse_attn_decode. */

@@ -64,6 +64,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                          _p, _i64, _p, _p, _i64, _i64, _i32, _p]),
     "skv_topk_gather": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p]),
     "skv_sparse_attn_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "skv_sparse_attn_xcd_check": (_i32, [_p, _p, _p]),
     "skv_rmsnorm": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "skv_silu_and_mul": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p]),
     "skv_linear": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p]),

@@ -2,7 +2,7 @@
 //
 // Replaces flash_attn_with_kvcache(q, k, v, causal=True) at models/attention/shadow.py:48
 // (q_len = 1, so causality masks nothing). Split-L flash decoding for CDNA4:
-//   attn_split_kernel: workgroup = (kv head, split of 128 keys); all G query heads that
+//   attn_split_kernel: workgroup = (kv head, split of 64 or 128 keys); all G query heads that
 //     share the kv head are served by one pass over its K and V rows, so every K/V byte is read
 //     once from HBM. Scores on MFMA: v_mfma_f32_16x16x32_bf16 with the (up to 16) query heads as
 //     the A rows and 16 keys as the B columns, so each lane ends up holding finished scores (no
@@ -10,8 +10,20 @@
 //     P.V on MFMA for 9..16 query heads (P in bf16 as the A operand, the V tile read transposed
 //     from LDS as B, each wave owning 32 dims), in fp32 for 1..8 (16 key streams x 8 dims per
 //     lane, the streams summed through LDS).
-//   attn_combine_kernel: log-sum-exp merge of the splits in one pass (running maximum), every
-//     load of a 32-split chunk issued before the first is used; bf16 output.
+//   Merge of the splits, one of two ways:
+//   - fused (on request; rows of at most 64 splits): every split of a (sequence, kv head) row runs on one XCD
+//     (the grid is ordered so that they share blockIdx mod 8, and the dispatcher hands workgroup w
+//     to XCD w mod 8; a probe kernel checks that mapping once per device, and every workgroup
+//     checks its own XCC id against it). The split partials then meet in that XCD's L2: each
+//     workgroup waits for its partial stores to reach the L2, counts itself in on the row's
+//     arrival counter (a wrapping atomic increment in the L2, so the last arrival leaves it at
+//     zero for the next call or graph replay), and the last one merges the row's splits, reading
+//     the partials with L1-bypassing loads. One launch, and no cross-XCD write-back or
+//     invalidation of the L2s (the agent-scope fence such a hand-off would otherwise need cost
+//     ten times the kernel on MI355X).
+//   - attn_combine_kernel (the default): a second launch,
+//     a log-sum-exp merge of the splits in one pass (running maximum), every load of a 32-split
+//     chunk issued before the first is used; bf16 output.
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -23,11 +35,21 @@ namespace {
 using skv::u32x4;
 
 constexpr int kThreads = 256;
-// Keys per split workgroup. 128 rather than 256: twice the workgroups in flight at decode batch
-// sizes (MI355X, cold K/V, Llama-3-8B shape batch 8: 24 vs 29 us; GLM-4-9B batch 4: 19 vs 27 us).
-constexpr int kSplit = 128;
+// Keys per split workgroup: 128 (rather than 256: twice the workgroups in flight at decode batch
+// sizes; MI355X, cold K/V, Llama-3-8B shape batch 8: 24 vs 29 us; GLM-4-9B batch 4: 19 vs 27 us),
+// or 64 for grids that would otherwise give fewer than two workgroups per CU.
+constexpr int kSplitLong = 128;
+constexpr int kSplitShort = 64;
 constexpr int kHeadDim = 128;
 constexpr int kMaxKvLen = 262144;
+// Fused merge: rows of at most kMaxFusedSplits splits, at most kMaxFusedRows (sequence, kv head)
+// rows per call (their arrival counters sit at the head of the workspace).
+constexpr int kMaxFusedSplits = 64;
+constexpr int kMaxFusedRows = 4096;
+constexpr int64_t kArrivalBytes = kMaxFusedRows * sizeof(uint32_t);
+constexpr int kXcds = 8;
+// s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4): the XCC (XCD) the wave runs on.
+constexpr int kHwRegXccId = (3 << 11) | (0 << 6) | 20;
 
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -57,6 +79,13 @@ struct AttnArgs {
   // selection sit `delta` rows further (after the pool's pool_slots chunks).
   const int32_t* slot;
   int sp0, sel, chunk, pool_slots, delta;
+  // Fused merge: one arrival counter per (b, kv head) row (zero between calls), the row count,
+  // the XCC id the mapping probe saw for each blockIdx class mod 8 (4 bits each), and a flag set
+  // by any workgroup that finds itself elsewhere.
+  uint32_t* arrivals;
+  int rows;
+  uint32_t xcc_map;
+  uint32_t* misplaced;
 };
 
 __device__ __forceinline__ int live_length(const AttnArgs& a) {
@@ -66,16 +95,122 @@ __device__ __forceinline__ int live_length(const AttnArgs& a) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// Fused-merge thread layout: units of (query head, 4 dims), each summed over a share of the
+// splits (kParts threads per unit when the units do not fill the workgroup) or, for 16 heads,
+// two units per thread.
+template <int GP>
+struct MergeShape {
+  static constexpr int kUnits = GP * 32;
+  static constexpr int kParts = kUnits >= kThreads ? 1 : kThreads / kUnits;
+  static constexpr int kPerThread = kUnits > kThreads ? kUnits / kThreads : 1;
+  static constexpr int kBytes = (kParts - 1) * kUnits * 16;  // the parts' float4 sums
+};
+
+// The last workgroup of row bh merges its `used` splits (used <= kMaxFusedSplits): weights
+// w[g][s] = exp(m[g][s] - M_g) and denominators from the (m, l) pairs, then each unit's
+// sum_s w[g][s] o[g][s][4 dims], every partial read with buffer loads that bypass the L1 (sc1;
+// served by the XCD's L2, where the row's other workgroups left them).
+template <int GP>
+__device__ __forceinline__ void fused_merge(const AttnArgs& a, int bh, int used, float (*wt)[kMaxFusedSplits],
+                                            float* lsum, unsigned char* part_lds) {
+  using MS = MergeShape<GP>;
+  const int G = a.G;
+  const int Hq = a.Hkv * G;
+  const int b = bh / a.Hkv;
+  const int h = bh - b * a.Hkv;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row0 = static_cast<int64_t>(b) * Hq + h * G;  // first (b, query head) row of the kv head
+  constexpr uint32_t kSc1 = 16;                               // cache policy: device scope, L1 miss
+  constexpr int kDw3 = 0x00020000;                            // buffer resource word 3 (gfx9)
+  const __amdgpu_buffer_rsrc_t mlr = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + row0 * a.splits * 2, 0, static_cast<int>(G * a.splits * 8), kDw3);
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o + row0 * a.splits * kHeadDim, 0, static_cast<int>(G * a.splits * kHeadDim * 4), kDw3);
+  constexpr int kHeadsPerWave = (GP + 3) / 4;
+  float mv[kHeadsPerWave], lv[kHeadsPerWave];
+#pragma unroll
+  for (int t = 0; t < kHeadsPerWave; ++t) {
+    const int g = wave + 4 * t;
+    const bool ok = g < G && lane < used;
+    const auto p = __builtin_amdgcn_raw_buffer_load_b64(mlr, ((min(g, G - 1) * a.splits + min(lane, used - 1)) * 8),
+                                                        0, kSc1);
+    mv[t] = ok ? __uint_as_float(p[0]) : -INFINITY;
+    lv[t] = ok ? __uint_as_float(p[1]) : 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < kHeadsPerWave; ++t) {
+    const int g = wave + 4 * t;
+    if (g < G) {  // wave-uniform
+      const float M = skv::wave_max_dpp(mv[t]);  // every live split has a finite maximum
+      const float w = lane < used ? expf(mv[t] - M) : 0.f;
+      const float l = skv::wave_sum_dpp(w * lv[t]);
+      wt[g][lane] = w;
+      if (lane == 0) lsum[g] = l;
+    }
+  }
+  __syncthreads();
+  float4* parts = reinterpret_cast<float4*>(part_lds);
+#pragma unroll
+  for (int k = 0; k < MS::kPerThread; ++k) {
+    const int u = MS::kPerThread > 1 ? threadIdx.x + k * kThreads : threadIdx.x % MS::kUnits;
+    const int p = MS::kParts > 1 ? threadIdx.x / MS::kUnits : 0;
+    const int g = u >> 5, d4 = u & 31;
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (g < G) {
+      constexpr int kBatch = 8;
+      for (int s0 = p; s0 < used; s0 += kBatch * MS::kParts) {
+        uint32_t __attribute__((ext_vector_type(4))) v[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const int sp = min(s0 + i * MS::kParts, used - 1);
+          v[i] = __builtin_amdgcn_raw_buffer_load_b128(orr, ((g * a.splits + sp) * kHeadDim + 4 * d4) * 4, 0, kSc1);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const int sp = s0 + i * MS::kParts;
+          const float w = sp < used ? wt[g][sp] : 0.f;
+          acc.x = fmaf(w, __uint_as_float(v[i][0]), acc.x);
+          acc.y = fmaf(w, __uint_as_float(v[i][1]), acc.y);
+          acc.z = fmaf(w, __uint_as_float(v[i][2]), acc.z);
+          acc.w = fmaf(w, __uint_as_float(v[i][3]), acc.w);
+        }
+      }
+    }
+    if constexpr (MS::kParts > 1) {
+      if (p > 0) parts[(p - 1) * MS::kUnits + u] = acc;
+      __syncthreads();
+      if (p > 0) continue;  // (kPerThread == 1 here)
+#pragma unroll
+      for (int q = 1; q < MS::kParts; ++q) {
+        const float4 o = parts[(q - 1) * MS::kUnits + u];
+        acc.x += o.x;
+        acc.y += o.y;
+        acc.z += o.z;
+        acc.w += o.w;
+      }
+    }
+    if (g < G) {
+      const float inv = 1.f / lsum[g];
+      uint16_t* dst = a.out + b * a.o_sb + (h * G + g) * a.o_sh + 4 * d4;
+      *reinterpret_cast<uint32_t __attribute__((ext_vector_type(2)))*>(dst) = {skv::f2bf2(acc.x * inv, acc.y * inv),
+                                                                              skv::f2bf2(acc.z * inv, acc.w * inv)};
+    }
+  }
+}
+
 // kSplit keys per workgroup; the split's V rows are requested right after the scores, so their
 // latency overlaps the softmax (requesting them with K, at entry, measured no faster and holds
-// more registers).
-template <int GP, bool kPaged>
+// more registers). kFused: blockIdx.x enumerates (row, split) so that a row's splits share
+// blockIdx mod 8 (one XCD), and the last split of each row merges them (fused_merge).
+template <int GP, bool kPaged, int kSplit, bool kFused>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   constexpr int kRows = kSplit / 16;        // keys per P.V stream
   constexpr int kGroups = kSplit / 4 / 16;  // 16-key MFMA groups per wave
   constexpr int kPerLane = kSplit / 64;     // softmax entries per lane
   constexpr int kVals = GP * 8;              // P.V partial sums per lane: [head][8 dims]
   constexpr int kKept = kVals / 4;           // per lane after the in-wave stream fold
+  static_assert(kSplit == 64 || kSplit == 128, "64 or 128 keys per split");
   __shared__ float p_lds[GP][kSplit];
   // [wave][lane][value] for the fp32 P.V path; the MFMA P.V path (GP == 16) stages the V tile here
   // instead ([key][kVtLd] bf16, rows padded so the 4 key groups of an operand read hit disjoint
@@ -83,18 +218,36 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   constexpr int kVtLd = kHeadDim + 4;
   constexpr int kRedBytes = 4 * 64 * kKept * 4;
   constexpr int kVtBytes = GP == 16 ? kSplit * kVtLd * 2 : 0;
-  __shared__ __align__(16) unsigned char big[kRedBytes > kVtBytes ? kRedBytes : kVtBytes];
+  constexpr int kMergeBytes = kFused ? MergeShape<GP>::kBytes : 0;
+  constexpr int kBigBytes = kRedBytes > kVtBytes ? (kRedBytes > kMergeBytes ? kRedBytes : kMergeBytes)
+                                                 : (kVtBytes > kMergeBytes ? kVtBytes : kMergeBytes);
+  __shared__ __align__(16) unsigned char big[kBigBytes];
   float (*red)[64][kKept] = reinterpret_cast<float (*)[64][kKept]>(big);
   __shared__ float ml[GP][2];
   __shared__ int prow[kPaged ? kSplit : 1];  // physical row of each key of the split (paged)
 
-  const int split = blockIdx.x;
-  const int bh = blockIdx.y;
+  int split, bh;
+  if constexpr (kFused) {
+    // w = x + 8 j: XCD x takes rows x, x + 8, ... and their splits in order.
+    const int w = blockIdx.x;
+    const int x = w & (kXcds - 1), j = w >> 3;
+    const int i = j / a.splits;
+    split = j - i * a.splits;
+    bh = x + kXcds * i;
+    if (bh >= a.rows) return;  // workgroup-uniform: padding of the last row group
+    if (threadIdx.x == 0) {
+      const uint32_t xcc = __builtin_amdgcn_s_getreg(kHwRegXccId) & 15u;
+      if (xcc != ((a.xcc_map >> (4 * x)) & 15u)) *a.misplaced = 1u;  // (never seen: the probe confirmed the map)
+    }
+  } else {
+    split = blockIdx.x;
+    bh = blockIdx.y;
+  }
   const int b = bh / a.Hkv;
   const int h = bh - b * a.Hkv;
   const int L = live_length(a);
   const int s0 = split * kSplit;
-  if (s0 >= L) return;  // workgroup-uniform: splits past the live length do nothing
+  if (s0 >= L) return;  // workgroup-uniform: splits past the live length do nothing (nor count)
   const int s1 = min(s0 + kSplit, L);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -260,70 +413,86 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       a.ws_ml[r * 2] = ml[g][0];
       a.ws_ml[r * 2 + 1] = ml[g][1];
     }
-    return;
-  }
-
-  float acc[GP][8];
+  } else {
+    float acc[GP][8];
 #pragma unroll
-  for (int g = 0; g < GP; ++g)
+    for (int g = 0; g < GP; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    const int jl = i * 16 + stream;
-    if (s0 + jl < s1) {
-      float vf[8];
-      unpack8(vr[i], vf);
+    for (int i = 0; i < kRows; ++i) {
+      const int jl = i * 16 + stream;
+      if (s0 + jl < s1) {
+        float vf[8];
+        unpack8(vr[i], vf);
 #pragma unroll
-      for (int g = 0; g < GP; ++g) {
-        if (g < G) {
-          const float p = p_lds[g][jl];
+        for (int g = 0; g < GP; ++g) {
+          if (g < G) {
+            const float p = p_lds[g][jl];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+          }
         }
       }
     }
-  }
 
-  // Sum the 16 key streams. The 4 streams of a wave (lane bits 5 and 4) fold in registers:
-  // v_permlane32_swap / v_permlane16_swap with the lower half of the values as one operand and
-  // the upper half as the other hand every lane its own kept value and its partner's copy of
-  // it, so each step is a swap and an add and halves the values a lane holds. Lane (grp, li)
-  // then holds flattened values [grp*kKept, +kKept) of [head][8 dims] for dims li*8..+8; the 4
-  // waves are summed through LDS.
-  float v[kVals];
+    // Sum the 16 key streams. The 4 streams of a wave (lane bits 5 and 4) fold in registers:
+    // v_permlane32_swap / v_permlane16_swap with the lower half of the values as one operand and
+    // the upper half as the other hand every lane its own kept value and its partner's copy of
+    // it, so each step is a swap and an add and halves the values a lane holds. Lane (grp, li)
+    // then holds flattened values [grp*kKept, +kKept) of [head][8 dims] for dims li*8..+8; the 4
+    // waves are summed through LDS.
+    float v[kVals];
 #pragma unroll
-  for (int g = 0; g < GP; ++g)
+    for (int g = 0; g < GP; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[g * 8 + e] = acc[g][e];
+      for (int e = 0; e < 8; ++e) v[g * 8 + e] = acc[g][e];
 #pragma unroll
-  for (int j = 0; j < kVals / 2; ++j) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[kVals / 2 + j]), false,
-                                                    false);
-    v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-#pragma unroll
-  for (int j = 0; j < kKept; ++j) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[kKept + j]), false,
-                                                    false);
-    v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-#pragma unroll
-  for (int j = 0; j < kKept; ++j) red[wave][lane][j] = v[j];
-  __syncthreads();
-  const int Hq = a.Hkv * G;
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kThreads) {
-    const int g = idx / kHeadDim, d = idx - g * kHeadDim;
-    const int f = g * 8 + (d & 7);                        // flattened value index
-    const int src = (f / kKept) * 16 + (d >> 3);           // lane (grp, li) that holds it
-    const int j = f % kKept;
-    const float o = (red[0][src][j] + red[1][src][j]) + (red[2][src][j] + red[3][src][j]);
-    const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
-    a.ws_o[r * kHeadDim + d] = o;
-    if (d == 0) {
-      a.ws_ml[r * 2] = ml[g][0];
-      a.ws_ml[r * 2 + 1] = ml[g][1];
+    for (int j = 0; j < kVals / 2; ++j) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[kVals / 2 + j]),
+                                                      false, false);
+      v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
+#pragma unroll
+    for (int j = 0; j < kKept; ++j) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[kKept + j]), false,
+                                                      false);
+      v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < kKept; ++j) red[wave][lane][j] = v[j];
+    __syncthreads();
+    const int Hq = a.Hkv * G;
+    for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kThreads) {
+      const int g = idx / kHeadDim, d = idx - g * kHeadDim;
+      const int f = g * 8 + (d & 7);                        // flattened value index
+      const int src = (f / kKept) * 16 + (d >> 3);           // lane (grp, li) that holds it
+      const int j = f % kKept;
+      const float o = (red[0][src][j] + red[1][src][j]) + (red[2][src][j] + red[3][src][j]);
+      const int64_t r = (static_cast<int64_t>(b) * Hq + h * G + g) * a.splits + split;
+      a.ws_o[r * kHeadDim + d] = o;
+      if (d == 0) {
+        a.ws_ml[r * 2] = ml[g][0];
+        a.ws_ml[r * 2 + 1] = ml[g][1];
+      }
+    }
+  }
+  if constexpr (kFused) {
+    // This workgroup's partials must be in the L2 before it counts itself in: every thread waits
+    // for its own stores (a workgroup-scope release does not wait for them), then one arrival.
+    __shared__ int last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    const int used = (L + kSplit - 1) / kSplit;  // live splits of the row, each counted once
+    if (threadIdx.x == 0) {
+      // Wrapping increment: the used-th arrival sees used - 1 and leaves 0 behind.
+      const uint32_t seen = __builtin_amdgcn_atomic_inc32(a.arrivals + bh, static_cast<uint32_t>(used - 1),
+                                                          __ATOMIC_RELAXED, "workgroup");
+      last = seen == static_cast<uint32_t>(used - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    fused_merge<GP>(a, bh, used, reinterpret_cast<float (*)[kMaxFusedSplits]>(&p_lds[0][0]), &ml[0][0], big);
   }
 }
 
@@ -408,14 +577,126 @@ __global__ void __launch_bounds__(kHeadDim * kMaxCombineGroups) attn_combine_ker
 
 int splits_for(int kv_len, int split_keys) { return (kv_len + split_keys - 1) / split_keys; }
 
+constexpr int kMaxDevices = 64;
+
+// XCD mapping probe: workgroup w of a 1-D grid records the XCC id it runs on.
+constexpr int kProbeWorkgroups = 4096;
+
+__global__ void xcc_probe_kernel(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = __builtin_amdgcn_s_getreg(kHwRegXccId) & 15u;
+}
+
 }  // namespace
+
+static __device__ uint32_t xcc_probe_out[kProbeWorkgroups];
+static __device__ uint32_t xcc_misplaced;  // set by a fused attention workgroup off its expected XCD
+
+namespace {
+
+struct XccMap {
+  int state = 0;      // 0 not probed, 1 confirmed, -1 not confirmed
+  uint32_t map = 0;   // XCC id of blockIdx class x (mod 8) in bits [4x, 4x + 4)
+  uint32_t* misplaced = nullptr;
+};
+std::mutex g_xcc_mu;
+XccMap g_xcc[kMaxDevices];
+
+// Whether this device's dispatcher hands every workgroup of a 1-D grid with the same blockIdx mod
+// 8 to one XCC (probed once per device with kProbeWorkgroups workgroups; on MI355X workgroup w
+// runs on XCD w mod 8). Not probed while `stream` is capturing a graph (the probe waits for its
+// result): such a call takes the two-launch merge.
+bool fused_mapping(hipStream_t stream, uint32_t* map, uint32_t** misplaced) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_xcc_mu);
+  XccMap& m = g_xcc[dev];
+  if (m.state == 0) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+    void* out = nullptr;
+    void* mis = nullptr;
+    uint32_t h[kProbeWorkgroups];
+    bool ok = hipGetSymbolAddress(&out, HIP_SYMBOL(xcc_probe_out)) == hipSuccess &&
+              hipGetSymbolAddress(&mis, HIP_SYMBOL(xcc_misplaced)) == hipSuccess && out && mis;
+    if (ok) {
+      hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbeWorkgroups), dim3(64), 0, stream, static_cast<uint32_t*>(out));
+      ok = hipGetLastError() == hipSuccess &&
+           hipMemcpyAsync(h, out, sizeof(h), hipMemcpyDeviceToHost, stream) == hipSuccess &&
+           hipStreamSynchronize(stream) == hipSuccess;
+    }
+    uint32_t packed = 0;
+    for (int x = 0; ok && x < kXcds; ++x) packed |= (h[x] & 15u) << (4 * x);
+    for (int w = 0; ok && w < kProbeWorkgroups; ++w) ok = h[w] == h[w % kXcds];
+    m.state = ok ? 1 : -1;
+    m.map = packed;
+    m.misplaced = static_cast<uint32_t*>(mis);
+  }
+  *map = m.map;
+  *misplaced = m.misplaced;
+  return m.state == 1;
+}
+
+}  // namespace
+
+extern "C" int skv_sparse_attn_xcd_check(int32_t* state, uint32_t* xcc_map, uint32_t* misplaced) {
+  int dev = -1;
+  if (!state || !xcc_map || !misplaced) {
+    skv_set_error("sparse_attn_xcd_check: null pointer");
+    return SKV_EINVAL;
+  }
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    skv_set_error("sparse_attn_xcd_check: no usable current device");
+    return SKV_ELAUNCH;
+  }
+  {
+    std::lock_guard<std::mutex> lock(g_xcc_mu);
+    *state = g_xcc[dev].state;
+    *xcc_map = g_xcc[dev].map;
+  }
+  *misplaced = 0;
+  const hipError_t e = hipMemcpyFromSymbol(misplaced, HIP_SYMBOL(xcc_misplaced), sizeof(uint32_t), 0,
+                                           hipMemcpyDeviceToHost);
+  if (e != hipSuccess) {
+    skv_set_error("sparse_attn_xcd_check: %s", hipGetErrorString(e));
+    return SKV_ELAUNCH;
+  }
+  return SKV_OK;
+}
 
 extern "C" int64_t skv_sparse_attn_workspace_bytes(int batch_size, int q_heads, int kv_len) {
   if (batch_size < 1 || q_heads < 1 || kv_len < 1) return 0;
-  return static_cast<int64_t>(batch_size) * q_heads * splits_for(kv_len, kSplit) * (kHeadDim + 2) * sizeof(float);
+  // Arrival counters, then the partials of the shorter split (the launch may choose either).
+  return kArrivalBytes +
+         static_cast<int64_t>(batch_size) * q_heads * splits_for(kv_len, kSplitShort) * (kHeadDim + 2) * sizeof(float);
 }
 
 namespace {
+
+// Keys per split: 128. SKV_ATTN_SPLIT=64 forces 64-key splits (twice the workgroups; measured
+// slower at every decode shape on MI355X: Llama-3-8B batch 4 23.1 vs 15.5 us, GLM-4-9B batch 4
+// 11.7 vs 10.8 us with the two-launch merge).
+int choose_split_keys(int rows, int kv_len) {
+  (void)rows, (void)kv_len;
+  const char* e = getenv("SKV_ATTN_SPLIT");
+  const int forced = e ? atoi(e) : 0;
+  if (forced == kSplitShort || forced == kSplitLong) return forced;
+  return kSplitLong;
+}
+
+template <bool kPaged, int kSplit, bool kFused>
+void launch_split(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
+  if (G == 1) hipLaunchKernelGGL((attn_split_kernel<1, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else if (G == 2) hipLaunchKernelGGL((attn_split_kernel<2, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 4) hipLaunchKernelGGL((attn_split_kernel<4, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 8) hipLaunchKernelGGL((attn_split_kernel<8, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((attn_split_kernel<16, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+}
+
+template <bool kPaged, bool kFused>
+void launch_split_keys(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
+  if (a.split_keys == kSplitShort) launch_split<kPaged, kSplitShort, kFused>(G, grid, s, a);
+  else launch_split<kPaged, kSplitLong, kFused>(G, grid, s, a);
+}
 
 int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
                 const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, int batch_size,
@@ -436,10 +717,11 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
     skv_set_error("%s: %d query heads per kv head (max 16)", what, G);
     return SKV_EUNSUPPORTED;
   }
-  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) &
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
+       reinterpret_cast<uintptr_t>(workspace)) &
           15u ||
       q_stride_b % 8 || q_stride_h % 8 || kv_stride_b % 8 || kv_stride_h % 8 || kv_stride_s % 8) {
-    skv_set_error("%s: q/K/V rows must be 16-byte aligned", what);
+    skv_set_error("%s: q/K/V rows and the workspace must be 16-byte aligned", what);
     return SKV_EINVAL;
   }
   if (kv_len > kMaxKvLen) {
@@ -456,6 +738,7 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
     skv_set_error("%s: workspace of %lld bytes, %lld needed", what, (long long)workspace_bytes, (long long)need);
     return SKV_EINVAL;
   }
+  const int rows = batch_size * kv_heads;
   AttnArgs a{};
   a.q = q;
   a.q_sb = q_stride_b;
@@ -469,10 +752,11 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
   a.G = G;
   a.L = kv_len;
   a.L_dev = kv_len_dev;
-  a.split_keys = kSplit;
+  a.split_keys = choose_split_keys(rows, kv_len);
   a.splits = splits_for(kv_len, a.split_keys);
   a.scale = scale;
-  a.ws_o = static_cast<float*>(workspace);
+  a.arrivals = static_cast<uint32_t*>(workspace);
+  a.ws_o = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + kArrivalBytes);
   a.ws_ml = a.ws_o + static_cast<int64_t>(batch_size) * q_heads * a.splits * kHeadDim;
   a.out = out;
   a.o_sb = o_stride_b;
@@ -483,18 +767,27 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
   a.chunk = chunk;
   a.pool_slots = pool_slots;
   a.delta = (pool_slots - select_sets) * chunk;
+  a.rows = rows;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(a.splits, batch_size * kv_heads);
-  auto go = [&](auto paged) {
-    constexpr bool P = decltype(paged)::value;
-    if (G == 1) hipLaunchKernelGGL((attn_split_kernel<1, P>), grid, dim3(kThreads), 0, s, a);
-    else if (G == 2) hipLaunchKernelGGL((attn_split_kernel<2, P>), grid, dim3(kThreads), 0, s, a);
-    else if (G <= 4) hipLaunchKernelGGL((attn_split_kernel<4, P>), grid, dim3(kThreads), 0, s, a);
-    else if (G <= 8) hipLaunchKernelGGL((attn_split_kernel<8, P>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_split_kernel<16, P>), grid, dim3(kThreads), 0, s, a);
-  };
-  if (slot) go(std::true_type{});
-  else go(std::false_type{});
+  // The merge folded into the split launch, on request (SKV_ATTN_FUSED=1): rows of at most 64
+  // splits, at least one row per XCD (the rows of one XCD share its 32 CUs), the XCD mapping
+  // confirmed on this device. Not the default: on MI355X it measured even with the second launch
+  // alone (Llama-3-8B shape batch 4: 15.5 vs 15.8 us; batch 8: 23.8 vs 23.6; GLM-4-9B batch 4,
+  // 16 heads merged by one workgroup: 12.2 vs 10.8) and slower inside the pipelined decode step,
+  // beside the other lane's host-link fetch (36.7 vs 23.5 + 10.0 us per lane-layer).
+  const char* fe = getenv("SKV_ATTN_FUSED");
+  bool fused = fe && fe[0] == '1' && rows >= kXcds && rows <= kMaxFusedRows && a.splits <= kMaxFusedSplits &&
+               (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && o_stride_b % 4 == 0 && o_stride_h % 4 == 0;  // 8-byte stores
+  if (fused) fused = fused_mapping(s, &a.xcc_map, &a.misplaced);
+  if (fused) {
+    const dim3 grid(static_cast<unsigned>(kXcds * ((rows + kXcds - 1) / kXcds) * a.splits));
+    if (slot) launch_split_keys<true, true>(G, grid, s, a);
+    else launch_split_keys<false, true>(G, grid, s, a);
+    return skv_check_launch(what);
+  }
+  const dim3 grid(a.splits, rows);
+  if (slot) launch_split_keys<true, false>(G, grid, s, a);
+  else launch_split_keys<false, false>(G, grid, s, a);
   int rc = skv_check_launch(what);
   if (rc) return rc;
   // Several merge groups only when there are chunks for them (the split count by the maximum length).
@@ -540,10 +833,11 @@ extern "C" int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_
 // (hipGetSymbolAddress with that device current) and only that address is handed to kernels;
 // the array's name is a host-side stand-in in host code. The partials need no clearing: every
 // live split writes its own before the merge reads them, and the merge reads live splits only.
+// The arrival counters at its head start at zero (the array is zero when the code object loads)
+// and every fused call leaves them at zero.
 namespace {
 
 constexpr int64_t kNoallocScratchBytes = 32ll << 20;  // 32 MiB per GPU
-constexpr int kMaxDevices = 64;
 
 std::mutex g_scratch_mu;
 void* g_scratch_dev[kMaxDevices] = {};

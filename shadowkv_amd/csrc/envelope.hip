@@ -88,8 +88,11 @@ extern "C" int skv_mfma_peak_probe(int workgroups, int iters, float* sink, int64
     skv_set_error("%s: null or misaligned sink", what);
     return SKV_EINVAL;
   }
-  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 20)) {
-    skv_set_error("%s: workgroups=%d (1..2^20) iters=%d (1..2^20)", what, workgroups, iters);
+  // The product bounds one launch's work: 2^24 workgroup-iterations of 4 waves x 4 MFMA chains is
+  // about 8.8 TFLOP, ~4 ms at the measured rate, far from the GPU's watchdog (the bench runs 2048 x 1024).
+  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 20) ||
+      static_cast<int64_t>(workgroups) * iters > (int64_t{1} << 24)) {
+    skv_set_error("%s: workgroups=%d (1..2^20) iters=%d (1..2^20), product at most 2^24", what, workgroups, iters);
     return SKV_EINVAL;
   }
   if (sink_bytes < static_cast<int64_t>(workgroups) * kThreads * 4) {

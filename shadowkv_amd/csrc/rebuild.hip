@@ -344,15 +344,18 @@ int fused_fetch_workgroups(const skv::FetchArgs<int32_t>& f, int waves) {
 }
 
 template <int kMode, int KS, typename IdxT, int kNW, int kIters, bool kFused>
-void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, const skv::FetchArgs<int32_t>* f) {
+int launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, const skv::FetchArgs<int32_t>* f) {
   // Ranks above 176 need more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU): raise the
   // kernel's limit once.
   const int max_lds = static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) + 2 * kMaxTileRows * sizeof(int32_t) +
                                        kMaxWaves * 16 * kStLd * sizeof(uint16_t));
   if constexpr (kFused && KS == 6 && kIters == 2) {
     // Not instantiated: ranks above 160 with 256-row tiles spill beside the fetch role's
-    // registers, so launch_rebuild gives fused launches of that rank 128-row tiles.
+    // registers, so launch_rebuild gives fused launches of that rank 128-row tiles. Reaching
+    // this is a bug in that choice: fail instead of leaving the key buffer stale.
     (void)grid, (void)lds, (void)stream, (void)a, (void)f;
+    skv_set_error("fetch_misses_rebuild_k_rope: no fused kernel for rank %d with 256-row tiles", a.rank);
+    return SKV_EUNSUPPORTED;
   } else if constexpr (kFused) {
     if (lds > 65536) {
       static const hipError_t raised = hipFuncSetAttribute(
@@ -364,6 +367,7 @@ void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, 
     ff.workgroups = fused_fetch_workgroups(ff, kNW);
     hipLaunchKernelGGL((fetch_rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), dim3(grid.x + ff.workgroups),
                        dim3(kNW * 64), lds, stream, a, ff);
+    return SKV_OK;
   } else {
     (void)f;
     if (lds > 65536) {
@@ -373,30 +377,31 @@ void launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, 
       (void)raised;
     }
     hipLaunchKernelGGL((rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), grid, dim3(kNW * 64), lds, stream, a);
+    return SKV_OK;
   }
 }
 
 template <int kMode, typename IdxT, int kNW, int kIters, bool kFused>
-void launch_tile(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
-                 const skv::FetchArgs<int32_t>* f) {
+int launch_tile(int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
+                const skv::FetchArgs<int32_t>* f) {
   switch (ks) {
-    case 1: launch_ks<kMode, 1, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
-    case 2: launch_ks<kMode, 2, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
-    case 3: launch_ks<kMode, 3, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
-    case 4: launch_ks<kMode, 4, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
-    case 5: launch_ks<kMode, 5, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
-    default: launch_ks<kMode, 6, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f); break;
+    case 1: return launch_ks<kMode, 1, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f);
+    case 2: return launch_ks<kMode, 2, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f);
+    case 3: return launch_ks<kMode, 3, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f);
+    case 4: return launch_ks<kMode, 4, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f);
+    case 5: return launch_ks<kMode, 5, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f);
+    default: return launch_ks<kMode, 6, IdxT, kNW, kIters, kFused>(grid, lds, stream, a, f);
   }
 }
 
 // tile_rows: 256 (4 waves x 2 iterations), 128 (4 x 1) or 64 (2 x 1). kFused: the launch also
 // takes the value fetch's workgroups (fetch_rebuild_kernel).
 template <int kMode, typename IdxT, bool kFused = false>
-void launch_mode(int tile_rows, int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
-                 const skv::FetchArgs<int32_t>* f = nullptr) {
-  if (tile_rows == 256) launch_tile<kMode, IdxT, 4, 2, kFused>(ks, grid, lds, stream, a, f);
-  else if (tile_rows == 128) launch_tile<kMode, IdxT, 4, 1, kFused>(ks, grid, lds, stream, a, f);
-  else launch_tile<kMode, IdxT, 2, 1, kFused>(ks, grid, lds, stream, a, f);
+int launch_mode(int tile_rows, int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
+                const skv::FetchArgs<int32_t>* f = nullptr) {
+  if (tile_rows == 256) return launch_tile<kMode, IdxT, 4, 2, kFused>(ks, grid, lds, stream, a, f);
+  if (tile_rows == 128) return launch_tile<kMode, IdxT, 4, 1, kFused>(ks, grid, lds, stream, a, f);
+  return launch_tile<kMode, IdxT, 2, 1, kFused>(ks, grid, lds, stream, a, f);
 }
 
 // Rows per workgroup: the largest tile that still gives the grid about 1.5 workgroups per CU
@@ -456,18 +461,20 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
   const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * tile_rows * sizeof(int32_t) +
                      static_cast<size_t>(waves) * 16 * kStLd * sizeof(uint16_t);
   const int ks = (a.rank + 31) / 32;
+  int rc;
   if (fetch) {  // (the fused launch: the RoPE modes with int64 chunk ids of skv_rebuild_k_rope)
-    if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
-    else launch_mode<kRopeGlm, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+    if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+    else rc = launch_mode<kRopeGlm, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
   } else if (ids64) {
-    if (mode == kPlain) launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a);
-    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a);
-    else launch_mode<kRopeGlm, int64_t>(tile_rows, ks, grid, lds, stream, a);
+    if (mode == kPlain) rc = launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a);
+    else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a);
+    else rc = launch_mode<kRopeGlm, int64_t>(tile_rows, ks, grid, lds, stream, a);
   } else {
-    if (mode == kPlain) launch_mode<kPlain, int32_t>(tile_rows, ks, grid, lds, stream, a);
-    else if (mode == kRopeHalf) launch_mode<kRopeHalf, int32_t>(tile_rows, ks, grid, lds, stream, a);
-    else launch_mode<kRopeGlm, int32_t>(tile_rows, ks, grid, lds, stream, a);
+    if (mode == kPlain) rc = launch_mode<kPlain, int32_t>(tile_rows, ks, grid, lds, stream, a);
+    else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int32_t>(tile_rows, ks, grid, lds, stream, a);
+    else rc = launch_mode<kRopeGlm, int32_t>(tile_rows, ks, grid, lds, stream, a);
   }
+  if (rc) return rc;
   return skv_check_launch(what);
 }
 

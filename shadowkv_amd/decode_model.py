@@ -197,6 +197,9 @@ class SyntheticDecoder:
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
                                         self.cos_sin)
             cache.use_device_lengths()
+            # The selection launch also moves the value buffer's hits (both buffers' with one lane),
+            # so the value fetch follows it directly; this decoder fetches only through the cache.
+            cache.fold_hit_moves = True
             # One lane: the step runs on the compute stream alone, the value fetch and key rebuild
             # as one launch after a selection that moved both buffers' hits (no cross-stream wait
             # before or after the fetch: GLM-4-9B batch 4 and Llama-3-8B-1M, measured in DESIGN).
@@ -403,16 +406,17 @@ class SyntheticDecoder:
 
     def capture(self, tokens: torch.Tensor, steps: int = 1) -> None:
         """Capture `steps` decode steps (one continuous lane pipeline), reading and then
-        overwriting a static token buffer, in a HIP graph. The graph's only side streams are the
-        lanes' value-fetch and key-rebuild streams, each forked from the capture stream and joined
-        back to it. Nothing runs during capture; host counters touched by the traced Python are
+        overwriting a static token buffer, in a HIP graph, captured on the process's "capture" side
+        stream. The graph's only other streams are the lanes' value-fetch and key-rebuild streams,
+        each forked from the capture stream and joined back to it. Nothing runs during capture; host counters touched by the traced Python are
         restored."""
         self.static_tokens = tokens.clone()
         saved = [(c.gen_offset, c.kv_offset) for c in self._caches()]
         for c in self._caches():
             c.check_capacity(steps)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        # On the process's capture side stream, so the capture adds no stream beyond the fixed set.
+        with torch.cuda.graph(g, stream=side_stream(self.device, "capture")):
             self.static_tokens.copy_(self.decode_steps(self.static_tokens, steps))
         for c, (gen, kv) in zip(self._caches(), saved):
             c.gen_offset, c.kv_offset = gen, kv

@@ -16,6 +16,7 @@ sparse_attn_decode) expose the fused kernels used by the decode path.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -26,7 +27,8 @@ __all__ = [
     "gather_copy", "gather_copy_d2d_with_offsets", "reorder_keys_and_compute_offsets", "gather_copy_with_offsets",
     "apply_rotary_pos_emb_new", "apply_rotary_pos_emb_push_cache_opt", "apply_rotary_pos_emb_push_cache_opt_glm",
     "batch_gather_gemm", "batch_gemm_softmax", "score_gqa_max", "score_logits", "softmax_gqa_max", "select_chunks", "topk_gather", "rebuild_k_rope",
-    "sparse_attn_workspace_bytes", "sparse_attn_decode", "device_address", "select_workspace_bytes",
+    "sparse_attn_workspace_bytes", "sparse_attn_workspace", "sparse_attn_decode", "sparse_attn_xcd_check",
+    "device_address", "select_workspace_bytes",
 ]
 
 
@@ -599,11 +601,26 @@ def sparse_attn_workspace_bytes(batch_size: int, q_heads: int, kv_len: int) -> i
     return int(_lib.lib().skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len))
 
 
+def sparse_attn_workspace(batch_size: int, q_heads: int, kv_len: int, device) -> torch.Tensor:
+    """A zero-filled attention workspace for calls of up to these sizes."""
+    return torch.zeros(sparse_attn_workspace_bytes(batch_size, q_heads, kv_len), dtype=torch.uint8, device=device)
+
+
+def sparse_attn_xcd_check() -> dict:
+    """The one-launch merge's XCD mapping on the current device: state (1 confirmed, -1 not, 0 not
+    probed), the XCC id per blockIdx class mod 8, and whether any fused workgroup ran elsewhere."""
+    st, mp, mis = ctypes.c_int32(0), ctypes.c_uint32(0), ctypes.c_uint32(0)
+    _lib.call("skv_sparse_attn_xcd_check", ctypes.byref(st), ctypes.byref(mp), ctypes.byref(mis))
+    return dict(state=st.value, xcc=[(mp.value >> (4 * x)) & 15 for x in range(8)], misplaced=mis.value)
+
+
 def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, kv_len_dev=None, pool=None):
     """out[b, hq] = softmax(scale q[b,hq] K[b,h,:L]^T) V[b,h,:L], h = hq // (Hq/Hkv).
 
     q: [B, Hq, 128] view; k_cache/v_cache: [B, Hkv, >=kv_len, 128] views; out: [B, Hq, 128];
-    workspace: uint8 device tensor of sparse_attn_workspace_bytes(B, Hq, kv_len) bytes.
+    workspace: uint8 device tensor of sparse_attn_workspace_bytes(B, Hq, kv_len) bytes, zero-filled
+    before its first use (sparse_attn_workspace allocates one); every call leaves its arrival
+    counters at zero again.
     L = kv_len, or, with kv_len_dev (device int32 [1]), the value it holds when the kernel runs,
     clamped to [1, kv_len].
     pool: optional (slot_list [B, Hkv, S] int32, sparse_start, S, chunk, pool_slots): the keys

@@ -136,11 +136,15 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.position_ids = torch.full((L, B, H, self.select_sets), -1, device=device, dtype=torch.int64)
         self.selected_chunks = torch.zeros(B, H, self.select_sets, device=device, dtype=torch.int64)
         self.keep_selected = False  # also emit the selected ids in top-k order into selected_chunks
-        # Fold the value buffer's hit moves into the selection's last launch, so that the value fetch
-        # follows the selection directly (the key buffer's moves stay a launch of the key path,
-        # which overlaps the fetch); _folded[l] names the buffers whose hits the last selection of
-        # layer l already moved, consumed by get_value_cache / get_key_cache.
-        self.fold_hit_moves = True
+        # Optional (off by default, as the reference's get_retrieval_position_ids only computes ids,
+        # offsets and counts): fold the value buffer's hit moves into the selection's last launch,
+        # so that the value fetch follows the selection directly (the key buffer's moves stay a
+        # launch of the key path, which overlaps the fetch). With it on, get_retrieval_position_ids
+        # also moves buffer contents: callers must then fetch through get_value_cache /
+        # get_key_cache / fetch_and_rebuild, which skip the moves already done (_folded[l] names the
+        # buffers whose hits the last selection of layer l moved); a second compaction through the
+        # shadowkv module's gather_copy_with_offsets would move the hits twice.
+        self.fold_hit_moves = False
         self._folded = [set() for _ in range(L)]
         # One-stream fetch (callers that run the whole step on one stream): the selection moves
         # both buffers' hits, and fetch_and_rebuild() issues the value fetch and the key rebuild
@@ -516,8 +520,7 @@ class ShadowKVCache_CPU(KVCacheBase):
 
     def _alloc_attention(self):
         B, Hq = self.batch_size, self.num_attention_heads
-        nbytes = shadowkv.sparse_attn_workspace_bytes(B, Hq, self.buf_len)
-        self.attn_workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        self.attn_workspace = shadowkv.sparse_attn_workspace(B, Hq, self.buf_len, self.device)  # zero-filled
         self.attn_out = torch.empty(B, Hq, self.head_dim, dtype=self.dtype, device=self.device)
 
     def check_capacity(self, incoming: int = 1):

@@ -4,8 +4,9 @@ HIP maps a process's streams onto at most GPU_MAX_HW_QUEUES hardware queues (4 b
 setting of the MI355X hosts this runs on). With more streams than queues, two streams share one
 queue; a cross-stream wait queued in that shared queue ahead of the work it waits for can then
 block the queue for good. The decode path therefore uses at most 4 streams: the caller's compute
-stream and three side streams per device, one per role (the value fetch, the key rebuild, a
-spare), created once and shared by every cache and decoder of the process. Work of different
+stream and three side streams per device, one per role (the value fetch, the key rebuild, and
+the stream a decoder captures its HIP graph on: torch.cuda.graph would otherwise create a capture
+stream of its own), created once and shared by every cache and decoder of the process. Work of different
 caches on one side stream runs in issue order, as the host link serialises the fetches anyway.
 """
 from __future__ import annotations
@@ -15,7 +16,7 @@ import threading
 import torch
 
 MAX_STREAMS = 4  # compute stream + side streams, per process
-ROLES = ("fetch", "rebuild", "spare")
+ROLES = ("fetch", "rebuild", "capture")
 assert len(ROLES) + 1 <= MAX_STREAMS
 
 _lock = threading.Lock()

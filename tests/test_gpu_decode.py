@@ -165,3 +165,35 @@ def test_decode_capacity_is_an_error(gpu):
         cache.update_kv_cache(k, k, 0)
     with pytest.raises(RuntimeError, match="decode capacity"):
         cache.update_kv_cache(k, k, 0)
+
+
+@pytest.mark.parametrize("fold", [False, True])
+def test_selection_moves_buffers_only_when_folding(gpu, fold):
+    """The drop-in get_retrieval_position_ids leaves both buffers untouched, as the reference's
+    does (ids, offsets and counts only); with fold_hit_moves it moves the value buffer's hits, and
+    the cache's get_value_cache then moves nothing a second time (same buffer as the reference
+    sequence of selection + gather_copy_with_offsets)."""
+    print(f"selection buffer side effects, fold_hit_moves={fold}", flush=True)
+    case = make_golden.decode_small_case()
+    q = case["q"].to(gpu).view(1, -1, 1, case["dims"]["D"])
+    caches = []
+    for f in (False, fold):
+        cache = build_cache(case, gpu)
+        cache.fold_hit_moves = f
+        caches.append(cache)
+    ref, cache = caches
+    assert ref.fold_hit_moves is False
+    kb, vb = cache.k_cache_buffer[0].clone(), cache.v_cache_buffer[0].clone()
+    ids = cache.get_retrieval_position_ids(0, q)
+    ref_ids = ref.get_retrieval_position_ids(0, q)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ref_ids)
+    assert torch.equal(cache.k_cache_buffer[0].view(torch.int16), kb.view(torch.int16))
+    hits = int(cache.cnts.sum())
+    assert hits > 0
+    moved = not torch.equal(cache.v_cache_buffer[0].view(torch.int16), vb.view(torch.int16))
+    assert moved == fold
+    cache.get_value_cache(0, ids)
+    ref.get_value_cache(0, ref_ids)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.v_cache_buffer[0].view(torch.int16), ref.v_cache_buffer[0].view(torch.int16))

@@ -96,6 +96,29 @@ def test_low_rank_factors(gpu):
     assert ((svt.cpu().double().norm(dim=-1) - s[..., :R]).abs() / s[..., :R]).max().item() < 1e-3
 
 
+def test_get_svd_head_split(gpu):
+    """ShadowKVCache_CPU.get_svd's per-head SV (shadow.py:437-442): U @ SV[h]^T gives back head h's
+    pre-RoPE keys down to the closed-form noise floor of the rank-R truncation, on both fixtures;
+    the transposed split of the same factors does not."""
+    from tests import svd_pins
+
+    for case in (make_golden.decode_small_case(), make_golden.single_layer_case()):
+        k_pre, d = case["k_pre"], case["dims"]
+        _say(f"get_svd head split H={d['H']} ctx={d['ctx']} rank={d['rank']}")
+        B, H, ctx, D = k_pre.shape
+        cfg = types.SimpleNamespace(num_attention_heads=H * d["G"], num_key_value_heads=H, hidden_size=H * d["G"] * D,
+                                    num_hidden_layers=1)
+        cache = ShadowKVCache_CPU(cfg, batch_size=B, max_length=ctx, device=str(gpu), sparse_budget=d["budget"],
+                                  chunk_size=d["chunk"], rank=d["rank"])
+        cache.get_svd(k_pre.to(gpu), 0)
+        torch.cuda.synchronize()
+        U, SV = cache.U[0].cpu(), cache.SV[0].cpu()
+        err = svd_pins.head_errors(k_pre, U, SV)
+        lim = svd_pins.bound(k_pre, d["rank"])
+        assert (err <= lim).all(), (err, lim)
+        assert (svd_pins.head_errors(k_pre, U, svd_pins.transposed_split(SV)) > 2 * lim).all()
+
+
 def _prefill_on_gpu(gpu, k_pre, v, q_pre_last, cos_sin, chunk, budget, rank):
     B, H, ctx, D = k_pre.shape
     Hq = q_pre_last.shape[1]

@@ -84,3 +84,5 @@ def test_mfma_probe_flops_and_output(gpu):
     from shadowkv_amd import _lib
     with pytest.raises(RuntimeError, match="sink of"):  # and the library's own
         _lib.call("skv_mfma_peak_probe", 4, 5, sink.data_ptr(), sink.numel() * 4, 0)
+    with pytest.raises(RuntimeError, match="product at most"):  # one launch's work is bounded
+        _lib.call("skv_mfma_peak_probe", 1 << 13, 1 << 12, sink.data_ptr(), 1 << 40, 0)

@@ -276,7 +276,7 @@ def test_sparse_attention(gpu, B, Hq, Hk, L, strided):
     V = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
     q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16)
     want = oracle.sparse_attention(q, K, V, L)
-    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+    ws = shadowkv.sparse_attn_workspace(B, Hq, L, gpu)
     out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
     shadowkv.sparse_attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), L, out, ws)
     torch.cuda.synchronize()
@@ -291,7 +291,7 @@ def test_attention_identical_keys_is_mean_of_values(gpu):
     K = torch.randn(B, Hk, 1, 128).to(torch.bfloat16).expand(-1, -1, L, -1).contiguous()
     V = torch.randn(B, Hk, L, 128).to(torch.bfloat16)
     q = torch.randn(B, Hq, 128).to(torch.bfloat16)
-    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+    ws = shadowkv.sparse_attn_workspace(B, Hq, L, gpu)
     out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
     shadowkv.sparse_attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), L, out, ws)
     torch.cuda.synchronize()
@@ -307,7 +307,7 @@ def test_attention_device_length_matches_host_length(gpu):
     K = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
     V = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
     q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16).to(gpu)
-    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, Lmax), dtype=torch.uint8, device=gpu)
+    ws = shadowkv.sparse_attn_workspace(B, Hq, Lmax, gpu)
     ldev = torch.zeros(1, dtype=torch.int32, device=gpu)
     for L, eff in ((1, 1), (255, 255), (256, 256), (257, 257), (1024, 1024), (1100, 1100), (0, 1), (5000, 1100)):
         _say(f"attention device length {L}")
@@ -315,7 +315,7 @@ def test_attention_device_length_matches_host_length(gpu):
         got = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
         shadowkv.sparse_attn_decode(q, K, V, Lmax, got, ws, kv_len_dev=ldev)
         want = torch.empty_like(got)
-        ws2 = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, eff), dtype=torch.uint8, device=gpu)
+        ws2 = shadowkv.sparse_attn_workspace(B, Hq, eff, gpu)
         shadowkv.sparse_attn_decode(q, K, V, eff, want, ws2)
         torch.cuda.synchronize()
         assert torch.equal(got.cpu(), want.cpu()), L
@@ -323,15 +323,19 @@ def test_attention_device_length_matches_host_length(gpu):
         torch.testing.assert_close(got.cpu().float(), ref.float(), rtol=RTOL, atol=ATOL)
 
 
-def test_attention_device_length_long_rows(gpu):
-    """Rows long enough for several merge groups (more than 32 splits): a device length below the
-    maximum merges in the same order as the same host length (bit for bit)."""
+def test_attention_device_length_long_rows(gpu, monkeypatch):
+    """Rows long enough for several merge groups (more than 32 splits) of the two-launch merge: a
+    device length below the maximum merges in the same order as the same host length (bit for
+    bit). The split size and the merge are pinned (by default the shorter host lengths would take
+    64-key splits and the one-launch merge, which sum in another order)."""
+    monkeypatch.setenv("SKV_ATTN_SPLIT", "128")
+    monkeypatch.setenv("SKV_ATTN_FUSED", "0")
     B, Hq, Hk, Lmax = 1, 32, 8, 12000
     g = torch.Generator().manual_seed(4)
     K = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
     V = torch.randn(B, Hk, Lmax, 128, generator=g).to(torch.bfloat16).to(gpu)
     q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16).to(gpu)
-    ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, Lmax), dtype=torch.uint8, device=gpu)
+    ws = shadowkv.sparse_attn_workspace(B, Hq, Lmax, gpu)
     ldev = torch.zeros(1, dtype=torch.int32, device=gpu)
     for L in (3000, 4096, 4097, 8300, 12000):
         _say(f"attention long rows, device length {L}")
@@ -339,7 +343,7 @@ def test_attention_device_length_long_rows(gpu):
         got = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
         shadowkv.sparse_attn_decode(q, K, V, Lmax, got, ws, kv_len_dev=ldev)
         want = torch.empty_like(got)
-        ws2 = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+        ws2 = shadowkv.sparse_attn_workspace(B, Hq, L, gpu)
         shadowkv.sparse_attn_decode(q, K, V, L, want, ws2)
         torch.cuda.synchronize()
         assert torch.equal(got.cpu(), want.cpu()), L
@@ -466,7 +470,7 @@ def test_sparse_attention_random_shapes(gpu):
         V = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
         q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16)
         want = oracle.sparse_attention(q, K, V, L)
-        ws = torch.empty(shadowkv.sparse_attn_workspace_bytes(B, Hq, L), dtype=torch.uint8, device=gpu)
+        ws = shadowkv.sparse_attn_workspace(B, Hq, L, gpu)
         out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
         shadowkv.sparse_attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), L, out, ws)
         torch.cuda.synchronize()

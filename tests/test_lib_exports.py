@@ -62,7 +62,8 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert rc == 1 and "k=200" in _lib.last_error()
     rc = lib.skv_batch_gemm_softmax(p, p, p, p, p, p, 1, 4, 10, 64, 1.0, 0.0, None)
     assert rc == 2 and "k=64" in _lib.last_error()
-    assert lib.skv_sparse_attn_workspace_bytes(8, 32, 2600) == 8 * 32 * 21 * 130 * 4  # 128-key splits
+    # the arrival counters (4096 rows x 4 bytes), then the partials of 64-key splits (the shorter choice)
+    assert lib.skv_sparse_attn_workspace_bytes(8, 32, 2600) == 16384 + 8 * 32 * 41 * 130 * 4
 
 
 def test_selection_workspace_plan():

@@ -257,3 +257,22 @@ def test_rope_two_tables_bit_exact_vs_numpy():
     ch = torch.cat((c[:, :64], c[:, :64]), dim=-1)
     sh = torch.cat((s[:, :64], s[:, :64]), dim=-1)
     assert torch.equal(oracle.rope_two_tables(x, ch, sh), oracle.rope_half_split(x, c[:, :64], s[:, :64]))
+
+
+def test_encode_layer_sv_head_split():
+    """encode_layer's per-head SV (shadow.py:437-442): for every head of both fixtures U @ SV[h]^T
+    gives back that head's pre-RoPE keys down to the noise the rank-R truncation must leave; a
+    transposed split and a head permutation of the same factors exceed the bound over twice."""
+    from tests import svd_pins
+
+    for case in (make_golden.decode_small_case(), make_golden.single_layer_case()):
+        st, k_pre, R = case["st"], case["k_pre"], case["dims"]["rank"]
+        err = svd_pins.head_errors(k_pre, st.U, st.SV)
+        lim = svd_pins.bound(k_pre, R)
+        floor = svd_pins.noise_floor(k_pre, R)
+        assert (err <= lim).all(), (err, lim)
+        assert (err >= 0.97 * floor).all(), (err, floor)  # not better than the noise allows
+        wrong = svd_pins.head_errors(k_pre, st.U, svd_pins.transposed_split(st.SV))
+        assert (wrong > 2 * lim).all(), (wrong, lim)
+        swapped = svd_pins.head_errors(k_pre, st.U, st.SV.flip(1))
+        assert (swapped > 2 * lim).all(), (swapped, lim)

@@ -56,6 +56,40 @@ def test_side_streams_are_limited_to_the_hardware_queues(monkeypatch):
         streams.side_stream("cuda:0", "lane2")
 
 
+def test_decoder_capture_stays_on_the_fixed_streams(monkeypatch):
+    """SyntheticDecoder.capture hands torch.cuda.graph the process's capture side stream (a
+    stand-in graph context records it), so a capture creates no stream of its own."""
+    from shadowkv_amd import decode_model, streams
+
+    class FakeStream:
+        def __init__(self, device=None):
+            self.device = device
+
+    seen = []
+
+    class FakeGraphCtx:
+        def __init__(self, graph, stream=None, **kw):
+            seen.append(stream)
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *exc):
+            return False
+
+    monkeypatch.setattr(streams.torch.cuda, "Stream", FakeStream)
+    monkeypatch.setattr(streams, "_streams", {})
+    monkeypatch.setattr(decode_model.torch.cuda, "CUDAGraph", lambda: object())
+    monkeypatch.setattr(decode_model.torch.cuda, "graph", FakeGraphCtx)
+    dec = decode_model.SyntheticDecoder.__new__(decode_model.SyntheticDecoder)
+    dec.device = "cuda:0"
+    dec.lanes = []
+    dec.decode_steps = lambda tokens, steps: tokens
+    dec.capture(torch.zeros(2, 1, dtype=torch.long), steps=2)
+    assert seen == [streams.side_stream("cuda:0", "capture")]
+    assert streams.side_streams_created() + 1 <= streams.MAX_STREAMS
+
+
 def test_qkv_rope_weight_row_order():
     """The QKV weight (and bias) row order of the RoPE epilogue, on the CPU: each q and k head's rows
     interleaved as (0, 64, 1, 65, ...) so that a rotation pair (d, d + 64) sits in adjacent rows, v

@@ -24,7 +24,7 @@ def _run_ws(q, k, v, L, L_dev, out):
     B, Hq = q.shape[0], q.shape[1]
     lib = _lib.lib()
     nbytes = lib.skv_sparse_attn_workspace_bytes(B, Hq, L)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=q.device)  # zero-filled before first use
     rc = lib.skv_sparse_attn_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), k.stride(0),
                                     k.stride(1), k.stride(2), B, Hq, k.shape[1], 128, L,
                                     L_dev.data_ptr() if L_dev is not None else None, 128 ** -0.5, ws.data_ptr(),
