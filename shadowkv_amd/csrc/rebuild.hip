@@ -9,9 +9,11 @@
 // bf16 k(r) itself is written (reference batch_gather_gemm output).
 //
 // Work decomposition (gfx950, wave64):
-//   * workgroup = kNW waves, owns kTileRows = kNW x kIters x 32 consecutive rows of one head
+//   * workgroup = kNW waves, owns up to kTileRows = kNW x kIters x 32 consecutive rows of one head
 //     (256 = 4 waves x 2 iterations when the grid has enough workgroups to fill the GPU, else
-//     128 = 4 x 1 or 64 = 2 x 1, so that few rows still spread over the CUs). At entry it stages
+//     128 = 4 x 1 or 64 = 2 x 1, so that few rows still spread over the CUs); the grid has the
+//     tiles of a head with no hits, and a head's miss rows are dealt evenly over its tiles, so
+//     hits shorten every workgroup instead of idling some. At entry it stages
 //     SV of that head (128 x rank bf16, 40 KB at rank 160) and the U row of each of its rows
 //     (chunk id * chunk + r % chunk) into LDS;
 //   * a wave computes 32 rows x 128 columns per iteration, two iterations, with
@@ -62,6 +64,7 @@ struct RebuildArgs {
   int64_t o_sb, o_sh, o_ss;
   int o_start;
   int B, H, S, chunk, rank, tiles;
+  int spread;  // deal a head's miss rows evenly over its tiles (else whole tiles, hit tiles idle)
   // Optional destination slots (chunk pool): row r of entry i goes to cache row
   // o_start + dst_slot[i] * chunk + r % chunk; entries outside [0, pool_slots) are skipped.
   const int32_t* dst_slot;
@@ -124,10 +127,16 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
   const int b = head / a.H;
   const int h = head - b * a.H;
 
+  // spread: the head's miss rows [miss_begin, total_rows) are dealt evenly over its a.tiles
+  // workgroups in 32-row blocks (span <= kTileRows, as a.tiles covers total_rows), so cache hits
+  // shorten every workgroup of the head instead of idling whole tiles. Otherwise tile t owns rows
+  // [t, t + 1) x kTileRows and tiles of hits only return at once.
   const int total_rows = a.S * a.chunk;
   const int miss_begin = min(a.cnts[head], a.S) * a.chunk;
-  const int row_begin = tile * kTileRows;
-  const int row_end = min(row_begin + kTileRows, total_rows);
+  const int miss_rows = total_rows - miss_begin;
+  const int span = a.spread ? ((miss_rows + a.tiles - 1) / a.tiles + 31) / 32 * 32 : kTileRows;
+  const int row_begin = a.spread ? miss_begin + tile * span : tile * kTileRows;
+  const int row_end = min(row_begin + span, total_rows);
   if (row_end <= miss_begin || row_begin >= row_end) return;
 
   // Issue order (vector loads retire in order): this thread's chunk id, the SV tile, then, after
@@ -176,11 +185,13 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
   uint16_t* st = kst + wave * 16 * kStLd;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  const int lr0 = wave * kIters * 32;
+  // 32-row block of iteration it: blocks go to the waves first (block it * kNW + wave), so a span
+  // shorter than the tile keeps every wave busy on its first iteration.
+  auto lr_of = [&](int it) { return (it * kNW + wave) * 32; };
   bool active[kIters];
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
-    const int rb = row_begin + lr0 + it * 32;
+    const int rb = row_begin + lr_of(it);
     active[it] = rb < row_end && rb + 32 > miss_begin;  // wave-uniform
   }
   // U fragments (B operand) of both 32-row blocks.
@@ -189,7 +200,7 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
   for (int it = 0; it < kIters; ++it) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const int r = lr0 + it * 32 + m * 16 + li;
+      const int r = lr_of(it) + m * 16 + li;
       const int grow = row_begin + r;
       const int32_t pos = pos_lds[r];
       const bool valid = active[it] && grow >= miss_begin && grow < row_end && pos >= 0 && pos < a.u_rows;
@@ -214,7 +225,7 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
         if (kMode == kPlain) continue;
         const int unit = lane + 64 * q;
         const int r = unit / U::kPerRow, j = unit % U::kPerRow;
-        const int32_t pos = pos_lds[lr0 + it * 32 + m * 16 + r];
+        const int32_t pos = pos_lds[lr_of(it) + m * 16 + r];
         const bool ok = active[it] && pos >= 0 && pos < a.cs_rows;
         const uint16_t* c = a.cs + static_cast<int64_t>(ok ? pos : 0) * a.cs_stride;
         if (kMode == kRopeHalf) {
@@ -240,7 +251,7 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     if (!active[it]) continue;
-    const int lr = lr0 + it * 32;
+    const int lr = lr_of(it);
 
     f32x4_t acc[2][8];
 #pragma unroll
@@ -349,12 +360,12 @@ int launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, c
   // kernel's limit once.
   const int max_lds = static_cast<int>(kHeadDim * (kMaxRank + 8) * sizeof(uint16_t) + 2 * kMaxTileRows * sizeof(int32_t) +
                                        kMaxWaves * 16 * kStLd * sizeof(uint16_t));
-  if constexpr (kFused && KS == 6 && kIters == 2) {
-    // Not instantiated: ranks above 160 with 256-row tiles spill beside the fetch role's
-    // registers, so launch_rebuild gives fused launches of that rank 128-row tiles. Reaching
-    // this is a bug in that choice: fail instead of leaving the key buffer stale.
+  if constexpr (KS == 6 && kIters == 2) {
+    // Not instantiated: ranks above 160 with 256-row tiles spill, so launch_rebuild gives that
+    // rank 128-row tiles. Reaching this is a bug in that choice: fail instead of leaving the key
+    // buffer stale.
     (void)grid, (void)lds, (void)stream, (void)a, (void)f;
-    skv_set_error("fetch_misses_rebuild_k_rope: no fused kernel for rank %d with 256-row tiles", a.rank);
+    skv_set_error("rebuild_k_rope: no kernel for rank %d with 256-row tiles", a.rank);
     return SKV_EUNSUPPORTED;
   } else if constexpr (kFused) {
     if (lds > 65536) {
@@ -453,9 +464,17 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
   }
   const int BH = a.B * a.H;
   int tile_rows = choose_tile_rows(BH, a.S * a.chunk);
-  if (fetch && tile_rows == 256 && a.rank > 160) tile_rows = 128;  // (no spill-free fused 256-row kernel there)
+  if (tile_rows == 256 && a.rank > 160) tile_rows = 128;  // (no spill-free 256-row kernel there)
   const int waves = tile_rows == 64 ? 2 : 4;
   a.tiles = (a.S * a.chunk + tile_rows - 1) / tile_rows;
+  // Deal the miss rows over every tile while the grid is at most ~4 workgroups per CU (all of it
+  // in flight at once: hits then shorten each workgroup; MI355X, batch 8 with 154 of 256 chunks
+  // hit, 18.2 -> 13.5 us); larger grids keep whole tiles, which stage SV once per 256 rows
+  // (batch 32: 39.6 vs 45.3 us). SKV_REBUILD_SPREAD=0/1 forces either.
+  {
+    const char* e = getenv("SKV_REBUILD_SPREAD");
+    a.spread = e ? (e[0] == '1') : (static_cast<int64_t>(BH) * a.tiles <= 1024);
+  }
   const int heads_padded = (BH + kXcds - 1) / kXcds * kXcds;
   const dim3 grid(static_cast<unsigned>(heads_padded * a.tiles));
   const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * tile_rows * sizeof(int32_t) +

@@ -353,8 +353,9 @@ def test_attention_device_length_long_rows(gpu, monkeypatch):
 
 @pytest.mark.parametrize("glm", [False, True])
 def test_rebuild_tile_shapes_agree(gpu, glm, monkeypatch):
-    """Workgroups of 256, 128 and 64 rows (chosen by the grid size, forced here) run the same
-    per-row MFMA sequence: bit-identical keys, and within tolerance of the oracle."""
+    """Workgroups of 256, 128 and 64 rows (chosen by the grid size, forced here), with the miss
+    rows in whole tiles or dealt evenly over every tile (also chosen by the grid size), run the
+    same per-row MFMA sequence: bit-identical keys, and within tolerance of the oracle."""
     B, H, ctx, R, S, c = 2, 8, 4096, 160, 256, 8
     _say(f"rebuild tile shapes glm={glm}")
     U, SV, ids, cnts = _rebuild_case(B, H, ctx, R, S, c, 21, True, False)
@@ -363,12 +364,14 @@ def test_rebuild_tile_shapes_agree(gpu, glm, monkeypatch):
     cache = torch.randn(B, H, start + S * c + 32, 128).to(torch.bfloat16)
     outs = []
     for tile in (256, 128, 64):
-        monkeypatch.setenv("SKV_REBUILD_TILE", str(tile))
-        cg = cache.to(gpu)
-        shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
-        torch.cuda.synchronize()
-        outs.append(cg.cpu())
-    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+        for spread in ("0", "1"):  # whole tiles (hit tiles idle) or the miss rows dealt over every tile
+            monkeypatch.setenv("SKV_REBUILD_TILE", str(tile))
+            monkeypatch.setenv("SKV_REBUILD_SPREAD", spread)
+            cg = cache.to(gpu)
+            shadowkv.rebuild_k_rope(U.to(gpu), SV.to(gpu), ids.to(gpu), cnts.to(gpu), cs.to(gpu), cg, start, c)
+            torch.cuda.synchronize()
+            outs.append(cg.cpu())
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
     want = oracle.rebuild_k_rope(U, SV, ids, cnts, cs, c, cache.clone(), start, glm=glm)
     torch.testing.assert_close(outs[0].float(), want.float(), rtol=RTOL, atol=ATOL)
 
