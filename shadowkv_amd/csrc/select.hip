@@ -588,11 +588,13 @@ __global__ void __launch_bounds__(kThreads) select_kernel(SelectArgs a) {
 // one workgroup per (slice, row):
 //   part_hist_kernel<1>: high-byte histogram of the slice            -> h1[row][part][256]
 //   part_hist_kernel<2>: bin b1 of the S-th largest key from sum(h1); low-byte histogram of the
-//                        slice's keys in bin b1                      -> h2[row][part][256]
-//   part_count_kernel:   threshold T (S-th largest key) from sum(h1), sum(h2); the slice's counts
-//                        of keys > T and == T                        -> cnt[row][part]
-//   part_emit_kernel:    the slice's winners (keys > T, and keys == T ranked by index among all
-//                        ties, the lowest need_eq indices winning) at their rank positions
+//                        slice's keys in bin b1, and its count of keys above bin b1
+//                                                                    -> h2[row][part][256], cnt[row][part][0]
+//   part_emit_kernel:    threshold T (S-th largest key) from sum(h1), sum(h2); the slice's first
+//                        ranks from the earlier slices' counts above b1 and low-byte histograms
+//                        (so no launch counts the slices' keys > T and == T first); the slice's
+//                        winners (keys > T, and keys == T ranked by index among all ties, the
+//                        lowest need_eq indices winning) at their rank positions
 //                                                                    -> win[row][0, S)
 //   select_finish_kernel (one workgroup per row): winners' chunk ids into the selection bitmap,
 //                        the reorder, and the top-k order when requested.
@@ -605,10 +607,11 @@ struct PartArgs {
   int n, S, parts, part_len;
   uint32_t* h1;   // [rows][parts][256]
   uint32_t* h2;   // [rows][parts][256]
-  int32_t* cnt;   // [rows][parts][2]: keys > T, keys == T
-  int32_t* thr;   // [rows][4]: T, keys > T over the row, ties that win
+  int32_t* cnt;   // [rows][parts][2]: [0] the slice's keys above the threshold's high-byte bin
+  int32_t* hb;    // [rows][4]: [0] the threshold's high-byte bin b1, [1] the row's keys above it
   uint64_t* win;  // [rows][S]: (0xffff - key) << 32 | landmark index
   int h1_parts;   // partial histograms per row in h1 (parts, or the softmax kernel's workgroups)
+  int vec;        // rows of 16-byte aligned, multiple-of-8 length: keys loaded as 16-byte vectors
 };
 
 // Sums the rows' partial histograms h[parts][256] into tot and finds the bin of the want-th
@@ -650,11 +653,29 @@ __device__ __forceinline__ void load_part_keys(const PartArgs& a, int row, int p
   const int lo = min(j1, j0 + static_cast<int>(threadIdx.x) * E), hi = min(j1, lo + E);
   const uint16_t* sr = a.scores + static_cast<int64_t>(row) * a.n;
   uint32_t v = 0;
+  if (a.vec && (E & 7) == 0) {
+    // 16-byte vectors: j0, E and n are multiples of 8 here, so a vector is either wholly inside
+    // [lo, hi) or wholly past it.
 #pragma unroll
-  for (int u = 0; u < kPartE; ++u) {
-    const bool ok = u < E && lo + u < hi;
-    kv[u] = skv::bf16_order_key(sr[ok ? lo + u : 0]);
-    v |= static_cast<uint32_t>(ok) << u;
+    for (int w = 0; w < kPartE / 8; ++w) {
+      const int j = lo + 8 * w;
+      const bool ok = 8 * w < E && j < hi;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(sr + (ok ? j : 0));
+      const uint32_t words[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kv[8 * w + 2 * e] = skv::bf16_order_key(static_cast<uint16_t>(words[e] & 0xffffu));
+        kv[8 * w + 2 * e + 1] = skv::bf16_order_key(static_cast<uint16_t>(words[e] >> 16));
+      }
+      v |= (ok ? 0xffu : 0u) << (8 * w);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kPartE; ++u) {
+      const bool ok = u < E && lo + u < hi;
+      kv[u] = skv::bf16_order_key(sr[ok ? lo + u : 0]);
+      v |= static_cast<uint32_t>(ok) << u;
+    }
   }
   *valid = v;
   *lo_out = lo;
@@ -666,12 +687,17 @@ __global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
   __shared__ uint32_t tot[256];
   __shared__ uint32_t part_tot[kPartThreads / 64][256];
   __shared__ int found[2];
+  __shared__ int scan[kPartThreads / 64 + 1];
   const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   for (int b = tid; b < 256; b += kPartThreads) hist[b] = 0;
   uint32_t b1 = 0;
   if (kPass == 2) {
     sum_select(a.h1 + static_cast<int64_t>(row) * a.h1_parts * 256, a.h1_parts, a.S, tot, part_tot, found);
     b1 = static_cast<uint32_t>(found[0]);
+    if (part == 0 && tid == 0) {  // for the emit pass, which then sums only the low-byte histograms
+      a.hb[row * 4] = found[0];
+      a.hb[row * 4 + 1] = found[1];
+    }
   } else {
     __syncthreads();
   }
@@ -682,6 +708,7 @@ __global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
   // adjacent high-byte bins), LDS atomics outside that window; pass 2 spreads over 256 bins.
   uint32_t wc[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
   int wbase = -1;
+  int above = 0;  // pass 2: keys above bin b1
 #pragma unroll
   for (int u = 0; u < kPartE; ++u) {
     if (!((valid >> u) & 1u)) continue;
@@ -698,6 +725,8 @@ __global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
       }
     } else if ((k >> 8) == b1) {
       atomicAdd(&hist[k & 255u], 1u);
+    } else {
+      above += (k >> 8) > b1;
     }
   }
   if (kPass == 1) {
@@ -708,81 +737,55 @@ __global__ void __launch_bounds__(kPartThreads) part_hist_kernel(PartArgs a) {
   __syncthreads();
   uint32_t* out = (kPass == 1 ? a.h1 : a.h2) + (static_cast<int64_t>(row) * a.parts + part) * 256;
   for (int b = tid; b < 256; b += kPartThreads) out[b] = hist[b];
+  if (kPass == 2) {
+    int total;
+    skv::block_exclusive_scan(above, scan, &total);
+    if (tid == 0) a.cnt[(static_cast<int64_t>(row) * a.parts + part) * 2] = total;
+  }
 }
 
-// T, keys > T over the row (c_gt) and the ties that win (need_eq), from the summed histograms.
+// T, keys > T over the row (c_gt) and the ties that win (need_eq): the high-byte bin b1 as the
+// histogram pass found it, the low byte from the summed low-byte histograms.
 __device__ void row_threshold(const PartArgs& a, int row, uint32_t* tot, uint32_t (*part_tot)[256], int* found,
                               uint32_t* T, int* c_gt, int* need_eq) {
-  sum_select(a.h1 + static_cast<int64_t>(row) * a.h1_parts * 256, a.h1_parts, a.S, tot, part_tot, found);
-  const uint32_t b1 = static_cast<uint32_t>(found[0]);
-  const int above1 = found[1];
-  __syncthreads();  // tot and found are rewritten below
+  const uint32_t b1 = static_cast<uint32_t>(a.hb[row * 4]);
+  const int above1 = a.hb[row * 4 + 1];
   sum_select(a.h2 + static_cast<int64_t>(row) * a.parts * 256, a.parts, a.S - above1, tot, part_tot, found);
   *T = (b1 << 8) | static_cast<uint32_t>(found[0]);
   *c_gt = above1 + found[1];
   *need_eq = a.S - *c_gt;
 }
 
-__global__ void __launch_bounds__(kPartThreads) part_count_kernel(PartArgs a) {
+__global__ void __launch_bounds__(kPartThreads) part_emit_kernel(PartArgs a) {
   __shared__ uint32_t tot[256];
   __shared__ uint32_t part_tot[kPartThreads / 64][256];
   __shared__ int found[2];
   __shared__ int scan[kPartThreads / 64 + 1];
   const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  // Blocked ownership: thread t holds keys [lo, lo + E) of the slice in index order (requested
+  // first, so their latency overlaps the threshold's histogram sums).
+  uint32_t kv[kPartE], valid;
+  int lo;
+  load_part_keys(a, row, part, kv, &valid, &lo);
   uint32_t T;
   int c_gt, need_eq;
   row_threshold(a, row, tot, part_tot, found, &T, &c_gt, &need_eq);
-  uint32_t kv[kPartE], valid;
-  int lo;
-  load_part_keys(a, row, part, kv, &valid, &lo);
-  int gt = 0, eq = 0;
-#pragma unroll
-  for (int u = 0; u < kPartE; ++u) {
-    const bool ok = (valid >> u) & 1u;
-    gt += ok && kv[u] > T;
-    eq += ok && kv[u] == T;
-  }
-  int gt_total, eq_total;
-  skv::block_exclusive_scan(gt, scan, &gt_total);
-  skv::block_exclusive_scan(eq, scan, &eq_total);
-  if (tid == 0) {
-    int32_t* c = a.cnt + (static_cast<int64_t>(row) * a.parts + part) * 2;
-    c[0] = gt_total;
-    c[1] = eq_total;
-    if (part == 0) {
-      int32_t* t = a.thr + static_cast<int64_t>(row) * 4;
-      t[0] = static_cast<int32_t>(T);
-      t[1] = c_gt;
-      t[2] = need_eq;
-    }
-  }
-}
-
-__global__ void __launch_bounds__(kPartThreads) part_emit_kernel(PartArgs a) {
-  __shared__ int scan[kPartThreads / 64 + 1];
-  __shared__ int bases[2];
-  const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-  const int32_t* t = a.thr + static_cast<int64_t>(row) * 4;
-  const uint32_t T = static_cast<uint32_t>(t[0]);
-  const int c_gt = t[1], need_eq = t[2];
-  if (tid < 64) {  // this slice's first ranks: the counts of the slices before it
+  // This slice's first ranks: over the slices before it, the keys above bin b1 (counted by pass
+  // 2) plus those of bin b1 above T's low byte, and the ties (low byte == T's), from their
+  // low-byte histograms (thread t sums bin t).
+  const uint32_t tl = T & 255u;
+  int bin_sum = 0, hi_sum = 0;
+  {
+    const uint32_t* h2 = a.h2 + static_cast<int64_t>(row) * a.parts * 256 + tid;
+    for (int q = 0; q < part; ++q) bin_sum += static_cast<int>(h2[q * 256]);
     const int32_t* c = a.cnt + static_cast<int64_t>(row) * a.parts * 2;
-    int g = 0, e = 0;
-    for (int q = tid; q < part; q += 64) {
-      g += c[2 * q];
-      e += c[2 * q + 1];
-    }
-    g = __builtin_amdgcn_readlane(skv::wave_inclusive_scan(g), 63);
-    e = __builtin_amdgcn_readlane(skv::wave_inclusive_scan(e), 63);
-    if (tid == 0) {
-      bases[0] = g;
-      bases[1] = e;
-    }
+    for (int q = tid; q < part; q += kPartThreads) hi_sum += c[2 * q];
   }
-  // Blocked ownership: thread t holds keys [lo, lo + E) of the slice in index order.
-  uint32_t kv[kPartE], valid;
-  int lo;
-  load_part_keys(a, row, part, kv, &valid, &lo);
+  int base_gt, base_eq, hi_total;
+  skv::block_exclusive_scan(static_cast<uint32_t>(tid) > tl ? bin_sum : 0, scan, &base_gt);
+  skv::block_exclusive_scan(static_cast<uint32_t>(tid) == tl ? bin_sum : 0, scan, &base_eq);
+  skv::block_exclusive_scan(hi_sum, scan, &hi_total);
+  base_gt += hi_total;
   int gt = 0, eq = 0;
 #pragma unroll
   for (int u = 0; u < kPartE; ++u) {
@@ -793,8 +796,8 @@ __global__ void __launch_bounds__(kPartThreads) part_emit_kernel(PartArgs a) {
   int gt_total, eq_total;
   int gr = skv::block_exclusive_scan(gt, scan, &gt_total);
   int er = skv::block_exclusive_scan(eq, scan, &eq_total);
-  gr += bases[0];
-  er += bases[1];
+  gr += base_gt;
+  er += base_eq;
   uint64_t* w = a.win + static_cast<int64_t>(row) * a.S;
 #pragma unroll
   for (int u = 0; u < kPartE; ++u) {
@@ -864,7 +867,7 @@ void part_plan(int rows, int n, int* parts, int* part_len) {
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
-// Workspace layout of skv_select_chunks_ws: h1, h2, cnt, thr, win, then the softmax kernel's
+// Workspace layout of skv_select_chunks_ws: h1, h2, cnt, hb, win, then the softmax kernel's
 // per-workgroup key histograms (hs: [rows][softmax_hist_parts][256]; *hs_out when asked).
 size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws, uint32_t** hs_out = nullptr) {
   int parts, len;
@@ -882,7 +885,7 @@ size_t part_workspace(int rows, int n, int S, PartArgs* pa, void* ws, uint32_t**
     pa->h1_parts = parts;
     pa->h2 = reinterpret_cast<uint32_t*>(p + h);
     pa->cnt = reinterpret_cast<int32_t*>(p + 2 * h);
-    pa->thr = reinterpret_cast<int32_t*>(p + 2 * h + c);
+    pa->hb = reinterpret_cast<int32_t*>(p + 2 * h + c);
     pa->win = reinterpret_cast<uint64_t*>(p + 2 * h + c + t);
   }
   if (hs_out) *hs_out = hs ? reinterpret_cast<uint32_t*>(p + 2 * h + c + t + wn) : nullptr;
@@ -1034,6 +1037,7 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
     pa.scores = out_scores;
     pa.n = n;
     pa.S = select_sets;
+    pa.vec = n % 8 == 0 && (reinterpret_cast<uintptr_t>(out_scores) & 15u) == 0;
     part_workspace(rows, n, select_sets, &pa, workspace);
     const dim3 pg(pa.parts, rows);
     if (hs) {  // the high-byte histograms are the softmax kernel's
@@ -1043,7 +1047,6 @@ int select_impl(const char* what, const uint16_t* D, const float* norm, const fl
       hipLaunchKernelGGL(part_hist_kernel<1>, pg, dim3(kPartThreads), 0, st, pa);
     }
     hipLaunchKernelGGL(part_hist_kernel<2>, pg, dim3(kPartThreads), 0, st, pa);
-    hipLaunchKernelGGL(part_count_kernel, pg, dim3(kPartThreads), 0, st, pa);
     hipLaunchKernelGGL(part_emit_kernel, pg, dim3(kPartThreads), 0, st, pa);
     const size_t fb = (fixed + 15) / 16 * 16;
     hipLaunchKernelGGL(select_finish_kernel, dim3(rows), dim3(kThreads), fb, st, a, pa);
