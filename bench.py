@@ -87,6 +87,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-breakdown", action="store_true")
+    p.add_argument("--summarize-trace", metavar="CSV",
+                   help="summarise a rocprofv3 --kernel-trace CSV of a decode run of this script (made with the "
+                        "same --model/--batch/--ctx/--budget/--steps/--warmup) into profiles/, then exit")
     p.add_argument("--two-stream-fetch", action="store_true",
                    help="one-lane decoders: value fetch on the copy stream and key rebuild on the compute stream "
                         "(the reference's arrangement) instead of one fused launch on the compute stream")
@@ -160,6 +163,113 @@ def scoring_launch_ms(model, rounds: int = 8, sweeps: int = 4):
     return (t * 1e3,
             f"HIP events around {rounds} replays of a HIP graph of {sweeps * L} back-to-back launches ({sweeps} "
             f"sweeps over the layers, each launch on its layer's live landmarks), after the timed steps")
+
+
+def a1a2_bytes(BH: int, G: int, n: int, S: int, D: int = 128) -> int:
+    """Algorithmic HBM bytes of the scoring + top-k unit per launch pair: landmarks and queries read,
+    the GQA-max scores and the selected ids written."""
+    return BH * (n * D * 2 + G * D * 2 + n * 2 + S * 8)
+
+
+def a1a2_unit_ms(model, rounds: int = 8, sweeps: int = 2):
+    """Average duration of the scoring + selection unit (score_logits, then select_chunks: softmax
+    tail, GQA max, top-k, id gather, reorder) on lane 0's live decode state: `sweeps` passes over
+    the layers, one pair per layer, captured in a HIP graph and replayed between HIP events. Runs
+    after the timed decode steps (it re-selects on the layers' slots)."""
+    import torch
+    from shadowkv_amd.kernels import shadowkv
+
+    cache = model.cache
+    B, H, G, D = cache.batch_size, cache.num_key_value_heads, cache.num_key_value_groups, cache.head_dim
+    BH, S, n = B * H, cache.select_sets, cache.k_landmark.shape[-2]
+    q = torch.randn(B, H * G, 1, D, device=cache.device).to(torch.bfloat16)
+    L = cache.num_layers
+
+    def launch(i):
+        layer = i % L
+        shadowkv.score_logits(q, cache.k_landmark[layer], cache.gemm_o, cache.norm, cache.sum, BH, G, n, D,
+                              1.0 / math.sqrt(128))
+        shadowkv.select_chunks(cache.gemm_o, cache.norm, cache.sum, BH, G, n, cache.k_landmark_idx[layer].view(BH, n),
+                               S, cache.chunks, cache.position_ids[layer].view(BH, -1), cache.offsets, cache.cnts,
+                               out_scores=cache.chunk_attn, workspace=cache.select_workspace)
+
+    t = gpu_time_per_call(launch, sweeps * L, rounds)
+    return (t * 1e3,
+            f"HIP events around {rounds} replays of a HIP graph of {sweeps * L} back-to-back scoring + selection "
+            f"pairs ({sweeps} sweeps over the layers of one lane, each on its layer's live landmarks and slots), "
+            f"after the timed steps")
+
+
+# The kernels of each sparse-step operation, by kernel-name prefix (rocprofv3 kernel traces).
+TRACE_OPS = {
+    "score_logits": ("logits_kernel",),
+    "select_chunks": ("softmax_vec_kernel", "softmax_kernel", "select_kernel", "part_hist_kernel", "part_emit_kernel",
+                      "select_finish_kernel"),
+    "gather_copy_d2d_with_offsets": ("compact_hits_kernel",),
+    "gather_copy_with_offsets": ("gather_chunks_kernel",),
+    "rebuild_k_rope": ("rebuild_kernel",),
+    "sparse_attn_decode": ("attn_split_kernel", "attn_combine_kernel"),
+}
+
+
+def summarize_trace(csv_path: str, layers: int, lanes: int, warmup: int, steps: int) -> dict:
+    """Per-kernel durations inside the timed decode steps of a rocprofv3 kernel trace (CSV) of this
+    script's decode run: the window is the logits launches of the timed steps (one per layer and
+    lane per step, after `warmup` eager steps). Per operation of the sparse step, the device time
+    per lane-layer (the sum of its kernels' durations per step / (layers x lanes))."""
+    import collections
+    import csv
+
+    rows = sorted(csv.DictReader(open(csv_path)), key=lambda r: int(r["Start_Timestamp"]))
+    li = [i for i, r in enumerate(rows) if "logits_kernel" in r["Kernel_Name"]]
+    per = layers * lanes
+    a, b = li[warmup * per], li[(warmup + steps) * per]
+    win = rows[a:b]
+    span_ms = (int(rows[b]["Start_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e6 / steps
+    agg = collections.defaultdict(list)
+    for r in win:
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        agg[name].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    kernels = {k: {"launches_per_step": round(len(v) / steps, 2), "avg_us": round(sum(v) / len(v), 2),
+                   "ms_per_step": round(sum(v) / steps / 1e3, 4)} for k, v in sorted(agg.items())}
+    ops = {}
+    for op, prefixes in TRACE_OPS.items():
+        tot = sum(sum(v) for k, v in agg.items() if k.startswith(prefixes))
+        if tot:
+            ops[op] = round(tot / steps / per, 2)
+    return {"trace_window_ms_per_step": round(span_ms, 3), "kernels": kernels, "op_us_per_lane_layer": ops}
+
+
+def trace_summary_path(args) -> Path:
+    """The committed kernel-trace summary of this decode workload's timed steps."""
+    return ROOT / "profiles" / f"decode_{args.model}_b{args.batch}_ctx{args.ctx}_trace.json"
+
+
+def trace_workload(args, lanes: int) -> dict:
+    return {"model": args.model, "batch": args.batch, "ctx": args.ctx, "budget": args.budget, "chunk": args.chunk,
+            "lanes": lanes}
+
+
+def apply_trace_summary(kernels: list, args, lanes: int) -> None:
+    """In-step figures of the kernel table from the committed kernel trace of this workload's timed
+    graph replays (when one exists for it): the eager instrumented figure moves to
+    eager_instrumented_us."""
+    path = trace_summary_path(args)
+    if not path.exists():
+        return
+    rec = json.loads(path.read_text())
+    if rec.get("workload") != trace_workload(args, lanes):
+        return
+    ops = rec["op_us_per_lane_layer"]
+    for k in kernels:
+        if not k["trace_ops"] or not all(o in ops for o in k["trace_ops"]):
+            continue
+        us = sum(ops[o] for o in k["trace_ops"])
+        k["eager_instrumented_us"] = k["in_step_us"]
+        k["in_step_us"] = round(us, 2)
+        k["in_step_frac"] = round(k["algorithmic_bytes"] / us / 1e3 / k["peak"], 4)
+        k["in_step_source"] = (f"{path.relative_to(ROOT)}: rocprofv3 kernel trace of the timed graph replays of "
+                               f"this workload (device time per lane-layer; not measured in this run)")
 
 
 def host_cpu() -> tuple[int, str]:
@@ -452,12 +562,15 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
 
     res = []
 
-    def add(kernel, bound, nbytes, iso_us, step_us, peak, unit="GB/s", extra=None):
+    def add(kernel, bound, nbytes, iso_us, step_us, peak, unit="GB/s", extra=None, ops=()):
         e = {"kernel": kernel, "bound": bound, "algorithmic_bytes": int(nbytes), "isolated_us": round(iso_us, 2),
              "in_step_us": round(step_us, 2) if step_us else None,
              "isolated_GBps": round(nbytes / iso_us / 1e3, 1), "peak": round(peak, 1), "unit": unit,
              "isolated_frac": round(nbytes / iso_us / 1e3 / peak, 4),
-             "in_step_frac": round(nbytes / step_us / 1e3 / peak, 4) if step_us else None}
+             "in_step_frac": round(nbytes / step_us / 1e3 / peak, 4) if step_us else None,
+             "in_step_source": "eager instrumented step (HIP events around the call, its stream drained and held "
+                               "by a device spin first; not the timed graph's schedule)",
+             "trace_ops": list(ops)}
         if extra:
             e.update(extra)
         res.append(e)
@@ -467,18 +580,19 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
                                                     1.0 / math.sqrt(128)))
     lb = logits_bytes(BH, G, n)
     add("score_logits (a1 logits + per-tile softmax partials)", "hbm", lb, score_us, ops_in_step.get("score_logits"),
-        HBM_PEAK_GBS)
+        HBM_PEAK_GBS, ops=("score_logits",))
     # a1 tail + a2 + a3: softmax normalisation, GQA max, top-k, id gather, reorder (the selection chain)
     sel_us = t_us(lambda i: shadowkv.select_chunks(
         c.gemm_o, c.norm, c.sum, BH, G, n, c.k_landmark_idx[i % L].view(BH, n), S, c.chunks,
         c.position_ids[i % L].view(BH, -1), c.offsets, c.cnts, out_scores=c.chunk_attn, workspace=c.select_workspace))
     sel_bytes = BH * (G * n * 2 + G * ((n + 255) // 256) * 8 + n * 8 + n * 2 + S * 8 * 2 + S * 4)
     add("select_chunks (softmax tail + GQA max + top-k + id gather + reorder)", "latency", sel_bytes, sel_us,
-        ops_in_step.get("select_chunks"), HBM_PEAK_GBS)
+        ops_in_step.get("select_chunks"), HBM_PEAK_GBS, ops=("select_chunks",))
     # the survey's a1+a2 unit: landmarks + q read, scores and ids written, over scoring + selection
-    unit_bytes = BH * (n * D * 2 + G * D * 2 + n * 2 + S * 8)
+    unit_bytes = a1a2_bytes(BH, G, n, S)
     step_unit = (ops_in_step.get("score_logits", 0) + ops_in_step.get("select_chunks", 0)) or None
-    add("a1+a2 unit (scoring + selection chain)", "hbm", unit_bytes, score_us + sel_us, step_unit, HBM_PEAK_GBS)
+    add("a1+a2 unit (scoring + selection chain)", "hbm", unit_bytes, score_us + sel_us, step_unit, HBM_PEAK_GBS,
+        ops=("score_logits", "select_chunks"))
     # a4/a5: in-buffer hit compaction (K and V: two launches of this per layer)
     comp_bytes = 2 * mean_hits * chunk_bytes
     comp_us = t_us(lambda i: shadowkv.gather_copy_d2d_with_offsets(
@@ -486,7 +600,7 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
         c.kernel_stride, S))
     folded = getattr(c, "fold_hit_moves", False) and not c.pooled
     add("gather_copy_d2d_with_offsets (hit compaction, per buffer)", "hbm", comp_bytes, comp_us,
-        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS,
+        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS, ops=("gather_copy_d2d_with_offsets",),
         extra={"mean_hits": round(mean_hits, 1),
                "in_step": ("key buffer only: the value buffer's hits move inside the select_chunks launch"
                            if folded else "both buffers")})
@@ -497,7 +611,7 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
         int(c.max_ctx_chunks_len * D), int(c.sparse_budget * D), c.kernel_offset, c.kernel_stride, S,
         misses_only=True))
     add("gather_copy_with_offsets (value fetch of the misses, host link)", "host link", fetch_bytes, fetch_us,
-        ops_in_step.get("gather_copy_with_offsets"), link_peak,
+        ops_in_step.get("gather_copy_with_offsets"), link_peak, ops=("gather_copy_with_offsets",),
         extra={"peak_source": "SDMA copy (hipMemcpyAsync) of 256 MiB pinned host memory, measured in this run",
                "nominal_link_GBps": 64.0})
     # a5-a7: low-rank key rebuild + RoPE of the miss rows
@@ -507,14 +621,14 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
                                                    model.cos_sin, c.k_cache_buffer[i % L], c.sparse_start, ch))
     flops = 2 * rows * R * D
     add("rebuild_k_rope (gather-GEMM on MFMA + RoPE epilogue)", "hbm", rb_bytes, rb_us,
-        ops_in_step.get("rebuild_k_rope"), HBM_PEAK_GBS,
+        ops_in_step.get("rebuild_k_rope"), HBM_PEAK_GBS, ops=("rebuild_k_rope",),
         extra={"mfma_flops": int(flops), "isolated_mfma_util": round(flops / (rb_us * 1e-6) / MFMA_BF16_PEAK, 4)})
     # a8: sparse attention (split + merge launches)
     at_bytes = BH * 2 * kv_len * D * 2 + 2 * B * H * G * D * 2
     at_us = t_us(lambda i: shadowkv.sparse_attn_decode(qa, c.k_cache_buffer[i % L][:, :, :kv_len],
                                                        c.v_cache_buffer[i % L][:, :, :kv_len], kv_len, out, ws))
     add("sparse_attn_decode (split + merge)", "hbm", at_bytes, at_us, ops_in_step.get("sparse_attn_decode"),
-        HBM_PEAK_GBS, extra={"kv_len": kv_len})
+        HBM_PEAK_GBS, extra={"kv_len": kv_len}, ops=("sparse_attn_decode",))
     return res
 
 
@@ -1164,6 +1278,18 @@ def main() -> int:
              "llama3_8b_1m": decode_model.LLAMA3_8B_1M}[args.model]
     if args.layers:
         shape = replace(shape, layers=args.layers)
+    if args.summarize_trace:
+        lanes = args.lanes if args.lanes else decode_model.auto_lanes(shape, args.batch, args.budget)
+        lanes = lanes if args.batch % lanes == 0 else 1
+        rec = {"workload": trace_workload(args, lanes),
+               "trace": f"rocprofv3 --kernel-trace of python bench.py --model {args.model} --batch {args.batch} "
+                        f"--ctx {args.ctx} --budget {args.budget} --steps {args.steps} --warmup {args.warmup} "
+                        f"--no-cpu-baseline --no-breakdown (timed steps as HIP graph replays)",
+               **summarize_trace(args.summarize_trace, shape.layers, lanes, args.warmup, args.steps)}
+        path = trace_summary_path(args)
+        path.write_text(json.dumps(rec, indent=1) + "\n")
+        print(f"wrote {path.relative_to(ROOT)}: {rec['op_us_per_lane_layer']}")
+        return 0
     t0 = time.time()
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
     lanes = args.lanes if args.lanes else decode_model.auto_lanes(shape, args.batch, args.budget)
@@ -1235,6 +1361,11 @@ def main() -> int:
             traffic_source = (f"{tfile.relative_to(ROOT)}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this "
                               f"launch shape, scaled by the counters' reading of a plain copy (not measured in this run)")
 
+    S = cache.select_sets
+    ub = a1a2_bytes(BH, G, n, S)
+    u_ms, u_timing = a1a2_unit_ms(model)
+    u_achieved = ub / (u_ms * 1e-3) / 1e9
+
     detail = None
     if not args.no_breakdown:
         detail, per_layer = breakdown(model, tok)
@@ -1247,6 +1378,7 @@ def main() -> int:
                   nominal_GBps=64.0)
         if not cache.pooled:
             detail["kernels"] = kernel_table(model, per_layer, detail["op_us_per_layer"], link_peak)
+            apply_trace_summary(detail["kernels"], args, lanes)
             for k in detail["kernels"]:
                 log(f"kernel {k['kernel'][:40]:40s} isolated {k['isolated_us']:8.2f} us "
                     f"({k['isolated_frac'] * 100:5.1f}%), in step {k['in_step_us']} us")
@@ -1299,6 +1431,12 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_source, "algorithmic_bytes_per_launch": lb,
                      "avg_launch_us": round(k_ms * 1e3, 2), "timing": timing},
+        "roofline_a1a2": {"kernel": "scoring + selection unit (score_logits, then select_chunks: softmax tail, GQA "
+                                    "max, top-k, id gather, reorder)", "bound": "hbm",
+                          "achieved": round(u_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(u_achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": ub,
+                          "bytes": "per (b, h) row: landmarks n*D*2 + queries G*D*2 read, GQA-max scores n*2 and "
+                                   "ids S*8 written", "avg_launch_us": round(u_ms * 1e3, 2), "timing": u_timing},
         "cpu_baseline": cpu,
     }
     if detail is not None:
