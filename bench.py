@@ -59,6 +59,12 @@ def parse() -> argparse.Namespace:
                    help="after the main (reference-mode) measurement, time the same decode with a device chunk "
                         "pool of this many slots per (b, h) and layer and report it in detail.chunk_pool "
                         "(0: skip; only with the breakdown)")
+    p.add_argument("--encoded-variant", type=int, default=1,
+                   help="also time the decode from a prompt state built by the device encoder and report it in "
+                        "detail.encoded_state (0: skip; only with the breakdown)")
+    p.add_argument("--state", choices=["synthetic", "encoded"], default="synthetic",
+                   help="prompt state of the main measurement: synthesized random contents of the exact shapes, "
+                        "or built by the device encoder from low-rank keys")
     p.add_argument("--no-act-epilogue", action="store_true",
                    help="form SiLU-and-mul outside the gate/up projection (the down projection reading "
                         "[gate | up], or the SiLU-and-mul kernel) instead of in its epilogue, for comparison")
@@ -716,6 +722,71 @@ def pool_variant(args, shape, lanes) -> dict:
     return res
 
 
+def step_hit_rate(model, tok):
+    """Fraction of the chunks selected by one eager decode step (every layer and lane) that the
+    previous step had selected too (the cache hits), and the step's tokens."""
+    import torch
+
+    before = [lane.cache.position_ids.clone() for lane in model.lanes]
+    tok = model.decode_step(tok)
+    torch.cuda.synchronize()
+    hits = total = 0
+    for lane, b0 in zip(model.lanes, before):
+        S = lane.cache.select_sets
+        new = lane.cache.position_ids.reshape(-1, S)
+        old = b0.reshape(-1, S).sort(dim=-1).values
+        idx = torch.searchsorted(old, new).clamp_max(S - 1)
+        hits += int((old.gather(-1, idx) == new).sum())
+        total += new.numel()
+    return hits / total, tok
+
+
+def encoded_variant(args, shape, lanes) -> dict:
+    """The same decode workload from a prompt state built by the device encoder (decode_model
+    .encode_state: rank-160 keys plus noise, get_svd, RoPE, prefill_kv_cache) instead of the
+    synthesized random state, timed as the main measurement; the per-step hit rate is measured on
+    one eager step after the timed replays. The main decoder is released first."""
+    import gc
+    import torch
+    from shadowkv_amd import decode_model
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+    log("encoded-state variant: building the prompt state with the device encoder")
+    t0 = time.time()
+    em = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
+                                       decode_len=args.warmup + args.steps + 9, lanes=lanes, state="encoded")
+    t_enc = time.time() - t0
+    tok = torch.randint(0, shape.vocab, (args.batch, 1), device="cuda")
+    for _ in range(args.warmup):
+        tok = em.decode_step(tok)
+    per_call = math.gcd(args.steps, max(1, args.graph_steps))
+    em.capture(tok, steps=per_call)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps // per_call):
+        tok = em.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    hit_rate, tok = step_hit_rate(em, tok)
+    res = {"tokens_per_s": round(args.batch * args.steps / elapsed, 3), "ms_per_step": round(elapsed * 1e3 / args.steps, 3),
+           "hit_rate": round(hit_rate, 4), "encode_s": round(t_enc, 1),
+           "state": "device encoder (get_svd, RoPE, prefill_kv_cache) over seeded prompts: pre-RoPE keys "
+                    "A(ctx x 160).B(160 x H*128) + 0.05 N(0,1) with A, B of variance 1/sqrt(160), values and the "
+                    "last prompt query ~ N(0,1); the initial selection from that query",
+           "note": "decode queries come from the random-weight model, independent of the prompt, so hits are "
+                   "chunks that consecutive queries both rank in their top S"}
+    log(f"encoded-state variant {res}")
+    del em
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+    return res
+
+
 def envelope_microbench(args) -> int:
     """HBM streaming envelope of this GPU at decode-kernel sizes: the landmark scoring kernel (a
     pure stream of landmark rows with a little MFMA work, the bench line's roofline kernel),
@@ -1296,7 +1367,7 @@ def main() -> int:
     lanes = lanes if args.batch % lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes,
-                                          chunk_cache=args.chunk_cache)
+                                          chunk_cache=args.chunk_cache, state=args.state)
     if args.separate_hit_moves:
         for lane in model.lanes:
             lane.cache.fold_hit_moves = False
@@ -1397,9 +1468,12 @@ def main() -> int:
             detail["single_layer"].update(sl)
             log(f"single layer CPU {sl}")
 
-    if detail is not None and args.chunk_cache is None and args.pool_variant > 0:
+    if detail is not None and args.chunk_cache is None and (args.pool_variant > 0 or args.encoded_variant):
         model = cache = step = None  # release the reference-mode decoder first
-        detail["chunk_pool"] = pool_variant(args, shape, lanes)
+        if args.pool_variant > 0:
+            detail["chunk_pool"] = pool_variant(args, shape, lanes)
+        if args.encoded_variant and args.state == "synthetic":
+            detail["encoded_state"] = encoded_variant(args, shape, lanes)
 
     out = {
         "metric": ("decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util"
@@ -1414,7 +1488,10 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: random-init weights, seeded random ShadowKV state of the exact shapes, greedy tokens",
+        "data": ("synthetic: random-init weights, seeded random ShadowKV state of the exact shapes, greedy tokens"
+                 if args.state == "synthetic" else
+                 "synthetic: random-init weights, ShadowKV state built by the device encoder from seeded low-rank "
+                 "prompt keys, greedy tokens"),
         "config": {"workload": f"{shape.name}-shape {shape.layers}-layer decode, batch {args.batch}, ctx {args.ctx}, "
                                f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, V in pinned host memory, "
                                + (f"device chunk pool of {args.chunk_cache} slots, " if args.chunk_cache else "")

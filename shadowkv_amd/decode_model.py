@@ -26,7 +26,8 @@ import torch.nn.functional as F
 from .kernels import shadowkv
 from .models.attention import ShadowAttention
 from .models.kvcache import ShadowKVCache_CPU
-from .models.tensor_op import build_cos_sin_cache, build_glm_cos_sin_cache
+from .models.tensor_op import (apply_rotary_pos_emb_cuda, apply_rotary_pos_emb_glm_single, build_cos_sin_cache,
+                               build_glm_cos_sin_cache)
 from .streams import side_stream
 
 
@@ -121,6 +122,46 @@ def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin:
     cache._alloc_attention()
 
 
+def encode_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin: torch.Tensor | None = None,
+                 rope: str = "half") -> None:
+    """Give `cache` the post-prefill state of a ctx-token prompt built by the device encoder, one
+    sequence at a time through every layer (shadow.py:411-544 as the reference's prefill drives it,
+    models/base.py:292-340): pre-RoPE keys K = A.B + 0.05 N(0, 1) with A [ctx, R] and B [R, H*D]
+    of variance 1/sqrt(R) (a rank-R signal of unit variance plus noise, R = the cache's rank),
+    values and the last prompt query ~ N(0, 1), bf16, all seeded; then get_svd, RoPE by token
+    position (`rope`: "half" or "glm" with the matching table), and prefill_kv_cache (chunk
+    statistics, outliers, landmarks, value offload to the pinned host store, initial selection
+    from the last query)."""
+    dev = torch.device(cache.device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    L, B, H, D, R = cache.num_layers, cache.batch_size, cache.num_key_value_heads, cache.head_dim, cache.rank
+    Hq = cache.num_attention_heads
+    if cos_sin is None:
+        cos_sin = build_cos_sin_cache(ctx + 4096, 500000.0, D, device=dev)
+    pos = torch.arange(ctx, device=dev)
+
+    def rotate(x: torch.Tensor, p: torch.Tensor) -> torch.Tensor:  # x [1, h, s, D] by token positions p [s]
+        if rope == "glm":
+            return apply_rotary_pos_emb_glm_single(x, cos_sin, p)
+        return apply_rotary_pos_emb_cuda(x, cos_sin, p.view(1, 1, -1).expand(x.shape[0], x.shape[1], -1))
+
+    for _ in range(B):
+        for layer in range(L):
+            a = torch.randn(ctx, R, generator=g, device=dev) / R ** 0.25
+            b = torch.randn(R, H * D, generator=g, device=dev) / R ** 0.25
+            k = torch.addmm(torch.randn(ctx, H * D, generator=g, device=dev), a, b, beta=0.05).to(cache.dtype)
+            del a, b
+            cache.get_svd(k.view(1, ctx, H * D), layer)
+            k_rot = rotate(k.view(1, ctx, H, D).transpose(1, 2).contiguous(), pos)
+            del k
+            v = torch.randn(1, H, ctx, D, generator=g, device=dev).to(cache.dtype)
+            q = torch.randn(1, Hq, 1, D, generator=g, device=dev).to(cache.dtype)
+            cache.prefill_kv_cache(v, layer, k_rot, rotate(q, pos[ctx - 1:]))
+            del k_rot, v, q
+    torch.cuda.synchronize()
+    cache._alloc_attention()
+
+
 def _fill_selected_values(cache: ShadowKVCache_CPU, layer: int, values: torch.Tensor) -> None:
     """Selected value region <- the chunks named by position_ids, through the cached-copy kernel
     with zero hits (every slot is a miss)."""
@@ -153,7 +194,7 @@ class SyntheticDecoder:
     def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
                  dtype=torch.bfloat16, lanes: int = 1, fused: bool = True, chunk_cache: int | None = None,
-                 one_stream_fetch: bool | None = None):
+                 one_stream_fetch: bool | None = None, state: str = "synthetic", host_stores: int | None = None):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
         # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels and
         # the projections on the skinny linear kernel (libshadowkv_amd), instead of torch operations
@@ -191,8 +232,15 @@ class SyntheticDecoder:
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
                                       chunk_size=chunk_size, rank=rank, max_decode_len=decode_len,
-                                      zero_host_store=False, chunk_cache=chunk_cache)
-            synthesize_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin)
+                                      zero_host_store=False, chunk_cache=chunk_cache, host_stores=host_stores)
+            # The prompt's state: random contents of the exact shapes, or built by the device encoder
+            # from low-rank keys (encode_state).
+            if state == "encoded":
+                encode_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin, rope=shape.rope)
+            elif state == "synthetic":
+                synthesize_state(cache, ctx, seed=seed + 1 + i, cos_sin=self.cos_sin)
+            else:
+                raise ValueError(f"state must be 'synthetic' or 'encoded', not {state!r}")
             lane = _Lane(slice(i * lb, (i + 1) * lb), cache)
             lane.attn = ShadowAttention(cache, s.heads // s.kv_heads, D, s.hidden, self._rope_for(lane), None,
                                         self.cos_sin)

@@ -64,7 +64,8 @@ class ShadowKVCache_CPU(KVCacheBase):
     def __init__(self, config, batch_size: int = 1, max_length: int = 32 * 1024, device: str = "cuda:0",
                  dtype=torch.bfloat16, sparse_budget: int = 2048, chunk_size: int = 8, rank: int = 160,
                  max_decode_len: int | None = None, zero_host_store: bool = True,
-                 chunk_cache: int | None = None, copy_stream: torch.cuda.Stream | None = None) -> None:
+                 chunk_cache: int | None = None, copy_stream: torch.cuda.Stream | None = None,
+                 host_stores: int | None = None) -> None:
         self.config = config
         self.batch_size = batch_size
         self.max_length = max_length
@@ -98,9 +99,15 @@ class ShadowKVCache_CPU(KVCacheBase):
         # One pinned host buffer per layer, [B, H, max_length/c, c*D] each (indexable like the reference's
         # [L, ...] tensor): torch's pinned allocator rounds each request up to a power of two, which a
         # single 64 GB allocation (Llama-3-8B, batch 8, 122K) would double.
+        # host_stores (None: one per layer): k distinct stores, layer l using store l % k. Layers
+        # then share the host copy of their values (what the last layer to write a store wrote),
+        # for callers that need the decode shapes but not distinct contents per layer (the
+        # full-size tests: one process may pin only about 65 GiB on the MI355X hosts).
         alloc = torch.zeros if zero_host_store else torch.empty
-        self.v_cache_cpu = [alloc(B, H, max_length // chunk_size, D * chunk_size, dtype=dtype, pin_memory=True)
-                            for _ in range(L)]
+        stores = L if host_stores is None else max(1, min(L, int(host_stores)))
+        own = [alloc(B, H, max_length // chunk_size, D * chunk_size, dtype=dtype, pin_memory=True)
+               for _ in range(stores)]
+        self.v_cache_cpu = [own[l % stores] for l in range(L)]
         # Sparse region ends at most at (local 4 chunks + 7 alignment chunks + 7 tokens) + outliers + budget.
         ref_len = self.sparse_budget + 128 + (self.outlier_chunk + self.local_chunk) * chunk_size
         if max_decode_len is None:

@@ -10,6 +10,7 @@
   against oracle.decode_layer_step from the device's own scores (selection, offsets, hit
   counts, slot ids and value buffer bit-exact; keys and attention within rtol/atol 2e-2).
   The step checked is the second one, so the generated tail holds a token of the first.
+* The same Llama-3.1-8B step from a prompt state built by the device encoder (two layers).
 * The prefill's rank-160 factors at ctx 122880 against torch.linalg.svd on the device.
 """
 import gc
@@ -128,14 +129,16 @@ def test_rebuild_microbench_sizes(gpu, u_per_head, B):
 
 # ------------------------------------------------------------------ decode workloads
 
-def _decode_and_check(shape, batch, ctx, budget, layers_checked, gpu):
-    # The value stores of these workloads take 20-64 GiB of pinned host memory, close to what one
-    # process may pin on the MI355X hosts (about 65 GiB): release blocks cached by earlier tests.
+def _decode_and_check(shape, batch, ctx, budget, layers_checked, gpu, state="synthetic"):
+    # The value stores of these workloads would take 20-64 GiB of pinned host memory, close to what
+    # one process may pin on the MI355X hosts (about 65 GiB): the layers share two host stores (the
+    # oracle reads the same store the device fetched from), and blocks cached by earlier tests are
+    # released first.
     _release()
     lanes = decode_model.auto_lanes(shape, batch, budget)
-    _say(f"{shape.name} batch {batch} ctx {ctx} budget {budget}: building ({lanes} lane(s))")
+    _say(f"{shape.name} batch {batch} ctx {ctx} budget {budget}: building ({lanes} lane(s), {state} state)")
     dec = decode_model.SyntheticDecoder(shape, batch, ctx, sparse_budget=budget, decode_len=8, lanes=lanes,
-                                        seed=7)
+                                        seed=7, state=state, host_stores=2)
     tok = torch.randint(0, shape.vocab, (batch, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(1))
     tok = dec.decode_step(tok)  # the first step; the checked one follows
     probe = LayerProbe(dec, layers_checked)
@@ -161,6 +164,14 @@ def test_decode_glm4_9b_batch4_ctx262144(gpu):
 
 def test_decode_llama3_8b_1m_batch1_ctx1048576(gpu):
     _decode_and_check(decode_model.LLAMA3_8B_1M, 1, 1048576, 16384, [0, 15, 31], gpu)
+
+
+def test_decode_llama31_8b_batch8_ctx122880_encoded_state(gpu):
+    """The Llama-3.1-8B batch-8 ctx-122880 step from a prompt state built by the device encoder
+    (decode_model.encode_state: rank-160 keys plus noise through get_svd, RoPE, prefill_kv_cache),
+    two layers of every lane against the oracle."""
+    from dataclasses import replace
+    _decode_and_check(replace(decode_model.LLAMA31_8B, layers=2), 8, CTX, 2048, [0, 1], gpu, state="encoded")
 
 
 # ------------------------------------------------------------------ prefill factors at size
