@@ -10,8 +10,9 @@
 //
 // Work decomposition (gfx950, wave64):
 //   * workgroup = kNW waves, owns up to kTileRows = kNW x kIters x 32 consecutive rows of one head
-//     (256 = 4 waves x 2 iterations when the grid has enough workgroups to fill the GPU, else
-//     128 = 4 x 1 or 64 = 2 x 1, so that few rows still spread over the CUs); the grid has the
+//     (256 = 4 waves x 2 iterations when the grid has enough workgroups to fill the GPU, 256 = 8 x
+//     1 where that gives one workgroup per CU, else 128 = 4 x 1 or 64 = 2 x 1, so that few rows
+//     still spread over the CUs); the grid has the
 //     tiles of a head with no hits, and a head's miss rows are dealt evenly over its tiles, so
 //     hits shorten every workgroup instead of idling some. At entry it stages
 //     SV of that head (128 x rank bf16, 40 KB at rank 160) and the U row of each of its rows
@@ -41,7 +42,7 @@ using skv::u32x4;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxWaves = 4;
+constexpr int kMaxWaves = 8;
 constexpr int kMaxTileRows = 256;  // rows per workgroup: at most 4 waves x 2 iterations x 32 rows
 constexpr int kHeadDim = 128;
 constexpr int kMaxRank = 192;
@@ -320,7 +321,7 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
 }
 
 template <int kMode, int KS, typename IdxT, int kNW, int kIters>
-__global__ void __launch_bounds__(kNW * 64, 2) rebuild_kernel(RebuildArgs a) {
+__global__ void __launch_bounds__(kNW * 64, kNW > 4 ? 1 : 2) rebuild_kernel(RebuildArgs a) {
   rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, blockIdx.x);
 }
 
@@ -409,23 +410,39 @@ int launch_tile(int ks, dim3 grid, size_t lds, hipStream_t stream, const Rebuild
 // takes the value fetch's workgroups (fetch_rebuild_kernel).
 template <int kMode, typename IdxT, bool kFused = false>
 int launch_mode(int tile_rows, int ks, dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a,
-                const skv::FetchArgs<int32_t>* f = nullptr) {
+                const skv::FetchArgs<int32_t>* f = nullptr, bool wide = false) {
+  if constexpr (!kFused) {
+    if (wide) return launch_tile<kMode, IdxT, 8, 1, false>(ks, grid, lds, stream, a, f);
+  }
   if (tile_rows == 256) return launch_tile<kMode, IdxT, 4, 2, kFused>(ks, grid, lds, stream, a, f);
   if (tile_rows == 128) return launch_tile<kMode, IdxT, 4, 1, kFused>(ks, grid, lds, stream, a, f);
   return launch_tile<kMode, IdxT, 2, 1, kFused>(ks, grid, lds, stream, a, f);
 }
 
-// Rows per workgroup: the largest tile that still gives the grid about 1.5 workgroups per CU
-// (256 CUs), so few (b, h) rows - GLM's 2 kv heads, a batch lane of 4 sequences - spread over
-// the GPU instead of leaving most CUs idle. SKV_REBUILD_TILE=64/128/256 forces one.
-int choose_tile_rows(int BH, int rows) {
+// Workgroup shape: the largest tile that still gives the grid about 1.5 workgroups per CU (256
+// CUs), so few (b, h) rows - GLM's 2 kv heads, a batch lane of 4 sequences - spread over the GPU
+// instead of leaving most CUs idle: 256 rows (4 waves x 2), 128 (4 x 1) or 64 (2 x 1). Where
+// 256-row tiles give about one workgroup per CU, 256 rows of 8 waves x 1 instead (*wide): the
+// waves per CU of two 128-row workgroups, SV staged half as often (MI355X, 32 heads x 2048 rows:
+// 15.1 vs 15.3 us without hits, 9.6 vs 10.9 us with 154 of 256 chunks hit; with the fetch in the
+// same launch never). SKV_REBUILD_TILE=64/128/256/w256 forces one.
+int choose_tile_rows(int BH, int rows, bool allow_wide, bool* wide) {
+  *wide = false;
   const char* e = getenv("SKV_REBUILD_TILE");
+  if (e && e[0] == 'w' && allow_wide) {
+    *wide = true;
+    return 256;
+  }
   const int forced = e ? atoi(e) : 0;
   if (forced == 64 || forced == 128 || forced == 256) return forced;
   constexpr int kFill = 384;
-  for (int t : {256, 128}) {
-    if (static_cast<int64_t>(BH) * ((rows + t - 1) / t) >= kFill) return t;
+  const int64_t t256 = static_cast<int64_t>(BH) * ((rows + 255) / 256);
+  if (t256 >= kFill) return 256;
+  if (allow_wide && t256 >= 256) {
+    *wide = true;
+    return 256;
   }
+  if (static_cast<int64_t>(BH) * ((rows + 127) / 128) >= kFill) return 128;
   return 64;
 }
 
@@ -463,9 +480,10 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
     return SKV_EUNSUPPORTED;
   }
   const int BH = a.B * a.H;
-  int tile_rows = choose_tile_rows(BH, a.S * a.chunk);
-  if (tile_rows == 256 && a.rank > 160) tile_rows = 128;  // (no spill-free 256-row kernel there)
-  const int waves = tile_rows == 64 ? 2 : 4;
+  bool wide = false;
+  int tile_rows = choose_tile_rows(BH, a.S * a.chunk, fetch == nullptr, &wide);
+  if (!wide && tile_rows == 256 && a.rank > 160) tile_rows = 128;  // (no spill-free 4 x 2 kernel there)
+  const int waves = wide ? 8 : tile_rows == 64 ? 2 : 4;
   a.tiles = (a.S * a.chunk + tile_rows - 1) / tile_rows;
   // Deal the miss rows over every tile while the grid is at most ~4 workgroups per CU (all of it
   // in flight at once: hits then shorten each workgroup; MI355X, batch 8 with 154 of 256 chunks
@@ -485,13 +503,13 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
     if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
     else rc = launch_mode<kRopeGlm, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
   } else if (ids64) {
-    if (mode == kPlain) rc = launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a);
-    else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a);
-    else rc = launch_mode<kRopeGlm, int64_t>(tile_rows, ks, grid, lds, stream, a);
+    if (mode == kPlain) rc = launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
+    else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
+    else rc = launch_mode<kRopeGlm, int64_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
   } else {
-    if (mode == kPlain) rc = launch_mode<kPlain, int32_t>(tile_rows, ks, grid, lds, stream, a);
-    else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int32_t>(tile_rows, ks, grid, lds, stream, a);
-    else rc = launch_mode<kRopeGlm, int32_t>(tile_rows, ks, grid, lds, stream, a);
+    if (mode == kPlain) rc = launch_mode<kPlain, int32_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
+    else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int32_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
+    else rc = launch_mode<kRopeGlm, int32_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
   }
   if (rc) return rc;
   return skv_check_launch(what);

@@ -363,7 +363,7 @@ def test_rebuild_tile_shapes_agree(gpu, glm, monkeypatch):
     start = 448
     cache = torch.randn(B, H, start + S * c + 32, 128).to(torch.bfloat16)
     outs = []
-    for tile in (256, 128, 64):
+    for tile in (256, 128, 64, "w256"):
         for spread in ("0", "1"):  # whole tiles (hit tiles idle) or the miss rows dealt over every tile
             monkeypatch.setenv("SKV_REBUILD_TILE", str(tile))
             monkeypatch.setenv("SKV_REBUILD_SPREAD", spread)
