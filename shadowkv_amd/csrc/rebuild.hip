@@ -133,7 +133,7 @@ __device__ __forceinline__ void rebuild_role(const RebuildArgs& a, int bid) {
   // shorten every workgroup of the head instead of idling whole tiles. Otherwise tile t owns rows
   // [t, t + 1) x kTileRows and tiles of hits only return at once.
   const int total_rows = a.S * a.chunk;
-  const int miss_begin = min(a.cnts[head], a.S) * a.chunk;
+  const int miss_begin = min(max(a.cnts[head], 0), a.S) * a.chunk;  // (a count outside [0, S] is clamped)
   const int miss_rows = total_rows - miss_begin;
   const int span = a.spread ? ((miss_rows + a.tiles - 1) / a.tiles + 31) / 32 * 32 : kTileRows;
   const int row_begin = a.spread ? miss_begin + tile * span : tile * kTileRows;
