@@ -208,7 +208,7 @@ def a1a2_unit_ms(model, rounds: int = 8, sweeps: int = 2):
 
 # The kernels of each sparse-step operation, by kernel-name prefix (rocprofv3 kernel traces).
 TRACE_OPS = {
-    "score_logits": ("logits_kernel",),
+    "score_logits": ("logits_kernel", "logits_rows_kernel"),
     "select_chunks": ("softmax_vec_kernel", "softmax_kernel", "select_kernel", "part_hist_kernel", "part_emit_kernel",
                       "select_finish_kernel"),
     "gather_copy_d2d_with_offsets": ("compact_hits_kernel",),
@@ -227,7 +227,7 @@ def summarize_trace(csv_path: str, layers: int, lanes: int, warmup: int, steps: 
     import csv
 
     rows = sorted(csv.DictReader(open(csv_path)), key=lambda r: int(r["Start_Timestamp"]))
-    li = [i for i, r in enumerate(rows) if "logits_kernel" in r["Kernel_Name"]]
+    li = [i for i, r in enumerate(rows) if any(k in r["Kernel_Name"] for k in TRACE_OPS["score_logits"])]
     per = layers * lanes
     a, b = li[warmup * per], li[(warmup + steps) * per]
     win = rows[a:b]

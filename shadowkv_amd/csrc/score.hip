@@ -14,8 +14,13 @@
 //     dots (no cross-lane reduction); logits are staged in LDS, written out coalesced, and the
 //     tile's max and sum(exp) partials (DPP wave reductions) go to norm/sum [z][i][tile] (the
 //     reference's 256-column partial layout).
+//   logits_rows_kernel: the same tile and outputs for up to 4 queries with the dots on the vector
+//     ALUs (bf16 dot2), so that every wave load reads 4 whole landmark rows (1 KB contiguous)
+//     instead of 64 bytes of 16 rows; the 16 lanes of a row meet by DPP.
 //   softmax_kernel: each workgroup merges the partials of its z, then normalises its 256
 //     columns for every query row and keeps the running max over rows.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "softmax_keys.h"
@@ -41,6 +46,45 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// A finished tile's logits (bf16-rounded, -inf past n) from s_tile[i][0, kTile) to D (coalesced
+// bf16 stores) and the tile's (max, sum exp) partials into norm / sum [z][i][tile]. Wave w takes
+// query rows w, w + 4, ...
+__device__ __forceinline__ void store_tile(const float (*s_tile)[kTile], uint16_t* __restrict__ D, float* __restrict__ norm,
+                                           float* __restrict__ sum, int z, int m, int n, int tile, int tiles) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int i = wave; i < m; i += 4) {
+    float x[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      x[u] = s_tile[i][lane * 4 + u];
+      mx = fmaxf(mx, x[u]);
+    }
+    const int j0 = tile * kTile + lane * 4;
+    uint16_t* Drow = D + (static_cast<int64_t>(z) * m + i) * n;
+    if (j0 + 3 < n && (n & 3) == 0) {
+      uint2 packed;
+      packed.x = static_cast<uint32_t>(skv::f2bf(x[0])) | (static_cast<uint32_t>(skv::f2bf(x[1])) << 16);
+      packed.y = static_cast<uint32_t>(skv::f2bf(x[2])) | (static_cast<uint32_t>(skv::f2bf(x[3])) << 16);
+      *reinterpret_cast<uint2*>(Drow + j0) = packed;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (j0 + u < n) Drow[j0 + u] = skv::f2bf(x[u]);
+    }
+    mx = skv::wave_max_dpp(mx);
+    float se = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) se += (x[u] == -INFINITY) ? 0.f : expf(x[u] - mx);
+    se = skv::wave_sum_dpp(se);
+    if (lane == 0) {
+      norm[(static_cast<int64_t>(z) * m + i) * tiles + tile] = mx;
+      sum[(static_cast<int64_t>(z) * m + i) * tiles + tile] = se;
+    }
+  }
+}
 
 template <int M>
 __global__ void __launch_bounds__(kThreads) logits_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
@@ -88,37 +132,123 @@ __global__ void __launch_bounds__(kThreads) logits_kernel(const uint16_t* __rest
     }
   }
   __syncthreads();
+  store_tile(s_tile, D, norm, sum, z, m, n, tile, tiles);
+}
 
-  for (int i = wave; i < m; i += 4) {
-    float x[4];
-    float mx = -INFINITY;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// acc + a.lo * b.lo + a.hi * b.hi over two bf16 pairs, fp32 accumulation (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+// DPP exchanges within a quad of lanes (quad_perm): the value of lane (l ^ 1), of lane (l ^ 2).
+__device__ __forceinline__ float quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+}
+
+// Sums v[0, MP) over the 16 lanes of a DPP row (lane c = lane & 15). The exchanges with lane c ^ 1
+// and then c ^ 2 each keep half of the values (the lane with the bit set keeps the upper half), so
+// lane c is left with R = max(1, MP / 4) partial sums, of indices row_sum_base<MP>(c) + [0, R),
+// over the lanes of its class c mod 4; rotations by 4 and 8 within the row add the class's four
+// lanes. Every lane ends with its class's R totals in v[0, R).
+template <int MP>
+__device__ __forceinline__ void row_sums(float* v, int c) {
+  if constexpr (MP >= 2) {
+    constexpr int H = MP / 2;
+    const bool up = (c & 1) != 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      x[u] = s_tile[i][lane * 4 + u];
-      mx = fmaxf(mx, x[u]);
+    for (int t = 0; t < H; ++t) {
+      const float send = up ? v[t] : v[t + H];
+      const float keep = up ? v[t + H] : v[t];
+      v[t] = keep + quad_xor1(send);
     }
-    const int j0 = tile * kTile + lane * 4;
-    uint16_t* Drow = D + (static_cast<int64_t>(z) * m + i) * n;
-    if (j0 + 3 < n && (n & 3) == 0) {
-      uint2 packed;
-      packed.x = static_cast<uint32_t>(skv::f2bf(x[0])) | (static_cast<uint32_t>(skv::f2bf(x[1])) << 16);
-      packed.y = static_cast<uint32_t>(skv::f2bf(x[2])) | (static_cast<uint32_t>(skv::f2bf(x[3])) << 16);
-      *reinterpret_cast<uint2*>(Drow + j0) = packed;
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (j0 + u < n) Drow[j0 + u] = skv::f2bf(x[u]);
-    }
-    mx = skv::wave_max_dpp(mx);
-    float se = 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) se += (x[u] == -INFINITY) ? 0.f : expf(x[u] - mx);
-    se = skv::wave_sum_dpp(se);
-    if (lane == 0) {
-      norm[(static_cast<int64_t>(z) * m + i) * tiles + tile] = mx;
-      sum[(static_cast<int64_t>(z) * m + i) * tiles + tile] = se;
-    }
+  } else {
+    v[0] += quad_xor1(v[0]);
   }
+  if constexpr (MP >= 4) {
+    constexpr int H = MP / 4;
+    const bool up = (c & 2) != 0;
+#pragma unroll
+    for (int t = 0; t < H; ++t) {
+      const float send = up ? v[t] : v[t + H];
+      const float keep = up ? v[t + H] : v[t];
+      v[t] = keep + quad_xor2(send);
+    }
+  } else {
+    v[0] += quad_xor2(v[0]);
+  }
+  constexpr int R = MP >= 4 ? MP / 4 : 1;
+#pragma unroll
+  for (int t = 0; t < R; ++t) {
+    v[t] += skv::row_ror<4>(v[t]);
+    v[t] += skv::row_ror<8>(v[t]);
+  }
+}
+template <int MP>
+__device__ __forceinline__ int row_sum_base(int c) {
+  return (MP >= 2 ? (c & 1) * (MP / 2) : 0) + (MP >= 4 ? ((c >> 1) & 1) * (MP / 4) : 0);
+}
+
+// Few queries (m <= MP <= 4): the dots on the vector ALUs, so that every wave load covers whole
+// landmark rows (the MFMA operand order splits each row's 256 bytes over four loads of 16 rows,
+// which streams 5-10% slower). Workgroup = one 256-landmark tile of one z. Lane (r, c) =
+// (lane >> 4, lane & 15) holds dims [8c, 8c + 8) of landmark 4u + r of its wave's 64 in wave load
+// u = 0..15 (1 KB of consecutive bytes, non-temporal: the landmarks are read once), all 16 loads
+// requested at entry; it sums its 8 products per query (four bf16 dot2 instructions, fp32
+// accumulation), and the 16 lanes of a landmark meet in row_sums.
+template <int MP>
+__global__ void __launch_bounds__(kThreads) logits_rows_kernel(const uint16_t* __restrict__ A,
+                                                               const uint16_t* __restrict__ B, uint16_t* __restrict__ D,
+                                                               float* __restrict__ norm, float* __restrict__ sum, int m,
+                                                               int n, float alpha, int tiles) {
+  static_assert(MP == 1 || MP == 2 || MP == 4, "1, 2 or 4 queries per instance");
+  constexpr int kWriters = MP;  // lanes c < MP of each landmark hold its MP sums, one each
+  __shared__ float s_tile[MP][kTile];
+  const int z = blockIdx.y;
+  const int tile = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane >> 4;
+  const int c = lane & 15;
+  // Landmark rows past n (the last tile's) read row n - 1 instead; their logits are replaced by
+  // -inf before any use.
+  const u32x4* Bz = reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(z) * n * kHeadDim) + c;
+  const int jb = tile * kTile + wave * 64 + r;
+  u32x4 lf[16];
+  if (tile * kTile + kTile <= n) {
+    const u32x4* p = Bz + static_cast<int64_t>(jb) * (kHeadDim / 8);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) lf[u] = skv::load_nt(p + u * 4 * (kHeadDim / 8));
+  } else {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) lf[u] = skv::load_nt(Bz + static_cast<int64_t>(min(jb + 4 * u, n - 1)) * (kHeadDim / 8));
+  }
+  u32x4 qv[MP];  // dims [8c, 8c + 8) of each query, as bf16 pairs
+  const uint16_t* Az = A + static_cast<int64_t>(z) * m * kHeadDim + 8 * c;
+#pragma unroll
+  for (int i = 0; i < MP; ++i) qv[i] = skv::load16_or_zero(Az + min(i, m - 1) * kHeadDim, i < m);
+  const int base = row_sum_base<MP>(c);
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    float acc[MP];
+#pragma unroll
+    for (int i = 0; i < MP; ++i) {
+      acc[i] = dot2(lf[u].x, qv[i].x, 0.f);
+      acc[i] = dot2(lf[u].y, qv[i].y, acc[i]);
+      acc[i] = dot2(lf[u].z, qv[i].z, acc[i]);
+      acc[i] = dot2(lf[u].w, qv[i].w, acc[i]);
+    }
+    row_sums<MP>(acc, c);
+    const int jl = wave * 64 + 4 * u + r;
+    const int j = tile * kTile + jl;
+    if (c < kWriters && base < m) s_tile[base][jl] = (j < n) ? skv::bf2f(skv::f2bf(alpha * acc[0])) : -INFINITY;
+  }
+  __syncthreads();
+  store_tile(s_tile, D, norm, sum, z, m, n, tile, tiles);
 }
 
 template <bool kWriteSoftmax, bool kWriteMax>
@@ -244,6 +374,22 @@ int check_scoring_shape(const char* what, int batch_count, int m, int n, int k) 
   return SKV_OK;
 }
 
+// Scoring kernel choice: logits_rows_kernel for m <= 4 queries over at least 1024 tiles in all,
+// else logits_kernel (MFMA). Measured on MI355X, cold, rows vs MFMA: 32 x 4 x 15304 (the
+// Llama-3-8B lane of 4 sequences) 23.7-24.4 vs 24.9 us, 64 x 4 x 15304 43.6-45.3 vs 48.3 us,
+// 8 x 4 x 130680 47.3-50.3 vs 51.6 us; 16 x 4 x 15304 13.9 vs 14.1 us; 8 x 4 x 15304 8.7 vs
+// 7.8 us; 8 x 8 x 15304 (twice the dot work per byte, fewer waves) 13.0 vs 8.3 us. Workgroups of
+// 2-8 consecutive tiles (the next tile's loads requested before the current tile's dots) measured
+// slower at every size. Environment SKV_SCORE_PATH=mfma / rows forces a kernel (rows only for
+// m <= 4), read per call.
+bool score_rows(int batch_count, int m, int tiles) {
+  if (m > 4) return false;
+  const char* e = getenv("SKV_SCORE_PATH");
+  if (e && strcmp(e, "mfma") == 0) return false;
+  if (e && strcmp(e, "rows") == 0) return true;
+  return static_cast<int64_t>(tiles) * batch_count >= 1024;
+}
+
 int launch_logits(const char* what, const uint16_t* A, const uint16_t* B, uint16_t* D, float* norm, float* sum,
                   int batch_count, int m, int n, int k, float alpha, hipStream_t stream) {
   if (!A || !B || !D || !norm || !sum) {
@@ -258,6 +404,12 @@ int launch_logits(const char* what, const uint16_t* A, const uint16_t* B, uint16
   }
   const int tiles = (n + kTile - 1) / kTile;
   const dim3 grid(tiles, batch_count);
+  if (score_rows(batch_count, m, tiles)) {
+    if (m == 1) hipLaunchKernelGGL(logits_rows_kernel<1>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
+    else if (m == 2) hipLaunchKernelGGL(logits_rows_kernel<2>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
+    else hipLaunchKernelGGL(logits_rows_kernel<4>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
+    return skv_check_launch(what);
+  }
   if (m == 1) hipLaunchKernelGGL(logits_kernel<1>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
   else if (m == 2) hipLaunchKernelGGL(logits_kernel<2>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);
   else if (m <= 4) hipLaunchKernelGGL(logits_kernel<4>, grid, dim3(kThreads), 0, stream, A, B, D, norm, sum, m, n, alpha, tiles);

@@ -231,6 +231,36 @@ def _scoring_case(gpu, Z, m, n, seed):
     assert torch.equal(out.cpu(), Pg.cpu().max(dim=1).values)  # GQA max of the kernel's own probabilities
 
 
+@pytest.mark.parametrize("Z,m,n", [(32, 4, 15304), (5, 3, 1000), (3, 2, 777), (9, 1, 4100), (2, 4, 100)])
+def test_scoring_kernels_agree(gpu, Z, m, n, monkeypatch):
+    """The two scoring kernels for m <= 4 queries, the row-contiguous one (vector-ALU dots) and the
+    MFMA one, each forced: logits within one rounding step of the oracle's and of each other,
+    the tile partials within rounding of each other (sums taken in another order)."""
+    _say(f"scoring kernels Z={Z} m={m} n={n}")
+    g = torch.Generator().manual_seed(Z * n + m)
+    q = torch.randn(Z, m, 128, generator=g).to(torch.bfloat16)
+    L = torch.randn(Z, n, 128, generator=g).to(torch.bfloat16)
+    alpha = 1.0 / math.sqrt(128)
+    Dw, _ = oracle.score_logits_softmax(q, L, alpha)
+    qg, Lg = q.to(gpu), L.to(gpu)
+    tiles = (n + 255) // 256
+    runs = {}
+    for path in ("mfma", "rows"):
+        monkeypatch.setenv("SKV_SCORE_PATH", path)
+        D = torch.full((Z, m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        norm = torch.full((Z, m, tiles), float("nan"), device=gpu)
+        ssum = torch.full_like(norm, float("nan"))
+        shadowkv.score_logits(qg, Lg, D, norm, ssum, Z, m, n, 128, alpha)
+        torch.cuda.synchronize()
+        _assert_rounding_close(D.cpu(), Dw)
+        runs[path] = (D.cpu(), norm.cpu(), ssum.cpu())
+    (D, norm, ssum), ref = runs["mfma"], runs["rows"]
+    _assert_rounding_close(D, ref[0])
+    _assert_rounding_close(norm, ref[1])  # tile maxima of logits at most one step apart
+    # sum exp(x - max) * exp(max): the tile's sum of exp(x), whichever maximum it was taken against
+    torch.testing.assert_close(ssum * norm.exp(), ref[2] * ref[1].exp(), rtol=1e-2, atol=0)
+
+
 @pytest.mark.parametrize("Z,m,n", [(8, 16, 32712), (32, 4, 15304), (2, 4, 140000), (3, 8, 2048), (1, 1, 8),
                                    (256, 4, 4096), (128, 16, 4096)])
 def test_softmax_vector_and_scalar_paths_agree(gpu, Z, m, n):
