@@ -98,7 +98,9 @@ def parse() -> argparse.Namespace:
                         "same --model/--batch/--ctx/--budget/--steps/--warmup) into profiles/, then exit")
     p.add_argument("--two-stream-fetch", action="store_true",
                    help="one-lane decoders: value fetch on the copy stream and key rebuild on the compute stream "
-                        "(the reference's arrangement) instead of one fused launch on the compute stream")
+                        "(the reference's arrangement) instead of one fused launch on the compute stream; two-lane "
+                        "decoders: the lanes' fetches on one shared fetch stream and their key rebuilds on one shared "
+                        "rebuild stream instead of each lane's fused launch on a side stream of its own")
     return p.parse_args()
 
 
@@ -214,6 +216,7 @@ TRACE_OPS = {
     "gather_copy_d2d_with_offsets": ("compact_hits_kernel",),
     "gather_copy_with_offsets": ("gather_chunks_kernel",),
     "rebuild_k_rope": ("rebuild_kernel",),
+    "fetch_misses_rebuild_k_rope": ("fetch_rebuild_kernel",),
     "sparse_attn_decode": ("attn_split_kernel", "attn_combine_kernel"),
 }
 
@@ -605,10 +608,16 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
         c.v_cache_buffer[i % L], offs[i % L], cnts[i % L], B, H, int(c.sparse_budget * D), c.kernel_offset,
         c.kernel_stride, S))
     folded = getattr(c, "fold_hit_moves", False) and not c.pooled
+    # the timed step's value fetch and key rebuild as one launch (fetch_rebuild_kernel), after a
+    # selection that moved both buffers' hits
+    fused_fetch = all(ln.cache.one_stream_active() for ln in model.lanes)
     add("gather_copy_d2d_with_offsets (hit compaction, per buffer)", "hbm", comp_bytes, comp_us,
-        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS, ops=("gather_copy_d2d_with_offsets",),
+        ops_in_step.get("gather_copy_d2d_with_offsets"), HBM_PEAK_GBS,
+        ops=() if fused_fetch else ("gather_copy_d2d_with_offsets",),
         extra={"mean_hits": round(mean_hits, 1),
-               "in_step": ("key buffer only: the value buffer's hits move inside the select_chunks launch"
+               "in_step": ("none in the timed step: both buffers' hits move inside the select_chunks launch"
+                           if fused_fetch else
+                           "key buffer only: the value buffer's hits move inside the select_chunks launch"
                            if folded else "both buffers")})
     # a4: value fetch of the misses from pinned host memory
     fetch_bytes = mean_miss * chunk_bytes
@@ -617,9 +626,12 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
         int(c.max_ctx_chunks_len * D), int(c.sparse_budget * D), c.kernel_offset, c.kernel_stride, S,
         misses_only=True))
     add("gather_copy_with_offsets (value fetch of the misses, host link)", "host link", fetch_bytes, fetch_us,
-        ops_in_step.get("gather_copy_with_offsets"), link_peak, ops=("gather_copy_with_offsets",),
+        ops_in_step.get("gather_copy_with_offsets"), link_peak,
+        ops=("fetch_misses_rebuild_k_rope",) if fused_fetch else ("gather_copy_with_offsets",),
         extra={"peak_source": "SDMA copy (hipMemcpyAsync) of 256 MiB pinned host memory, measured in this run",
-               "nominal_link_GBps": 64.0})
+               "nominal_link_GBps": 64.0,
+               **({"in_step": "the timed step's one launch of the value fetch and the key rebuild "
+                              "(fetch_misses_rebuild_k_rope), host-link bound"} if fused_fetch else {})})
     # a5-a7: low-rank key rebuild + RoPE of the miss rows
     rows = mean_miss * ch
     rb_bytes = rows * (R * 2 + D * 2 + D * 2) + BH * (R * D * 2 + S * 8)
@@ -627,8 +639,10 @@ def kernel_table(model, per_layer, ops_in_step, link_peak, sweeps: int = 2) -> l
                                                    model.cos_sin, c.k_cache_buffer[i % L], c.sparse_start, ch))
     flops = 2 * rows * R * D
     add("rebuild_k_rope (gather-GEMM on MFMA + RoPE epilogue)", "hbm", rb_bytes, rb_us,
-        ops_in_step.get("rebuild_k_rope"), HBM_PEAK_GBS, ops=("rebuild_k_rope",),
-        extra={"mfma_flops": int(flops), "isolated_mfma_util": round(flops / (rb_us * 1e-6) / MFMA_BF16_PEAK, 4)})
+        ops_in_step.get("rebuild_k_rope"), HBM_PEAK_GBS, ops=() if fused_fetch else ("rebuild_k_rope",),
+        extra={"mfma_flops": int(flops), "isolated_mfma_util": round(flops / (rb_us * 1e-6) / MFMA_BF16_PEAK, 4),
+               **({"in_step": "runs inside the value fetch's launch in the timed step (no separate "
+                              "duration)"} if fused_fetch else {})})
     # a8: sparse attention (split + merge launches)
     at_bytes = BH * 2 * kv_len * D * 2 + 2 * B * H * G * D * 2
     at_us = t_us(lambda i: shadowkv.sparse_attn_decode(qa, c.k_cache_buffer[i % L][:, :, :kv_len],
@@ -1367,7 +1381,8 @@ def main() -> int:
     lanes = lanes if args.batch % lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes,
-                                          chunk_cache=args.chunk_cache, state=args.state)
+                                          chunk_cache=args.chunk_cache, state=args.state,
+                                          one_stream_fetch=False if args.two_stream_fetch else None)
     if args.separate_hit_moves:
         for lane in model.lanes:
             lane.cache.fold_hit_moves = False
@@ -1375,10 +1390,8 @@ def main() -> int:
         model.act_epilogue = False
     if args.no_qkv_rope_epilogue:
         model.qkv_rope_epilogue = False
-    if args.two_stream_fetch:
-        for lane in model.lanes:
-            lane.cache.one_stream_fetch = False
     cache_one_stream = all(lane.cache.one_stream_active() for lane in model.lanes)
+    lane_streams = model.lane_streams
     qkv_rope_epi = model.qkv_rope_epilogue
     cache = model.cache
     log(f"setup done in {time.time() - t0:.1f}s; sparse_start {cache.sparse_start} sparse_end {cache.sparse_end} "
@@ -1498,7 +1511,9 @@ def main() -> int:
                                + f"{lanes} interleaved batch lane(s), "
                                + ("hit moves in their own launches, " if args.separate_hit_moves else
                                   "hit moves in the selection launch, ")
-                               + ("value fetch and key rebuild in one launch on the compute stream, "
+                               + (("value fetch and key rebuild in one launch on each lane's own stream, "
+                                   if lane_streams else
+                                   "value fetch and key rebuild in one launch on the compute stream, ")
                                   if cache_one_stream else "")
                                + ("RoPE + KV append in the QKV projection's epilogue, "
                                   if qkv_rope_epi else "")

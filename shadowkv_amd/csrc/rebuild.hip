@@ -344,12 +344,14 @@ __global__ void __launch_bounds__(kNW * 64, 2) fetch_rebuild_kernel(RebuildArgs 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Fetch workgroups of a fused launch with `waves`-wave workgroups: the target in 4-wave
-// workgroups (skv::fused_fetch_workgroups_target) scaled to the workgroup size, then as few as give
-// every workgroup the same number of tiles (the launch lasts as long as its busiest fetch
-// workgroup), rounded up to a multiple of 8 for the rebuild tiles' XCD map.
+// workgroups (the caller's f.workgroups when positive, else skv::fused_fetch_workgroups_target)
+// scaled to the workgroup size, then as few as give every workgroup the same number of tiles (the
+// launch lasts as long as its busiest fetch workgroup), rounded up to a multiple of 8 for the
+// rebuild tiles' XCD map.
 int fused_fetch_workgroups(const skv::FetchArgs<int32_t>& f, int waves) {
   const int tiles = std::max(f.rows * f.tiles, 1);
-  const int target = std::max(1, skv::fused_fetch_workgroups_target() * 4 / waves);
+  const int t4 = f.workgroups > 0 ? f.workgroups : skv::fused_fetch_workgroups_target();
+  const int target = std::max(1, t4 * 4 / waves);
   const int per = (tiles + target - 1) / target;  // tiles per workgroup
   const int want = (tiles + per - 1) / per;
   return (want + kXcds - 1) / kXcds * kXcds;
@@ -607,8 +609,12 @@ extern "C" int skv_fetch_misses_rebuild_k_rope(
     const int64_t* position_ids, int64_t pid_stride_b, int64_t pid_stride_h, const int32_t* cnts,
     const uint16_t* cos_sin, int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode, uint16_t* cache,
     int64_t stride_cache_b, int64_t stride_cache_h, int64_t stride_cache_s, int sparse_start, int batch_size,
-    int heads, int num_chunks, int chunk_size, int rank, int head_dim, void* stream) {
+    int heads, int num_chunks, int chunk_size, int rank, int head_dim, int fetch_workgroups, void* stream) {
   const char* what = "fetch_misses_rebuild_k_rope";
+  if (fetch_workgroups < 0 || fetch_workgroups > 65536) {
+    skv_set_error("%s: fetch_workgroups=%d (0 for the default, at most 65536)", what, fetch_workgroups);
+    return SKV_EINVAL;
+  }
   if (head_dim != kHeadDim || (rope_mode != 0 && rope_mode != 1)) {
     skv_set_error("%s: head_dim=%d (must be 128), rope_mode=%d (0 half-split, 1 GLM)", what, head_dim, rope_mode);
     return SKV_EUNSUPPORTED;
@@ -645,6 +651,7 @@ extern "C" int skv_fetch_misses_rebuild_k_rope(
   f.src_chunks = cpu_v_length / chunk_elems;
   f.rows = batch_size * heads;
   f.tiles = (num_chunks + skv::kChunksPerFetchWG - 1) / skv::kChunksPerFetchWG;
+  f.workgroups = fetch_workgroups;  // the target (0: default); the launch sets the count
   RebuildArgs r{};
   r.u = u;
   r.u_sb = u_stride_b;

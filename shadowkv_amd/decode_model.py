@@ -53,6 +53,11 @@ GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="
 
 
 
+# Fetch workgroups (4-wave) of each lane's one-launch fetch + rebuild with two lanes on their own
+# side streams (the two launches overlap on the host link).
+LANE_FETCH_WORKGROUPS = 56
+
+
 def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int) -> int:
     """Batch lanes for the decode step: 2 when a layer's value fetch over the host link outlasts
     three passes over the layer's dense weights, else 1. Each lane streams the dense weights once
@@ -194,7 +199,8 @@ class SyntheticDecoder:
     def __init__(self, shape: ModelShape, batch: int, ctx: int, *, sparse_budget: int = 2048, rank: int = 160,
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
                  dtype=torch.bfloat16, lanes: int = 1, fused: bool = True, chunk_cache: int | None = None,
-                 one_stream_fetch: bool | None = None, state: str = "synthetic", host_stores: int | None = None):
+                 one_stream_fetch: bool | None = None, state: str = "synthetic", host_stores: int | None = None,
+                 lane_streams: bool | None = None):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
         # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels and
         # the projections on the skinny linear kernel (libshadowkv_amd), instead of torch operations
@@ -228,6 +234,12 @@ class SyntheticDecoder:
         cfg = types.SimpleNamespace(num_attention_heads=s.heads, num_key_value_heads=s.kv_heads,
                                     hidden_size=s.heads * D, num_hidden_layers=s.layers)
         lb = batch // lanes
+        # Two lanes, no chunk pool: each lane's one-launch fetch + rebuild on its own side stream
+        # (default), else the shared fetch and rebuild streams.
+        self.lane_streams = (lanes == 2 and chunk_cache is None and one_stream_fetch is not False) \
+            if lane_streams is None else bool(lane_streams)
+        if self.lane_streams and (lanes != 2 or chunk_cache is not None):
+            raise ValueError("lane_streams takes two lanes and no chunk pool")
         self.lanes = []
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
@@ -250,10 +262,24 @@ class SyntheticDecoder:
             cache.fold_hit_moves = True
             # One lane: the step runs on the compute stream alone, the value fetch and key rebuild
             # as one launch after a selection that moved both buffers' hits (no cross-stream wait
-            # before or after the fetch: GLM-4-9B batch 4 and Llama-3-8B-1M, measured in DESIGN).
+            # before or after the fetch; MI355X tokens/s vs the two-stream step: GLM-4-9B batch 4
+            # 429.8 vs 418.4, Llama-3-8B-1M 38.42 vs 37.81).
             cache.one_stream_fetch = (lanes == 1 and chunk_cache is None) if one_stream_fetch is None \
                 else bool(one_stream_fetch)
-            if lanes > 1:
+            if self.lane_streams:
+                # Each lane's value fetch and key rebuild as one launch on a side stream of its own
+                # (lane 0 on the fetch stream, lane 1 on the rebuild stream), after a selection that
+                # moved both buffers' hits. A lane's fetch can then start while the other lane's is
+                # still running: with one shared fetch stream each fetch followed the previous one
+                # only ~10 us after it ended (the cross-stream dependency on its selection, resolved
+                # long before, still costs that in a graph replay), idling the host link for 5% of
+                # the step. 56 fetch workgroups per launch (the two launches overlap): measured on
+                # MI355X, Llama-3.1-8B batch 8 ctx 122880, tokens/s by fetch workgroups 40 / 48 / 56 /
+                # 64: 384 / 397 / 402 / 396, against 386 with the shared streams.
+                cache.one_stream_fetch = True
+                cache.lane_stream = side_stream(device, ("fetch", "rebuild")[i])
+                cache.fused_fetch_workgroups = LANE_FETCH_WORKGROUPS
+            elif lanes > 1:
                 # All lanes share one value-fetch stream and one key-rebuild stream (their fetches
                 # follow one another on the host link anyway); taking the key rebuild off the
                 # compute stream keeps it out of the stretch between two lanes' fetches.

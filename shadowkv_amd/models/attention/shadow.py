@@ -60,11 +60,19 @@ class ShadowAttention(AttentionBase):
         kv_cache = self.kv_cache
         position_ids = kv_cache.get_retrieval_position_ids(layer_idx=layer_idx, query_states=query_states)
 
-        if kv_cache.one_stream_active():
-            # the value fetch and the key rebuild as one launch on this stream (hits moved by the selection)
-            key_states, value_states = kv_cache.fetch_and_rebuild(layer_idx, position_ids, self.cos_sin_cache)
-            return query_states, key_states, value_states, []
         curr_stream = torch.cuda.current_stream()
+        if kv_cache.one_stream_active():
+            # the value fetch and the key rebuild as one launch (hits moved by the selection), on this
+            # stream or on the cache's lane_stream, joined in decode_end
+            lane_stream = getattr(kv_cache, "lane_stream", None)
+            if lane_stream is None:
+                key_states, value_states = kv_cache.fetch_and_rebuild(layer_idx, position_ids, self.cos_sin_cache)
+                return query_states, key_states, value_states, []
+            with torch.cuda.stream(lane_stream):
+                lane_stream.wait_stream(curr_stream)
+                key_states, value_states = kv_cache.fetch_and_rebuild(layer_idx, position_ids, self.cos_sin_cache)
+                done = [lane_stream.record_event()]
+            return query_states, key_states, value_states, done
         copy_stream = kv_cache.copy_stream
         # The value hits move within the GPU buffer here, so the copy stream (whose transfers
         # follow one another on the host link) carries the host-link gather alone.

@@ -161,6 +161,11 @@ class ShadowKVCache_CPU(KVCacheBase):
         # value-fetch stream: the given one, else the process's shared fetch side stream
         self.copy_stream = copy_stream if copy_stream is not None else side_stream(device, "fetch")
         self.key_stream = None  # optional: run the key rebuild on this stream (joined before attention)
+        # optional: run the one-launch value fetch + key rebuild (one_stream_active) on this stream
+        # instead of the current one (joined before attention), with this many fetch workgroups
+        # (4-wave workgroups; 0: the library default)
+        self.lane_stream = None
+        self.fused_fetch_workgroups = 0
         self.attn_workspace = None
         self.attn_out = None
         self.select_workspace = None  # allocated with the landmarks
@@ -507,7 +512,8 @@ class ShadowKVCache_CPU(KVCacheBase):
                                              self.cnts, int(self.max_ctx_chunks_len * self.head_dim),
                                              self.kernel_offset, self.kernel_stride, self.U[layer_idx],
                                              self.SV[layer_idx], position_ids, cos_sin_cache,
-                                             self.k_cache_buffer[layer_idx], self.sparse_start, self.chunk_size)
+                                             self.k_cache_buffer[layer_idx], self.sparse_start, self.chunk_size,
+                                             fetch_workgroups=self.fused_fetch_workgroups)
         return (self._live_view(self.k_cache_buffer[layer_idx], layer_idx),
                 self._live_view(self.v_cache_buffer[layer_idx], layer_idx))
 

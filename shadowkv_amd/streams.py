@@ -7,7 +7,9 @@ block the queue for good. The decode path therefore uses at most 4 streams: the 
 stream and three side streams per device, one per role (the value fetch, the key rebuild, and
 the stream a decoder captures its HIP graph on: torch.cuda.graph would otherwise create a capture
 stream of its own), created once and shared by every cache and decoder of the process. Work of different
-caches on one side stream runs in issue order, as the host link serialises the fetches anyway.
+caches on one side stream runs in issue order. A two-lane decoder gives each lane one of the
+first two (its one-launch value fetch + key rebuild runs there), so that the lanes' fetches can
+overlap on the host link.
 """
 from __future__ import annotations
 

@@ -6,6 +6,8 @@
   bit, as the separate in-buffer compaction launches (one lane and two lanes);
 * the QKV projection with RoPE + append in its epilogue gives the same tokens and cache state, bit
   for bit, as the projection followed by the RoPE + append kernel;
+* two lanes, each with its one-launch fetch + rebuild on its own side stream, give the same tokens
+  and cache state, bit for bit, as the lanes sharing one fetch and one rebuild stream;
 * the fused new-token step (residual + RMSNorm, skinny linear, SiLU-and-mul, RoPE + append
   kernels) agrees with the reference call sequence on torch operations (F.rms_norm, F.linear,
   F.silu, apply_rotary_pos_emb_new + update_kv_cache) within bf16 tolerance."""
@@ -123,6 +125,37 @@ def test_qkv_rope_epilogue_matches_two_kernels(gpu, model, lanes):
         torch.cuda.synchronize()
         assert torch.equal(te, tt), ("replay", t)
         for a, b in zip(_state(epi), _state(two)):
+            assert torch.equal(a, b), ("replay", t)
+
+
+def test_lane_streams_match_shared_streams(gpu):
+    """Two lanes with each lane's one-launch value fetch + key rebuild on a side stream of its own
+    (the decoder's default) give the same tokens and cache state, bit for bit, as the lanes sharing
+    one fetch stream and one rebuild stream, eager and in captured graphs."""
+    print("lane streams vs shared fetch / rebuild streams, batch 8 in 2 lanes", flush=True)
+    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    kw = dict(sparse_budget=2048, decode_len=12, lanes=2, seed=19)
+    own = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    shared = decode_model.SyntheticDecoder(shape, 8, 16384, lane_streams=False, **kw)
+    assert own.lane_streams and not shared.lane_streams
+    assert all(lane.cache.one_stream_active() and lane.cache.lane_stream is not None for lane in own.lanes)
+    assert own.lanes[0].cache.lane_stream is not own.lanes[1].cache.lane_stream
+    assert not any(lane.cache.one_stream_active() for lane in shared.lanes)
+    to = ts = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(9))
+    for t in range(3):
+        to = own.decode_step(to)
+        ts = shared.decode_step(ts)
+        torch.cuda.synchronize()
+        assert torch.equal(to, ts), t
+        for a, b in zip(_state(own), _state(shared)):
+            assert torch.equal(a, b), t
+    own.capture(to, steps=2)
+    shared.capture(ts, steps=2)
+    for t in range(2):
+        to, ts = own.replay(), shared.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(to, ts), ("replay", t)
+        for a, b in zip(_state(own), _state(shared)):
             assert torch.equal(a, b), ("replay", t)
 
 
