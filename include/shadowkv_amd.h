@@ -403,7 +403,11 @@ int skv_gather_rows(const uint16_t* src, int rows, int src_rows, const int64_t* 
  * the pair at models/kvcache/shadow.py:578-593 (value fetch on copy_stream, key rebuild on the
  * current stream) for callers that run the step on one stream, saving the two cross-stream waits
  * around the fetch. Results are those of the two calls. fetch_workgroups: the fetch workgroups to
- * aim for, counted in 4-wave workgroups (0: the library default, 64, or SKV_FUSED_FETCH_WGS). */
+ * aim for, counted in 4-wave workgroups (0: the library default, 64, or SKV_FUSED_FETCH_WGS).
+ * rebuild_workgroups: 0 gives every rebuild tile a workgroup of its own; a positive cap (rounded
+ * up to a multiple of 8) makes that many workgroups loop over the tiles, so the rebuild spreads over
+ * the fetch instead of filling the GPU at its start (taken by the half-split RoPE instances of rank
+ * <= 160 with 128-row tiles, the tiles of a 4-sequence decode lane; the others ignore it). */
 int skv_fetch_misses_rebuild_k_rope(const void* values, void* v_cache_buffer, const int32_t* offsets,
                                     int64_t cpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
                                     const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
@@ -413,7 +417,8 @@ int skv_fetch_misses_rebuild_k_rope(const void* values, void* v_cache_buffer, co
                                     int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode, uint16_t* cache,
                                     int64_t stride_cache_b, int64_t stride_cache_h, int64_t stride_cache_s,
                                     int sparse_start, int batch_size, int heads, int num_chunks, int chunk_size,
-                                    int rank, int head_dim, int fetch_workgroups, void* stream);
+                                    int rank, int head_dim, int fetch_workgroups, int rebuild_workgroups,
+                                    void* stream);
 
 /* ---- f3: device chunk pool (a GPU cache of P >= S chunk slots per (b, h) and layer) ------
  * No reference counterpart: extends the slot reuse of reorder_keys_and_compute_offsets

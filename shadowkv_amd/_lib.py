@@ -90,7 +90,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                _i64, _p, _i64, _p]),
     "skv_fetch_misses_rebuild_k_rope": (
         _i32, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
-               _i64, _i64, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
+               _i64, _i64, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "skv_hbm_read_probe": (_i32, [_p, _i64, _i32, _i32, _p, _i64, _p]),
     "skv_mfma_peak_probe": (_i32, [_i32, _i32, _p, _i64, _p]),
     "skv_mfma_peak_probe_flops": (_i64, [_i32, _i32]),

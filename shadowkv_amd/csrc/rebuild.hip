@@ -66,6 +66,8 @@ struct RebuildArgs {
   int o_start;
   int B, H, S, chunk, rank, tiles;
   int spread;  // deal a head's miss rows evenly over its tiles (else whole tiles, hit tiles idle)
+  int grid_tiles;  // tile workgroups of the unfused grid (heads padded to 8 x tiles)
+  int rebuild_wgs;  // fused launch: cap on the rebuild workgroups, which then loop over the tiles (0: one per tile)
   // Optional destination slots (chunk pool): row r of entry i goes to cache row
   // o_start + dst_slot[i] * chunk + r % chunk; entries outside [0, pool_slots) are skipped.
   const int32_t* dst_slot;
@@ -325,6 +327,12 @@ __global__ void __launch_bounds__(kNW * 64, kNW > 4 ? 1 : 2) rebuild_kernel(Rebu
   rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, blockIdx.x);
 }
 
+// Fused instances whose rebuild workgroups can loop over several tiles without spilling (half-split
+// RoPE, ranks up to 160, 128-row tiles of 4 waves: the tiles of a decode lane); the others keep
+// one workgroup per tile.
+template <int kMode, int KS, int kNW, int kIters>
+constexpr bool kFusedLoops = kIters == 1 && KS <= 5 && kNW == 4 && kMode == kRopeHalf;
+
 // The value fetch of the misses and the key rebuild in one launch: workgroups [0, f.workgroups)
 // gather the miss chunks from the pinned host store (skv::fetch_role, host-link bound), the rest
 // rebuild the key rows (HBM bound), side by side. Both need only the selection's offsets and
@@ -338,7 +346,18 @@ __global__ void __launch_bounds__(kNW * 64, 2) fetch_rebuild_kernel(RebuildArgs 
     skv::fetch_role(f, wg, f.workgroups);
     return;
   }
-  rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, wg - f.workgroups);
+  // The rebuild workgroups (a multiple of 8) walk the tiles with their count as the stride, so a
+  // tile keeps the XCD of its unfused workgroup; each pass ends at a barrier before the next
+  // tile's LDS writes.
+  if constexpr (kFusedLoops<kMode, KS, kNW, kIters>) {
+    const int nrb = static_cast<int>(gridDim.x) - f.workgroups;
+    for (int t = wg - f.workgroups; t < a.grid_tiles; t += nrb) {
+      rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, t);
+      __syncthreads();
+    }
+  } else {
+    rebuild_role<kMode, KS, IdxT, kNW, kIters>(a, wg - f.workgroups);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -379,7 +398,11 @@ int launch_ks(dim3 grid, size_t lds, hipStream_t stream, const RebuildArgs& a, c
     }
     skv::FetchArgs<int32_t> ff = *f;
     ff.workgroups = fused_fetch_workgroups(ff, kNW);
-    hipLaunchKernelGGL((fetch_rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), dim3(grid.x + ff.workgroups),
+    // rebuild workgroups: the caller's cap (a multiple of 8) where the instance loops over tiles
+    const int cap = (a.rebuild_wgs + kXcds - 1) / kXcds * kXcds;
+    const int rb = cap > 0 && kFusedLoops<kMode, KS, kNW, kIters> ? std::min(static_cast<int>(grid.x), cap)
+                                                                   : static_cast<int>(grid.x);
+    hipLaunchKernelGGL((fetch_rebuild_kernel<kMode, KS, IdxT, kNW, kIters>), dim3(rb + ff.workgroups),
                        dim3(kNW * 64), lds, stream, a, ff);
     return SKV_OK;
   } else {
@@ -497,6 +520,7 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
   }
   const int heads_padded = (BH + kXcds - 1) / kXcds * kXcds;
   const dim3 grid(static_cast<unsigned>(heads_padded * a.tiles));
+  a.grid_tiles = static_cast<int>(grid.x);
   const size_t lds = static_cast<size_t>(kHeadDim) * (a.rank + 8) * sizeof(uint16_t) + 2 * tile_rows * sizeof(int32_t) +
                      static_cast<size_t>(waves) * 16 * kStLd * sizeof(uint16_t);
   const int ks = (a.rank + 31) / 32;
@@ -609,10 +633,12 @@ extern "C" int skv_fetch_misses_rebuild_k_rope(
     const int64_t* position_ids, int64_t pid_stride_b, int64_t pid_stride_h, const int32_t* cnts,
     const uint16_t* cos_sin, int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode, uint16_t* cache,
     int64_t stride_cache_b, int64_t stride_cache_h, int64_t stride_cache_s, int sparse_start, int batch_size,
-    int heads, int num_chunks, int chunk_size, int rank, int head_dim, int fetch_workgroups, void* stream) {
+    int heads, int num_chunks, int chunk_size, int rank, int head_dim, int fetch_workgroups, int rebuild_workgroups,
+    void* stream) {
   const char* what = "fetch_misses_rebuild_k_rope";
-  if (fetch_workgroups < 0 || fetch_workgroups > 65536) {
-    skv_set_error("%s: fetch_workgroups=%d (0 for the default, at most 65536)", what, fetch_workgroups);
+  if (fetch_workgroups < 0 || fetch_workgroups > 65536 || rebuild_workgroups < 0 || rebuild_workgroups > 65536) {
+    skv_set_error("%s: fetch_workgroups=%d rebuild_workgroups=%d (0 for the default, at most 65536)", what,
+                  fetch_workgroups, rebuild_workgroups);
     return SKV_EINVAL;
   }
   if (head_dim != kHeadDim || (rope_mode != 0 && rope_mode != 1)) {
@@ -679,6 +705,7 @@ extern "C" int skv_fetch_misses_rebuild_k_rope(
   r.S = num_chunks;
   r.chunk = chunk_size;
   r.rank = rank;
+  r.rebuild_wgs = rebuild_workgroups;
   return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, true, r, static_cast<hipStream_t>(stream), &f);
 }
 

@@ -54,8 +54,13 @@ GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="
 
 
 # Fetch workgroups (4-wave) of each lane's one-launch fetch + rebuild with two lanes on their own
-# side streams (the two launches overlap on the host link).
+# side streams (the two launches overlap on the host link), and the cap on its rebuild workgroups,
+# which then loop over the key tiles: the rebuild spreads over the ~300 us fetch instead of
+# filling the GPU at its start, where it slowed the other lane's attention and projections
+# (MI355X, Llama-3.1-8B batch 8 ctx 122880, tokens/s by cap 32 / 40 / 48 / 56: 400.6 / 402.3 /
+# 405.2 / 399.6, against 395.0 with one workgroup per tile on the same box).
 LANE_FETCH_WORKGROUPS = 56
+LANE_REBUILD_WORKGROUPS = 48
 
 
 def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int) -> int:
@@ -279,6 +284,7 @@ class SyntheticDecoder:
                 cache.one_stream_fetch = True
                 cache.lane_stream = side_stream(device, ("fetch", "rebuild")[i])
                 cache.fused_fetch_workgroups = LANE_FETCH_WORKGROUPS
+                cache.fused_rebuild_workgroups = LANE_REBUILD_WORKGROUPS
             elif lanes > 1:
                 # All lanes share one value-fetch stream and one key-rebuild stream (their fetches
                 # follow one another on the host link anyway); taking the key rebuild off the

@@ -395,13 +395,16 @@ def _rebuild_geometry(u, sv, position_ids, cnts, cos_sin, cache, sparse_start, c
 
 
 def fetch_misses_rebuild_k_rope(values, v_cache_buffer, offsets, cnts, cpu_v_length, gpu_v_offset, gpu_v_stride,
-                                u, sv, position_ids, cos_sin, cache, sparse_start, chunk_size, fetch_workgroups=0):
+                                u, sv, position_ids, cos_sin, cache, sparse_start, chunk_size, fetch_workgroups=0,
+                                rebuild_workgroups=0):
     """The value fetch of the misses (gather_copy_with_offsets(..., misses_only=True)) and the key
     rebuild (rebuild_k_rope) in one launch on the current stream, their workgroups side by side.
     Both buffers' hits must already be in place (select_chunks with move=(v_buffer, k_buffer, ...)).
     Same arguments and results as the two calls; the value chunk is chunk_size * 128 elements.
     fetch_workgroups: the fetch workgroups to aim for, in 4-wave workgroups (0: the library's
-    default)."""
+    default). rebuild_workgroups: 0 gives every rebuild tile its own workgroup; a positive cap makes
+    that many workgroups loop over the tiles (where the kernel instance supports it), spreading the
+    rebuild over the fetch."""
     B, H, S = position_ids.shape
     _dev(position_ids, "position_ids", torch.int64)
     u_sb, u_sh, u_sr, u_rows, sv_sb, sv_sh, sv_sn, mode, rank = _rebuild_geometry(
@@ -420,7 +423,8 @@ def fetch_misses_rebuild_k_rope(values, v_cache_buffer, offsets, cnts, cpu_v_len
               row_stride, gpu_v_offset, gpu_v_stride, u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb,
               sv_sh, sv_sn, position_ids.data_ptr(), position_ids.stride(0), position_ids.stride(1), cnts.data_ptr(),
               cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0),
-              cache.stride(1), cache.stride(2), sparse_start, B, H, S, chunk_size, rank, 128, int(fetch_workgroups), _stream())
+              cache.stride(1), cache.stride(2), sparse_start, B, H, S, chunk_size, rank, 128, int(fetch_workgroups),
+              int(rebuild_workgroups), _stream())
 
 
 # ---------------------------------------------------------------------------------------------

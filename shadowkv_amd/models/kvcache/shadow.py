@@ -163,9 +163,11 @@ class ShadowKVCache_CPU(KVCacheBase):
         self.key_stream = None  # optional: run the key rebuild on this stream (joined before attention)
         # optional: run the one-launch value fetch + key rebuild (one_stream_active) on this stream
         # instead of the current one (joined before attention), with this many fetch workgroups
-        # (4-wave workgroups; 0: the library default)
+        # (4-wave workgroups; 0: the library default) and at most this many rebuild workgroups
+        # looping over the tiles (0: one per tile)
         self.lane_stream = None
         self.fused_fetch_workgroups = 0
+        self.fused_rebuild_workgroups = 0
         self.attn_workspace = None
         self.attn_out = None
         self.select_workspace = None  # allocated with the landmarks
@@ -513,7 +515,8 @@ class ShadowKVCache_CPU(KVCacheBase):
                                              self.kernel_offset, self.kernel_stride, self.U[layer_idx],
                                              self.SV[layer_idx], position_ids, cos_sin_cache,
                                              self.k_cache_buffer[layer_idx], self.sparse_start, self.chunk_size,
-                                             fetch_workgroups=self.fused_fetch_workgroups)
+                                             fetch_workgroups=self.fused_fetch_workgroups,
+                                             rebuild_workgroups=self.fused_rebuild_workgroups)
         return (self._live_view(self.k_cache_buffer[layer_idx], layer_idx),
                 self._live_view(self.v_cache_buffer[layer_idx], layer_idx))
 

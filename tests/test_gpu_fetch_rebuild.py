@@ -1,8 +1,9 @@
 """The value fetch of the misses and the key rebuild as one launch (skv_fetch_misses_rebuild_k_rope)
 against the two calls it replaces (gather_copy_with_offsets(..., misses_only=True) and
 rebuild_k_rope): value and key buffers bit-identical, for every rebuild tile shape (64-, 128- and
-256-row workgroups, so 2- and 4-wave fused grids), both rotary layouts, and rows whose chunks are
-all hits or all misses; and one-lane decoders with the one-launch step against the two-stream one."""
+256-row workgroups, so 2- and 4-wave fused grids), both rotary layouts, rows whose chunks are all
+hits or all misses, and rebuild workgroups capped so that they loop over the tiles; and one-lane
+decoders with the one-launch step against the two-stream one."""
 from dataclasses import replace
 
 import pytest
@@ -62,12 +63,15 @@ def _one_launch_case(gpu, B, H, S, glm, R, c, seed):
     shadowkv.gather_copy_with_offsets(values, va, None, off_d, cnts_d, None, B, H, chunks * c * D, S * c * D,
                                       sparse_start * D, stride, S, misses_only=True)
     shadowkv.rebuild_k_rope(U, SV, pos_d, cnts_d, cos_sin, ka, sparse_start, c)
-    vb, kb = v0.clone(), k0.clone()
-    shadowkv.fetch_misses_rebuild_k_rope(values, vb, off_d, cnts_d, chunks * c * D, sparse_start * D, stride, U, SV,
-                                         pos_d, cos_sin, kb, sparse_start, c)
-    torch.cuda.synchronize()
-    assert torch.equal(vb.view(torch.int16), va.view(torch.int16))
-    assert torch.equal(kb.view(torch.int16), ka.view(torch.int16))
+    # rebuild workgroups: one per tile, or capped at 8 / 48 / 1000 (looping over the tiles where the
+    # kernel instance supports it: the half-split rank-160 128-row tiles of 32 heads x 2048 rows)
+    for cap in (0, 8, 48, 1000):
+        vb, kb = v0.clone(), k0.clone()
+        shadowkv.fetch_misses_rebuild_k_rope(values, vb, off_d, cnts_d, chunks * c * D, sparse_start * D, stride, U,
+                                             SV, pos_d, cos_sin, kb, sparse_start, c, rebuild_workgroups=cap)
+        torch.cuda.synchronize()
+        assert torch.equal(vb.view(torch.int16), va.view(torch.int16)), cap
+        assert torch.equal(kb.view(torch.int16), ka.view(torch.int16)), cap
     # the launch did write: every miss chunk of row 0 now holds its host chunk
     r0 = vb[0, 0, sparse_start:sparse_start + S * c].reshape(S, c * D).cpu()
     assert torch.equal(r0.view(torch.int16), values[0, 0, pos[0, 0]].view(torch.int16))
