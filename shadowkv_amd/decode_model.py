@@ -56,10 +56,12 @@ GLM4_9B = ModelShape("GLM-4-9B", 40, 4096, 13696, 32, 2, 151552, 10000.0, rope="
 # Fetch workgroups (4-wave) of each lane's one-launch fetch + rebuild with two lanes on their own
 # side streams (the two launches overlap on the host link), and the cap on its rebuild workgroups,
 # which then loop over the key tiles: the rebuild spreads over the ~300 us fetch instead of
-# filling the GPU at its start, where it slowed the other lane's attention and projections
-# (MI355X, Llama-3.1-8B batch 8 ctx 122880, tokens/s by cap 32 / 40 / 48 / 56: 400.6 / 402.3 /
-# 405.2 / 399.6, against 395.0 with one workgroup per tile on the same box).
-LANE_FETCH_WORKGROUPS = 56
+# filling the GPU at its start, where it slowed the other lane's attention and projections.
+# Measured on MI355X, Llama-3.1-8B batch 8 ctx 122880, tokens/s: with 56 fetch workgroups, rebuild
+# cap 32 / 40 / 48 / 56 / 64: 400.6 / 402.3 / 405.2 / 399.6 / 396.4, against 395.0 with one
+# workgroup per tile; with the cap at 48, fetch workgroups 48 / 56 / 64 / 80 / 96: 396.8 / 404.4 /
+# 408.1 / 364.5 / 351.4 (two lanes' 80 or more host-read workgroups at once slow the link).
+LANE_FETCH_WORKGROUPS = 64
 LANE_REBUILD_WORKGROUPS = 48
 
 
@@ -278,9 +280,8 @@ class SyntheticDecoder:
                 # still running: with one shared fetch stream each fetch followed the previous one
                 # only ~10 us after it ended (the cross-stream dependency on its selection, resolved
                 # long before, still costs that in a graph replay), idling the host link for 5% of
-                # the step. 56 fetch workgroups per launch (the two launches overlap): measured on
-                # MI355X, Llama-3.1-8B batch 8 ctx 122880, tokens/s by fetch workgroups 40 / 48 / 56 /
-                # 64: 384 / 397 / 402 / 396, against 386 with the shared streams.
+                # the step (Llama-3.1-8B batch 8 ctx 122880 on MI355X: 402 vs 386 tokens/s with 56
+                # fetch workgroups and one rebuild workgroup per tile; the workgroup counts above).
                 cache.one_stream_fetch = True
                 cache.lane_stream = side_stream(device, ("fetch", "rebuild")[i])
                 cache.fused_fetch_workgroups = LANE_FETCH_WORKGROUPS
