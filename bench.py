@@ -96,6 +96,12 @@ def parse() -> argparse.Namespace:
     p.add_argument("--summarize-trace", metavar="CSV",
                    help="summarise a rocprofv3 --kernel-trace CSV of a decode run of this script (made with the "
                         "same --model/--batch/--ctx/--budget/--steps/--warmup) into profiles/, then exit")
+    p.add_argument("--value-store", choices=["host", "device"], default="host",
+                   help="where the value store lives: pinned host memory (the workload as configured) or device "
+                        "memory (HBM; the whole store fits MI355X's 288 GB)")
+    p.add_argument("--device-store-variant", type=int, default=1,
+                   help="also time the same decode with the value store in device memory, reported in detail "
+                        "(0 to skip)")
     p.add_argument("--two-stream-fetch", action="store_true",
                    help="one-lane decoders: value fetch on the copy stream and key rebuild on the compute stream "
                         "(the reference's arrangement) instead of one fused launch on the compute stream; two-lane "
@@ -733,6 +739,52 @@ def pool_variant(args, shape, lanes) -> dict:
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     torch._C._host_emptyCache()
+    return res
+
+
+def device_store_variant(args, shape) -> dict:
+    """The same decode workload with the value store in device memory instead of pinned host memory
+    (ShadowKVCache_CPU(value_store="device"); the Llama-3.1-8B batch-8 ctx-122880 store is 64 GB,
+    which MI355X's 288 GB of HBM holds beside the rest of the state): the same kernels gather the
+    missed chunks from HBM and nothing crosses the host link, so one lane (auto_lanes) and the
+    step is set by the compute. Timed as the main measurement; the host-store decoder is released
+    first."""
+    import gc
+    import torch
+    from shadowkv_amd import decode_model
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+    lanes = decode_model.auto_lanes(shape, args.batch, args.budget, "device")
+    log(f"device value store variant: {lanes} lane(s)")
+    dm = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
+                                       decode_len=args.warmup + args.steps + 8, lanes=lanes, value_store="device")
+    tok = torch.randint(0, shape.vocab, (args.batch, 1), device="cuda")
+    for _ in range(args.warmup):
+        tok = dm.decode_step(tok)
+    per_call = math.gcd(args.steps, max(1, args.graph_steps))
+    dm.capture(tok, steps=per_call)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps // per_call):
+        tok = dm.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    store_gb = sum(t.numel() * t.element_size() for t in {id(t): t for t in dm.cache.v_cache_cpu}.values()) \
+        * len(dm.lanes) / 1e9
+    res = {"tokens_per_s": round(args.batch * args.steps / elapsed, 3),
+           "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "lanes": lanes,
+           "value_store_device_GB": round(store_gb, 1),
+           "note": "same workload with the value store in device memory (HBM) instead of pinned host memory: the "
+                   "same kernels gather the missed chunks from HBM, nothing crosses the host link; the tokens "
+                   "and state equal the host-store decoder's bit for bit (tests/test_gpu_decoder_variants.py)"}
+    log(f"device value store variant {res}")
+    del dm
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     return res
 
 
@@ -1377,12 +1429,13 @@ def main() -> int:
         return 0
     t0 = time.time()
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
-    lanes = args.lanes if args.lanes else decode_model.auto_lanes(shape, args.batch, args.budget)
+    lanes = args.lanes if args.lanes else decode_model.auto_lanes(shape, args.batch, args.budget, args.value_store)
     lanes = lanes if args.batch % lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes,
                                           chunk_cache=args.chunk_cache, state=args.state,
-                                          one_stream_fetch=False if args.two_stream_fetch else None)
+                                          one_stream_fetch=False if args.two_stream_fetch else None,
+                                          value_store=args.value_store)
     if args.separate_hit_moves:
         for lane in model.lanes:
             lane.cache.fold_hit_moves = False
@@ -1481,12 +1534,16 @@ def main() -> int:
             detail["single_layer"].update(sl)
             log(f"single layer CPU {sl}")
 
-    if detail is not None and args.chunk_cache is None and (args.pool_variant > 0 or args.encoded_variant):
+    host_store = args.value_store == "host"
+    if detail is not None and args.chunk_cache is None and host_store and \
+            (args.pool_variant > 0 or args.encoded_variant or args.device_store_variant):
         model = cache = step = None  # release the reference-mode decoder first
         if args.pool_variant > 0:
             detail["chunk_pool"] = pool_variant(args, shape, lanes)
         if args.encoded_variant and args.state == "synthetic":
             detail["encoded_state"] = encoded_variant(args, shape, lanes)
+        if args.device_store_variant:
+            detail["device_value_store"] = device_store_variant(args, shape)
 
     out = {
         "metric": ("decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util"
@@ -1506,7 +1563,8 @@ def main() -> int:
                  "synthetic: random-init weights, ShadowKV state built by the device encoder from seeded low-rank "
                  "prompt keys, greedy tokens"),
         "config": {"workload": f"{shape.name}-shape {shape.layers}-layer decode, batch {args.batch}, ctx {args.ctx}, "
-                               f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, V in pinned host memory, "
+                               f"ShadowKV rank 160 chunk {args.chunk} budget {args.budget}, "
+                               + ("V in pinned host memory, " if host_store else "V in device memory, ")
                                + (f"device chunk pool of {args.chunk_cache} slots, " if args.chunk_cache else "")
                                + f"{lanes} interleaved batch lane(s), "
                                + ("hit moves in their own launches, " if args.separate_hit_moves else

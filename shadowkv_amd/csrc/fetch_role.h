@@ -47,6 +47,31 @@ inline int fused_fetch_workgroups_target() {
   return wgs;
 }
 
+// Whether the value store at p is device memory (a store kept in HBM, e.g. value_store="device"
+// of the cache) rather than pinned host memory read over the host link; false when the runtime
+// cannot tell. A gather from HBM has none of the host reads' cost to concurrent kernels and wants
+// the whole GPU: the fetch launches then take kDeviceFetchWGs workgroups (MI355X, Llama-3.1-8B
+// batch 8 ctx 122880 with the store in HBM, one-launch fetch + rebuild, tokens/s at 64 / 128 /
+// 256 / 512 fetch workgroups: 741.7 / 887.0 / 989.8 / 997.8).
+constexpr int kDeviceFetchWGs = 512;
+
+inline bool is_device_memory(const void* p) {
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();  // (an unregistered host pointer: not device memory; clear the error it left)
+    return false;
+  }
+  return a.type == hipMemoryTypeDevice;
+}
+
+// Fetch workgroups for a launch over `tiles` fetch tiles reading `src`: every tile its own
+// workgroup up to kDeviceFetchWGs for a store in device memory, fetch_workgroups() for one in
+// pinned host memory.
+inline int fetch_workgroups_for(const void* src, int tiles) {
+  const int cap = is_device_memory(src) ? kDeviceFetchWGs : fetch_workgroups();
+  return tiles < cap ? tiles : cap;
+}
+
 // dst slot i of row <- src chunk ids[row*S + i] of row, for i in [start, S) where start =
 // cnts[row] (or 0 without cnts). With dst_slot, entry i goes to destination slot
 // dst_slot[row*S + i] (skipped outside [0, pool_slots)). Ids outside [0, src_chunks) are

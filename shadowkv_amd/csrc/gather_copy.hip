@@ -172,7 +172,7 @@ void fetch_args(const void* values, void* v_cache_buffer, const int32_t* offsets
   f->src_chunks = cpu_v_length / chunk_elems;
   f->rows = rows;
   f->tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
-  f->workgroups = std::min(rows * f->tiles, fetch_workgroups());
+  f->workgroups = skv::fetch_workgroups_for(values, rows * f->tiles);
 }
 
 // Shared by the two value-fetch entry points: argument checks, then (compact) the in-buffer hit
@@ -270,7 +270,7 @@ extern "C" int skv_gather_copy(const void* values, void* v_cache_buffer, const i
   f.src_chunks = cpu_v_length / chunk_elems;
   f.rows = rows;
   f.tiles = (map_size + kChunksPerFetchWG - 1) / kChunksPerFetchWG;
-  f.workgroups = std::min(rows * f.tiles, fetch_workgroups());
+  f.workgroups = skv::fetch_workgroups_for(values, rows * f.tiles);
   hipLaunchKernelGGL(gather_chunks_kernel<int64_t>, dim3(f.workgroups), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), f);
   return skv_check_launch(what);

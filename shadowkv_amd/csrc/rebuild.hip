@@ -363,13 +363,16 @@ __global__ void __launch_bounds__(kNW * 64, 2) fetch_rebuild_kernel(RebuildArgs 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Fetch workgroups of a fused launch with `waves`-wave workgroups: the target in 4-wave
-// workgroups (the caller's f.workgroups when positive, else skv::fused_fetch_workgroups_target)
+// workgroups (the caller's f.workgroups when positive, else skv::kDeviceFetchWGs for a value
+// store in device memory and skv::fused_fetch_workgroups_target for one in pinned host memory)
 // scaled to the workgroup size, then as few as give every workgroup the same number of tiles (the
 // launch lasts as long as its busiest fetch workgroup), rounded up to a multiple of 8 for the
 // rebuild tiles' XCD map.
 int fused_fetch_workgroups(const skv::FetchArgs<int32_t>& f, int waves) {
   const int tiles = std::max(f.rows * f.tiles, 1);
-  const int t4 = f.workgroups > 0 ? f.workgroups : skv::fused_fetch_workgroups_target();
+  const int t4 = f.workgroups > 0              ? f.workgroups
+                 : skv::is_device_memory(f.src) ? skv::kDeviceFetchWGs
+                                                : skv::fused_fetch_workgroups_target();
   const int target = std::max(1, t4 * 4 / waves);
   const int per = (tiles + target - 1) / target;  // tiles per workgroup
   const int want = (tiles + per - 1) / per;

@@ -65,14 +65,16 @@ LANE_FETCH_WORKGROUPS = 64
 LANE_REBUILD_WORKGROUPS = 48
 
 
-def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int) -> int:
+def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int, value_store: str = "host") -> int:
     """Batch lanes for the decode step: 2 when a layer's value fetch over the host link outlasts
     three passes over the layer's dense weights, else 1. Each lane streams the dense weights once
     per layer, so a second lane only pays off where the fetch it hides is long: measured on one
     MI355X (tokens/s, 1 vs 2 lanes): Llama-3.1-8B ctx 122880 batch 2 197 / 160 (fetch / weights
     2.2), batch 4 262 / 271 (4.4), batch 8 271 / 383 (8.9); GLM-4-9B ctx 262144 batch 4 393 / 261
-    (1.2). Rates: 52 GB/s host link, 6 TB/s weight stream."""
-    if batch % 2:
+    (1.2). Rates: 52 GB/s host link, 6 TB/s weight stream. With the value store in device memory
+    there is no host-link fetch to hide: one lane (Llama-3.1-8B batch 8: 740.6 vs 640.6 tokens/s
+    for two lanes)."""
+    if batch % 2 or value_store == "device":
         return 1
     d = shape.head_dim
     weights = 2 * shape.hidden * ((shape.heads + 2 * shape.kv_heads) * d + shape.heads * d + 3 * shape.ffn)
@@ -207,7 +209,7 @@ class SyntheticDecoder:
                  chunk_size: int = 8, decode_len: int = 128, device: str = "cuda:0", seed: int = 0,
                  dtype=torch.bfloat16, lanes: int = 1, fused: bool = True, chunk_cache: int | None = None,
                  one_stream_fetch: bool | None = None, state: str = "synthetic", host_stores: int | None = None,
-                 lane_streams: bool | None = None):
+                 lane_streams: bool | None = None, value_store: str = "host"):
         self.shape, self.batch, self.ctx, self.device, self.dtype = shape, batch, ctx, device, dtype
         # fused: residual add + RMSNorm, SiLU-and-mul and RoPE + KV append as single kernels and
         # the projections on the skinny linear kernel (libshadowkv_amd), instead of torch operations
@@ -251,7 +253,8 @@ class SyntheticDecoder:
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
                                       chunk_size=chunk_size, rank=rank, max_decode_len=decode_len,
-                                      zero_host_store=False, chunk_cache=chunk_cache, host_stores=host_stores)
+                                      zero_host_store=False, chunk_cache=chunk_cache, host_stores=host_stores,
+                                      value_store=value_store)
             # The prompt's state: random contents of the exact shapes, or built by the device encoder
             # from low-rank keys (encode_state).
             if state == "encoded":
@@ -284,8 +287,9 @@ class SyntheticDecoder:
                 # fetch workgroups and one rebuild workgroup per tile; the workgroup counts above).
                 cache.one_stream_fetch = True
                 cache.lane_stream = side_stream(device, ("fetch", "rebuild")[i])
-                cache.fused_fetch_workgroups = LANE_FETCH_WORKGROUPS
-                cache.fused_rebuild_workgroups = LANE_REBUILD_WORKGROUPS
+                if value_store == "host":  # (a store in HBM takes the library's wide fetch)
+                    cache.fused_fetch_workgroups = LANE_FETCH_WORKGROUPS
+                    cache.fused_rebuild_workgroups = LANE_REBUILD_WORKGROUPS
             elif lanes > 1:
                 # All lanes share one value-fetch stream and one key-rebuild stream (their fetches
                 # follow one another on the host link anyway); taking the key rebuild off the

@@ -5,7 +5,8 @@ State per layer l (B = batch, H = kv heads, G = query heads per kv head, D = 128
     shared across heads as in the reference (get_svd, shadow.py:411-444);
   * k_landmark[l] [B, H, n, D] / k_landmark_idx[l] [B, H, n]: chunk means of the post-RoPE keys
     that are not outliers, and their chunk ids (shadow.py:486-519);
-  * v_cache_cpu[l] [B, H, max_length/c, c*D] in pinned host memory: every value chunk;
+  * v_cache_cpu[l] [B, H, max_length/c, c*D] in pinned host memory (or, with
+    value_store="device", in device memory): every value chunk;
   * k/v_cache_buffer[l] [B, H, buf_len, D] on the device: [local | outliers | S selected chunks
     | generated tokens], the selected region at sparse_start..sparse_end in slot order;
   * position_ids[l] [B, H, S] (int64): chunk id held by each slot.
@@ -65,7 +66,7 @@ class ShadowKVCache_CPU(KVCacheBase):
                  dtype=torch.bfloat16, sparse_budget: int = 2048, chunk_size: int = 8, rank: int = 160,
                  max_decode_len: int | None = None, zero_host_store: bool = True,
                  chunk_cache: int | None = None, copy_stream: torch.cuda.Stream | None = None,
-                 host_stores: int | None = None) -> None:
+                 host_stores: int | None = None, value_store: str = "host") -> None:
         self.config = config
         self.batch_size = batch_size
         self.max_length = max_length
@@ -103,10 +104,16 @@ class ShadowKVCache_CPU(KVCacheBase):
         # then share the host copy of their values (what the last layer to write a store wrote),
         # for callers that need the decode shapes but not distinct contents per layer (the
         # full-size tests: one process may pin only about 65 GiB on the MI355X hosts).
+        # value_store="device" keeps the value store in device memory instead (the whole store of the
+        # Llama-3.1-8B batch-8 ctx-122880 workload, 64 GB, fits MI355X's 288 GB of HBM): the same
+        # kernels then gather the missed chunks from HBM, and nothing crosses the host link.
+        if value_store not in ("host", "device"):
+            raise ValueError(f"value_store must be 'host' or 'device', not {value_store!r}")
+        self.value_store = value_store
         alloc = torch.zeros if zero_host_store else torch.empty
         stores = L if host_stores is None else max(1, min(L, int(host_stores)))
-        own = [alloc(B, H, max_length // chunk_size, D * chunk_size, dtype=dtype, pin_memory=True)
-               for _ in range(stores)]
+        where = dict(pin_memory=True) if value_store == "host" else dict(device=device)
+        own = [alloc(B, H, max_length // chunk_size, D * chunk_size, dtype=dtype, **where) for _ in range(stores)]
         self.v_cache_cpu = [own[l % stores] for l in range(L)]
         # Sparse region ends at most at (local 4 chunks + 7 alignment chunks + 7 tokens) + outliers + budget.
         ref_len = self.sparse_budget + 128 + (self.outlier_chunk + self.local_chunk) * chunk_size

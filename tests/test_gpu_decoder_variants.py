@@ -8,6 +8,8 @@
   for bit, as the projection followed by the RoPE + append kernel;
 * two lanes, each with its one-launch fetch + rebuild on its own side stream, give the same tokens
   and cache state, bit for bit, as the lanes sharing one fetch and one rebuild stream;
+* the value store in device memory gives the same tokens and cache state, bit for bit, as the
+  pinned host store;
 * the fused new-token step (residual + RMSNorm, skinny linear, SiLU-and-mul, RoPE + append
   kernels) agrees with the reference call sequence on torch operations (F.rms_norm, F.linear,
   F.silu, apply_rotary_pos_emb_new + update_kv_cache) within bf16 tolerance."""
@@ -195,3 +197,35 @@ def test_fused_step_matches_reference_call_sequence(gpu):
                        (cf.v_cache_buffer[l][:, :, row], cr.v_cache_buffer[l][:, :, row])):
             rel = ((bf.float() - br.float()).norm() / br.float().norm()).item()
             assert rel < 1e-2, (l, rel)
+
+
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_device_value_store_matches_host_store(gpu, lanes):
+    """The value store in device memory (value_store="device") gives the same tokens and cache
+    state, bit for bit, as the pinned host store: the same kernels gather the same chunks, from HBM
+    instead of over the host link. Eager steps and captured graph replays, one and two lanes."""
+    print(f"device value store vs pinned host store, batch 8 in {lanes} lane(s)", flush=True)
+    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    kw = dict(sparse_budget=2048, decode_len=12, lanes=lanes, seed=29)
+    host = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    dev = decode_model.SyntheticDecoder(shape, 8, 16384, value_store="device", **kw)
+    for hl, dl in zip(host.lanes, dev.lanes):
+        assert hl.cache.v_cache_cpu[0].is_pinned() and dl.cache.v_cache_cpu[0].is_cuda
+        for a, b in zip(hl.cache.v_cache_cpu, dl.cache.v_cache_cpu):
+            assert torch.equal(a, b.cpu())
+    th = td = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(4))
+    for t in range(3):
+        th = host.decode_step(th)
+        td = dev.decode_step(td)
+        torch.cuda.synchronize()
+        assert torch.equal(th, td), t
+        for a, b in zip(_state(host), _state(dev)):
+            assert torch.equal(a, b), t
+    host.capture(th, steps=2)
+    dev.capture(td, steps=2)
+    for t in range(2):
+        th, td = host.replay(), dev.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(th, td), ("replay", t)
+        for a, b in zip(_state(host), _state(dev)):
+            assert torch.equal(a, b), ("replay", t)

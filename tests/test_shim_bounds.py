@@ -35,6 +35,7 @@ def test_auto_lanes_follows_the_measured_choices():
     assert dm.auto_lanes(dm.GLM4_9B, 4, 2048) == 1      # 393 vs 261
     assert dm.auto_lanes(dm.LLAMA3_8B_1M, 1, 16384) == 1  # one sequence: nothing to pipeline
     assert dm.auto_lanes(dm.LLAMA31_8B, 7, 2048) == 1   # odd batch
+    assert dm.auto_lanes(dm.LLAMA31_8B, 8, 2048, value_store="device") == 1  # no host link to hide: 741 vs 641
 
 
 def test_side_streams_are_limited_to_the_hardware_queues(monkeypatch):
