@@ -467,6 +467,24 @@ int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_b, int64_t 
                                  const int32_t* slot_list, int sparse_start, int select_sets, int chunk_size,
                                  int pool_slots, void* stream);
 
+/* skv_sparse_attn_decode with the selected region's values read in place from the value store. No
+ * reference counterpart: it is for a value store kept in device memory (HBM), where gathering the
+ * selected chunks into v_cache first would only copy them. Keys [0, kv_len) and the values outside
+ * [sparse_start, sparse_start + select_sets*chunk_size) come from k_cache / v_cache as in
+ * skv_sparse_attn_decode; value row sparse_start + j*chunk_size + r is row c*chunk_size + r of
+ * (b, h) in v_store, c = position_ids[(b*kv_heads + h)*select_sets + j] (clamped to
+ * [0, store_chunks)), rows of head_dim elements, (b, h) at vs_stride_b / vs_stride_h elements.
+ * The same arithmetic as skv_sparse_attn_decode over a v_cache holding those rows: the results are
+ * bit-identical. */
+int skv_sparse_attn_decode_vstore(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+                                  const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h,
+                                  int64_t kv_stride_s, int batch_size, int q_heads, int kv_heads, int head_dim,
+                                  int kv_len, const int32_t* kv_len_dev, float scale, void* workspace,
+                                  int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+                                  const uint16_t* v_store, int64_t vs_stride_b, int64_t vs_stride_h,
+                                  int64_t store_chunks, const int64_t* position_ids, int sparse_start,
+                                  int select_sets, int chunk_size, void* stream);
+
 /* Replaces the new token's rotary embedding (vllm rotary_embedding, models/llama.py:149-150,
  * models/glm.py:200-201) and the
  * KV append of update_kv_cache (models/kvcache/shadow.py:621-633) in one launch. qkv row of batch b:

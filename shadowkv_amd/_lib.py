@@ -82,6 +82,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                          _p]),
     "skv_sparse_attn_decode_paged": (_i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
                                              _p, _f32, _p, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p]),
+    "skv_sparse_attn_decode_vstore": (_i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+                                              _p, _f32, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i32, _i32,
+                                              _i32, _p]),
     "skv_rope_qk_append": (
         _i32, [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _i64, _i64, _p,
                _i64, _p]),

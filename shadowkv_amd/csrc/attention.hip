@@ -79,6 +79,13 @@ struct AttnArgs {
   // selection sit `delta` rows further (after the pool's pool_slots chunks).
   const int32_t* slot;
   int sp0, sel, chunk, pool_slots, delta;
+  // Values read in place (a value store in device memory): the selected region's value rows
+  // [sp0, sp0 + sel*chunk) come from row cid*chunk + r of (b, h) in the store, cid = vids[(b*Hkv +
+  // h)*sel + j] the chunk id of slot j (clamped to [0, vs_chunks)); the keys and every other value
+  // row come from k / v as usual.
+  const uint16_t* vs;
+  int64_t vs_sb, vs_sh, vs_chunks;
+  const int64_t* vids;
   // Fused merge: one arrival counter per (b, kv head) row (zero between calls), the row count,
   // the XCC id the mapping probe saw for each blockIdx class mod 8 (4 bits each), and a flag set
   // by any workgroup that finds itself elsewhere.
@@ -203,7 +210,9 @@ __device__ __forceinline__ void fused_merge(const AttnArgs& a, int bh, int used,
 // latency overlaps the softmax (requesting them with K, at entry, measured no faster and holds
 // more registers). kFused: blockIdx.x enumerates (row, split) so that a row's splits share
 // blockIdx mod 8 (one XCD), and the last split of each row merges them (fused_merge).
-template <int GP, bool kPaged, int kSplit, bool kFused>
+// kMap: 0 keys and values at their rows; 1 the selected region through the chunk pool's slot list
+// (a.slot); 2 the selected region's values in place in the value store (a.vs).
+template <int GP, int kMap, int kSplit, bool kFused>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   constexpr int kRows = kSplit / 16;        // keys per P.V stream
   constexpr int kGroups = kSplit / 4 / 16;  // 16-key MFMA groups per wave
@@ -224,7 +233,8 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
   __shared__ __align__(16) unsigned char big[kBigBytes];
   float (*red)[64][kKept] = reinterpret_cast<float (*)[64][kKept]>(big);
   __shared__ float ml[GP][2];
-  __shared__ int prow[kPaged ? kSplit : 1];  // physical row of each key of the split (paged)
+  __shared__ int prow[kMap == 1 ? kSplit : 1];  // physical row of each key of the split (pool)
+  __shared__ const uint16_t* vrow[kMap == 2 ? kSplit : 1];  // value row of each key (values in place)
 
   int split, bh;
   if constexpr (kFused) {
@@ -265,7 +275,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) qf[ks] = skv::load16_or_zero(qrow + 32 * ks, li < G);
   // Key jl of the split (clamped to the live keys) lives at row key_row(jl).
-  if (kPaged) {
+  if (kMap == 1) {
     for (int jl = threadIdx.x; jl < kSplit; jl += kThreads) {
       const int sk = min(s0 + jl, s1 - 1);
       int r = sk;
@@ -282,7 +292,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
-  auto key_row = [&](int jl) -> int64_t { return kPaged ? prow[jl] : min(s0 + jl, s1 - 1); };
+  auto key_row = [&](int jl) -> int64_t { return kMap == 1 ? prow[jl] : min(s0 + jl, s1 - 1); };
   // K as MFMA B operand: lane (li, grp) holds key (wave*64 + 16*kg + li), same dims.
   u32x4 kf[kGroups][4];
 #pragma unroll
@@ -291,6 +301,19 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     const uint16_t* krow = kh + key_row(s - s0) * a.kv_ss + 8 * grp;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) kf[kg][ks] = skv::load16_or_zero(krow + 32 * ks, s < s1);
+  }
+  if (kMap == 2) {
+    // After the K loads are issued (the chunk-id loads overlap them); read after the barrier below.
+    for (int jl = threadIdx.x; jl < kSplit; jl += kThreads) {
+      const int sk = min(s0 + jl, s1 - 1);
+      const int j = sk - a.sp0;
+      const uint16_t* r = vh + sk * a.kv_ss;
+      if (j >= 0 && j < a.sel * a.chunk) {
+        const int64_t cid = min(max(a.vids[static_cast<int64_t>(bh) * a.sel + j / a.chunk], int64_t{0}), a.vs_chunks - 1);
+        r = a.vs + b * a.vs_sb + h * a.vs_sh + (cid * a.chunk + j % a.chunk) * kHeadDim;
+      }
+      vrow[jl] = r;
+    }
   }
   // V for P.V: stream (wave, grp) takes keys s0 + 16*i + stream, lane li its dims [8*li, +8), so
   // each wave load reads 4 consecutive rows (1 KB when rows are contiguous). Non-temporal loads:
@@ -303,7 +326,8 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
       const int s = s0 + i * 16 + stream;
-      const u32x4 x = skv::load_nt(reinterpret_cast<const u32x4*>(vh + key_row(i * 16 + stream) * a.kv_ss + li * 8));
+      const uint16_t* vp = kMap == 2 ? vrow[i * 16 + stream] : vh + key_row(i * 16 + stream) * a.kv_ss;
+      const u32x4 x = skv::load_nt(reinterpret_cast<const u32x4*>(vp + li * 8));
       vr[i] = s < s1 ? x : u32x4{0u, 0u, 0u, 0u};
     }
   };
@@ -323,6 +347,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       if (g < G) p_lds[g][jl] = live ? d[v] * a.scale : -INFINITY;
     }
   }
+  if (kMap == 2) __syncthreads();  // vrow written
   load_v();
   __syncthreads();
 
@@ -683,26 +708,34 @@ int choose_split_keys(int rows, int kv_len) {
   return kSplitLong;
 }
 
-template <bool kPaged, int kSplit, bool kFused>
+template <int kMap, int kSplit, bool kFused>
 void launch_split(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
-  if (G == 1) hipLaunchKernelGGL((attn_split_kernel<1, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
-  else if (G == 2) hipLaunchKernelGGL((attn_split_kernel<2, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
-  else if (G <= 4) hipLaunchKernelGGL((attn_split_kernel<4, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
-  else if (G <= 8) hipLaunchKernelGGL((attn_split_kernel<8, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((attn_split_kernel<16, kPaged, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  if (G == 1) hipLaunchKernelGGL((attn_split_kernel<1, kMap, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else if (G == 2) hipLaunchKernelGGL((attn_split_kernel<2, kMap, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 4) hipLaunchKernelGGL((attn_split_kernel<4, kMap, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 8) hipLaunchKernelGGL((attn_split_kernel<8, kMap, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((attn_split_kernel<16, kMap, kSplit, kFused>), grid, dim3(kThreads), 0, s, a);
 }
 
-template <bool kPaged, bool kFused>
+template <int kMap, bool kFused>
 void launch_split_keys(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
-  if (a.split_keys == kSplitShort) launch_split<kPaged, kSplitShort, kFused>(G, grid, s, a);
-  else launch_split<kPaged, kSplitLong, kFused>(G, grid, s, a);
+  if (a.split_keys == kSplitShort) launch_split<kMap, kSplitShort, kFused>(G, grid, s, a);
+  else launch_split<kMap, kSplitLong, kFused>(G, grid, s, a);
 }
+
+// The selected region's values read in place from a value store (skv_sparse_attn_decode_vstore).
+struct VStore {
+  const uint16_t* store;
+  int64_t stride_b, stride_h, chunks;
+  const int64_t* ids;
+};
 
 int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
                 const uint16_t* v_cache, int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, int batch_size,
                 int q_heads, int kv_heads, int head_dim, int kv_len, const int32_t* kv_len_dev, float scale,
                 void* workspace, int64_t workspace_bytes, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
-                const int32_t* slot, int sparse_start, int select_sets, int chunk, int pool_slots, void* stream) {
+                const int32_t* slot, int sparse_start, int select_sets, int chunk, int pool_slots, void* stream,
+                const VStore* vsm = nullptr) {
   if (!q || !k_cache || !v_cache || !workspace || !out) {
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
@@ -731,6 +764,13 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
   if (slot && (sparse_start < 0 || select_sets < 1 || chunk < 1 || pool_slots < select_sets)) {
     skv_set_error("%s: paged region sparse_start=%d select_sets=%d chunk=%d pool_slots=%d", what, sparse_start,
                   select_sets, chunk, pool_slots);
+    return SKV_EINVAL;
+  }
+  if (vsm && (!vsm->store || !vsm->ids || sparse_start < 0 || select_sets < 1 || chunk < 1 || vsm->chunks < 1 ||
+              (reinterpret_cast<uintptr_t>(vsm->store) & 15u) || vsm->stride_b % 8 || vsm->stride_h % 8)) {
+    skv_set_error("%s: value store (16-byte aligned, strides multiples of 8 elements, ids) and region "
+                  "sparse_start=%d select_sets=%d chunk=%d store_chunks=%lld", what, sparse_start, select_sets, chunk,
+                  (long long)(vsm ? vsm->chunks : 0));
     return SKV_EINVAL;
   }
   const int64_t need = skv_sparse_attn_workspace_bytes(batch_size, q_heads, kv_len);
@@ -768,6 +808,13 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
   a.pool_slots = pool_slots;
   a.delta = (pool_slots - select_sets) * chunk;
   a.rows = rows;
+  if (vsm) {
+    a.vs = vsm->store;
+    a.vs_sb = vsm->stride_b;
+    a.vs_sh = vsm->stride_h;
+    a.vs_chunks = vsm->chunks;
+    a.vids = vsm->ids;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   // The merge folded into the split launch, on request (SKV_ATTN_FUSED=1): rows of at most 64
   // splits, at least one row per XCD (the rows of one XCD share its 32 CUs), the XCD mapping
@@ -776,18 +823,19 @@ int attn_decode(const char* what, const uint16_t* q, int64_t q_stride_b, int64_t
   // 16 heads merged by one workgroup: 12.2 vs 10.8) and slower inside the pipelined decode step,
   // beside the other lane's host-link fetch (36.7 vs 23.5 + 10.0 us per lane-layer).
   const char* fe = getenv("SKV_ATTN_FUSED");
-  bool fused = fe && fe[0] == '1' && rows >= kXcds && rows <= kMaxFusedRows && a.splits <= kMaxFusedSplits &&
+  bool fused = !vsm && fe && fe[0] == '1' && rows >= kXcds && rows <= kMaxFusedRows && a.splits <= kMaxFusedSplits &&
                (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && o_stride_b % 4 == 0 && o_stride_h % 4 == 0;  // 8-byte stores
   if (fused) fused = fused_mapping(s, &a.xcc_map, &a.misplaced);
   if (fused) {
     const dim3 grid(static_cast<unsigned>(kXcds * ((rows + kXcds - 1) / kXcds) * a.splits));
-    if (slot) launch_split_keys<true, true>(G, grid, s, a);
-    else launch_split_keys<false, true>(G, grid, s, a);
+    if (slot) launch_split_keys<1, true>(G, grid, s, a);
+    else launch_split_keys<0, true>(G, grid, s, a);
     return skv_check_launch(what);
   }
   const dim3 grid(a.splits, rows);
-  if (slot) launch_split_keys<true, false>(G, grid, s, a);
-  else launch_split_keys<false, false>(G, grid, s, a);
+  if (vsm) launch_split_keys<2, false>(G, grid, s, a);
+  else if (slot) launch_split_keys<1, false>(G, grid, s, a);
+  else launch_split_keys<0, false>(G, grid, s, a);
   int rc = skv_check_launch(what);
   if (rc) return rc;
   // Several merge groups only when there are chunks for them (the split count by the maximum length).
@@ -825,6 +873,22 @@ extern "C" int skv_sparse_attn_decode_paged(const uint16_t* q, int64_t q_stride_
                      kv_stride_h, kv_stride_s, batch_size, q_heads, kv_heads, head_dim, kv_len, kv_len_dev, scale,
                      workspace, workspace_bytes, out, o_stride_b, o_stride_h, slot_list, sparse_start, select_sets,
                      chunk_size, pool_slots, stream);
+}
+
+extern "C" int skv_sparse_attn_decode_vstore(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
+                                             const uint16_t* k_cache, const uint16_t* v_cache, int64_t kv_stride_b,
+                                             int64_t kv_stride_h, int64_t kv_stride_s, int batch_size, int q_heads,
+                                             int kv_heads, int head_dim, int kv_len, const int32_t* kv_len_dev,
+                                             float scale, void* workspace, int64_t workspace_bytes, uint16_t* out,
+                                             int64_t o_stride_b, int64_t o_stride_h, const uint16_t* v_store,
+                                             int64_t vs_stride_b, int64_t vs_stride_h, int64_t store_chunks,
+                                             const int64_t* position_ids, int sparse_start, int select_sets,
+                                             int chunk_size, void* stream) {
+  const VStore vsm{v_store, vs_stride_b, vs_stride_h, store_chunks, position_ids};
+  return attn_decode("sparse_attn_decode_vstore", q, q_stride_b, q_stride_h, k_cache, v_cache, kv_stride_b,
+                     kv_stride_h, kv_stride_s, batch_size, q_heads, kv_heads, head_dim, kv_len, kv_len_dev, scale,
+                     workspace, workspace_bytes, out, o_stride_b, o_stride_h, nullptr, sparse_start, select_sets,
+                     chunk_size, select_sets, stream, &vsm);
 }
 
 // ---- allocation-free variant ---------------------------------------------------------------

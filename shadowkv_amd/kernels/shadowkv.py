@@ -620,7 +620,8 @@ def sparse_attn_xcd_check() -> dict:
     return dict(state=st.value, xcc=[(mp.value >> (4 * x)) & 15 for x in range(8)], misplaced=mis.value)
 
 
-def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, kv_len_dev=None, pool=None):
+def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, kv_len_dev=None, pool=None,
+                       vstore=None):
     """out[b, hq] = softmax(scale q[b,hq] K[b,h,:L]^T) V[b,h,:L], h = hq // (Hq/Hkv).
 
     q: [B, Hq, 128] view; k_cache/v_cache: [B, Hkv, >=kv_len, 128] views; out: [B, Hq, 128];
@@ -632,6 +633,10 @@ def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, 
     pool: optional (slot_list [B, Hkv, S] int32, sparse_start, S, chunk, pool_slots): the keys
     [sparse_start, sparse_start + S*chunk) are read through the slot list (a chunk pool), the
     later keys (pool_slots - S)*chunk rows further down.
+    vstore: optional (store [B, Hkv, chunks, chunk*128] device tensor, position_ids [B, Hkv, S] int64,
+    sparse_start, S, chunk): the values of [sparse_start, sparse_start + S*chunk) read in place
+    from the store (slot j holds chunk position_ids[b, h, j]) instead of from v_cache; results are
+    bit-identical to v_cache holding those rows.
     """
     _dev(q, "q", torch.bfloat16)
     _dev(k_cache, "k_cache", torch.bfloat16)
@@ -659,6 +664,26 @@ def sparse_attn_decode(q, k_cache, v_cache, kv_len, out, workspace, scale=None, 
         ldev = kv_len_dev.data_ptr()
     _need_offsets(q, (B, Hq, D), q.stride(), "q")
     _need_offsets(out, (B, Hq, D), out.stride(), "out")
+    if vstore is not None:
+        if pool is not None:
+            raise ValueError("pool and vstore are exclusive")
+        store, pids, sp0, S, chunk = vstore
+        _dev(store, "store", torch.bfloat16)
+        _dev(pids, "position_ids", torch.int64)
+        Hk = k_cache.shape[1]
+        if store.dim() != 4 or store.shape[:2] != (B, Hk) or store.shape[3] != chunk * D or \
+                store.stride(3) != 1 or store.stride(2) != chunk * D:
+            raise ValueError("store must be [B, Hkv, chunks, chunk*128] with contiguous chunks")
+        if not pids.is_contiguous() or pids.numel() != B * Hk * S:
+            raise ValueError("position_ids must be contiguous [B, Hkv, S]")
+        if not 0 <= sp0 <= sp0 + S * chunk <= k_cache.shape[2]:
+            raise ValueError("the selected region lies outside the buffers")
+        _lib.call("skv_sparse_attn_decode_vstore", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
+                  v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, Hk, D, kv_len,
+                  ldev, float(scale), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                  out.data_ptr(), out.stride(0), out.stride(1), store.data_ptr(), store.stride(0), store.stride(1),
+                  store.shape[2], pids.data_ptr(), sp0, S, chunk, _stream())
+        return
     if pool is not None:
         _lib.call("skv_sparse_attn_decode_paged", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
                   v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), B, Hq, k_cache.shape[1],

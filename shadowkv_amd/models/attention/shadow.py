@@ -67,12 +67,12 @@ class ShadowAttention(AttentionBase):
             lane_stream = getattr(kv_cache, "lane_stream", None)
             if lane_stream is None:
                 key_states, value_states = kv_cache.fetch_and_rebuild(layer_idx, position_ids, self.cos_sin_cache)
-                return query_states, key_states, value_states, []
+                return query_states, key_states, value_states, [], layer_idx
             with torch.cuda.stream(lane_stream):
                 lane_stream.wait_stream(curr_stream)
                 key_states, value_states = kv_cache.fetch_and_rebuild(layer_idx, position_ids, self.cos_sin_cache)
                 done = [lane_stream.record_event()]
-            return query_states, key_states, value_states, done
+            return query_states, key_states, value_states, done, layer_idx
         copy_stream = kv_cache.copy_stream
         # The value hits move within the GPU buffer here, so the copy stream (whose transfers
         # follow one another on the host link) carries the host-link gather alone.
@@ -89,7 +89,7 @@ class ShadowAttention(AttentionBase):
                 key_stream.wait_stream(curr_stream)
                 key_states = self._key_path(layer_idx, position_ids)
                 done.append(key_stream.record_event())
-        return query_states, key_states, value_states, done
+        return query_states, key_states, value_states, done, layer_idx
 
     def _key_path(self, layer_idx, position_ids):
         return self.kv_cache.get_key_cache(layer_idx=layer_idx, position_ids=position_ids,
@@ -98,8 +98,10 @@ class ShadowAttention(AttentionBase):
 
     def decode_end(self, pending):
         """Second half of decode(), on the stream decode_begin() ran on: wait for the value fetch,
-        then sparse attention of the new token over the assembled buffers -> [B, 1, Hq, D]."""
-        query_states, key_states, value_states, done = pending
+        then sparse attention of the new token over the assembled buffers -> [B, 1, Hq, D] (with
+        a value store in device memory read in place, the selected values from the store).
+        `pending` is decode_begin()'s result."""
+        query_states, key_states, value_states, done, layer_idx = pending
         kv_cache = self.kv_cache
         for event in done:
             torch.cuda.current_stream().wait_event(event)
@@ -112,5 +114,6 @@ class ShadowAttention(AttentionBase):
         out = torch.empty(B, Hq, query_states.shape[-1], dtype=query_states.dtype, device=query_states.device)
         kv_len, pool = kv_cache.attention_args(key_states.shape[2])
         shadowkv.sparse_attn_decode(q, key_states, value_states, kv_len, out, kv_cache.attn_workspace,
-                                    kv_len_dev=kv_cache.kv_len_dev, pool=pool)
+                                    kv_len_dev=kv_cache.kv_len_dev, pool=pool,
+                                    vstore=kv_cache.value_store_args(layer_idx))
         return out.view(B, 1, Hq, -1)

@@ -110,6 +110,11 @@ class ShadowKVCache_CPU(KVCacheBase):
         if value_store not in ("host", "device"):
             raise ValueError(f"value_store must be 'host' or 'device', not {value_store!r}")
         self.value_store = value_store
+        # With the store in device memory (and no chunk pool) the selected values are not gathered
+        # into v_cache_buffer at all: the attention reads them in place from the store
+        # (skv_sparse_attn_decode_vstore; bit-identical to the gathered buffer), and only the key
+        # buffer's hits move. False: gather from the device store as from a host one.
+        self.values_in_place = value_store == "device" and chunk_cache is None
         alloc = torch.zeros if zero_host_store else torch.empty
         stores = L if host_stores is None else max(1, min(L, int(host_stores)))
         where = dict(pin_memory=True) if value_store == "host" else dict(device=device)
@@ -422,7 +427,12 @@ class ShadowKVCache_CPU(KVCacheBase):
         # chunk_attn; the selected ids in top-k order (selected_chunks) only when keep_selected is set. With
         # fold_hit_moves the same launch also moves the value buffer's hits to their new slots.
         move = None
-        if self.fold_hit_moves:
+        if self.fold_hit_moves and self.values_in_place:
+            # (no value buffer to update: the key buffer's hits, where the key rebuild follows at once)
+            if self.one_stream_active():
+                move = (self.k_cache_buffer[layer_idx], None, self.kernel_offset, self.kernel_stride,
+                        self.chunk_size * D)
+        elif self.fold_hit_moves:
             move = (self.v_cache_buffer[layer_idx], self.k_cache_buffer[layer_idx] if self.one_stream_active() else None,
                     self.kernel_offset, self.kernel_stride, self.chunk_size * D)
         shadowkv.select_chunks(self.gemm_o, self.norm, self.sum, B * H, G, n, self.k_landmark_idx[layer_idx].view(B * H, n),
@@ -430,7 +440,12 @@ class ShadowKVCache_CPU(KVCacheBase):
                                self.cnts, out_scores=self.chunk_attn,
                                out_selected=self.selected_chunks if self.keep_selected else None,
                                workspace=self.select_workspace, move=move)
-        self._folded[layer_idx] = set() if move is None else {"v", "k"} if move[1] is not None else {"v"}
+        if move is None:
+            self._folded[layer_idx] = set()
+        elif self.values_in_place:
+            self._folded[layer_idx] = {"k"}
+        else:
+            self._folded[layer_idx] = {"v", "k"} if move[1] is not None else {"v"}
         return self.position_ids[layer_idx]
 
     def _gen_len(self, layer_idx: int) -> int:
@@ -450,6 +465,14 @@ class ShadowKVCache_CPU(KVCacheBase):
         return view_len - self.pool_delta, (self.slot_list.view(B, H, -1), self.sparse_start, self.select_sets,
                                             self.chunk_size, self.pool_slots)
 
+    def value_store_args(self, layer_idx: int):
+        """The attention's vstore argument (store, position_ids, sparse_start, S, chunk) when the
+        selected values are read in place from a device store, else None."""
+        if not self.values_in_place:
+            return None
+        return (self.v_cache_cpu[layer_idx], self.position_ids[layer_idx], self.sparse_start, self.select_sets,
+                self.chunk_size)
+
     def get_value_cache(self, layer_idx: int, position_ids: torch.Tensor, hits_moved: bool = False) -> torch.Tensor:
         """The layer's value buffer with the selected chunks in place: cache hits moved to their
         new slots (unless move_value_hits already did, hits_moved) and misses gathered from host.
@@ -461,6 +484,8 @@ class ShadowKVCache_CPU(KVCacheBase):
                                                  int(self.max_ctx_chunks_len * D), self.sparse_start * D,
                                                  self.buf_len * D, self.select_sets, self.pool_slots,
                                                  self.chunk_size * D)
+            return self._live_view(self.v_cache_buffer[layer_idx], layer_idx)
+        if self.values_in_place:  # the attention reads the selected values from the store
             return self._live_view(self.v_cache_buffer[layer_idx], layer_idx)
         if "v" in self._folded[layer_idx]:  # the selection moved the hits
             self._folded[layer_idx].discard("v")
@@ -476,7 +501,7 @@ class ShadowKVCache_CPU(KVCacheBase):
         """The in-buffer half of the value fetch alone (hit rows to their new slots), so that a
         later get_value_cache(..., hits_moved=True) on the copy stream is host-link work only.
         Nothing to move with a chunk pool, nor when the selection already moved them."""
-        if self.pooled or "v" in self._folded[layer_idx]:
+        if self.pooled or self.values_in_place or "v" in self._folded[layer_idx]:
             return
         shadowkv.gather_copy_d2d_with_offsets(self.v_cache_buffer[layer_idx], self.offsets, self.cnts, self.batch_size,
                                               self.num_key_value_heads, int(self.sparse_budget * self.head_dim),
@@ -511,12 +536,18 @@ class ShadowKVCache_CPU(KVCacheBase):
         value chunks gathered from the host store beside the misses' key rebuild + RoPE, after a
         selection that moved both buffers' hits (one_stream_fetch). Returns (keys, values), the
         live views of the two buffers."""
-        if self.pooled or self._folded[layer_idx] != {"v", "k"}:
+        if self.pooled or self._folded[layer_idx] != ({"k"} if self.values_in_place else {"v", "k"}):
             raise RuntimeError("fetch_and_rebuild needs a selection that moved both buffers' hits "
-                               "(one_stream_fetch, no chunk pool)")
+                               "(the key buffer's with the values read in place; one_stream_fetch, no chunk pool)")
         self._folded[layer_idx].clear()
         if position_ids.dtype != torch.int64:
             position_ids = position_ids.to(torch.int64)
+        if self.values_in_place:  # nothing to fetch: the key rebuild alone
+            batch_gather_gemm_rotary_pos_emb_cuda(self.U[layer_idx], self.SV[layer_idx], cos_sin_cache, position_ids,
+                                                  self.output, self.chunk_size, self.k_cache_buffer[layer_idx],
+                                                  self.sparse_start, self.sparse_end, self.cnts)
+            return (self._live_view(self.k_cache_buffer[layer_idx], layer_idx),
+                    self._live_view(self.v_cache_buffer[layer_idx], layer_idx))
         shadowkv.fetch_misses_rebuild_k_rope(self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.offsets,
                                              self.cnts, int(self.max_ctx_chunks_len * self.head_dim),
                                              self.kernel_offset, self.kernel_stride, self.U[layer_idx],

@@ -199,27 +199,44 @@ def test_fused_step_matches_reference_call_sequence(gpu):
             assert rel < 1e-2, (l, rel)
 
 
-@pytest.mark.parametrize("lanes", [1, 2])
-def test_device_value_store_matches_host_store(gpu, lanes):
+def _state_outside_selection(model):
+    """_state with the value buffers' selected regions left out (values read in place never fill them)."""
+    out = [model.pos.clone()]
+    for lane in model.lanes:
+        c = lane.cache
+        v = c.v_cache_buffer.clone()
+        v[:, :, :, c.sparse_start:c.sparse_start + c.select_sets * c.chunk_size] = 0
+        out += [c.position_ids.clone(), c.cnts.clone(), c.offsets.clone(), c.k_cache_buffer.clone(), v,
+                c.kv_len_dev.clone(), c.chunk_attn.clone()]
+    return out
+
+
+@pytest.mark.parametrize("lanes,in_place", [(1, True), (1, False), (2, True), (2, False)])
+def test_device_value_store_matches_host_store(gpu, lanes, in_place):
     """The value store in device memory (value_store="device") gives the same tokens and cache
     state, bit for bit, as the pinned host store: the same kernels gather the same chunks, from HBM
-    instead of over the host link. Eager steps and captured graph replays, one and two lanes."""
-    print(f"device value store vs pinned host store, batch 8 in {lanes} lane(s)", flush=True)
+    instead of over the host link, or (in_place, the device store's default) the attention reads the
+    selected values in place from the store and the value buffer's selected region is never
+    filled (compared outside it). Eager steps and captured graph replays, one and two lanes."""
+    print(f"device value store (in place {in_place}) vs pinned host store, batch 8 in {lanes} lane(s)", flush=True)
     shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
     kw = dict(sparse_budget=2048, decode_len=12, lanes=lanes, seed=29)
     host = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
     dev = decode_model.SyntheticDecoder(shape, 8, 16384, value_store="device", **kw)
     for hl, dl in zip(host.lanes, dev.lanes):
         assert hl.cache.v_cache_cpu[0].is_pinned() and dl.cache.v_cache_cpu[0].is_cuda
+        assert not hl.cache.values_in_place and dl.cache.values_in_place
+        dl.cache.values_in_place = in_place
         for a, b in zip(hl.cache.v_cache_cpu, dl.cache.v_cache_cpu):
             assert torch.equal(a, b.cpu())
+    state = _state_outside_selection if in_place else _state
     th = td = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(4))
     for t in range(3):
         th = host.decode_step(th)
         td = dev.decode_step(td)
         torch.cuda.synchronize()
         assert torch.equal(th, td), t
-        for a, b in zip(_state(host), _state(dev)):
+        for a, b in zip(state(host), state(dev)):
             assert torch.equal(a, b), t
     host.capture(th, steps=2)
     dev.capture(td, steps=2)
@@ -227,5 +244,5 @@ def test_device_value_store_matches_host_store(gpu, lanes):
         th, td = host.replay(), dev.replay()
         torch.cuda.synchronize()
         assert torch.equal(th, td), ("replay", t)
-        for a, b in zip(_state(host), _state(dev)):
+        for a, b in zip(state(host), state(dev)):
             assert torch.equal(a, b), ("replay", t)

@@ -316,6 +316,45 @@ def test_sparse_attention(gpu, B, Hq, Hk, L, strided):
             assert torch.equal(out.cpu()[:, hq], V[:, hq // (Hq // Hk), 0])
 
 
+@pytest.mark.parametrize("B,Hq,Hk,sp0,S,chunk,gen", [(2, 32, 8, 448, 256, 8, 7), (4, 32, 2, 448, 256, 8, 1),
+                                                     (1, 8, 8, 40, 13, 4, 0), (3, 12, 4, 64, 20, 16, 5)])
+def test_attention_values_in_place_from_store(gpu, B, Hq, Hk, sp0, S, chunk, gen):
+    """skv_sparse_attn_decode_vstore (the selected values read in place from a value store in
+    device memory, slot j holding chunk position_ids[b, h, j]) equals skv_sparse_attn_decode over a
+    value buffer holding those rows, bit for bit (also with a device-resident length), and the
+    oracle on the gathered values."""
+    _say(f"attention values in place B={B} Hq={Hq} Hk={Hk} S={S} chunk={chunk}")
+    g = torch.Generator().manual_seed(S + chunk + B)
+    L = sp0 + S * chunk + gen
+    buf = L + 9
+    nchunks = 3 * S + 5
+    K = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
+    V = torch.randn(B, Hk, buf, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16)
+    store = torch.randn(B, Hk, nchunks, chunk * 128, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(nchunks, generator=g)[:S] for _ in range(B * Hk)]).view(B, Hk, S)
+    Vg = V.clone()  # the gathered form: the selected rows copied into the value buffer
+    rows = store.view(B, Hk, nchunks * chunk, 128)
+    sel = (ids[..., None] * chunk + torch.arange(chunk)).reshape(B, Hk, S * chunk)
+    Vg[:, :, sp0:sp0 + S * chunk] = torch.gather(rows, 2, sel[..., None].expand(-1, -1, -1, 128))
+    want = oracle.sparse_attention(q, K, Vg, L)
+    Kd, Vd, Vgd, qd, sd, idd = K.to(gpu), V.to(gpu), Vg.to(gpu), q.to(gpu), store.to(gpu), ids.to(gpu)
+    ws = shadowkv.sparse_attn_workspace(B, Hq, buf, gpu)
+    ldev = torch.full((1,), L, dtype=torch.int32, device=gpu)
+    outs = []
+    for kw in (dict(), dict(kv_len_dev=ldev)):
+        ref = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=gpu)
+        got = torch.empty_like(ref)
+        n = buf if kw else L
+        shadowkv.sparse_attn_decode(qd, Kd, Vgd, n, ref, ws, **kw)
+        shadowkv.sparse_attn_decode(qd, Kd, Vd, n, got, ws, vstore=(sd, idd, sp0, S, chunk), **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), ref.cpu()), kw
+        torch.testing.assert_close(got.cpu().float(), want.float(), rtol=RTOL, atol=ATOL)
+        outs.append(got.cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_attention_identical_keys_is_mean_of_values(gpu):
     B, Hq, Hk, L = 2, 32, 8, 777
     K = torch.randn(B, Hk, 1, 128).to(torch.bfloat16).expand(-1, -1, L, -1).contiguous()
