@@ -302,18 +302,20 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) kf[kg][ks] = skv::load16_or_zero(krow + 32 * ks, s < s1);
   }
-  if (kMap == 2) {
-    // After the K loads are issued (the chunk-id loads overlap them); read after the barrier below.
-    for (int jl = threadIdx.x; jl < kSplit; jl += kThreads) {
-      const int sk = min(s0 + jl, s1 - 1);
-      const int j = sk - a.sp0;
-      const uint16_t* r = vh + sk * a.kv_ss;
-      if (j >= 0 && j < a.sel * a.chunk) {
-        const int64_t cid = min(max(a.vids[static_cast<int64_t>(bh) * a.sel + j / a.chunk], int64_t{0}), a.vs_chunks - 1);
-        r = a.vs + b * a.vs_sb + h * a.vs_sh + (cid * a.chunk + j % a.chunk) * kHeadDim;
-      }
-      vrow[jl] = r;
-    }
+  // Values in place: the wave's own V keys (stream 4*wave + grp of every 16, see load_v) get their
+  // rows from lanes t < kRows * 4 of the wave, key (t / 4) * 16 + 4 * wave + t % 4, each lane's
+  // chunk id requested here, after the K loads; the wave reads them back from LDS after its scores,
+  // so no workgroup barrier is needed.
+  const int vkey = ((lane >> 2) * 16 + 4 * wave + (lane & 3));  // (lanes below kRows * 4)
+  const uint16_t* vself = nullptr;
+  int64_t vcid = 0;
+  bool vin = false;
+  if (kMap == 2 && lane < kRows * 4) {
+    const int sk = min(s0 + vkey, s1 - 1);
+    const int j = sk - a.sp0;
+    vself = vh + sk * a.kv_ss;
+    vin = j >= 0 && j < a.sel * a.chunk;
+    if (vin) vcid = a.vids[static_cast<int64_t>(bh) * a.sel + j / a.chunk];
   }
   // V for P.V: stream (wave, grp) takes keys s0 + 16*i + stream, lane li its dims [8*li, +8), so
   // each wave load reads 4 consecutive rows (1 KB when rows are contiguous). Non-temporal loads:
@@ -347,7 +349,18 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
       if (g < G) p_lds[g][jl] = live ? d[v] * a.scale : -INFINITY;
     }
   }
-  if (kMap == 2) __syncthreads();  // vrow written
+  if (kMap == 2) {
+    if (lane < kRows * 4) {
+      if (vin) {
+        const int j = min(s0 + vkey, s1 - 1) - a.sp0;
+        const int64_t cid = min(max(vcid, int64_t{0}), a.vs_chunks - 1);
+        vself = a.vs + b * a.vs_sb + h * a.vs_sh + (cid * a.chunk + j % a.chunk) * kHeadDim;
+      }
+      vrow[vkey] = vself;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS
+    __builtin_amdgcn_wave_barrier();
+  }
   load_v();
   __syncthreads();
 
