@@ -150,6 +150,18 @@ class LayerProbe:
         lane.attn.decode_end = probe_end
 
 
+def _virtual_vbuf(vbuf, store, pos, sp0, S, c):
+    """The value buffer as the gathering path would hold it: with the values read in place from a
+    device store the selected region of the device buffer is never filled, so it is taken from the
+    store through the slot ids (slot j of (b, h) holds chunk pos[b, h, j])."""
+    B, H, nch, _ = store.shape
+    out = vbuf.clone()
+    rows = store.reshape(B, H, nch * c, -1)
+    sel = (pos[..., None] * c + torch.arange(c)).reshape(B, H, S * c)
+    out[:, :, sp0:sp0 + S * c] = torch.gather(rows, 2, sel[..., None].expand(-1, -1, -1, rows.shape[-1]))
+    return out
+
+
 def check_layer_record(rec, cache, layer, cos_sin_cpu, what=""):
     """One recorded layer step of one lane against the oracle: the scoring within one bf16
     rounding step; from the device's own GQA-max scores, the selection, offsets, hit counts, slot
@@ -169,9 +181,12 @@ def check_layer_record(rec, cache, layer, cos_sin_cpu, what=""):
     assert_bf16_close(logits_dev, logits_ref, what=f"{what} logits")
     probs = torch.softmax(logits_dev.float(), dim=-1).to(torch.bfloat16).max(dim=1).values
     assert_bf16_close(rec["scores"].view(B * H, n), probs, what=f"{what} gqa-max probabilities")
+    host_v = cache.v_cache_cpu[layer].cpu()
+    in_place = getattr(cache, "values_in_place", False)
+    vbuf0 = _virtual_vbuf(rec["vbuf"], host_v, rec["pos_before"], sp0, S, c) if in_place else rec["vbuf"].clone()
     st = oracle.LayerState(U=cache.U[layer].cpu(), SV=cache.SV[layer].cpu(), landmarks=landmarks,
-                           landmark_idx=cache.k_landmark_idx[layer].cpu(), host_v=cache.v_cache_cpu[layer],
-                           kbuf=rec["kbuf"].clone(), vbuf=rec["vbuf"].clone(), position_ids=rec["pos_before"].clone(),
+                           landmark_idx=cache.k_landmark_idx[layer].cpu(), host_v=host_v,
+                           kbuf=rec["kbuf"].clone(), vbuf=vbuf0, position_ids=rec["pos_before"].clone(),
                            prefill_local=cache.prefill_local, sparse_start=sp0, sparse_end=sp1, chunk=c,
                            budget=cache.sparse_budget, ctx=cache.prefill, buf_len=cache.buf_len, chunks=cache.chunks)
     L = rec["kv_len"]
@@ -181,7 +196,9 @@ def check_layer_record(rec, cache, layer, cos_sin_cpu, what=""):
     assert torch.equal(rec["cnts"], torch.from_numpy(res["cnts"])), f"{what}: hit counts"
     assert torch.equal(rec["offsets"], torch.from_numpy(res["offsets"])), f"{what}: offsets"
     assert torch.equal(rec["pos_after"], st.position_ids), f"{what}: slot ids"
-    assert torch.equal(rec["vbuf_after"], st.vbuf[:, :, :L]), f"{what}: value buffer"
+    vbuf_after = _virtual_vbuf(rec["vbuf_after"], host_v, rec["pos_after"], sp0, S, c) if in_place \
+        else rec["vbuf_after"]
+    assert torch.equal(vbuf_after, st.vbuf[:, :, :L]), f"{what}: value buffer"
     kdev, kref = rec["kbuf_after"], st.kbuf[:, :, :L]
     for r in range(B * H):
         b, h = divmod(r, H)

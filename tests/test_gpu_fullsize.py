@@ -129,16 +129,17 @@ def test_rebuild_microbench_sizes(gpu, u_per_head, B):
 
 # ------------------------------------------------------------------ decode workloads
 
-def _decode_and_check(shape, batch, ctx, budget, layers_checked, gpu, state="synthetic"):
+def _decode_and_check(shape, batch, ctx, budget, layers_checked, gpu, state="synthetic", value_store="host"):
     # The value stores of these workloads would take 20-64 GiB of pinned host memory, close to what
     # one process may pin on the MI355X hosts (about 65 GiB): the layers share two host stores (the
     # oracle reads the same store the device fetched from), and blocks cached by earlier tests are
     # released first.
     _release()
-    lanes = decode_model.auto_lanes(shape, batch, budget)
-    _say(f"{shape.name} batch {batch} ctx {ctx} budget {budget}: building ({lanes} lane(s), {state} state)")
+    lanes = decode_model.auto_lanes(shape, batch, budget, value_store)
+    _say(f"{shape.name} batch {batch} ctx {ctx} budget {budget}: building ({lanes} lane(s), {state} state, "
+         f"{value_store} value store)")
     dec = decode_model.SyntheticDecoder(shape, batch, ctx, sparse_budget=budget, decode_len=8, lanes=lanes,
-                                        seed=7, state=state, host_stores=2)
+                                        seed=7, state=state, host_stores=2, value_store=value_store)
     tok = torch.randint(0, shape.vocab, (batch, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(1))
     tok = dec.decode_step(tok)  # the first step; the checked one follows
     probe = LayerProbe(dec, layers_checked)
@@ -156,6 +157,12 @@ def _decode_and_check(shape, batch, ctx, budget, layers_checked, gpu, state="syn
 
 def test_decode_llama31_8b_batch8_ctx122880(gpu):
     _decode_and_check(decode_model.LLAMA31_8B, 8, CTX, 2048, [0, 15, 31], gpu)
+
+
+def test_decode_llama31_8b_batch8_ctx122880_device_store(gpu):
+    """The same step with the value store in device memory: one lane, the attention reading the
+    selected values in place from the store (checked through the buffer the gather would build)."""
+    _decode_and_check(decode_model.LLAMA31_8B, 8, CTX, 2048, [0, 15, 31], gpu, value_store="device")
 
 
 def test_decode_glm4_9b_batch4_ctx262144(gpu):
