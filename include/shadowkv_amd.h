@@ -503,7 +503,7 @@ int skv_rope_qk_append(const uint16_t* qkv, int64_t qkv_stride_b, int batch_size
                        int64_t kv_stride_s, const int64_t* append_row, int64_t buf_len, void* stream);
 
 /* The fused QKV projection (models/llama.py:192, models/glm.py:165 with its bias) with
- * skv_rope_qk_append in its epilogue: the [q | k | v] row of each of the m (<= 4) token rows x[b]
+ * skv_rope_qk_append in its epilogue: the [q | k | v] row of each of the m (<= 8) token rows x[b]
  * (k elements) is formed against the weight (plus bias, when not NULL, in the same row order) and
  * rounded to bf16, then rotated and appended exactly as skv_rope_qk_append does it (same arguments
  * and results; the fused row itself is not written). For rope_mode 0 the weight (and bias) is the

@@ -380,7 +380,8 @@ void launch_qkv_rope(const uint16_t* x, int64_t xs, const uint16_t* w, int64_t w
                      const RopeEpi& re) {
   if (m == 1) launch<16, 1, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
   else if (m == 2) launch<8, 2, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
-  else launch<8, 4, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
+  else if (m <= 4) launch<8, 4, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
+  else launch<8, 8, false, false, kRope>(x, xs, w, ws, nullptr, 0, m, n, k, s, re);
 }
 
 }  // namespace
@@ -398,8 +399,8 @@ extern "C" int skv_linear_qkv_rope_append(const uint16_t* x, int64_t x_stride, c
     skv_set_error("%s: null pointer", what);
     return SKV_EINVAL;
   }
-  if (m < 1 || m > 4 || k < 8 || k % 8 || q_heads < 1 || kv_heads < 1 || (rope_mode != 0 && rope_mode != 1)) {
-    skv_set_error("%s: m=%d (1..4) k=%d (a multiple of 8) q_heads=%d kv_heads=%d rope_mode=%d", what, m, k, q_heads,
+  if (m < 1 || m > 8 || k < 8 || k % 8 || q_heads < 1 || kv_heads < 1 || (rope_mode != 0 && rope_mode != 1)) {
+    skv_set_error("%s: m=%d (1..8) k=%d (a multiple of 8) q_heads=%d kv_heads=%d rope_mode=%d", what, m, k, q_heads,
                   kv_heads, rope_mode);
     return SKV_EUNSUPPORTED;
   }

@@ -314,7 +314,7 @@ class SyntheticDecoder:
         self.act_epilogue = fused and lanes == 1
         # The QKV projection with the new token's RoPE and KV append in its epilogue (q/k weight rows
         # of half-split heads interleaved; bit-identical to the projection followed by the RoPE +
-        # append kernel, one launch fewer per layer): lanes of at most 4 rows.
+        # append kernel, one launch fewer per layer): lanes of at most 8 rows.
         self.qkv_rope_epilogue = fused and lb <= shadowkv.QKV_ROPE_MAX_ROWS
         if fused:
             for lw in self.layers:

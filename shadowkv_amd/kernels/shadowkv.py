@@ -882,7 +882,7 @@ def qkv_rope_weight(weight, q_heads, kv_heads, glm):
     return weight.index_select(0, idx).contiguous()
 
 
-QKV_ROPE_MAX_ROWS = 4
+QKV_ROPE_MAX_ROWS = 8
 
 
 def linear_qkv_rope_append(x, weight_rope, q_heads, kv_heads, positions, cos_sin, q_out, k_cache, v_cache,

@@ -97,12 +97,13 @@ def test_silu_epilogue_matches_two_kernels(gpu, lanes):
             assert torch.equal(a, b), t
 
 
-@pytest.mark.parametrize("model,lanes", [("llama", 1), ("llama", 2), ("glm", 1)])
-def test_qkv_rope_epilogue_matches_two_kernels(gpu, model, lanes):
+@pytest.mark.parametrize("model,lanes,per_lane", [("llama", 1, 4), ("llama", 2, 4), ("glm", 1, 4), ("llama", 1, 8),
+                                                   ("glm", 1, 6)])
+def test_qkv_rope_epilogue_matches_two_kernels(gpu, model, lanes, per_lane):
     """The QKV projection with RoPE + append in its epilogue gives the same tokens and cache state,
     bit for bit, as the projection followed by the RoPE + append kernel (half-split and GLM
-    rotations; one and two lanes of 4 rows), eager and in captured graphs."""
-    batch = 4 * lanes
+    rotations; one and two lanes of 4 rows, one lane of 6 and 8), eager and in captured graphs."""
+    batch = per_lane * lanes
     print(f"QKV RoPE epilogue vs two kernels, {model} batch {batch} in {lanes} lane(s)", flush=True)
     base = decode_model.GLM4_9B if model == "glm" else decode_model.LLAMA31_8B
     shape = replace(base, layers=2, vocab=1000)
