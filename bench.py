@@ -674,12 +674,12 @@ def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
     the call's index, so a caller can rotate through several input sets."""
     import torch
 
-    from shadowkv_amd.streams import side_stream
+    from shadowkv_amd.streams import capture_graph
 
     fn(0)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=side_stream(torch.cuda.current_device(), "capture")):
+    with capture_graph(g, torch.cuda.current_device()):
         for i in range(reps):
             fn(i)
     g.replay()

@@ -28,7 +28,7 @@ from .models.attention import ShadowAttention
 from .models.kvcache import ShadowKVCache_CPU
 from .models.tensor_op import (apply_rotary_pos_emb_cuda, apply_rotary_pos_emb_glm_single, build_cos_sin_cache,
                                build_glm_cos_sin_cache)
-from .streams import side_stream
+from .streams import capture_graph, side_stream
 
 
 @dataclass(frozen=True)
@@ -500,8 +500,9 @@ class SyntheticDecoder:
         for c in self._caches():
             c.check_capacity(steps)
         g = torch.cuda.CUDAGraph()
-        # On the process's capture side stream, so the capture adds no stream beyond the fixed set.
-        with torch.cuda.graph(g, stream=side_stream(self.device, "capture")):
+        # On the process's capture side stream, so the capture adds no stream beyond the fixed set;
+        # no garbage collection (and so no destructor of a dead decoder) runs inside it.
+        with capture_graph(g, self.device):
             self.static_tokens.copy_(self.decode_steps(self.static_tokens, steps))
         for c, (gen, kv) in zip(self._caches(), saved):
             c.gen_offset, c.kv_offset = gen, kv

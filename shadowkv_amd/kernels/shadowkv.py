@@ -889,7 +889,7 @@ def linear_qkv_rope_append(x, weight_rope, q_heads, kv_heads, positions, cos_sin
                            append_row, bias_rope=None):
     """linear(x, wqkv[, bias]) followed by rope_qk_append(...) in one launch, bit-identical, on the
     weight (and bias) in qkv_rope_weight's row order (half-split for a [rows, 128] cos_sin, GLM for
-    [rows, 64]). x: [..., k] token rows (at most 4); the other arguments as rope_qk_append's."""
+    [rows, 64]). x: [..., k] token rows (at most 8); the other arguments as rope_qk_append's."""
     D = 128
     _dev(x, "x", torch.bfloat16)
     _dev(weight_rope, "weight", torch.bfloat16)

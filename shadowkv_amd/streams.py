@@ -13,6 +13,8 @@ overlap on the host link.
 """
 from __future__ import annotations
 
+import contextlib
+import gc
 import threading
 
 import torch
@@ -42,3 +44,24 @@ def side_stream(device, role: str = "fetch") -> torch.cuda.Stream:
 def side_streams_created() -> int:
     """Side streams created so far on all devices."""
     return len(_streams)
+
+
+@contextlib.contextmanager
+def capture_graph(graph: torch.cuda.CUDAGraph, device):
+    """torch.cuda.graph(graph) on the process's capture side stream, with Python's cyclic garbage
+    collector run to completion first and switched off until the capture ends.
+
+    A collection that starts inside the traced code runs the destructors of whatever unreachable
+    objects it finds there: dead decoders (their lanes' RoPE closures refer back to them, so only
+    the collector frees them) with their HIP graphs, pinned host blocks and events. Freeing those
+    while a stream captures in global mode is an illegal call that aborts the process; collecting
+    before the capture frees them outside it."""
+    enabled = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, stream=side_stream(device, "capture")):
+            yield graph
+    finally:
+        if enabled:
+            gc.enable()

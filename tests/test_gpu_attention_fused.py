@@ -8,7 +8,7 @@ import torch
 
 import oracle
 from shadowkv_amd.kernels import shadowkv
-from shadowkv_amd.streams import side_stream
+from shadowkv_amd.streams import capture_graph
 
 pytestmark = pytest.mark.gpu
 
@@ -112,7 +112,7 @@ def test_fused_merge_graph_replays(gpu, monkeypatch):
     torch.cuda.synchronize()
     out = torch.empty_like(eager)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=side_stream(gpu, "capture")):
+    with capture_graph(g, gpu):
         shadowkv.sparse_attn_decode(q, K, V, L, out, ws, kv_len_dev=ldev)
     for r in range(4):
         _say(f"fused graph replay {r}")

@@ -179,16 +179,16 @@ def test_linear_qkv_rope_append_rejects(gpu):
     w = torch.zeros(n, k, dtype=torch.bfloat16, device=gpu)
     cs = torch.zeros(10, 128, dtype=torch.bfloat16, device=gpu)
     row = torch.zeros(1, dtype=torch.int64, device=gpu)
-    x5 = torch.zeros(5, k, dtype=torch.bfloat16, device=gpu)
-    kc = torch.zeros(5, Hk, 4, D, dtype=torch.bfloat16, device=gpu)
-    with pytest.raises(ValueError, match="at most 4"):
-        shadowkv.linear_qkv_rope_append(x5, w, Hq, Hk, torch.zeros(5, dtype=torch.int64, device=gpu), cs,
-                                        torch.empty(5, Hq, D, dtype=torch.bfloat16, device=gpu), kc, kc.clone(), row)
-    rc = _lib.lib().skv_linear_qkv_rope_append(x5.data_ptr(), k, w.data_ptr(), k, None, 5, k, Hq, Hk, row.data_ptr(),
+    x9 = torch.zeros(9, k, dtype=torch.bfloat16, device=gpu)  # one row past the epilogue's limit
+    kc = torch.zeros(9, Hk, 4, D, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="at most 8"):
+        shadowkv.linear_qkv_rope_append(x9, w, Hq, Hk, torch.zeros(9, dtype=torch.int64, device=gpu), cs,
+                                        torch.empty(9, Hq, D, dtype=torch.bfloat16, device=gpu), kc, kc.clone(), row)
+    rc = _lib.lib().skv_linear_qkv_rope_append(x9.data_ptr(), k, w.data_ptr(), k, None, 9, k, Hq, Hk, row.data_ptr(),
                                                cs.data_ptr(), 128, 10, 0, kc.data_ptr(), Hq * D, kc.data_ptr(),
                                                kc.data_ptr(), Hk * 4 * D, 4 * D, D, row.data_ptr(), 4, None)
     assert rc == 2  # SKV_EUNSUPPORTED
     with pytest.raises(ValueError, match="shape mismatch"):  # weight rows for other head counts
-        shadowkv.linear_qkv_rope_append(x5[:2], w[:-128], Hq, Hk, row.repeat(2), cs,
+        shadowkv.linear_qkv_rope_append(x9[:2], w[:-128], Hq, Hk, row.repeat(2), cs,
                                         torch.empty(2, Hq, D, dtype=torch.bfloat16, device=gpu), kc[:2],
                                         kc[:2].clone(), row)

@@ -91,6 +91,63 @@ def test_decoder_capture_stays_on_the_fixed_streams(monkeypatch):
     assert streams.side_streams_created() + 1 <= streams.MAX_STREAMS
 
 
+def test_capture_frees_dead_cycles_first_and_holds_the_collector_off(monkeypatch):
+    """A dead reference cycle (like a decoder whose lanes' RoPE closures refer back to it) is
+    freed before the capture starts, the cyclic collector stays off while the decode steps are
+    traced, and it is on again afterwards, also when tracing raises (stand-in graph context)."""
+    import gc
+    import weakref
+
+    from shadowkv_amd import decode_model, streams
+
+    class FakeStream:
+        def __init__(self, device=None):
+            self.device = device
+
+    class FakeGraphCtx:
+        def __init__(self, graph, stream=None, **kw):
+            pass
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *exc):
+            return False
+
+    class Cycle:
+        pass
+
+    monkeypatch.setattr(streams.torch.cuda, "Stream", FakeStream)
+    monkeypatch.setattr(streams, "_streams", {})
+    monkeypatch.setattr(decode_model.torch.cuda, "CUDAGraph", lambda: object())
+    monkeypatch.setattr(decode_model.torch.cuda, "graph", FakeGraphCtx)
+    dead = Cycle()
+    dead.me = dead
+    ref = weakref.ref(dead)
+    del dead
+    seen = []
+
+    def steps(tokens, steps):
+        seen.append((gc.isenabled(), ref() is None))
+        return tokens
+
+    dec = decode_model.SyntheticDecoder.__new__(decode_model.SyntheticDecoder)
+    dec.device = "cuda:0"
+    dec.lanes = []
+    dec.decode_steps = steps
+    assert gc.isenabled()
+    dec.capture(torch.zeros(2, 1, dtype=torch.long), steps=2)
+    assert seen == [(False, True)] and gc.isenabled()
+
+    def failing(tokens, steps):
+        raise RuntimeError("traced step failed")
+
+    dec.decode_steps = failing
+    with pytest.raises(RuntimeError):
+        dec.capture(torch.zeros(2, 1, dtype=torch.long))
+    assert gc.isenabled()
+
+
 def test_qkv_rope_weight_row_order():
     """The QKV weight (and bias) row order of the RoPE epilogue, on the CPU: each q and k head's rows
     interleaved as (0, 64, 1, 65, ...) so that a rotation pair (d, d + 64) sits in adjacent rows, v
