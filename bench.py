@@ -90,6 +90,8 @@ def parse() -> argparse.Namespace:
                         "envelope: HBM streaming rate of the scoring kernel, a device copy and the read-only probe by "
                              "transfer size")
     p.add_argument("--rebuild-batches", type=int, nargs="+", default=[1, 8, 32, 48])
+    p.add_argument("--linear-rows", type=int, nargs="+", default=[4, 8],
+                   help="token rows of the linear workload (the skinny kernel takes at most 16)")
     p.add_argument("--cpu-runs", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-breakdown", action="store_true")
@@ -102,6 +104,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--device-store-variant", type=int, default=1,
                    help="also time the same decode with the value store in device memory, reported in detail "
                         "(0 to skip)")
+    p.add_argument("--device-store-batch", type=int, default=-1,
+                   help="and once more at this batch with the value store in device memory (default: 24, the "
+                        "reference's published setting, for the Llama-3.1-8B shape at ctx 122880, else none; "
+                        "0 to skip)")
     p.add_argument("--two-stream-fetch", action="store_true",
                    help="one-lane decoders: value fetch on the copy stream and key rebuild on the compute stream "
                         "(the reference's arrangement) instead of one fused launch on the compute stream; two-lane "
@@ -742,26 +748,35 @@ def pool_variant(args, shape, lanes) -> dict:
     return res
 
 
-def device_store_variant(args, shape) -> dict:
-    """The same decode workload with the value store in device memory instead of pinned host memory
-    (ShadowKVCache_CPU(value_store="device"); the Llama-3.1-8B batch-8 ctx-122880 store is 64 GB,
-    which MI355X's 288 GB of HBM holds beside the rest of the state): the same kernels gather the
-    missed chunks from HBM and nothing crosses the host link, so one lane (auto_lanes) and the
-    step is set by the compute. Timed as the main measurement; the host-store decoder is released
-    first."""
+def device_store_variant(args, shape, batch: int) -> dict:
+    """The decode workload at `batch` with the value store in device memory instead of pinned host
+    memory (ShadowKVCache_CPU(value_store="device"); the Llama-3.1-8B ctx-122880 store is 8 GB per
+    sequence, so MI355X's 288 GB of HBM holds it beside the rest of the state up to about batch 24):
+    the attention reads the selected value chunks in place from the store and nothing crosses the
+    host link, so one lane (auto_lanes) and the step is set by the compute. Timed as the main
+    measurement; every other decoder is released first. A batch whose state does not fit reports
+    the allocation failure instead."""
     import gc
     import torch
     from shadowkv_amd import decode_model
 
-    gc.collect()
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
+    def release():
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+    release()
     torch._C._host_emptyCache()
-    lanes = decode_model.auto_lanes(shape, args.batch, args.budget, "device")
-    log(f"device value store variant: {lanes} lane(s)")
-    dm = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
-                                       decode_len=args.warmup + args.steps + 8, lanes=lanes, value_store="device")
-    tok = torch.randint(0, shape.vocab, (args.batch, 1), device="cuda")
+    lanes = decode_model.auto_lanes(shape, batch, args.budget, "device")
+    log(f"device value store variant: batch {batch}, {lanes} lane(s)")
+    try:
+        dm = decode_model.SyntheticDecoder(shape, batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
+                                           decode_len=args.warmup + args.steps + 8, lanes=lanes, value_store="device")
+    except torch.cuda.OutOfMemoryError as e:
+        release()
+        log(f"device value store variant: batch {batch} does not fit: {e}")
+        return {"batch": batch, "skipped": f"state does not fit in device memory: {str(e).splitlines()[0]}"}
+    tok = torch.randint(0, shape.vocab, (batch, 1), device="cuda")
     for _ in range(args.warmup):
         tok = dm.decode_step(tok)
     per_call = math.gcd(args.steps, max(1, args.graph_steps))
@@ -774,17 +789,17 @@ def device_store_variant(args, shape) -> dict:
     elapsed = time.perf_counter() - start
     store_gb = sum(t.numel() * t.element_size() for t in {id(t): t for t in dm.cache.v_cache_cpu}.values()) \
         * len(dm.lanes) / 1e9
-    res = {"tokens_per_s": round(args.batch * args.steps / elapsed, 3),
+    res = {"batch": batch, "tokens_per_s": round(batch * args.steps / elapsed, 3),
            "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "lanes": lanes,
            "value_store_device_GB": round(store_gb, 1),
+           "device_memory_used_GB": round(torch.cuda.memory_allocated() / 1e9, 1),
            "note": "same workload with the value store in device memory (HBM) instead of pinned host memory: the "
-                   "same kernels gather the missed chunks from HBM, nothing crosses the host link; the tokens "
-                   "and state equal the host-store decoder's bit for bit (tests/test_gpu_decoder_variants.py)"}
+                   "attention reads the selected value chunks in place from the store, nothing crosses the host "
+                   "link; the tokens and state equal the host-store decoder's bit for bit "
+                   "(tests/test_gpu_decoder_variants.py)"}
     log(f"device value store variant {res}")
     del dm
-    gc.collect()
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
+    release()
     return res
 
 
@@ -1127,7 +1142,7 @@ def select_microbench(args) -> int:
 
 def linear_microbench(args) -> int:
     """The skinny linear kernel on the Llama-3-8B decode projections (fused QKV, o, fused
-    gate/up, down, lm head) at 4 and 8 token rows, cold weights (distinct copies rotated past the
+    gate/up, down, lm head) at 4 and 8 token rows (--linear-rows), cold weights (distinct copies rotated past the
     last-level cache), next to torch's GEMM on the same operands. One JSON line per (shape, rows)."""
     import torch
     from shadowkv_amd.kernels import shadowkv
@@ -1141,7 +1156,7 @@ def linear_microbench(args) -> int:
         g = torch.Generator(device="cuda").manual_seed(n + k)
         ws = [(torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(sets)]
         set_reps = -(-reps // sets) * sets
-        for rows in (4, 8):
+        for rows in args.linear_rows:
             x = torch.randn(rows, k, generator=g, device="cuda").to(torch.bfloat16)
             y = torch.empty(rows, n, dtype=torch.bfloat16, device="cuda")
             t = gpu_time_per_call(lambda i: shadowkv.linear(x, ws[i % sets], y), set_reps)
@@ -1536,14 +1551,20 @@ def main() -> int:
 
     host_store = args.value_store == "host"
     if detail is not None and args.chunk_cache is None and host_store and \
-            (args.pool_variant > 0 or args.encoded_variant or args.device_store_variant):
+            (args.pool_variant > 0 or args.encoded_variant or args.device_store_variant or args.device_store_batch != 0):
         model = cache = step = None  # release the reference-mode decoder first
         if args.pool_variant > 0:
             detail["chunk_pool"] = pool_variant(args, shape, lanes)
         if args.encoded_variant and args.state == "synthetic":
             detail["encoded_state"] = encoded_variant(args, shape, lanes)
         if args.device_store_variant:
-            detail["device_value_store"] = device_store_variant(args, shape)
+            detail["device_value_store"] = device_store_variant(args, shape, args.batch)
+        if args.device_store_batch < 0:
+            args.device_store_batch = 24 if args.model == "llama31_8b" and args.ctx == 122880 else 0
+        if args.device_store_batch > 0:
+            # The reference's project page quotes its 122K-context throughput at batch 24 (Llama-3.1-8B:
+            # 245.90 tokens/s on one A100, values in host memory; index.html:211-213).
+            detail["device_value_store_batch"] = device_store_variant(args, shape, args.device_store_batch)
 
     out = {
         "metric": ("decode tokens/sec @122K ctx, Llama-3-8B shape; per-kernel HBM GB/s / MFMA util"

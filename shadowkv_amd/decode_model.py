@@ -65,6 +65,15 @@ LANE_FETCH_WORKGROUPS = 64
 LANE_REBUILD_WORKGROUPS = 48
 
 
+# Token rows up to which the decoder's projections use the library's skinny linear kernel; above
+# it, torch's GEMM (hipBLASLt). Measured on MI355X with cold Llama-3-8B weights, µs per launch,
+# skinny vs hipBLASLt: 8 rows qkv 13.1 / 14.4, o_proj 10.8 / 15.8, gate_up 50.6 / 58.9, down
+# 26.6 / 26.7; 12 rows 29.0 / 14.3, 21.0 / 15.8, 125.3 / 59.5, 63.3 / 25.8; 16 rows 30.9 / 14.3,
+# 21.6 / 15.7, 132.6 / 59.5, 64.8 / 26.6 (the kernel's 9-16-row form streams two weight rows per
+# workgroup).
+SKINNY_LINEAR_ROWS = 8
+
+
 def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int, value_store: str = "host") -> int:
     """Batch lanes for the decode step: 2 when a layer's value fetch over the host link outlasts
     three passes over the layer's dense weights, else 1. Each lane streams the dense weights once
@@ -350,9 +359,10 @@ class SyntheticDecoder:
         return F.rms_norm(x, (x.shape[-1],), w, self.shape.eps)
 
     def _linear(self, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
-        """x @ w.T (+ b); fused: the library's skinny linear (weights streamed once) up to its row limit."""
+        """x @ w.T (+ b); fused: the library's skinny linear (weights streamed once) up to
+        SKINNY_LINEAR_ROWS token rows."""
         rows = x.numel() // x.shape[-1]
-        if not self.fused or rows > shadowkv.LINEAR_MAX_ROWS:
+        if not self.fused or rows > SKINNY_LINEAR_ROWS:
             return F.linear(x, w, b)
         out = torch.empty(*x.shape[:-1], w.shape[0], dtype=self.dtype, device=self.device)
         shadowkv.linear(x, w, out, bias=b)
@@ -395,7 +405,7 @@ class SyntheticDecoder:
             o = self._linear(a.reshape(b, 1, s.heads * s.head_dim), lw.wo)
             h2, x2 = torch.empty_like(h), torch.empty_like(h)
             shadowkv.rmsnorm(o, lw.post_norm, s.eps, x2, residual=h, residual_out=h2)
-            if self.act_epilogue and b <= shadowkv.LINEAR_MAX_ROWS:  # SiLU-and-mul in the gate/up epilogue
+            if self.act_epilogue and b <= SKINNY_LINEAR_ROWS:  # SiLU-and-mul in the gate/up epilogue
                 act = torch.empty(b, 1, s.ffn, dtype=self.dtype, device=self.device)
                 shadowkv.linear_gate_up_silu(x2, lw.gate_up_il, act)
                 down = self._linear(act, lw.down)
