@@ -165,6 +165,13 @@ def test_decode_llama31_8b_batch8_ctx122880_device_store(gpu):
     _decode_and_check(decode_model.LLAMA31_8B, 8, CTX, 2048, [0, 15, 31], gpu, value_store="device")
 
 
+def test_decode_llama31_8b_batch24_ctx122880_device_store(gpu):
+    """Batch 24 (the batch of the reference's published 122K figure) with the value store in device
+    memory: one lane of 192 (b, h) rows, so the selection takes its one-workgroup-per-row path and
+    the projections run on hipBLASLt; the first and last layer against the oracle."""
+    _decode_and_check(decode_model.LLAMA31_8B, 24, CTX, 2048, [0, 31], gpu, value_store="device")
+
+
 def test_decode_glm4_9b_batch4_ctx262144(gpu):
     _decode_and_check(decode_model.GLM4_9B, 4, 262144, 2048, [0, 20, 39], gpu)
 
