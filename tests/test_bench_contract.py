@@ -66,3 +66,30 @@ def test_trace_summary_window_and_ops(tmp_path):
     assert table[0]["in_step_us"] == 60.0 and table[0]["eager_instrumented_us"] == 99.0
     assert table[0]["in_step_frac"] == round(480000 / 60.0 / 1e3 / 8000.0, 4)
     assert table[1]["in_step_us"] == 7.0 and "eager_instrumented_us" not in table[1]
+
+
+def test_device_store_variant_reports_a_state_that_does_not_fit(monkeypatch):
+    """The device-store variant at a batch whose state does not fit in device memory reports the
+    allocation failure in its detail entry instead of ending the bench run (stand-in decoder and
+    device calls, no GPU)."""
+    import importlib.util
+    import types
+
+    import torch
+
+    spec = importlib.util.spec_from_file_location("bench", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    from shadowkv_amd import decode_model
+
+    def no_room(*a, **kw):
+        raise torch.cuda.OutOfMemoryError("HIP out of memory. Tried to allocate 6.04 GiB\nmore text")
+
+    monkeypatch.setattr(decode_model, "SyntheticDecoder", no_room)
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **kw: None)
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda: None)
+    monkeypatch.setattr(torch._C, "_host_emptyCache", lambda: None)
+    args = types.SimpleNamespace(budget=2048, ctx=122880, chunk=8, warmup=1, steps=2, graph_steps=2)
+    res = bench.device_store_variant(args, decode_model.LLAMA31_8B, 64)
+    assert res == {"batch": 64, "skipped": "state does not fit in device memory: HIP out of memory. Tried to "
+                                          "allocate 6.04 GiB"}
