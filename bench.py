@@ -55,9 +55,9 @@ def parse() -> argparse.Namespace:
                         "GLM-4-9B (2 kv heads of 16 query heads, GLM RoPE), Llama-3-8B-1M (RoPE theta 3.58e6)")
     p.add_argument("--lanes", type=int, default=None,
                    help="independent batch slices pipelined per layer (default: 2 where the value fetch outweighs the dense layers, see decode_model.auto_lanes)")
-    p.add_argument("--pool-variant", type=int, default=2048,
+    p.add_argument("--pool-variant", type=int, nargs="+", default=[2048, 8192, 12288],
                    help="after the main (reference-mode) measurement, time the same decode with a device chunk "
-                        "pool of this many slots per (b, h) and layer and report it in detail.chunk_pool "
+                        "pool of each of these many slots per (b, h) and layer and report them in detail.chunk_pool "
                         "(0: skip; only with the breakdown)")
     p.add_argument("--encoded-variant", type=int, default=1,
                    help="also time the decode from a prompt state built by the device encoder and report it in "
@@ -699,7 +699,7 @@ def gpu_time_per_call(fn, reps: int, rounds: int = 5) -> float:
     return s.elapsed_time(e) * 1e-3 / (rounds * reps)
 
 
-def pool_variant(args, shape, lanes) -> dict:
+def pool_variant(args, shape, P: int) -> dict:
     """The same decode workload with a device chunk pool (f3: P >= S chunk slots per (b, h) and
     layer kept across steps, least recently used replaced; the same chunks are selected and the
     attention outputs equal the reference mode's to bf16 summation order), timed as the main
@@ -709,16 +709,23 @@ def pool_variant(args, shape, lanes) -> dict:
     import torch
     from shadowkv_amd import decode_model
 
-    P = args.pool_variant
     gc.collect()
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     torch._C._host_emptyCache()
-    log(f"chunk pool variant: {P} slots per (b, h) and layer")
+    # Untimed steps until the pool is full: each step brings in the selection's misses, so a pool of
+    # P slots fills in about P / S steps (a little more, as the hits grow); the timed steps then
+    # see the steady-state hit rate.
+    S = args.budget // args.chunk
+    warm = max(args.warmup, math.ceil(1.25 * P / S) + 1)
+    # lanes for the pool's share of the fetch (about ctx / chunk landmarks per row)
+    lanes = decode_model.auto_lanes(shape, args.batch, args.budget,
+                                    miss_fraction=decode_model.pool_miss_fraction(P, args.ctx // args.chunk))
+    log(f"chunk pool variant: {P} slots per (b, h) and layer, {lanes} lane(s), {warm} untimed steps")
     pm = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
-                                       decode_len=args.warmup + args.steps + 8, lanes=lanes, chunk_cache=P)
+                                       decode_len=warm + args.steps + 8, lanes=lanes, chunk_cache=P)
     tok = torch.randint(0, shape.vocab, (args.batch, 1), device="cuda")
-    for _ in range(args.warmup):
+    for _ in range(warm):
         tok = pm.decode_step(tok)
     per_call = math.gcd(args.steps, max(1, args.graph_steps))
     pm.capture(tok, steps=per_call)
@@ -731,14 +738,16 @@ def pool_variant(args, shape, lanes) -> dict:
     hits = [float(lane.cache.cnts.float().mean()) for lane in pm.lanes]  # last layer of the last step
     c = pm.cache
     extra = (P - c.select_sets) * c.chunk_size * c.head_dim * 2 * 2 * args.batch * shape.kv_heads * shape.layers
-    res = {"slots": P, "tokens_per_s": round(args.batch * args.steps / elapsed, 3),
+    res = {"slots": P, "lanes": lanes, "untimed_steps": warm,
+           "tokens_per_s": round(args.batch * args.steps / elapsed, 3),
            "ms_per_step": round(elapsed * 1e3 / args.steps, 3),
            "hit_rate_last_layer": round(statistics.fmean(hits) / c.select_sets, 4),
            "extra_device_GB": round(extra / 1e9, 2),
            "note": "same workload with a device chunk pool (f3): the same chunks selected and attention outputs "
                    "equal to the reference mode's within bf16 summation order (tests/test_gpu_pool.py); hits are "
                    "chunks still resident from earlier steps (synthetic queries are independent from step to step, "
-                   "so the hit rate is about slots / landmarks)"}
+                   "so the hit rate is about slots / landmarks once the pool is full, which the untimed steps wait "
+                   "for)"}
     log(f"chunk pool variant {res}")
     del pm
     gc.collect()
@@ -1444,7 +1453,9 @@ def main() -> int:
         return 0
     t0 = time.time()
     log(f"building {shape.name} batch {args.batch} ctx {args.ctx} (random weights, synthesized state)")
-    lanes = args.lanes if args.lanes else decode_model.auto_lanes(shape, args.batch, args.budget, args.value_store)
+    lanes = args.lanes if args.lanes else decode_model.auto_lanes(
+        shape, args.batch, args.budget, args.value_store,
+        miss_fraction=decode_model.pool_miss_fraction(args.chunk_cache, args.ctx // args.chunk))
     lanes = lanes if args.batch % lanes == 0 else 1
     model = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
                                           decode_len=args.warmup + args.steps + 8, lanes=lanes,
@@ -1551,10 +1562,12 @@ def main() -> int:
 
     host_store = args.value_store == "host"
     if detail is not None and args.chunk_cache is None and host_store and \
-            (args.pool_variant > 0 or args.encoded_variant or args.device_store_variant or args.device_store_batch != 0):
+            (any(p > 0 for p in args.pool_variant) or args.encoded_variant or args.device_store_variant or
+             args.device_store_batch != 0):
         model = cache = step = None  # release the reference-mode decoder first
-        if args.pool_variant > 0:
-            detail["chunk_pool"] = pool_variant(args, shape, lanes)
+        pools = [p for p in args.pool_variant if p > 0]
+        if pools:
+            detail["chunk_pool"] = [pool_variant(args, shape, p) for p in pools]
         if args.encoded_variant and args.state == "synthetic":
             detail["encoded_state"] = encoded_variant(args, shape, lanes)
         if args.device_store_variant:

@@ -455,6 +455,24 @@ int skv_rebuild_k_rope_slots(const uint16_t* u, int64_t u_stride_b, int64_t u_st
                              int batch_size, int heads, int num_chunks, int chunk_size, int rank, int head_dim,
                              void* stream);
 
+/* The chunk pool's miss gather (skv_gather_copy_misses_to_slots with pool_offset = gpu_v_offset,
+ * map_size = num_chunks) and key rebuild (skv_rebuild_k_rope_slots) in one launch, their
+ * workgroups side by side, as skv_fetch_misses_rebuild_k_rope does for the reference layout (the
+ * pool's hits keep their slots, so nothing moves first). No reference counterpart: the chunk pool
+ * extends the cache past the reference's select_sets slots (models/kvcache/shadow.py:574-593);
+ * for callers that run the pooled step on one stream. Results are those of the two calls. */
+int skv_fetch_misses_rebuild_k_rope_slots(const void* values, void* v_cache_buffer, int64_t cpu_v_length,
+                                          int64_t gpu_v_offset, int64_t gpu_v_stride, const uint16_t* u,
+                                          int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row,
+                                          int64_t u_rows, const uint16_t* sv, int64_t sv_stride_b,
+                                          int64_t sv_stride_h, int64_t sv_stride_n, const int32_t* miss_ids,
+                                          const int32_t* miss_slot, const int32_t* cnts, const uint16_t* cos_sin,
+                                          int64_t stride_cos_sin, int64_t cos_sin_rows, int rope_mode,
+                                          uint16_t* cache, int64_t stride_cache_b, int64_t stride_cache_h,
+                                          int64_t stride_cache_s, int pool_start, int pool_slots, int batch_size,
+                                          int heads, int num_chunks, int chunk_size, int rank, int head_dim,
+                                          int fetch_workgroups, int rebuild_workgroups, void* stream);
+
 /* skv_sparse_attn_decode over a chunk pool: virtual keys [0, kv_len) = rows [0, sparse_start) ++
  * the select_sets chunks of slot_list[(b*kv_heads + h)*select_sets + j] (rows sparse_start +
  * slot*chunk_size + ...) ++ rows from sparse_start + pool_slots*chunk_size on (the generated

@@ -80,6 +80,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "skv_rebuild_k_rope_slots": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64,
                                          _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                          _p]),
+    "skv_fetch_misses_rebuild_k_rope_slots": (
+        _i32, [_p, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64,
+               _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "skv_sparse_attn_decode_paged": (_i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
                                              _p, _f32, _p, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p]),
     "skv_sparse_attn_decode_vstore": (_i32, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,

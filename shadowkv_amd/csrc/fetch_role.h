@@ -128,13 +128,17 @@ __device__ __forceinline__ void fetch_tile(const FetchArgs<IdxT>& f, int row, in
 }
 
 // Workgroup wg of nwg: tile t of a row covers kChunksPerFetchWG consecutive slots starting at
-// start + t*kChunksPerFetchWG; the rows * tiles tiles are walked with a stride of nwg.
+// start + t*kChunksPerFetchWG; the rows * tiles tiles, numbered tile-major (tile t of every row,
+// then tile t + 1), are walked with a stride of nwg. With cache hits only a row's first tiles hold
+// misses, and in this order they are the ones dealt out first, over all the workgroups (numbered
+// row-major with nwg a multiple of the tiles per row, workgroup wg would always take tile wg mod
+// tiles, and most workgroups would find no misses).
 template <typename IdxT>
 __device__ void fetch_role(const FetchArgs<IdxT>& f, int wg, int nwg) {
   const int total_tiles = f.rows * f.tiles;
   for (int tile = wg; tile < total_tiles; tile += nwg) {
-    const int row = tile / f.tiles;
-    const int t = tile - row * f.tiles;
+    const int t = tile / f.rows;
+    const int row = tile - t * f.rows;
     const int start = f.cnts ? max(0, f.cnts[row]) : 0;
     const int i0 = start + t * kChunksPerFetchWG;
     if (i0 >= f.S) continue;

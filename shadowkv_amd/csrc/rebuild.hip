@@ -528,9 +528,15 @@ int launch_rebuild(const char* what, int mode, bool ids64, RebuildArgs a, hipStr
                      static_cast<size_t>(waves) * 16 * kStLd * sizeof(uint16_t);
   const int ks = (a.rank + 31) / 32;
   int rc;
-  if (fetch) {  // (the fused launch: the RoPE modes with int64 chunk ids of skv_rebuild_k_rope)
-    if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
-    else rc = launch_mode<kRopeGlm, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+  if (fetch) {  // (the fused launch: the RoPE modes, with the int64 chunk ids of skv_rebuild_k_rope or
+                // the int32 miss ids of skv_rebuild_k_rope_slots)
+    if (ids64) {
+      if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+      else rc = launch_mode<kRopeGlm, int64_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+    } else {
+      if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int32_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+      else rc = launch_mode<kRopeGlm, int32_t, true>(tile_rows, ks, grid, lds, stream, a, fetch);
+    }
   } else if (ids64) {
     if (mode == kPlain) rc = launch_mode<kPlain, int64_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
     else if (mode == kRopeHalf) rc = launch_mode<kRopeHalf, int64_t>(tile_rows, ks, grid, lds, stream, a, nullptr, wide);
@@ -761,4 +767,95 @@ extern "C" int skv_rebuild_k_rope_slots(const uint16_t* u, int64_t u_stride_b, i
   r.ds_sb = static_cast<int64_t>(num_chunks) * heads;
   r.pool_slots = pool_slots;
   return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, false, r, static_cast<hipStream_t>(stream));
+}
+
+// The chunk pool's value fetch of the misses (skv_gather_copy_misses_to_slots) and key rebuild
+// (skv_rebuild_k_rope_slots) in one launch, their workgroups side by side: entries i >= cnts[r] of
+// row r, chunk miss_ids[i] into slot miss_slot[i] of the value buffer (from the pinned host store)
+// and of the key cache (rebuilt + RoPE). The pool's hits stay in their slots, so nothing moves first.
+extern "C" int skv_fetch_misses_rebuild_k_rope_slots(
+    const void* values, void* v_cache_buffer, int64_t cpu_v_length, int64_t gpu_v_offset, int64_t gpu_v_stride,
+    const uint16_t* u, int64_t u_stride_b, int64_t u_stride_h, int64_t u_stride_row, int64_t u_rows,
+    const uint16_t* sv, int64_t sv_stride_b, int64_t sv_stride_h, int64_t sv_stride_n, const int32_t* miss_ids,
+    const int32_t* miss_slot, const int32_t* cnts, const uint16_t* cos_sin, int64_t stride_cos_sin,
+    int64_t cos_sin_rows, int rope_mode, uint16_t* cache, int64_t stride_cache_b, int64_t stride_cache_h,
+    int64_t stride_cache_s, int pool_start, int pool_slots, int batch_size, int heads, int num_chunks,
+    int chunk_size, int rank, int head_dim, int fetch_workgroups, int rebuild_workgroups, void* stream) {
+  const char* what = "fetch_misses_rebuild_k_rope_slots";
+  if (fetch_workgroups < 0 || fetch_workgroups > 65536 || rebuild_workgroups < 0 || rebuild_workgroups > 65536) {
+    skv_set_error("%s: fetch_workgroups=%d rebuild_workgroups=%d (0 for the default, at most 65536)", what,
+                  fetch_workgroups, rebuild_workgroups);
+    return SKV_EINVAL;
+  }
+  if (head_dim != kHeadDim || (rope_mode != 0 && rope_mode != 1)) {
+    skv_set_error("%s: head_dim=%d (must be 128), rope_mode=%d (0 half-split, 1 GLM)", what, head_dim, rope_mode);
+    return SKV_EUNSUPPORTED;
+  }
+  if (!values || !v_cache_buffer || !miss_ids || !miss_slot || !cnts) {
+    skv_set_error("%s: null value-fetch pointer", what);
+    return SKV_EINVAL;
+  }
+  if (batch_size <= 0 || heads <= 0 || num_chunks <= 0 || chunk_size <= 0 || pool_slots < num_chunks ||
+      static_cast<int64_t>(pool_slots) * chunk_size * head_dim > (int64_t{1} << 31)) {
+    skv_set_error("%s: invalid shape batch=%d heads=%d chunks=%d chunk=%d pool_slots=%d", what, batch_size, heads,
+                  num_chunks, chunk_size, pool_slots);
+    return SKV_EINVAL;
+  }
+  const int64_t chunk_elems = static_cast<int64_t>(chunk_size) * head_dim;
+  if (!aligned16(values) || !aligned16(v_cache_buffer) || cpu_v_length % 8 || gpu_v_offset % 8 || gpu_v_stride % 8 ||
+      cpu_v_length < chunk_elems || gpu_v_offset < 0 ||
+      gpu_v_stride < gpu_v_offset + static_cast<int64_t>(pool_slots) * chunk_elems) {
+    skv_set_error("%s: value rows must be 16-byte aligned and hold the pool (cpu_v_length=%lld offset=%lld "
+                  "stride=%lld)", what, (long long)cpu_v_length, (long long)gpu_v_offset, (long long)gpu_v_stride);
+    return SKV_EINVAL;
+  }
+  skv::FetchArgs<int32_t> f{};
+  f.src = static_cast<const u32x4*>(values);
+  f.src_row_vec = cpu_v_length / 8;
+  f.dst = static_cast<u32x4*>(v_cache_buffer);
+  f.dst_row_vec = gpu_v_stride / 8;
+  f.dst_offset_vec = gpu_v_offset / 8;
+  f.ids = miss_ids;
+  f.cnts = cnts;
+  f.dst_slot = miss_slot;
+  f.pool_slots = pool_slots;
+  f.S = num_chunks;
+  f.chunk_vec = static_cast<int>(chunk_elems / 8);
+  f.src_chunks = cpu_v_length / chunk_elems;
+  f.rows = batch_size * heads;
+  f.tiles = (num_chunks + skv::kChunksPerFetchWG - 1) / skv::kChunksPerFetchWG;
+  f.workgroups = fetch_workgroups;  // the target (0: default); the launch sets the count
+  RebuildArgs r{};
+  r.u = u;
+  r.u_sb = u_stride_b;
+  r.u_sh = u_stride_h;
+  r.u_sr = u_stride_row;
+  r.u_rows = u_rows;
+  r.sv = sv;
+  r.sv_sb = sv_stride_b;
+  r.sv_sh = sv_stride_h;
+  r.sv_sn = sv_stride_n;
+  r.ids = miss_ids;
+  r.id_sh = num_chunks;
+  r.id_sb = static_cast<int64_t>(num_chunks) * heads;
+  r.cnts = cnts;
+  r.cs = cos_sin;
+  r.cs_stride = stride_cos_sin;
+  r.cs_rows = cos_sin_rows;
+  r.out = cache;
+  r.o_sb = stride_cache_b;
+  r.o_sh = stride_cache_h;
+  r.o_ss = stride_cache_s;
+  r.o_start = pool_start;
+  r.B = batch_size;
+  r.H = heads;
+  r.S = num_chunks;
+  r.chunk = chunk_size;
+  r.rank = rank;
+  r.dst_slot = miss_slot;
+  r.ds_sh = num_chunks;
+  r.ds_sb = static_cast<int64_t>(num_chunks) * heads;
+  r.pool_slots = pool_slots;
+  r.rebuild_wgs = rebuild_workgroups;
+  return launch_rebuild(what, rope_mode == 0 ? kRopeHalf : kRopeGlm, false, r, static_cast<hipStream_t>(stream), &f);
 }

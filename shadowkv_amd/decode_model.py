@@ -74,7 +74,27 @@ LANE_REBUILD_WORKGROUPS = 48
 SKINNY_LINEAR_ROWS = 8
 
 
-def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int, value_store: str = "host") -> int:
+def pool_miss_fraction(pool_slots: int | None, landmarks: int) -> float:
+    """Expected fraction of a step's selected chunks that a chunk pool of pool_slots slots per
+    (b, h) misses once it is full, for selections independent from step to step (the synthetic
+    decode): 1 - pool_slots / landmarks (measured, Llama-3.1-8B ctx 122880, 15304 landmarks: hit
+    rates 16.7 / 32.6 / 61.8% with 2048 / 4096 / 8192 slots); 1 without a pool."""
+    return 1.0 if pool_slots is None else 1.0 - min(1.0, pool_slots / landmarks)
+
+
+def lane_fetch_workgroups(miss_fraction: float = 1.0) -> int:
+    """Fetch workgroups of a decode lane's one-launch fetch + rebuild: LANE_FETCH_WORKGROUPS for
+    the full miss traffic, fewer as a chunk pool takes misses away (host reads in flight slow the
+    other lane's kernels; the fetch then still ends within that lane's compute). Measured on
+    MI355X, Llama-3.1-8B batch 8 ctx 122880, two lanes, tokens/s by fetch workgroups: 2048 slots
+    48 / 64: 430.4 / 399.3; 4096 slots 32 / 64: 487.1 / 421.5; 8192 slots 16 / 32: 510.8 /
+    506.9. The rule: the square of the miss fraction times LANE_FETCH_WORKGROUPS, to the nearest
+    multiple of 8, at least 16."""
+    return max(16, 8 * round(LANE_FETCH_WORKGROUPS * miss_fraction * miss_fraction / 8))
+
+
+def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int, value_store: str = "host",
+               miss_fraction: float = 1.0) -> int:
     """Batch lanes for the decode step: 2 when a layer's value fetch over the host link outlasts
     three passes over the layer's dense weights, else 1. Each lane streams the dense weights once
     per layer, so a second lane only pays off where the fetch it hides is long: measured on one
@@ -82,12 +102,13 @@ def auto_lanes(shape: ModelShape, batch: int, sparse_budget: int, value_store: s
     2.2), batch 4 262 / 271 (4.4), batch 8 271 / 383 (8.9); GLM-4-9B ctx 262144 batch 4 393 / 261
     (1.2). Rates: 52 GB/s host link, 6 TB/s weight stream. With the value store in device memory
     there is no host-link fetch to hide: one lane (Llama-3.1-8B batch 8: 740.6 vs 640.6 tokens/s
-    for two lanes)."""
+    for two lanes). A chunk pool takes the fraction 1 - miss_fraction of the fetch away (12288
+    slots, 80% hits: 608.5 tokens/s with one lane vs 526.3 with two)."""
     if batch % 2 or value_store == "device":
         return 1
     d = shape.head_dim
     weights = 2 * shape.hidden * ((shape.heads + 2 * shape.kv_heads) * d + shape.heads * d + 3 * shape.ffn)
-    fetch = batch * shape.kv_heads * sparse_budget * d * 2
+    fetch = batch * shape.kv_heads * sparse_budget * d * 2 * miss_fraction
     return 2 if fetch / 52e9 > 3 * weights / 6e12 else 1
 
 def synthesize_state(cache: ShadowKVCache_CPU, ctx: int, seed: int = 0, cos_sin: torch.Tensor | None = None) -> None:
@@ -252,12 +273,12 @@ class SyntheticDecoder:
         cfg = types.SimpleNamespace(num_attention_heads=s.heads, num_key_value_heads=s.kv_heads,
                                     hidden_size=s.heads * D, num_hidden_layers=s.layers)
         lb = batch // lanes
-        # Two lanes, no chunk pool: each lane's one-launch fetch + rebuild on its own side stream
-        # (default), else the shared fetch and rebuild streams.
-        self.lane_streams = (lanes == 2 and chunk_cache is None and one_stream_fetch is not False) \
-            if lane_streams is None else bool(lane_streams)
-        if self.lane_streams and (lanes != 2 or chunk_cache is not None):
-            raise ValueError("lane_streams takes two lanes and no chunk pool")
+        # Two lanes: each lane's one-launch fetch + rebuild on its own side stream (default), else
+        # the shared fetch and rebuild streams.
+        self.lane_streams = (lanes == 2 and one_stream_fetch is not False) if lane_streams is None \
+            else bool(lane_streams)
+        if self.lane_streams and lanes != 2:
+            raise ValueError("lane_streams takes two lanes")
         self.lanes = []
         for i in range(lanes):
             cache = ShadowKVCache_CPU(cfg, batch_size=lb, max_length=ctx, device=device, sparse_budget=sparse_budget,
@@ -280,11 +301,11 @@ class SyntheticDecoder:
             # so the value fetch follows it directly; this decoder fetches only through the cache.
             cache.fold_hit_moves = True
             # One lane: the step runs on the compute stream alone, the value fetch and key rebuild
-            # as one launch after a selection that moved both buffers' hits (no cross-stream wait
+            # as one launch after a selection that moved both buffers' hits (with a chunk pool:
+            # after the pool's assignment, the hits staying in their slots) (no cross-stream wait
             # before or after the fetch; MI355X tokens/s vs the two-stream step: GLM-4-9B batch 4
             # 429.8 vs 418.4, Llama-3-8B-1M 38.42 vs 37.81).
-            cache.one_stream_fetch = (lanes == 1 and chunk_cache is None) if one_stream_fetch is None \
-                else bool(one_stream_fetch)
+            cache.one_stream_fetch = (lanes == 1) if one_stream_fetch is None else bool(one_stream_fetch)
             if self.lane_streams:
                 # Each lane's value fetch and key rebuild as one launch on a side stream of its own
                 # (lane 0 on the fetch stream, lane 1 on the rebuild stream), after a selection that
@@ -297,7 +318,8 @@ class SyntheticDecoder:
                 cache.one_stream_fetch = True
                 cache.lane_stream = side_stream(device, ("fetch", "rebuild")[i])
                 if value_store == "host":  # (a store in HBM takes the library's wide fetch)
-                    cache.fused_fetch_workgroups = LANE_FETCH_WORKGROUPS
+                    cache.fused_fetch_workgroups = lane_fetch_workgroups(
+                        pool_miss_fraction(chunk_cache, cache.k_landmark.shape[-2]))
                     cache.fused_rebuild_workgroups = LANE_REBUILD_WORKGROUPS
             elif lanes > 1:
                 # All lanes share one value-fetch stream and one key-rebuild stream (their fetches

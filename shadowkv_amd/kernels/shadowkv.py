@@ -427,6 +427,39 @@ def fetch_misses_rebuild_k_rope(values, v_cache_buffer, offsets, cnts, cpu_v_len
               int(rebuild_workgroups), _stream())
 
 
+def fetch_misses_rebuild_k_rope_slots(values, v_cache_buffer, miss_ids, cnts, miss_slot, cpu_v_length, pool_offset,
+                                      gpu_v_stride, u, sv, cos_sin, cache, sparse_start, chunk_size, pool_slots,
+                                      fetch_workgroups=0, rebuild_workgroups=0):
+    """A chunk pool's miss gather (gather_copy_misses_to_slots) and key rebuild (rebuild_k_rope with
+    miss_slot) in one launch on the current stream, their workgroups side by side: entries i >=
+    cnts[r] of pool_assign's miss list, chunk miss_ids[b, h, i] (int32 [B, H, S]) into slot
+    miss_slot[b, h, i] of both buffers. Same arguments and results as the two calls (pool_offset =
+    sparse_start * 128); fetch_workgroups / rebuild_workgroups as for fetch_misses_rebuild_k_rope."""
+    B, H, S = miss_ids.shape
+    _dev(miss_ids, "miss_ids", torch.int32)
+    _dev(miss_slot, "miss_slot", torch.int32)
+    if not (miss_ids.is_contiguous() and miss_slot.is_contiguous()) or miss_slot.numel() != B * H * S:
+        raise ValueError("miss_ids and miss_slot must be contiguous [B, H, S]")
+    if pool_slots < S:
+        raise ValueError(f"pool_slots={pool_slots} holds fewer than the {S} selected chunks")
+    u_sb, u_sh, u_sr, u_rows, sv_sb, sv_sh, sv_sn, mode, rank = _rebuild_geometry(
+        u, sv, miss_ids, cnts, cos_sin, cache, sparse_start, chunk_size, pool_slots)
+    rows = B * H
+    chunk_elems = chunk_size * 128
+    row_stride = _host_row_stride(values, rows, cpu_v_length)
+    _need(values, (rows - 1) * row_stride + row_stride, "values")
+    if values.dtype != torch.bfloat16:
+        raise ValueError("values must be bf16")
+    _dev(v_cache_buffer, "v_cache_buffer", torch.bfloat16)
+    _need(v_cache_buffer, (rows - 1) * gpu_v_stride + pool_offset + pool_slots * chunk_elems, "v_cache_buffer")
+    _lib.call("skv_fetch_misses_rebuild_k_rope_slots", device_address(values), v_cache_buffer.data_ptr(), row_stride,
+              pool_offset, gpu_v_stride, u.data_ptr(), u_sb, u_sh, u_sr, u_rows, sv.data_ptr(), sv_sb, sv_sh, sv_sn,
+              miss_ids.data_ptr(), miss_slot.data_ptr(), cnts.data_ptr(), cos_sin.data_ptr(), cos_sin.stride(0),
+              cos_sin.shape[0], mode, cache.data_ptr(), cache.stride(0), cache.stride(1), cache.stride(2),
+              sparse_start, pool_slots, B, H, S, chunk_size, rank, 128, int(fetch_workgroups),
+              int(rebuild_workgroups), _stream())
+
+
 # ---------------------------------------------------------------------------------------------
 # a1/a2: scoring, GQA max, top-k
 

@@ -528,17 +528,29 @@ class ShadowKVCache_CPU(KVCacheBase):
 
     def one_stream_active(self) -> bool:
         """The decode step's value fetch and key rebuild run as one launch on the current stream
-        (one_stream_fetch, with the selection moving both buffers' hits; no chunk pool)."""
-        return self.one_stream_fetch and self.fold_hit_moves and not self.pooled
+        (one_stream_fetch, with the selection moving both buffers' hits, or with a chunk pool, whose
+        hits stay in their slots)."""
+        return self.one_stream_fetch and (self.pooled or self.fold_hit_moves)
 
     def fetch_and_rebuild(self, layer_idx: int, position_ids: torch.Tensor, cos_sin_cache: torch.Tensor):
         """get_value_cache and get_key_cache as one launch on the current stream: the misses'
         value chunks gathered from the host store beside the misses' key rebuild + RoPE, after a
         selection that moved both buffers' hits (one_stream_fetch). Returns (keys, values), the
-        live views of the two buffers."""
-        if self.pooled or self._folded[layer_idx] != ({"k"} if self.values_in_place else {"v", "k"}):
+        live views of the two buffers. With a chunk pool: the miss list of pool_assign, each miss
+        fetched and rebuilt into its slot of both buffers."""
+        if self.pooled:
+            B, H, S, D = self.batch_size, self.num_key_value_heads, self.select_sets, self.head_dim
+            shadowkv.fetch_misses_rebuild_k_rope_slots(
+                self.v_cache_cpu[layer_idx], self.v_cache_buffer[layer_idx], self.miss_ids.view(B, H, S), self.cnts,
+                self.miss_slot.view(B, H, S), int(self.max_ctx_chunks_len * D), self.sparse_start * D,
+                self.buf_len * D, self.U[layer_idx], self.SV[layer_idx], cos_sin_cache, self.k_cache_buffer[layer_idx],
+                self.sparse_start, self.chunk_size, self.pool_slots, fetch_workgroups=self.fused_fetch_workgroups,
+                rebuild_workgroups=self.fused_rebuild_workgroups)
+            return (self._live_view(self.k_cache_buffer[layer_idx], layer_idx),
+                    self._live_view(self.v_cache_buffer[layer_idx], layer_idx))
+        if self._folded[layer_idx] != ({"k"} if self.values_in_place else {"v", "k"}):
             raise RuntimeError("fetch_and_rebuild needs a selection that moved both buffers' hits "
-                               "(the key buffer's with the values read in place; one_stream_fetch, no chunk pool)")
+                               "(the key buffer's with the values read in place; one_stream_fetch)")
         self._folded[layer_idx].clear()
         if position_ids.dtype != torch.int64:
             position_ids = position_ids.to(torch.int64)

@@ -131,13 +131,15 @@ def test_qkv_rope_epilogue_matches_two_kernels(gpu, model, lanes, per_lane):
             assert torch.equal(a, b), ("replay", t)
 
 
-def test_lane_streams_match_shared_streams(gpu):
+@pytest.mark.parametrize("pool", [None, 512])
+def test_lane_streams_match_shared_streams(gpu, pool):
     """Two lanes with each lane's one-launch value fetch + key rebuild on a side stream of its own
     (the decoder's default) give the same tokens and cache state, bit for bit, as the lanes sharing
-    one fetch stream and one rebuild stream, eager and in captured graphs."""
-    print("lane streams vs shared fetch / rebuild streams, batch 8 in 2 lanes", flush=True)
+    one fetch stream and one rebuild stream, eager and in captured graphs; also with a chunk pool
+    (the one launch then fetches and rebuilds the pool's misses into their slots)."""
+    print(f"lane streams vs shared fetch / rebuild streams, batch 8 in 2 lanes, pool {pool}", flush=True)
     shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
-    kw = dict(sparse_budget=2048, decode_len=12, lanes=2, seed=19)
+    kw = dict(sparse_budget=2048, decode_len=12, lanes=2, seed=19, chunk_cache=pool)
     own = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
     shared = decode_model.SyntheticDecoder(shape, 8, 16384, lane_streams=False, **kw)
     assert own.lane_streams and not shared.lane_streams

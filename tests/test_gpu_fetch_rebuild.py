@@ -78,6 +78,62 @@ def _one_launch_case(gpu, B, H, S, glm, R, c, seed):
     assert not torch.equal(kb.view(torch.int16), k0.view(torch.int16))
 
 
+@pytest.mark.parametrize("B,H,S,P,glm,R,c", [(4, 8, 256, 2048, False, 160, 8), (1, 8, 256, 512, False, 160, 8),
+                                               (4, 2, 256, 384, True, 160, 8), (2, 3, 40, 40, False, 96, 16),
+                                               (3, 2, 100, 333, True, 64, 4)])
+def test_one_launch_slots_equals_gather_then_rebuild(gpu, B, H, S, P, glm, R, c):
+    """The chunk pool's one-launch fetch + rebuild (fetch_misses_rebuild_k_rope_slots) against the
+    two calls it replaces (gather_copy_misses_to_slots, rebuild_k_rope with miss_slot): value and
+    key buffers bit-identical, pool rows of misses only and of hits only, rebuild workgroups
+    capped or not; slots the miss list does not name are left untouched."""
+    print(f"pool fetch+rebuild one launch B={B} H={H} S={S} P={P} glm={glm} rank={R} chunk={c}", flush=True)
+    D = 128
+    seed = B * 1000 + H * 100 + S + P
+    chunks = max(4 * S, 2048)
+    ctx = chunks * c
+    sparse_start = 64
+    buf_len = sparse_start + P * c + 24
+    g = torch.Generator().manual_seed(seed)
+    gd = torch.Generator(device=gpu).manual_seed(seed)
+    values = torch.randn(B, H, chunks, c * D, generator=g).to(torch.bfloat16).pin_memory()
+    U = torch.randn(B, ctx, R, generator=gd, device=gpu).to(torch.bfloat16)
+    SV = (torch.randn(B, H, D, R, generator=gd, device=gpu) / R ** 0.5).to(torch.bfloat16)
+    cos_sin = (build_glm_cos_sin_cache(ctx + 64, 10000.0, device=gpu) if glm
+               else build_cos_sin_cache(ctx + 64, 500000.0, D, device=gpu))
+    rows = B * H
+    cnts = torch.randint(0, S + 1, (rows,), generator=g, dtype=torch.int32)
+    cnts[0] = 0
+    if rows > 1:
+        cnts[-1] = S
+    # miss list as pool_assign leaves it: entries [cnts, S) name distinct chunks and distinct slots
+    miss_ids = torch.stack([torch.randperm(chunks, generator=g)[:S] for _ in range(rows)]).to(torch.int32)
+    miss_slot = torch.stack([torch.randperm(P, generator=g)[:S] for _ in range(rows)]).to(torch.int32)
+    v0 = torch.randn(B, H, buf_len, D, generator=gd, device=gpu).to(torch.bfloat16)
+    k0 = torch.randn(B, H, buf_len, D, generator=gd, device=gpu).to(torch.bfloat16)
+    ids_d, slot_d, cnts_d = miss_ids.view(B, H, S).to(gpu), miss_slot.view(B, H, S).to(gpu), cnts.to(gpu)
+    va, ka = v0.clone(), k0.clone()
+    shadowkv.gather_copy_misses_to_slots(values, va, ids_d, cnts_d, slot_d, B, H, chunks * c * D, sparse_start * D,
+                                         buf_len * D, S, P, c * D)
+    shadowkv.rebuild_k_rope(U, SV, ids_d, cnts_d, cos_sin, ka, sparse_start, c, miss_slot=slot_d, pool_slots=P)
+    for cap in (0, 8, 48):
+        vb, kb = v0.clone(), k0.clone()
+        shadowkv.fetch_misses_rebuild_k_rope_slots(values, vb, ids_d, cnts_d, slot_d, chunks * c * D,
+                                                   sparse_start * D, buf_len * D, U, SV, cos_sin, kb, sparse_start,
+                                                   c, P, rebuild_workgroups=cap)
+        torch.cuda.synchronize()
+        assert torch.equal(vb.view(torch.int16), va.view(torch.int16)), cap
+        assert torch.equal(kb.view(torch.int16), ka.view(torch.int16)), cap
+    # the launch did write: row 0 (misses only) holds each miss chunk in its slot, in both buffers
+    vr = vb[0, 0, sparse_start:sparse_start + P * c].reshape(P, c * D).cpu()
+    assert torch.equal(vr[miss_slot[0].long()].view(torch.int16), values[0, 0, miss_ids[0].long()].view(torch.int16))
+    untouched = torch.ones(P, dtype=torch.bool)
+    untouched[miss_slot[0].long()] = False
+    kr = kb[0, 0, sparse_start:sparse_start + P * c].reshape(P, c * D).cpu()
+    k0r = k0[0, 0, sparse_start:sparse_start + P * c].reshape(P, c * D).cpu()
+    assert torch.equal(kr[untouched].view(torch.int16), k0r[untouched].view(torch.int16))
+    assert not torch.equal(kr[~untouched].view(torch.int16), k0r[~untouched].view(torch.int16))
+
+
 def test_one_launch_rejects_inconsistent_buffers(gpu):
     B, H, S, c, D, R, chunks = 1, 2, 16, 8, 128, 160, 64
     values = torch.zeros(B, H, chunks, c * D, dtype=torch.bfloat16).pin_memory()

@@ -88,12 +88,22 @@ def test_pooled_decode_random_configurations(gpu):
         _pooled_decode(gpu, case, P, bool(i % 2), drift, steps=4, layers=1)
 
 
-def _pooled_decode(gpu, case, P, device_lengths, drift, steps, layers):
+@pytest.mark.parametrize("P,device_lengths", [(256, True), (160, False)])
+def test_pooled_decode_one_launch_matches_oracle(gpu, P, device_lengths):
+    """The pooled step with the misses' value fetch and key rebuild as one launch on the current
+    stream (one_stream_fetch: fetch_misses_rebuild_k_rope_slots) against the oracle's pooled step."""
+    _say(f"pooled decode, one-launch fetch + rebuild, P={P} device_lengths={device_lengths}")
+    _pooled_decode(gpu, make_golden.decode_small_case(), P, device_lengths, 0.3, steps=5, layers=2, one_stream=True)
+
+
+def _pooled_decode(gpu, case, P, device_lengths, drift, steps, layers, one_stream=False):
     d = case["dims"]
     B, H, G, D = d["B"], d["H"], d["G"], d["D"]
     cache = build_cache(case, gpu, max_decode_len=steps, num_layers=layers, chunk_cache=P)
     if device_lengths:
         cache.use_device_lengths()
+    cache.one_stream_fetch = one_stream
+    assert cache.one_stream_active() == one_stream
     cos_sin = case["cos_sin"]
     attn = ShadowAttention(cache, G, D, H * G * D, identity_rope(B, H * G, H, D), None, cos_sin.to(gpu))
     states = [fresh_oracle_state(case) for _ in range(layers)]

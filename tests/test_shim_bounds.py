@@ -36,6 +36,20 @@ def test_auto_lanes_follows_the_measured_choices():
     assert dm.auto_lanes(dm.LLAMA3_8B_1M, 1, 16384) == 1  # one sequence: nothing to pipeline
     assert dm.auto_lanes(dm.LLAMA31_8B, 7, 2048) == 1   # odd batch
     assert dm.auto_lanes(dm.LLAMA31_8B, 8, 2048, value_store="device") == 1  # no host link to hide: 741 vs 641
+    # a chunk pool takes misses away: 12288 of 15304 landmarks kept, 608.5 (one lane) vs 526.3
+    assert dm.auto_lanes(dm.LLAMA31_8B, 8, 2048, miss_fraction=dm.pool_miss_fraction(12288, 15304)) == 1
+    assert dm.auto_lanes(dm.LLAMA31_8B, 8, 2048, miss_fraction=dm.pool_miss_fraction(4096, 15304)) == 2  # 487 vs 392
+
+
+def test_lane_fetch_workgroups_follow_the_pool():
+    """A lane's fetch workgroups shrink with the square of the expected miss fraction (the nearest
+    multiple of 8, at least 16): the full 64 without a pool, 48 / 32 / 16 with 2048 / 4096 / 8192
+    of 15304 chunks pooled."""
+    from shadowkv_amd import decode_model as dm
+    assert dm.pool_miss_fraction(None, 15304) == 1.0
+    assert dm.pool_miss_fraction(20000, 15304) == 0.0
+    got = [dm.lane_fetch_workgroups(dm.pool_miss_fraction(p, 15304)) for p in (None, 256, 2048, 4096, 8192, 12288)]
+    assert got == [64, 64, 48, 32, 16, 16]
 
 
 def test_side_streams_are_limited_to_the_hardware_queues(monkeypatch):
