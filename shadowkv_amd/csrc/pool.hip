@@ -53,6 +53,7 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
   __shared__ int hist[256];
   __shared__ int scan[kThreads / 64 + 1];
   __shared__ int bin_sh, need_sh;
+  __shared__ uint32_t kmin_sh, kmax_sh;
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t* sel = selected + static_cast<int64_t>(row) * S;
@@ -75,6 +76,10 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
 #pragma unroll
   for (int u = 0; u < kSlotPer; ++u) key[u] = (v0 + u < v1) ? static_cast<uint32_t>(su[v0 + u] + 1) : 0xffffffffu;
   for (int w = tid; w < (P + 31) / 32; w += kThreads) hit_bits[w] = 0u;
+  if (tid == 0) {
+    kmin_sh = 0xffffffffu;
+    kmax_sh = 0u;
+  }
   __syncthreads();
   // Hits keep their slot; the thread remembers which of its entries missed.
   int s[kSelPer];
@@ -102,13 +107,40 @@ __global__ void __launch_bounds__(kThreads) pool_assign_kernel(const int64_t* __
     if (v < v1 && ((hit_bits[v >> 5] >> (v & 31)) & 1u)) key[u] = 0xffffffffu;
   }
 
-  // Victims: the m smallest keys over the slots (hit slots excluded by their key), by a 4-pass
-  // 8-bit radix select; ties to the lowest slot.
+  // Victims: the m smallest keys over the slots (hit slots excluded by their key), by an 8-bit
+  // radix select; ties to the lowest slot. Keys are step numbers, so the other slots' keys span
+  // few values: they are taken relative to their minimum, and the select runs only over the bytes
+  // that span needs (one or two passes instead of four for decodes of up to 65536 steps).
   uint32_t prefix = 0, mask = 0;
   int need = m;
   if (m > 0) {  // workgroup-uniform
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
+    uint32_t lmin = 0xffffffffu, lmax = 0u;
+#pragma unroll
+    for (int u = 0; u < kSlotPer; ++u) {
+      if (v0 + u < v1 && key[u] != 0xffffffffu) {
+        lmin = min(lmin, key[u]);
+        lmax = max(lmax, key[u]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lmin = min(lmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lmin), off)));
+      lmax = max(lmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lmax), off)));
+    }
+    if ((tid & 63) == 0) {
+      atomicMin(&kmin_sh, lmin);
+      atomicMax(&kmax_sh, lmax);
+    }
+    __syncthreads();
+    const uint32_t lo = kmin_sh, span = kmax_sh - kmin_sh;  // (m > 0: some slot is not a hit)
+    const int passes = span < (1u << 8) ? 1 : span < (1u << 16) ? 2 : span < (1u << 24) ? 3 : 4;
+#pragma unroll
+    for (int u = 0; u < kSlotPer; ++u)
+      if (key[u] != 0xffffffffu) key[u] -= lo;
+    // the bytes above the passes are zero for every other slot (and not for a hit slot's key)
+    mask = passes == 4 ? 0u : ~((1u << (8 * passes)) - 1u);
+    for (int pass = 0; pass < passes; ++pass) {
+      const int shift = 8 * (passes - 1 - pass);
       for (int i = tid; i < 256; i += kThreads) hist[i] = 0;
       __syncthreads();
 #pragma unroll

@@ -48,6 +48,48 @@ def test_pool_assign_matches_oracle(gpu, rows, chunks, S, P, drift):
             assert np.array_equal(d_t.cpu().numpy(), r_t), t
 
 
+@pytest.mark.parametrize("span,empty", [(200, 0.0), (300, 0.1), (70000, 0.05), (1 << 25, 0.0)])
+def test_pool_assign_after_long_decodes_matches_oracle(gpu, span, empty):
+    """pool_assign from tables a long decode leaves behind: every slot's last use spread over the
+    `span` steps before the clock (`empty` of the slots never used), so the victims' selection runs
+    over one, two, three or four key bytes; against the oracle for 4 steps."""
+    _say(f"pool_assign after a long decode: last uses over {span} steps, {empty:.0%} empty slots")
+    rows, chunks, S, P = 4, 30000, 256, 4096
+    rng = np.random.default_rng(span)
+    clock0 = span + 1000
+    slot_of = np.full((rows, chunks), -1, np.int32)
+    slot_chunk = np.full((rows, P), -1, np.int32)
+    slot_used = np.full((rows, P), -1, np.int32)
+    for r in range(rows):
+        held = rng.permutation(chunks)[:P]
+        used = rng.random(P) >= empty
+        slot_chunk[r, used] = held[used]
+        slot_of[r, held[used]] = np.nonzero(used)[0]
+        slot_used[r, used] = rng.integers(clock0 - span, clock0, size=int(used.sum()))
+    ref = [slot_of, slot_chunk, slot_used, np.full(rows, clock0, np.int32)]
+    dev = [torch.from_numpy(t.copy()).to(gpu) for t in ref]
+    slot_list = torch.empty(rows, S, dtype=torch.int32, device=gpu)
+    miss_ids = torch.empty(rows, S, dtype=torch.int32, device=gpu)
+    miss_slot = torch.empty(rows, S, dtype=torch.int32, device=gpu)
+    cnts = torch.empty(rows, dtype=torch.int32, device=gpu)
+    for t in range(4):
+        # half of each selection from the resident chunks, half from the others
+        sel = np.stack([np.concatenate([rng.permutation(slot_chunk[r][slot_chunk[r] >= 0])[:S // 2],
+                                        rng.permutation(np.setdiff1d(np.arange(chunks), slot_chunk[r]))[:S // 2]])
+                        for r in range(rows)]).astype(np.int64)
+        want = oracle.pool_assign(sel, *ref)
+        shadowkv.pool_assign(torch.from_numpy(sel).to(gpu), chunks, *dev, slot_list, miss_ids, miss_slot, cnts)
+        torch.cuda.synchronize()
+        assert np.array_equal(slot_list.cpu().numpy(), want[0]), t
+        assert np.array_equal(cnts.cpu().numpy(), want[3]), t
+        assert (want[3] == S // 2).all()
+        for r in range(rows):
+            assert np.array_equal(miss_ids.cpu().numpy()[r, S // 2:], want[1][r, S // 2:])
+            assert np.array_equal(miss_slot.cpu().numpy()[r, S // 2:], want[2][r, S // 2:])
+        for d_t, r_t in zip(dev, ref):
+            assert np.array_equal(d_t.cpu().numpy(), r_t), t
+
+
 def _queries(B, H, G, D, steps, layers, seed, drift):
     """Per-(step, layer) queries that drift slowly, so consecutive selections overlap."""
     g = torch.Generator().manual_seed(seed)
