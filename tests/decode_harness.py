@@ -125,11 +125,18 @@ class LayerProbe:
             rec = dict(q=q.reshape(q.shape[0], q.shape[1], -1).cpu(), kbuf=c.k_cache_buffer[idx].cpu(),
                        vbuf=c.v_cache_buffer[idx].cpu(), pos_before=c.position_ids[idx].cpu(),
                        kv_len=int(c.kv_len_dev.item()))
+            if c.pooled:  # the pool's tables before the step
+                rec.update(tables=[t[idx].cpu().numpy().copy() for t in (c.slot_of, c.slot_chunk, c.slot_used,
+                                                                         c.pool_clock)])
             pending = begin(q, idx)
             torch.cuda.synchronize()
             rows = c.batch_size * c.num_key_value_heads
             rec.update(gemm_o=c.gemm_o.cpu(), scores=c.chunk_attn.cpu(), offsets=c.offsets.view(rows, -1).cpu(),
                        cnts=c.cnts.cpu(), pos_after=c.position_ids[idx].cpu())
+            if c.pooled:
+                rec.update(slot_list=c.slot_list.view(rows, -1).cpu().numpy().copy(),
+                           tables_after=[t[idx].cpu().numpy().copy() for t in (c.slot_of, c.slot_chunk, c.slot_used,
+                                                                               c.pool_clock)])
             self.records[(i, idx)] = rec
             self._open[id(pending)] = (i, idx)
             return pending
@@ -141,9 +148,10 @@ class LayerProbe:
                 torch.cuda.synchronize()
                 rec = self.records[key]
                 L = rec["kv_len"]
+                end_row = L + (c.pool_delta if c.pooled else 0)
                 rec.update(out=out.reshape(out.shape[0], out.shape[2], -1).cpu(),
-                           kbuf_after=c.k_cache_buffer[key[1]][:, :, :L].cpu(),
-                           vbuf_after=c.v_cache_buffer[key[1]][:, :, :L].cpu())
+                           kbuf_after=c.k_cache_buffer[key[1]][:, :, :end_row].cpu(),
+                           vbuf_after=c.v_cache_buffer[key[1]][:, :, :end_row].cpu())
             return out
 
         lane.attn.decode_begin_appended = probe_begin
@@ -205,6 +213,61 @@ def check_layer_record(rec, cache, layer, cos_sin_cpu, what=""):
         miss = sp0 + int(res["cnts"][r]) * c
         assert torch.equal(kdev[b, h, :miss], kref[b, h, :miss]), f"{what}: key rows before the misses, row {r}"
         assert torch.equal(kdev[b, h, sp1:], kref[b, h, sp1:]), f"{what}: generated key rows, row {r}"
+    torch.testing.assert_close(kdev.float(), kref.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(rec["out"].float(), res["out"].float(), rtol=2e-2, atol=2e-2)
+    return res
+
+
+def check_pooled_layer_record(rec, cache, layer, cos_sin_cpu, what=""):
+    """One recorded layer step of one lane of a cache with a chunk pool against the oracle's pooled
+    step, from the device's own GQA-max scores and the pool's recorded tables: the hit counts, slot
+    list, misses and tables bit-exact; the value buffer (pool slots, local and generated rows)
+    bit-exact; key rows outside the misses' slots bit-exact, rebuilt ones and the attention output
+    within rtol 2e-2 / atol 2e-2."""
+    import numpy as np
+
+    import oracle
+    B, H = cache.batch_size, cache.num_key_value_heads
+    S, c, sp0, sp1 = cache.select_sets, cache.chunk_size, cache.sparse_start, cache.sparse_end
+    P, delta = cache.pool_slots, cache.pool_delta
+    landmarks = cache.k_landmark[layer].cpu()
+    n, D = landmarks.shape[-2], landmarks.shape[-1]
+    q = rec["q"]
+    G = q.shape[1] // H
+    logits_dev = rec["gemm_o"].view(B * H, G, n)
+    logits_ref, _ = oracle.score_logits_softmax(q.reshape(B * H, G, D), landmarks.reshape(B * H, n, D),
+                                                1.0 / 128 ** 0.5)
+    assert_bf16_close(logits_dev, logits_ref, what=f"{what} logits")
+    host_v = cache.v_cache_cpu[layer].cpu()
+    st = oracle.LayerState(U=cache.U[layer].cpu(), SV=cache.SV[layer].cpu(), landmarks=landmarks,
+                           landmark_idx=cache.k_landmark_idx[layer].cpu(), host_v=host_v,
+                           kbuf=rec["kbuf"].clone(), vbuf=rec["vbuf"].clone(), position_ids=rec["pos_before"].clone(),
+                           prefill_local=cache.prefill_local, sparse_start=sp0, sparse_end=sp1, chunk=c,
+                           budget=cache.sparse_budget, ctx=cache.prefill, buf_len=cache.buf_len - delta,
+                           chunks=cache.chunks)
+    slot_of, slot_chunk, slot_used, clock = (t.copy() for t in rec["tables"])
+    pool = dict(P=P, delta=delta, kbuf=rec["kbuf"].clone(), vbuf=rec["vbuf"].clone(), slot_of=slot_of,
+                slot_chunk=slot_chunk, slot_used=slot_used, clock=clock)
+    L = rec["kv_len"]
+    k_new, v_new = rec["kbuf"][:, :, L - 1 + delta], rec["vbuf"][:, :, L - 1 + delta]
+    res = oracle.decode_layer_step_pooled(st, pool, q, k_new, v_new, cos_sin_cpu, gen_offset=L - 1 - sp1,
+                                          scores=rec["scores"])
+    assert res["L"] == L
+    assert np.array_equal(rec["cnts"].numpy(), res["cnts"]), f"{what}: hit counts"
+    assert np.array_equal(rec["slot_list"], res["slot_list"]), f"{what}: slot list"
+    for got, want, name in zip(rec["tables_after"], (pool["slot_of"], pool["slot_chunk"], pool["slot_used"],
+                                                     pool["clock"]), ("slot_of", "slot_chunk", "slot_used", "clock")):
+        assert np.array_equal(got, want), f"{what}: {name}"
+    end_row = L + delta
+    assert torch.equal(rec["vbuf_after"], pool["vbuf"][:, :, :end_row]), f"{what}: value buffer"
+    kdev, kref = rec["kbuf_after"], pool["kbuf"][:, :, :end_row]
+    rebuilt = torch.zeros(B, H, end_row, dtype=torch.bool)
+    for r in range(B * H):
+        b, h = divmod(r, H)
+        for i in range(int(res["cnts"][r]), S):
+            v = int(res["miss_slot"][r, i])
+            rebuilt[b, h, sp0 + v * c:sp0 + (v + 1) * c] = True
+    assert torch.equal(kdev[~rebuilt], kref[~rebuilt]), f"{what}: key rows outside the misses' slots"
     torch.testing.assert_close(kdev.float(), kref.float(), rtol=2e-2, atol=2e-2)
     torch.testing.assert_close(rec["out"].float(), res["out"].float(), rtol=2e-2, atol=2e-2)
     return res

@@ -10,7 +10,9 @@
   against oracle.decode_layer_step from the device's own scores (selection, offsets, hit
   counts, slot ids and value buffer bit-exact; keys and attention within rtol/atol 2e-2).
   The step checked is the second one, so the generated tail holds a token of the first.
-* The same Llama-3.1-8B step from a prompt state built by the device encoder (two layers).
+* The same Llama-3.1-8B step from a prompt state built by the device encoder (two layers), with
+  the value store in device memory (batch 8 and batch 24), and with a chunk pool of 2048 slots
+  after 12 steps that fill it (against oracle.decode_layer_step_pooled from the recorded tables).
 * The prefill's rank-160 factors at ctx 122880 against torch.linalg.svd on the device.
 """
 import gc
@@ -24,7 +26,7 @@ from shadowkv_amd import decode_model
 from shadowkv_amd.kernels import shadowkv
 from shadowkv_amd.models.kvcache.shadow import low_rank_factors
 from shadowkv_amd.models.tensor_op import build_cos_sin_cache
-from tests.decode_harness import LayerProbe, assert_bf16_close, check_layer_record
+from tests.decode_harness import LayerProbe, assert_bf16_close, check_layer_record, check_pooled_layer_record
 
 pytestmark = pytest.mark.gpu
 
@@ -170,6 +172,37 @@ def test_decode_llama31_8b_batch24_ctx122880_device_store(gpu):
     memory: one lane of 192 (b, h) rows, so the selection takes its one-workgroup-per-row path and
     the projections run on hipBLASLt; the first and last layer against the oracle."""
     _decode_and_check(decode_model.LLAMA31_8B, 24, CTX, 2048, [0, 31], gpu, value_store="device")
+
+
+def test_decode_llama31_8b_batch8_ctx122880_pool(gpu):
+    """The batch-8 ctx-122880 step with a chunk pool of 2048 slots per (b, h) and layer, after 12
+    steps that fill it (about 13% of a step's chunks then hit): every lane's first and last layer
+    against the oracle's pooled step from the recorded tables (two lanes, each lane's misses
+    fetched and rebuilt into their slots by one launch on its own stream)."""
+    shape, batch, ctx, budget, P = decode_model.LLAMA31_8B, 8, CTX, 2048, 2048
+    _release()
+    lanes = decode_model.auto_lanes(shape, batch, budget,
+                                    miss_fraction=decode_model.pool_miss_fraction(P, ctx // 8))
+    _say(f"{shape.name} batch {batch} ctx {ctx} budget {budget}: building ({lanes} lane(s), pool of {P} slots)")
+    dec = decode_model.SyntheticDecoder(shape, batch, ctx, sparse_budget=budget, decode_len=16, lanes=lanes, seed=7,
+                                        host_stores=2, chunk_cache=P)
+    assert all(lane.cache.one_stream_active() for lane in dec.lanes)
+    tok = torch.randint(0, shape.vocab, (batch, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(1))
+    for _ in range(12):
+        tok = dec.decode_step(tok)
+    probe = LayerProbe(dec, [0, 31])
+    dec.decode_step(tok)
+    torch.cuda.synchronize()
+    _say(f"{shape.name}: pooled step done, checking {len(probe.records)} lane-layers against the oracle")
+    cs = dec.cos_sin.cpu()
+    for (i, layer), rec in sorted(probe.records.items()):
+        res = check_pooled_layer_record(rec, dec.lanes[i].cache, layer, cs, what=f"pool lane {i} layer {layer}")
+        hits = int(res["cnts"].sum())
+        _say(f"  lane {i} layer {layer}: hits {hits} of {res['cnts'].size * dec.cache.select_sets}, ok")
+        assert hits > 0
+    assert len(probe.records) == len(dec.lanes) * 2
+    del dec, probe
+    _release()
 
 
 def test_decode_glm4_9b_batch4_ctx262144(gpu):
