@@ -86,9 +86,25 @@ def test_one_launch_slots_equals_gather_then_rebuild(gpu, B, H, S, P, glm, R, c)
     two calls it replaces (gather_copy_misses_to_slots, rebuild_k_rope with miss_slot): value and
     key buffers bit-identical, pool rows of misses only and of hits only, rebuild workgroups
     capped or not; slots the miss list does not name are left untouched."""
+    _one_launch_slots_case(gpu, B, H, S, P, glm, R, c, B * 1000 + H * 100 + S + P)
+
+
+def test_one_launch_slots_random_shapes(gpu):
+    """The same equality on 8 seeded random pools: batch 1-4, 1-8 heads, 1-300 selected chunks of
+    4, 8 or 16 rows in pools of S to 4S slots, ranks 8-192, both rotary layouts."""
+    import numpy as np
+    rng = np.random.default_rng(97)
+    for case in range(8):
+        B, H = int(rng.integers(1, 5)), int(rng.choice([1, 2, 3, 8]))
+        S, c = int(rng.integers(1, 301)), int(rng.choice([4, 8, 16]))
+        P = int(rng.integers(S, 4 * S + 1))
+        R, glm = 8 * int(rng.integers(1, 25)), bool(rng.integers(0, 2))
+        _one_launch_slots_case(gpu, B, H, S, P, glm, R, c, 7000 + case)
+
+
+def _one_launch_slots_case(gpu, B, H, S, P, glm, R, c, seed):
     print(f"pool fetch+rebuild one launch B={B} H={H} S={S} P={P} glm={glm} rank={R} chunk={c}", flush=True)
     D = 128
-    seed = B * 1000 + H * 100 + S + P
     chunks = max(4 * S, 2048)
     ctx = chunks * c
     sparse_start = 64
