@@ -249,3 +249,33 @@ def test_device_value_store_matches_host_store(gpu, lanes, in_place):
         assert torch.equal(th, td), ("replay", t)
         for a, b in zip(state(host), state(dev)):
             assert torch.equal(a, b), ("replay", t)
+
+
+def test_device_value_store_with_chunk_pool_matches_host_store(gpu):
+    """A chunk pool over a value store in device memory (the pool's misses gathered from HBM by the
+    slot-mapped one launch, no in-place reads) gives the same tokens and cache state, bit for bit,
+    as the same pool over the pinned host store; eager steps and captured graph replays."""
+    print("device value store vs pinned host store, both with a pool of 512 slots, batch 8 in 1 lane", flush=True)
+    shape = replace(decode_model.LLAMA31_8B, layers=2, vocab=1000)
+    kw = dict(sparse_budget=2048, decode_len=12, lanes=1, seed=31, chunk_cache=512)
+    host = decode_model.SyntheticDecoder(shape, 8, 16384, **kw)
+    dev = decode_model.SyntheticDecoder(shape, 8, 16384, value_store="device", **kw)
+    for hl, dl in zip(host.lanes, dev.lanes):
+        assert hl.cache.v_cache_cpu[0].is_pinned() and dl.cache.v_cache_cpu[0].is_cuda
+        assert not dl.cache.values_in_place and dl.cache.one_stream_active() and hl.cache.one_stream_active()
+    th = td = torch.randint(0, shape.vocab, (8, 1), device=gpu, generator=torch.Generator(device=gpu).manual_seed(5))
+    for t in range(3):
+        th = host.decode_step(th)
+        td = dev.decode_step(td)
+        torch.cuda.synchronize()
+        assert torch.equal(th, td), t
+        for a, b in zip(_state(host), _state(dev)):
+            assert torch.equal(a, b), t
+    host.capture(th, steps=2)
+    dev.capture(td, steps=2)
+    for t in range(2):
+        th, td = host.replay(), dev.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(th, td), ("replay", t)
+        for a, b in zip(_state(host), _state(dev)):
+            assert torch.equal(a, b), ("replay", t)
