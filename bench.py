@@ -785,17 +785,23 @@ def device_store_variant(args, shape, batch: int) -> dict:
         release()
         log(f"device value store variant: batch {batch} does not fit: {e}")
         return {"batch": batch, "skipped": f"state does not fit in device memory: {str(e).splitlines()[0]}"}
-    tok = torch.randint(0, shape.vocab, (batch, 1), device="cuda")
-    for _ in range(args.warmup):
-        tok = dm.decode_step(tok)
-    per_call = math.gcd(args.steps, max(1, args.graph_steps))
-    dm.capture(tok, steps=per_call)
-    torch.cuda.synchronize()
-    start = time.perf_counter()
-    for _ in range(args.steps // per_call):
-        tok = dm.replay()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
+    try:
+        tok = torch.randint(0, shape.vocab, (batch, 1), device="cuda")
+        for _ in range(args.warmup):
+            tok = dm.decode_step(tok)
+        per_call = math.gcd(args.steps, max(1, args.graph_steps))
+        dm.capture(tok, steps=per_call)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(args.steps // per_call):
+            tok = dm.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+    except torch.cuda.OutOfMemoryError as e:  # the step's own buffers (workspaces, graph pool) do not fit
+        del dm
+        release()
+        log(f"device value store variant: batch {batch} steps do not fit: {e}")
+        return {"batch": batch, "skipped": f"decode steps do not fit in device memory: {str(e).splitlines()[0]}"}
     store_gb = sum(t.numel() * t.element_size() for t in {id(t): t for t in dm.cache.v_cache_cpu}.values()) \
         * len(dm.lanes) / 1e9
     res = {"batch": batch, "tokens_per_s": round(batch * args.steps / elapsed, 3),
