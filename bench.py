@@ -722,8 +722,16 @@ def pool_variant(args, shape, P: int) -> dict:
     lanes = decode_model.auto_lanes(shape, args.batch, args.budget,
                                     miss_fraction=decode_model.pool_miss_fraction(P, args.ctx // args.chunk))
     log(f"chunk pool variant: {P} slots per (b, h) and layer, {lanes} lane(s), {warm} untimed steps")
-    pm = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget, chunk_size=args.chunk,
-                                       decode_len=warm + args.steps + 8, lanes=lanes, chunk_cache=P)
+    try:
+        pm = decode_model.SyntheticDecoder(shape, args.batch, args.ctx, sparse_budget=args.budget,
+                                           chunk_size=args.chunk, decode_len=warm + args.steps + 8, lanes=lanes,
+                                           chunk_cache=P)
+    except torch.cuda.OutOfMemoryError as e:
+        gc.collect()
+        torch.cuda.empty_cache()
+        torch._C._host_emptyCache()
+        log(f"chunk pool variant: {P} slots do not fit: {e}")
+        return {"slots": P, "skipped": f"the pool does not fit in device memory: {str(e).splitlines()[0]}"}
     tok = torch.randint(0, shape.vocab, (args.batch, 1), device="cuda")
     for _ in range(warm):
         tok = pm.decode_step(tok)
